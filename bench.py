@@ -1,0 +1,281 @@
+#!/usr/bin/env python3
+"""Benchmark of the W4A16 / PLE hot path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-extra]
+
+Headline (`value`): decode W4A16 GEMV, M=1, K=1536, N=6144 (the E2B
+gate/up shape; BF16 activations, BF16 group-32 scales, FP32 accumulate,
+FP32 output).  One step = one GEMV launch.  Steps rotate over 128 distinct
+device copies of the weights (680 MB, well beyond the 256 MB Infinity Cache
+and the 8 x 4 MB L2), so every step streams its 5.3 MB from HBM.  The launches
+are recorded once into a command buffer (HIP graph) and replayed, so the host
+launch path is not what is timed.  value = algorithmic bytes of K steps / time.
+
+Algorithmic bytes per GEMV = N*K/2 packed + N*(K/32)*2 scales + K*2 x (BF16)
++ N*4 y (FP32) = 5,336,064 B.
+
+Extras (same JSON line, "extra"): one E2B sliding decoder layer of 7 GEMVs
+(aggregate GB/s), PLE gather of 1 and 2048 ids over the full [262144, 8960]
+table, the tied BF16 LM head over 262144 rows, and the prefill GEMM
+(M=2048) at both shapes in TFLOP/s.
+
+cpu_baseline: the oracle's TF.js-semantics FP32 dequant + matMul
+restatement (single-threaded C, the reference's CPU path is single-threaded
+JS) timed on the host on a bounded number of config-0 GEMVs.
+"""
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "gemma4-js_amd"))
+
+import numpy as np  # noqa: E402
+
+import g4hip  # noqa: E402
+import synthetic as syn  # noqa: E402
+
+METRIC = "W4A16 GEMV GB/s (% of 8 TB/s HBM) + decode tok/s, E2B-shaped, 1 MI355X"
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+COLD_BYTES = 640e6  # rotation footprint: > 2x the 256 MB Infinity Cache
+
+
+def w4_bytes(n, k, m=1, x_bytes=2, y_bytes=4):
+    return n * k // 2 + n * (k // 32) * 2 + m * k * x_bytes + m * n * y_bytes
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def time_cmdbufs(cbs, reps):
+    """Submit each command buffer in `cbs` `reps` times; return elapsed ms."""
+    e0, e1 = g4hip.Event(), g4hip.Event()
+    e0.record()
+    for _ in range(reps):
+        for cb in cbs:
+            cb.submit()
+    e1.record()
+    return e0.elapsed_ms(e1)
+
+
+def record(fn):
+    with g4hip.Encoder() as enc:
+        fn()
+    return enc.cmdbuf
+
+
+def bench_gemv(n, k, steps, warmup, seed=0):
+    packed, scales, _ = syn.w4_weights(seed, n, k)
+    per = w4_bytes(n, k)
+    copies = max(2, int(math.ceil(COLD_BYTES / per)))
+    copies = min(copies, 128) if per > 4e6 else copies
+    lins = [g4hip.W4Linear(packed, scales) for _ in range(copies)]
+    x_bits, _ = syn.activations(seed, 1, k)
+    x = g4hip.Buffer.from_array(x_bits)
+    y = g4hip.Buffer(n * 4)
+
+    def launches(count):
+        def f():
+            for i in range(count):
+                lins[i % copies].linear(x.ptr, g4hip.BF16, 1, y.ptr, g4hip.F32)
+        return f
+
+    full = record(launches(copies))
+    rem = steps % copies
+    tail = record(launches(rem)) if rem else None
+    time_cmdbufs([full], max(1, warmup // copies))
+    g4hip.sync()
+    ms = time_cmdbufs([full], steps // copies)
+    if tail:
+        ms += time_cmdbufs([tail], 1)
+    return {"bytes_per_step": per, "copies": copies, "ms": ms, "steps": steps,
+            "gbs": per * steps / (ms * 1e-3) / 1e9}
+
+
+E2B_SLIDING_LAYER = [("q", 2048, 1536), ("k", 256, 1536), ("v", 256, 1536), ("o", 1536, 2048),
+                     ("gate", 6144, 1536), ("up", 6144, 1536), ("down", 1536, 6144)]
+
+
+def bench_layer(reps=50, seed=1):
+    """Config 2: the 7 GEMVs of one E2B sliding layer, M=1, chained through
+    their real input sizes; rotated over enough layer copies to stay cold."""
+    mats = [(name, syn.w4_weights(seed + i, n, k)[:2], n, k)
+            for i, (name, n, k) in enumerate(E2B_SLIDING_LAYER)]
+    layer_bytes = sum(w4_bytes(n, k) for _, _, n, k in mats)
+    copies = int(math.ceil(COLD_BYTES / layer_bytes))
+    layers = [[g4hip.W4Linear(p, s) for _, (p, s), _, _ in mats] for _ in range(copies)]
+    xs = {k: g4hip.Buffer.from_array(syn.activations(seed, 1, k)[0]) for k in (1536, 2048, 6144)}
+    ys = {n: g4hip.Buffer(n * 4) for n in (2048, 256, 1536, 6144)}
+
+    def f():
+        for layer in layers:
+            for lin, (_, _, n, k) in zip(layer, mats):
+                lin.linear(xs[k].ptr, g4hip.BF16, 1, ys[n].ptr, g4hip.F32)
+
+    cb = record(f)
+    time_cmdbufs([cb], 2)
+    ms = time_cmdbufs([cb], reps)
+    n_layers = reps * copies
+    return {"gemvs_per_layer": 7, "bytes_per_layer": layer_bytes, "copies": copies,
+            "us_per_layer": ms * 1e3 / n_layers,
+            "gbs": layer_bytes * n_layers / (ms * 1e-3) / 1e9}
+
+
+def bench_ple(reps=200, seed=2024):
+    vocab, width, rps = 262144, 8960, 4096
+    t0 = time.time()
+    shards = syn.ple_table(seed, vocab, width, rps, threads=16)
+    t = g4hip.PleTable(vocab, width, 32, rps)
+    for i, s in enumerate(shards):
+        t.upload_shard(i, s)
+    del shards
+    log("  PLE table generated+uploaded in %.1fs" % (time.time() - t0))
+    res = {}
+    for n in (1, 2048):
+        # distinct id sets per replay so rows are not re-served from cache
+        sets = [syn.token_ids(seed + r, n, vocab) for r in range(16)]
+        idb = [g4hip.Buffer.from_array(s) for s in sets]
+        for dtype, name in ((g4hip.F32, "f32"), (g4hip.BF16, "bf16")):
+            ob = g4hip.Buffer(n * width * (4 if dtype == g4hip.F32 else 2))
+
+            def f():
+                for b in idb:
+                    t.gather_dev(b.ptr, n, ob.ptr, dtype)
+
+            cb = record(f)
+            time_cmdbufs([cb], 2)
+            ms = time_cmdbufs([cb], reps // 16 if n > 1 else reps)
+            calls = len(idb) * (reps // 16 if n > 1 else reps)
+            per = n * (width // 2 + (width // 32) * 2 + 4) + n * width * (4 if dtype == g4hip.F32 else 2)
+            res["ids%d_%s" % (n, name)] = {"us_per_call": ms * 1e3 / calls, "bytes_per_call": per,
+                                          "gbs": per * calls / (ms * 1e-3) / 1e9}
+    t.free()
+    return res
+
+
+def bench_head(reps=20, seed=12):
+    vocab, k = 262144, 1536
+    rng = np.random.default_rng(seed)
+    E = g4hip.Buffer(vocab * k * 2)
+    step = 16384
+    for r0 in range(0, vocab, step):
+        E.upload(syn.bf16_rne(rng.standard_normal((step, k), dtype=np.float32) * np.float32(0.03)),
+                 r0 * k * 2)
+    h = g4hip.Buffer.from_array(rng.standard_normal(k).astype(np.float32))
+    out = g4hip.Buffer(vocab * 4)
+    cb = record(lambda: g4hip.bf16_head(h.ptr, E.ptr, vocab, k, out.ptr, 1.0, 30.0))
+    time_cmdbufs([cb], 2)
+    ms = time_cmdbufs([cb], reps)
+    per = vocab * k * 2 + k * 4 + vocab * 4
+    return {"us_per_call": ms * 1e3 / reps, "bytes_per_call": per,
+            "gbs": per * reps / (ms * 1e-3) / 1e9}
+
+
+def bench_gemm(reps=3, seed=3):
+    res = {}
+    for n, k in ((6144, 1536), (1536, 6144)):
+        packed, scales, _ = syn.w4_weights(seed, n, k)
+        lin = g4hip.W4Linear(packed, scales)
+        x = g4hip.Buffer.from_array(syn.activations(seed, 2048, k)[0])
+        y = g4hip.Buffer(2048 * n * 4)
+        cb = record(lambda: lin.linear(x.ptr, g4hip.BF16, 2048, y.ptr, g4hip.F32))
+        time_cmdbufs([cb], 1)
+        ms = time_cmdbufs([cb], reps)
+        flops = 2.0 * 2048 * n * k
+        tf = flops * reps / (ms * 1e-3) / 1e12
+        res["M2048_N%d_K%d" % (n, k)] = {"ms": ms / reps, "tflops": tf,
+                                         "frac_of_bf16_peak": tf / BF16_PEAK_TFLOPS}
+    return res
+
+
+def cpu_baseline(n, k, budget_s=10.0, seed=0):
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import g4oracle
+    packed, scales, _ = syn.w4_weights(seed, n, k)
+    _, x = syn.activations(seed, 1, k)
+    g4oracle.w4_linear(x, packed, scales)  # warm
+    calls, t0 = 0, time.perf_counter()
+    while True:
+        g4oracle.w4_linear(x, packed, scales)
+        calls += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s:
+            break
+    return {"value": w4_bytes(n, k) * calls / el / 1e9, "unit": "GB/s", "cores": 1,
+            "kind": "port",
+            "sample": "%d config-0 GEMVs (M1 K%d N%d) through the oracle's TF.js-semantics "
+                      "restatement (FP32 dequant per 256-row chunk, then blocked FP32 matMul), "
+                      "%.1f s, %.1f ms/GEMV" % (calls, k, n, el, el / calls * 1e3)}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=2048)
+    ap.add_argument("--warmup", type=int, default=256)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-extra", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py runs on one GPU: --gpus %d is not supported (the path is measured on a "
+              "single MI355X; multi-GPU sharding is design-only)" % args.gpus, file=sys.stderr)
+        sys.exit(2)
+
+    g4hip.init(0)
+    info = g4hip.device_info()
+    log("device:", info)
+    n, k = 6144, 1536
+    log("GEMV M1 K%d N%d: %d steps (+%d warmup)" % (k, n, args.steps, args.warmup))
+    g = bench_gemv(n, k, args.steps, args.warmup)
+    avg_us = g["ms"] * 1e3 / g["steps"]
+    achieved = g["bytes_per_step"] / (avg_us * 1e-6) / 1e9
+    log("  %.3f us/GEMV, %.1f GB/s" % (avg_us, g["gbs"]))
+
+    extra = {}
+    if not args.no_extra:
+        log("layer (config 2) ...")
+        extra["layer_e2b_sliding_7gemv"] = bench_layer()
+        log("  ", extra["layer_e2b_sliding_7gemv"])
+        log("PLE gather (config 1) ...")
+        extra["ple_gather"] = bench_ple()
+        log("  ", extra["ple_gather"])
+        log("BF16 LM head ...")
+        extra["lm_head_262144x1536"] = bench_head()
+        log("  ", extra["lm_head_262144x1536"])
+        log("prefill GEMM (config 3) ...")
+        extra["gemm_prefill"] = bench_gemm()
+        log("  ", extra["gemm_prefill"])
+
+    cpu = None
+    if not args.no_cpu:
+        log("CPU baseline (oracle, 1 core) ...")
+        cpu = cpu_baseline(n, k, args.cpu_seconds)
+        log("  ", cpu)
+
+    line = {
+        "metric": METRIC, "value": round(g["gbs"], 2), "unit": "GB/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": g["ms"] / args.steps,
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "fp32",
+        "data": "synthetic (seeded int4 weights in [-7,7], bf16 scales |N|*0.02, bf16 N(0,1) x)",
+        "config": {"workload": "W4A16 decode GEMV M=1 K=1536 N=6144, cold (128 rotating weight "
+                               "copies), BF16 x, FP32 y", "M": 1, "K": k, "N": n,
+                   "group": 32, "weight_copies": g["copies"], "device": info["name"],
+                   "cu_count": info["cu_count"]},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "w4_gemv_kernel", "avg_launch_us": round(avg_us, 4),
+                     "bytes_per_launch": g["bytes_per_step"]},
+        "cpu_baseline": cpu,
+        "extra": extra,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

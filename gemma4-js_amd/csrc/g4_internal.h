@@ -1,0 +1,104 @@
+// Internal helpers shared by the gfx950 translation units of libg4hip.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "g4hip.h"
+
+#define G4_API extern "C" __attribute__((visibility("default")))
+
+namespace g4 {
+
+// Records `code` and a printf-style message for g4_last_error(); returns code.
+int fail(int code, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
+// Clears the last error and returns G4_OK.
+int ok();
+
+// The library stream; nullptr until g4_init succeeded.
+hipStream_t stream();
+bool initialised();
+// True between g4_encoder_begin and g4_encoder_finish (stream capture).
+bool encoding();
+
+// Checks that [p, p + bytes) lies inside one live device allocation.  `what`
+// names the operand in the error message.  Returns G4_OK or G4_E_RANGE.
+int check_device_range(const void *p, size_t bytes, const char *what);
+
+// Stream-ordered device allocation used by the object handles (zero-filled).
+int device_alloc(size_t bytes, void **p);
+int device_free(void *p);
+
+// Device attribute cache.
+int cu_count();
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// Streaming (non-temporal) 16-byte loads and stores for data touched once.
+__device__ __forceinline__ uint4 ld_nt(const uint4 *p) {
+  const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p));
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ void st_nt(uint4 *p, uint4 v) {
+  const u32x4 u = {v.x, v.y, v.z, v.w};
+  __builtin_nontemporal_store(u, reinterpret_cast<u32x4 *>(p));
+}
+__device__ __forceinline__ void st_nt(float4 *p, float4 v) {
+  const f32x4 u = {v.x, v.y, v.z, v.w};
+  __builtin_nontemporal_store(u, reinterpret_cast<f32x4 *>(p));
+}
+
+}  // namespace g4
+
+#define G4_CHECK_INIT()                                                     \
+  do {                                                                      \
+    if (!::g4::initialised())                                               \
+      return ::g4::fail(G4_E_STATE, "%s: g4_init() has not been called",    \
+                        __func__);                                          \
+  } while (0)
+
+// Entry points that synchronise or move host memory cannot be recorded.
+#define G4_CHECK_NOT_ENCODING()                                              \
+  do {                                                                      \
+    if (::g4::encoding())                                                   \
+      return ::g4::fail(G4_E_STATE, "%s: not allowed while a command "      \
+                        "encoder is open", __func__);                       \
+  } while (0)
+
+#define G4_HIP_TRY(call)                                                    \
+  do {                                                                      \
+    hipError_t e_ = (call);                                                 \
+    if (e_ != hipSuccess)                                                   \
+      return ::g4::fail(G4_E_HIP, "%s failed: %s (%s:%d)", #call,           \
+                        hipGetErrorString(e_), __FILE__, __LINE__);         \
+  } while (0)
+
+// After a kernel launch: report a launch-configuration error, if any.
+#define G4_LAUNCH_CHECK(name)                                               \
+  do {                                                                      \
+    hipError_t e_ = hipGetLastError();                                      \
+    if (e_ != hipSuccess)                                                   \
+      return ::g4::fail(G4_E_HIP, "launch of %s failed: %s", name,          \
+                        hipGetErrorString(e_));                             \
+  } while (0)
+
+// ---- device-side helpers ---------------------------------------------------
+
+namespace g4 {
+
+__device__ __forceinline__ float bf16_to_f32(uint32_t bits16) {
+  return __uint_as_float(bits16 << 16);
+}
+
+// Round-to-nearest-even of the upper 16 bits, the exact arithmetic of
+// roundFloat32ToBF16 (official-w4a16.js:34-48): bits + 0x7fff + lsb, then
+// truncate.  Like the reference it has no special case for NaN payloads.
+__device__ __forceinline__ uint32_t f32_to_bf16_rne(float v) {
+  uint32_t b = __float_as_uint(v);
+  b += 0x7fffu + ((b >> 16) & 1u);
+  return b >> 16;
+}
+
+}  // namespace g4

@@ -1,0 +1,253 @@
+// Per-layer-embedding (PLE) W4 gather-dequant: the gfx950 replacement of
+// W4PleShardBundle.rowsToGpu + the PLE dequant shader
+// (custom-webgpu/gpu-runtime.js:190-256, 413-527).
+//
+// The reference gathers the rows of the requested token ids on the CPU (two
+// File.slice reads per id), uploads them and dequantizes on the GPU.  Here
+// the whole table stays resident in HBM (1.32 GB for [262144, 8960]) in the
+// exact byte layout of the builder's shards (tools/build_ple_w4_full.py:
+// 130-170), and the gather runs on the device:
+//
+//   shard s = id / rows_per_shard, local row = id - s * rows_per_shard
+//   packed  at shard_base + local * (width/2)                 (low nibble first,
+//                                                              two's complement)
+//   scales  at shard_base + rows_in_shard * (width/2) + local * (width/32 * 2)
+//
+// Element i of a row is nibble (i & 1) of byte i >> 1, i.e. bits 4k..4k+3 of
+// the little-endian 32-bit word holding elements 8w..8w+7 - the same order as
+// the W4 linear weights; only the signed decoding differs (q = n >= 8 ? n - 16
+// : n, ple-w4-shard-reader.js:89-96), which equals (n ^ 8) - 8.
+#include <string.h>
+
+#include "g4_internal.h"
+
+struct g4_ple {
+  int vocab, width, group, rows_per_shard, num_shards;
+  size_t packed_row, scale_row, full_shard_bytes, total_bytes;
+  uint8_t *table;
+  int32_t *ids_dev;     // device staging for host ids
+  int32_t *ids_host;    // pinned staging for host ids
+  int ids_cap;
+  hipEvent_t ids_done;  // last copy out of ids_host has finished
+};
+
+namespace {
+
+using namespace g4;
+
+// One thread per (token, 32-column group): a 16-byte packed load, one scale,
+// 32 outputs.  Consecutive threads walk consecutive groups of a row, so the
+// packed reads and the output writes are both contiguous streams.
+__global__ __launch_bounds__(256) void ple_gather_kernel(
+    const uint8_t *__restrict__ table, const int32_t *__restrict__ ids, int n,
+    void *__restrict__ out, int out_bf16, int vocab, int width,
+    int rows_per_shard, size_t packed_row, size_t scale_row,
+    size_t full_shard_bytes) {
+  const int gpr = width >> 5;  // groups per row
+  const size_t item = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (item >= (size_t)n * gpr) return;
+  const int j = (int)(item / gpr);
+  const int g = (int)(item - (size_t)j * gpr);
+  const int id = ids[j];
+  float v[32];
+  if (id < 0 || id >= vocab) {
+#pragma unroll
+    for (int i = 0; i < 32; ++i) v[i] = __uint_as_float(0x7fc00000u);
+  } else {
+    const int shard = id / rows_per_shard;
+    const int local = id - shard * rows_per_shard;
+    const int left = vocab - shard * rows_per_shard;
+    const int rows_in_shard = left < rows_per_shard ? left : rows_per_shard;
+    const uint8_t *base = table + (size_t)shard * full_shard_bytes;
+    const uint4 q = ld_nt(reinterpret_cast<const uint4 *>(base + (size_t)local * packed_row) + g);
+    const uint16_t sb = reinterpret_cast<const uint16_t *>(
+        base + (size_t)rows_in_shard * packed_row + (size_t)local * scale_row)[g];
+    const float s = bf16_to_f32(sb);
+    const uint32_t w[4] = {q.x ^ 0x88888888u, q.y ^ 0x88888888u, q.z ^ 0x88888888u,
+                           q.w ^ 0x88888888u};
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        v[8 * k + e] = (float)((int)((w[k] >> (4 * e)) & 15u) - 8) * s;
+  }
+  const size_t o = (size_t)j * width + (size_t)g * 32;
+  if (out_bf16) {
+    uint4 *dst = reinterpret_cast<uint4 *>(static_cast<uint16_t *>(out) + o);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      uint32_t p[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k)
+        p[k] = f32_to_bf16_rne(v[8 * i + 2 * k]) |
+               (f32_to_bf16_rne(v[8 * i + 2 * k + 1]) << 16);
+      st_nt(dst + i, make_uint4(p[0], p[1], p[2], p[3]));
+    }
+  } else {
+    float4 *dst = reinterpret_cast<float4 *>(static_cast<float *>(out) + o);
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      st_nt(dst + i, make_float4(v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]));
+  }
+}
+
+int launch_gather(const g4_ple *t, const int32_t *ids_dev, int n, void *out, int out_dtype) {
+  const size_t items = (size_t)n * (t->width / 32);
+  const unsigned blocks = (unsigned)((items + 255) / 256);
+  hipLaunchKernelGGL(ple_gather_kernel, dim3(blocks), dim3(256), 0, stream(), t->table,
+                     ids_dev, n, out, out_dtype == G4_BF16, t->vocab, t->width,
+                     t->rows_per_shard, t->packed_row, t->scale_row, t->full_shard_bytes);
+  G4_LAUNCH_CHECK("ple_gather_kernel");
+  return G4_OK;
+}
+
+int check_out(const g4_ple *t, int n, void *out, int out_dtype) {
+  if (out_dtype != G4_F32 && out_dtype != G4_BF16)
+    return fail(G4_E_ARG, "PLE gather: bad out dtype %d", out_dtype);
+  if ((reinterpret_cast<uintptr_t>(out) & 15u) != 0)
+    return fail(G4_E_ARG, "PLE gather: out must be 16-byte aligned");
+  return check_device_range(out, (size_t)n * t->width * (out_dtype == G4_F32 ? 4 : 2),
+                            "PLE gather out");
+}
+
+}  // namespace
+
+G4_API int g4_ple_create(int vocab, int width, int group, int rows_per_shard,
+                         g4_ple **out) {
+  G4_CHECK_INIT();
+  G4_CHECK_NOT_ENCODING();
+  if (!out) return fail(G4_E_ARG, "g4_ple_create: null output handle");
+  *out = nullptr;
+  if (vocab <= 0 || rows_per_shard <= 0)
+    return fail(G4_E_ARG, "g4_ple_create: bad vocab %d / rows_per_shard %d", vocab,
+                rows_per_shard);
+  // gpu-runtime.js:449-458 accepts width 8960 and group 32 only; the kernel
+  // needs width to be a multiple of the 32-column group.
+  if (group != 32 || width <= 0 || width % 32 != 0)
+    return fail(G4_E_ARG, "PLE shard manifest has unexpected geometry/layout.");
+  g4_ple *t = new g4_ple();
+  t->vocab = vocab;
+  t->width = width;
+  t->group = group;
+  t->rows_per_shard = rows_per_shard;
+  t->num_shards = (vocab + rows_per_shard - 1) / rows_per_shard;
+  t->packed_row = (size_t)width / 2;
+  t->scale_row = (size_t)(width / group) * 2;
+  t->full_shard_bytes = (size_t)rows_per_shard * (t->packed_row + t->scale_row);
+  t->total_bytes = (size_t)vocab * (t->packed_row + t->scale_row);
+  // Every shard must start 16-byte aligned for the kernel's 128-bit loads
+  // (true for the distribution: 4096 rows x 5040 bytes).
+  if (t->full_shard_bytes % 16 != 0) {
+    delete t;
+    return fail(G4_E_ARG, "g4_ple_create: shard size %d x %d bytes is not a multiple of 16",
+                rows_per_shard, width / 2 + (width / 32) * 2);
+  }
+  int rc = device_alloc(t->total_bytes, reinterpret_cast<void **>(&t->table));
+  if (rc) {
+    delete t;
+    return rc;
+  }
+  hipError_t e = hipEventCreateWithFlags(&t->ids_done, hipEventDisableTiming);
+  if (e != hipSuccess) {
+    device_free(t->table);
+    delete t;
+    return fail(G4_E_HIP, "hipEventCreate failed: %s", hipGetErrorString(e));
+  }
+  *out = t;
+  return ok();
+}
+
+G4_API int g4_ple_shard_bytes(const g4_ple *t, int shard, int *num_shards, size_t *bytes) {
+  if (!t) return fail(G4_E_ARG, "g4_ple_shard_bytes: null handle");
+  if (num_shards) *num_shards = t->num_shards;
+  if (shard < 0 || shard >= t->num_shards)
+    return fail(G4_E_RANGE, "PLE shard %d outside [0, %d)", shard, t->num_shards);
+  const int left = t->vocab - shard * t->rows_per_shard;
+  const int rows = left < t->rows_per_shard ? left : t->rows_per_shard;
+  if (bytes) *bytes = (size_t)rows * (t->packed_row + t->scale_row);
+  return ok();
+}
+
+G4_API int g4_ple_upload_shard(g4_ple *t, int shard, const void *bytes, size_t n) {
+  G4_CHECK_INIT();
+  G4_CHECK_NOT_ENCODING();
+  size_t want = 0;
+  int rc = g4_ple_shard_bytes(t, shard, nullptr, &want);
+  if (rc) return rc;
+  if (!bytes) return fail(G4_E_ARG, "g4_ple_upload_shard: null data");
+  if (n != want)
+    return fail(G4_E_ARG, "PLE shard %d has %zu bytes, expected %zu", shard, n, want);
+  G4_HIP_TRY(hipMemcpyAsync(t->table + (size_t)shard * t->full_shard_bytes, bytes, n,
+                            hipMemcpyHostToDevice, stream()));
+  G4_HIP_TRY(hipStreamSynchronize(stream()));
+  return ok();
+}
+
+G4_API int g4_ple_free(g4_ple *t) {
+  G4_CHECK_INIT();
+  G4_CHECK_NOT_ENCODING();
+  if (!t) return ok();
+  int rc = device_free(t->table);
+  if (t->ids_dev) device_free(t->ids_dev);
+  if (t->ids_host) {
+    (void)hipEventSynchronize(t->ids_done);
+    (void)hipHostFree(t->ids_host);
+  }
+  (void)hipEventDestroy(t->ids_done);
+  delete t;
+  return rc ? rc : ok();
+}
+
+G4_API int g4_ple_gather(const g4_ple *tc, const int32_t *ids, int n, void *out,
+                         int out_dtype) {
+  G4_CHECK_INIT();
+  G4_CHECK_NOT_ENCODING();
+  g4_ple *t = const_cast<g4_ple *>(tc);
+  if (!t) return fail(G4_E_ARG, "g4_ple_gather: null handle");
+  if (n < 0) return fail(G4_E_ARG, "g4_ple_gather: negative id count");
+  if (n == 0) return ok();
+  if (!ids) return fail(G4_E_ARG, "g4_ple_gather: null ids");
+  // _location (gpu-runtime.js:463-485): every id must be an integer in range.
+  for (int j = 0; j < n; ++j)
+    if (ids[j] < 0 || ids[j] >= t->vocab)
+      return fail(G4_E_RANGE, "PLE token id out of range: %d", ids[j]);
+  int rc = check_out(t, n, out, out_dtype);
+  if (rc) return rc;
+  if (n > t->ids_cap) {
+    G4_HIP_TRY(hipStreamSynchronize(stream()));
+    if (t->ids_dev) device_free(t->ids_dev);
+    if (t->ids_host) (void)hipHostFree(t->ids_host);
+    t->ids_dev = nullptr;
+    t->ids_host = nullptr;
+    t->ids_cap = 0;
+    int cap = n < 4096 ? 4096 : n;
+    rc = device_alloc((size_t)cap * 4, reinterpret_cast<void **>(&t->ids_dev));
+    if (rc) return rc;
+    G4_HIP_TRY(hipHostMalloc(reinterpret_cast<void **>(&t->ids_host), (size_t)cap * 4,
+                             hipHostMallocDefault));
+    t->ids_cap = cap;
+  } else {
+    // The previous gather may still be copying out of the pinned buffer.
+    G4_HIP_TRY(hipEventSynchronize(t->ids_done));
+  }
+  memcpy(t->ids_host, ids, (size_t)n * 4);
+  G4_HIP_TRY(hipMemcpyAsync(t->ids_dev, t->ids_host, (size_t)n * 4, hipMemcpyHostToDevice,
+                            stream()));
+  G4_HIP_TRY(hipEventRecord(t->ids_done, stream()));
+  rc = launch_gather(t, t->ids_dev, n, out, out_dtype);
+  return rc ? rc : ok();
+}
+
+G4_API int g4_ple_gather_dev(const g4_ple *t, const int32_t *ids_dev, int n, void *out,
+                             int out_dtype) {
+  G4_CHECK_INIT();
+  if (!t) return fail(G4_E_ARG, "g4_ple_gather_dev: null handle");
+  if (n < 0) return fail(G4_E_ARG, "g4_ple_gather_dev: negative id count");
+  if (n == 0) return ok();
+  int rc = check_device_range(ids_dev, (size_t)n * 4, "g4_ple_gather_dev ids");
+  if (rc) return rc;
+  rc = check_out(t, n, out, out_dtype);
+  if (rc) return rc;
+  rc = launch_gather(t, ids_dev, n, out, out_dtype);
+  return rc ? rc : ok();
+}

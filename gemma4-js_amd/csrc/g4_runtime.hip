@@ -1,0 +1,315 @@
+// Device, queue and buffer layer: the HIP replacement of gpu-runtime.js:6-38
+// (createBuffer / uploadBytes / uploadF32 / uploadU32 / readF32) and of the
+// WebGPU queue that orders every dispatch.
+//
+// One stream per process, created at g4_init with the default priority, plays
+// the role of device.queue: every upload, copy and kernel is enqueued on it,
+// so work runs in submission order as in the reference.
+#include <map>
+#include <mutex>
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include "g4_internal.h"
+
+namespace g4 {
+namespace {
+
+thread_local char g_err[1024] = "";
+hipStream_t g_stream = nullptr;
+bool g_encoding = false;
+int g_device = -1;
+int g_cu_count = 0;
+
+// Live device allocations: base -> size.  Used to bounds-check operands
+// before a kernel is launched.
+std::mutex g_mu;
+std::map<uintptr_t, size_t> g_allocs;
+
+}  // namespace
+
+int fail(int code, const char *fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof g_err, fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int ok() {
+  g_err[0] = '\0';
+  return G4_OK;
+}
+
+hipStream_t stream() { return g_stream; }
+bool initialised() { return g_stream != nullptr; }
+bool encoding() { return g_encoding; }
+int cu_count() { return g_cu_count; }
+
+int check_device_range(const void *p, size_t bytes, const char *what) {
+  if (p == nullptr) return fail(G4_E_ARG, "%s: null device pointer", what);
+  uintptr_t a = reinterpret_cast<uintptr_t>(p);
+  {
+    std::lock_guard<std::mutex> lk(g_mu);
+    auto it = g_allocs.upper_bound(a);
+    if (it != g_allocs.begin()) {
+      --it;
+      if (a >= it->first && a < it->first + it->second) {
+        if (bytes > it->first + it->second - a)
+          return fail(G4_E_RANGE,
+                      "%s: %zu bytes at offset %zu overrun its %zu-byte buffer",
+                      what, bytes, (size_t)(a - it->first), it->second);
+        return G4_OK;
+      }
+    }
+  }
+  // Not one of ours: ask the HIP runtime for the allocation's extent.
+  hipDeviceptr_t base = nullptr;
+  size_t size = 0;
+  if (hipMemGetAddressRange(&base, &size, (hipDeviceptr_t)p) != hipSuccess ||
+      base == nullptr) {
+    (void)hipGetLastError();
+    return fail(G4_E_RANGE, "%s: %p is not a device allocation", what, p);
+  }
+  size_t off = (size_t)(a - reinterpret_cast<uintptr_t>(base));
+  if (bytes > size - off)
+    return fail(G4_E_RANGE, "%s: %zu bytes at offset %zu overrun its %zu-byte buffer",
+                what, bytes, off, size);
+  return G4_OK;
+}
+
+int device_alloc(size_t bytes, void **p) {
+  if (!p) return fail(G4_E_ARG, "device_alloc: null output pointer");
+  size_t n = bytes < 4 ? 4 : (bytes + 3) & ~size_t(3);  // align4 (gpu-runtime.js:7)
+  void *d = nullptr;
+  hipError_t e = hipMalloc(&d, n);
+  if (e != hipSuccess) {
+    (void)hipGetLastError();
+    return fail(G4_E_NOMEM, "hipMalloc(%zu) failed: %s", n, hipGetErrorString(e));
+  }
+  e = hipMemsetAsync(d, 0, n, g_stream);
+  if (e != hipSuccess) {
+    (void)hipFree(d);
+    return fail(G4_E_HIP, "hipMemsetAsync failed: %s", hipGetErrorString(e));
+  }
+  {
+    std::lock_guard<std::mutex> lk(g_mu);
+    g_allocs[reinterpret_cast<uintptr_t>(d)] = n;
+  }
+  *p = d;
+  return G4_OK;
+}
+
+int device_free(void *p) {
+  if (!p) return G4_OK;
+  {
+    std::lock_guard<std::mutex> lk(g_mu);
+    auto it = g_allocs.find(reinterpret_cast<uintptr_t>(p));
+    if (it == g_allocs.end())
+      return fail(G4_E_ARG, "g4_free: %p was not allocated by g4_alloc", p);
+    g_allocs.erase(it);
+  }
+  // Work already queued may still read the buffer: drain the queue first
+  // (WebGPU's destroy() is likewise deferred until submitted work is done).
+  G4_HIP_TRY(hipStreamSynchronize(g_stream));
+  G4_HIP_TRY(hipFree(p));
+  return G4_OK;
+}
+
+}  // namespace g4
+
+using namespace g4;
+
+G4_API const char *g4_last_error(void) { return g4::g_err; }
+
+G4_API int g4_init(int device) {
+  if (g_stream) {
+    if (device == g_device) return ok();
+    return fail(G4_E_STATE, "g4_init: already initialised on device %d", g_device);
+  }
+  int n = 0;
+  G4_HIP_TRY(hipGetDeviceCount(&n));
+  if (device < 0 || device >= n)
+    return fail(G4_E_ARG, "g4_init: device %d out of range (%d visible)", device, n);
+  G4_HIP_TRY(hipSetDevice(device));
+  hipDeviceProp_t prop;
+  G4_HIP_TRY(hipGetDeviceProperties(&prop, device));
+  if (strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+    return fail(G4_E_STATE, "g4_init: device %d is %s; this library is built for gfx950",
+                device, prop.gcnArchName);
+  g_cu_count = prop.multiProcessorCount;
+  hipStream_t s = nullptr;
+  G4_HIP_TRY(hipStreamCreateWithFlags(&s, hipStreamNonBlocking));
+  g_stream = s;
+  g_device = device;
+  return ok();
+}
+
+G4_API int g4_device_info(char *name, size_t name_len, int *cu, size_t *hbm,
+                          int *clock_khz) {
+  G4_CHECK_INIT();
+  hipDeviceProp_t prop;
+  G4_HIP_TRY(hipGetDeviceProperties(&prop, g_device));
+  if (name && name_len) {
+    snprintf(name, name_len, "%s (%s)", prop.name, prop.gcnArchName);
+  }
+  if (cu) *cu = prop.multiProcessorCount;
+  if (hbm) *hbm = prop.totalGlobalMem;
+  if (clock_khz) *clock_khz = prop.clockRate;
+  return ok();
+}
+
+G4_API int g4_alloc(size_t bytes, void **dptr) {
+  G4_CHECK_INIT();
+  G4_CHECK_NOT_ENCODING();
+  int rc = device_alloc(bytes, dptr);
+  return rc ? rc : ok();
+}
+
+G4_API int g4_free(void *dptr) {
+  G4_CHECK_INIT();
+  G4_CHECK_NOT_ENCODING();
+  int rc = device_free(dptr);
+  return rc ? rc : ok();
+}
+
+G4_API int g4_upload(void *dst, size_t dst_off, const void *src, size_t n) {
+  G4_CHECK_INIT();
+  G4_CHECK_NOT_ENCODING();
+  if (n == 0) return ok();
+  if (!src) return fail(G4_E_ARG, "g4_upload: null host pointer");
+  int rc = check_device_range(static_cast<char *>(dst) + dst_off, n, "g4_upload dst");
+  if (rc) return rc;
+  // Pageable host memory: hipMemcpyAsync stages it, so `src` is free to reuse
+  // on return (queue.writeBuffer semantics).
+  G4_HIP_TRY(hipMemcpyAsync(static_cast<char *>(dst) + dst_off, src, n,
+                            hipMemcpyHostToDevice, g_stream));
+  G4_HIP_TRY(hipStreamSynchronize(g_stream));
+  return ok();
+}
+
+G4_API int g4_download(const void *src, size_t src_off, void *dst, size_t n) {
+  G4_CHECK_INIT();
+  G4_CHECK_NOT_ENCODING();
+  if (n == 0) return ok();
+  if (!dst) return fail(G4_E_ARG, "g4_download: null host pointer");
+  int rc = check_device_range(static_cast<const char *>(src) + src_off, n,
+                              "g4_download src");
+  if (rc) return rc;
+  G4_HIP_TRY(hipMemcpyAsync(dst, static_cast<const char *>(src) + src_off, n,
+                            hipMemcpyDeviceToHost, g_stream));
+  G4_HIP_TRY(hipStreamSynchronize(g_stream));
+  return ok();
+}
+
+G4_API int g4_copy(void *dst, size_t dst_off, const void *src, size_t src_off,
+                   size_t n) {
+  G4_CHECK_INIT();
+  if (n == 0) return ok();
+  int rc = check_device_range(static_cast<char *>(dst) + dst_off, n, "g4_copy dst");
+  if (rc) return rc;
+  rc = check_device_range(static_cast<const char *>(src) + src_off, n, "g4_copy src");
+  if (rc) return rc;
+  G4_HIP_TRY(hipMemcpyAsync(static_cast<char *>(dst) + dst_off,
+                            static_cast<const char *>(src) + src_off, n,
+                            hipMemcpyDeviceToDevice, g_stream));
+  return ok();
+}
+
+G4_API int g4_sync(void) {
+  G4_CHECK_INIT();
+  G4_CHECK_NOT_ENCODING();
+  G4_HIP_TRY(hipStreamSynchronize(g_stream));
+  return ok();
+}
+
+G4_API void *g4_stream(void) { return g_stream; }
+
+G4_API int g4_event_create(void **ev) {
+  G4_CHECK_INIT();
+  G4_CHECK_NOT_ENCODING();
+  if (!ev) return fail(G4_E_ARG, "g4_event_create: null output");
+  hipEvent_t e;
+  G4_HIP_TRY(hipEventCreate(&e));
+  *ev = e;
+  return ok();
+}
+
+G4_API int g4_event_record(void *ev) {
+  G4_CHECK_INIT();
+  G4_CHECK_NOT_ENCODING();
+  G4_HIP_TRY(hipEventRecord(static_cast<hipEvent_t>(ev), g_stream));
+  return ok();
+}
+
+G4_API int g4_event_elapsed_ms(void *start, void *stop, float *ms) {
+  G4_CHECK_INIT();
+  G4_CHECK_NOT_ENCODING();
+  if (!ms) return fail(G4_E_ARG, "g4_event_elapsed_ms: null output");
+  G4_HIP_TRY(hipEventSynchronize(static_cast<hipEvent_t>(stop)));
+  G4_HIP_TRY(hipEventElapsedTime(ms, static_cast<hipEvent_t>(start),
+                                 static_cast<hipEvent_t>(stop)));
+  return ok();
+}
+
+G4_API int g4_event_destroy(void *ev) {
+  G4_CHECK_INIT();
+  G4_CHECK_NOT_ENCODING();
+  G4_HIP_TRY(hipEventDestroy(static_cast<hipEvent_t>(ev)));
+  return ok();
+}
+
+// ---- command encoders: stream capture into a HIP graph ---------------------
+
+struct g4_cmdbuf {
+  hipGraph_t graph;
+  hipGraphExec_t exec;
+};
+
+G4_API int g4_encoder_begin(void) {
+  G4_CHECK_INIT();
+  if (g_encoding) return fail(G4_E_STATE, "g4_encoder_begin: an encoder is already open");
+  G4_HIP_TRY(hipStreamBeginCapture(g_stream, hipStreamCaptureModeRelaxed));
+  g_encoding = true;
+  return ok();
+}
+
+G4_API int g4_encoder_finish(g4_cmdbuf **out) {
+  G4_CHECK_INIT();
+  if (!g_encoding) return fail(G4_E_STATE, "g4_encoder_finish: no open encoder");
+  g_encoding = false;
+  hipGraph_t graph = nullptr;
+  G4_HIP_TRY(hipStreamEndCapture(g_stream, &graph));
+  if (!out) {
+    (void)hipGraphDestroy(graph);
+    return fail(G4_E_ARG, "g4_encoder_finish: null output");
+  }
+  hipGraphExec_t exec = nullptr;
+  hipError_t e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+  if (e != hipSuccess) {
+    (void)hipGraphDestroy(graph);
+    return fail(G4_E_HIP, "hipGraphInstantiate failed: %s", hipGetErrorString(e));
+  }
+  *out = new g4_cmdbuf{graph, exec};
+  return ok();
+}
+
+G4_API int g4_submit(const g4_cmdbuf *cb) {
+  G4_CHECK_INIT();
+  G4_CHECK_NOT_ENCODING();
+  if (!cb) return fail(G4_E_ARG, "g4_submit: null command buffer");
+  G4_HIP_TRY(hipGraphLaunch(cb->exec, g_stream));
+  return ok();
+}
+
+G4_API int g4_cmdbuf_free(g4_cmdbuf *cb) {
+  G4_CHECK_INIT();
+  G4_CHECK_NOT_ENCODING();
+  if (!cb) return ok();
+  G4_HIP_TRY(hipStreamSynchronize(g_stream));
+  (void)hipGraphExecDestroy(cb->exec);
+  (void)hipGraphDestroy(cb->graph);
+  delete cb;
+  return ok();
+}

@@ -1,0 +1,306 @@
+"""ctypes binding of libg4hip (include/g4hip.h) for the Python tests and benchmark.
+
+The Node addon (node/g4_napi.cc) is the reference-facing binding; this module
+is the same C ABI seen from Python.  It never computes anything itself: if
+libg4hip.so is missing it raises, it does not fall back to a CPU path.
+"""
+import ctypes
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "lib", "libg4hip.so")
+
+F32 = 0
+BF16 = 1
+
+G4_OK = 0
+G4_E_ARG = 1
+G4_E_RANGE = 2
+G4_E_STATE = 3
+G4_E_HIP = 4
+G4_E_NOMEM = 5
+
+_c = ctypes
+_vp = _c.c_void_p
+_int = _c.c_int
+_sz = _c.c_size_t
+
+# name -> (restype, argtypes); mirrors include/g4hip.h
+SIGNATURES = {
+    "g4_init": (_int, [_int]),
+    "g4_last_error": (_c.c_char_p, []),
+    "g4_device_info": (_int, [_c.c_char_p, _sz, _c.POINTER(_int), _c.POINTER(_sz), _c.POINTER(_int)]),
+    "g4_alloc": (_int, [_sz, _c.POINTER(_vp)]),
+    "g4_free": (_int, [_vp]),
+    "g4_upload": (_int, [_vp, _sz, _vp, _sz]),
+    "g4_download": (_int, [_vp, _sz, _vp, _sz]),
+    "g4_copy": (_int, [_vp, _sz, _vp, _sz, _sz]),
+    "g4_sync": (_int, []),
+    "g4_stream": (_vp, []),
+    "g4_encoder_begin": (_int, []),
+    "g4_encoder_finish": (_int, [_c.POINTER(_vp)]),
+    "g4_submit": (_int, [_vp]),
+    "g4_cmdbuf_free": (_int, [_vp]),
+    "g4_event_create": (_int, [_c.POINTER(_vp)]),
+    "g4_event_record": (_int, [_vp]),
+    "g4_event_elapsed_ms": (_int, [_vp, _vp, _c.POINTER(_c.c_float)]),
+    "g4_event_destroy": (_int, [_vp]),
+    "g4_w4_load": (_int, [_vp, _vp, _int, _int, _int, _c.POINTER(_vp)]),
+    "g4_w4_free": (_int, [_vp]),
+    "g4_w4_info": (_int, [_vp, _c.POINTER(_int), _c.POINTER(_int), _c.POINTER(_int), _c.POINTER(_sz)]),
+    "g4_w4_linear": (_int, [_vp, _vp, _int, _int, _vp, _int]),
+    "g4_w4_dequant": (_int, [_vp, _int, _int, _vp, _int]),
+    "g4_ple_create": (_int, [_int, _int, _int, _int, _c.POINTER(_vp)]),
+    "g4_ple_upload_shard": (_int, [_vp, _int, _vp, _sz]),
+    "g4_ple_shard_bytes": (_int, [_vp, _int, _c.POINTER(_int), _c.POINTER(_sz)]),
+    "g4_ple_free": (_int, [_vp]),
+    "g4_ple_gather": (_int, [_vp, _vp, _int, _vp, _int]),
+    "g4_ple_gather_dev": (_int, [_vp, _vp, _int, _vp, _int]),
+    "g4_bf16_head": (_int, [_vp, _vp, _int, _int, _vp, _c.c_float, _c.c_float]),
+}
+
+
+class G4Error(RuntimeError):
+    def __init__(self, code, msg):
+        super().__init__("[g4 status %d] %s" % (code, msg))
+        self.code = code
+
+
+_lib = None
+
+
+def lib(path=LIB_PATH):
+    """Load libg4hip.so once; raise if it has not been built."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(path):
+            raise FileNotFoundError(
+                "%s is missing: build it with `python3 gemma4-js_amd/build.py` "
+                "(there is no CPU fallback)" % path)
+        L = ctypes.CDLL(path)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def check(rc):
+    if rc != G4_OK:
+        raise G4Error(rc, lib().g4_last_error().decode(errors="replace"))
+
+
+def init(device=0):
+    check(lib().g4_init(device))
+
+
+def device_info():
+    name = ctypes.create_string_buffer(256)
+    cu, hbm, clk = _int(), _sz(), _int()
+    check(lib().g4_device_info(name, 256, ctypes.byref(cu), ctypes.byref(hbm), ctypes.byref(clk)))
+    return {"name": name.value.decode(), "cu_count": cu.value, "hbm_bytes": hbm.value,
+            "clock_khz": clk.value}
+
+
+def sync():
+    check(lib().g4_sync())
+
+
+class Buffer:
+    """A device buffer from g4_alloc (createBuffer)."""
+
+    def __init__(self, nbytes):
+        p = _vp()
+        check(lib().g4_alloc(int(nbytes), ctypes.byref(p)))
+        self.ptr = p.value
+        self.nbytes = int(nbytes)
+
+    @classmethod
+    def from_array(cls, a):
+        a = np.ascontiguousarray(a)
+        b = cls(a.nbytes)
+        b.upload(a)
+        return b
+
+    def upload(self, a, offset=0):
+        a = np.ascontiguousarray(a)
+        check(lib().g4_upload(self.ptr, int(offset), a.ctypes.data, a.nbytes))
+
+    def download(self, dtype, count=None, offset=0):
+        dtype = np.dtype(dtype)
+        if count is None:
+            count = (self.nbytes - offset) // dtype.itemsize
+        out = np.empty(int(count), dtype=dtype)
+        check(lib().g4_download(self.ptr, int(offset), out.ctypes.data, out.nbytes))
+        return out
+
+    def at(self, offset):
+        """Device address `offset` bytes into the buffer."""
+        return self.ptr + int(offset)
+
+    def free(self):
+        if self.ptr:
+            check(lib().g4_free(self.ptr))
+            self.ptr = None
+
+    def __del__(self):
+        try:
+            if self.ptr and _lib is not None:
+                _lib.g4_free(self.ptr)
+        except Exception:
+            pass
+
+
+class CommandBuffer:
+    """A finished command encoder (captured HIP graph); submit() replays it."""
+
+    def __init__(self, ptr):
+        self.ptr = ptr
+
+    def submit(self):
+        check(lib().g4_submit(self.ptr))
+
+    def free(self):
+        if self.ptr:
+            check(lib().g4_cmdbuf_free(self.ptr))
+            self.ptr = None
+
+    def __del__(self):
+        try:
+            if self.ptr and _lib is not None:
+                _lib.g4_cmdbuf_free(self.ptr)
+        except Exception:
+            pass
+
+
+class Encoder:
+    """`with Encoder() as enc:` records the launches made inside the block."""
+
+    def __enter__(self):
+        check(lib().g4_encoder_begin())
+        self.cmdbuf = None
+        return self
+
+    def __exit__(self, et, ev, tb):
+        p = _vp()
+        rc = lib().g4_encoder_finish(ctypes.byref(p))
+        if et is None:
+            check(rc)
+            self.cmdbuf = CommandBuffer(p.value)
+        return False
+
+
+class Event:
+    def __init__(self):
+        p = _vp()
+        check(lib().g4_event_create(ctypes.byref(p)))
+        self.ptr = p.value
+
+    def record(self):
+        check(lib().g4_event_record(self.ptr))
+
+    def elapsed_ms(self, stop):
+        ms = _c.c_float()
+        check(lib().g4_event_elapsed_ms(self.ptr, stop.ptr, ctypes.byref(ms)))
+        return ms.value
+
+    def __del__(self):
+        try:
+            if self.ptr and _lib is not None:
+                _lib.g4_event_destroy(self.ptr)
+        except Exception:
+            pass
+
+
+class W4Linear:
+    """GPUW4Linear: compressed-tensors W4A16 weights resident on the device."""
+
+    def __init__(self, packed, scales, group=32):
+        packed = np.ascontiguousarray(packed).view(np.uint32)
+        scales = np.ascontiguousarray(scales).view(np.uint16)
+        if packed.ndim != 2 or scales.ndim != 2:
+            raise ValueError("packed and scales must be rank-2")
+        self.out_dim = packed.shape[0]
+        self.in_dim = packed.shape[1] * 8
+        self.group = group
+        h = _vp()
+        check(lib().g4_w4_load(packed.ctypes.data, scales.ctypes.data, self.out_dim,
+                               self.in_dim, group, ctypes.byref(h)))
+        self.h = h.value
+
+    def info(self):
+        n, k, g, b = _int(), _int(), _int(), _sz()
+        check(lib().g4_w4_info(self.h, ctypes.byref(n), ctypes.byref(k), ctypes.byref(g),
+                               ctypes.byref(b)))
+        return {"out_dim": n.value, "in_dim": k.value, "group": g.value, "device_bytes": b.value}
+
+    def linear(self, x_ptr, x_dtype, rows, y_ptr, y_dtype=F32):
+        check(lib().g4_w4_linear(self.h, x_ptr, x_dtype, rows, y_ptr, y_dtype))
+
+    def dequant(self, row_start, row_count, out_ptr, out_dtype=F32):
+        check(lib().g4_w4_dequant(self.h, row_start, row_count, out_ptr, out_dtype))
+
+    def free(self):
+        if self.h:
+            check(lib().g4_w4_free(self.h))
+            self.h = None
+
+    def __del__(self):
+        try:
+            if self.h and _lib is not None:
+                _lib.g4_w4_free(self.h)
+        except Exception:
+            pass
+
+
+class PleTable:
+    """W4PleShardBundle with the whole table resident on the device."""
+
+    def __init__(self, vocab, width=8960, group=32, rows_per_shard=4096):
+        h = _vp()
+        check(lib().g4_ple_create(vocab, width, group, rows_per_shard, ctypes.byref(h)))
+        self.h = h.value
+        self.vocab, self.width, self.rows_per_shard = vocab, width, rows_per_shard
+        ns = _int()
+        check(lib().g4_ple_shard_bytes(self.h, 0, ctypes.byref(ns), None))
+        self.num_shards = ns.value
+
+    def shard_bytes(self, shard):
+        b = _sz()
+        check(lib().g4_ple_shard_bytes(self.h, shard, None, ctypes.byref(b)))
+        return b.value
+
+    def upload_shard(self, shard, data):
+        data = np.frombuffer(data, dtype=np.uint8) if isinstance(data, (bytes, bytearray)) \
+            else np.ascontiguousarray(data).view(np.uint8)
+        check(lib().g4_ple_upload_shard(self.h, shard, data.ctypes.data, data.nbytes))
+
+    def gather(self, ids, out_ptr, out_dtype=F32):
+        ids = np.ascontiguousarray(ids, dtype=np.int32)
+        check(lib().g4_ple_gather(self.h, ids.ctypes.data, ids.size, out_ptr, out_dtype))
+
+    def gather_dev(self, ids_ptr, n, out_ptr, out_dtype=F32):
+        check(lib().g4_ple_gather_dev(self.h, ids_ptr, n, out_ptr, out_dtype))
+
+    def free(self):
+        if self.h:
+            check(lib().g4_ple_free(self.h))
+            self.h = None
+
+    def __del__(self):
+        try:
+            if self.h and _lib is not None:
+                _lib.g4_ple_free(self.h)
+        except Exception:
+            pass
+
+
+def bf16_head(x_ptr, E_ptr, rows, in_dim, out_ptr, scale=1.0, softcap=30.0):
+    check(lib().g4_bf16_head(x_ptr, E_ptr, rows, in_dim, out_ptr, scale, softcap))
+
+
+def exported_symbols():
+    return sorted(SIGNATURES)

@@ -1,0 +1,107 @@
+"""GPU parity of the PLE W4 gather-dequant: bit-exact against the oracle.
+
+The full [262144, 8960] table (64 shards, 1.32 GB) is generated once per
+session in the builder's shard layout, uploaded shard by shard, and every
+gathered row is compared bit for bit with the oracle's readRows restatement;
+BF16 rows must equal round-to-nearest-even of the oracle's FP32 rows.
+"""
+import numpy as np
+import pytest
+
+import synthetic as syn
+
+pytestmark = pytest.mark.gpu
+
+VOCAB, WIDTH, RPS = 262144, 8960, 4096
+
+
+@pytest.fixture(scope="module")
+def table(g4):
+    shards = syn.ple_table(2024, VOCAB, WIDTH, RPS, threads=16)
+    t = g4.PleTable(VOCAB, WIDTH, 32, RPS)
+    assert t.num_shards == 64
+    for i, s in enumerate(shards):
+        assert s.nbytes == t.shard_bytes(i) == 20643840
+        t.upload_shard(i, s)
+    host = np.concatenate(shards)
+    del shards
+    yield t, host
+    t.free()
+
+
+def gather(g4, t, ids, dtype):
+    out = g4.Buffer(len(ids) * WIDTH * (4 if dtype == g4.F32 else 2))
+    t.gather(ids, out.ptr, dtype)
+    return out.download(np.float32 if dtype == g4.F32 else np.uint16).reshape(len(ids), WIDTH)
+
+
+def test_gather_2048_ids_fp32_and_bf16(g4, oracle, table):
+    t, host = table
+    ids = syn.token_ids(1, 2048, VOCAB)
+    ids[:6] = [0, VOCAB - 1, RPS - 1, RPS, 5 * RPS + 17, 0]  # edges and a duplicate
+    want = oracle.ple_gather(host, VOCAB, WIDTH, RPS, ids)
+    got = gather(g4, t, ids, g4.F32)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    got16 = gather(g4, t, ids, g4.BF16)
+    assert np.array_equal(got16.reshape(-1), oracle.f32_to_bf16_array(want))
+
+
+def test_gather_single_id(g4, oracle, table):
+    t, host = table
+    for tid in (0, 1, 123456, VOCAB - 1):
+        ids = np.array([tid], dtype=np.int32)
+        want = oracle.ple_gather(host, VOCAB, WIDTH, RPS, ids)
+        got = gather(g4, t, ids, g4.F32)
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def test_gather_values_are_in_the_quantized_range(g4, table):
+    t, host = table
+    got = gather(g4, t, syn.token_ids(3, 64, VOCAB), g4.F32)
+    assert np.isfinite(got).all()
+    assert np.abs(got).max() <= 7 * 0.05 * 6  # |q| <= 7, scale = bf16(|N|*0.05)
+
+
+def test_out_of_range_host_id_throws_before_launch(g4, table):
+    t, _ = table
+    out = g4.Buffer(3 * WIDTH * 4)
+    sentinel = np.full(3 * WIDTH, 7.0, dtype=np.float32)
+    out.upload(sentinel)
+    for bad in (-1, VOCAB):
+        with pytest.raises(g4.G4Error) as e:
+            t.gather(np.array([5, bad, 6], dtype=np.int32), out.ptr, g4.F32)
+        assert e.value.code == g4.G4_E_RANGE
+        assert "PLE token id out of range" in str(e.value)
+    assert np.array_equal(out.download(np.float32), sentinel)
+
+
+def test_device_ids_out_of_range_give_nan_rows(g4, oracle, table):
+    t, host = table
+    ids = np.array([10, -3, 262143, VOCAB + 5, 77], dtype=np.int32)
+    dev = g4.Buffer.from_array(ids)
+    out = g4.Buffer(ids.size * WIDTH * 4)
+    t.gather_dev(dev.ptr, ids.size, out.ptr, g4.F32)
+    got = out.download(np.float32).reshape(ids.size, WIDTH)
+    ok = np.array([0, 2, 4])
+    want = oracle.ple_gather(host, VOCAB, WIDTH, RPS, ids[ok])
+    assert np.array_equal(got[ok].view(np.uint32), want.view(np.uint32))
+    assert np.isnan(got[[1, 3]]).all()
+
+
+def test_short_last_shard(g4, oracle):
+    # vocab not a multiple of rows_per_shard: the last shard's scales block
+    # starts after its own (shorter) packed block.
+    vocab, rps, width = 9000, 4096, 8960
+    shards = syn.ple_table(7, vocab, width, rps, threads=4)
+    t = g4.PleTable(vocab, width, 32, rps)
+    assert t.num_shards == 3 and t.shard_bytes(2) == (9000 - 8192) * 5040
+    for i, s in enumerate(shards):
+        t.upload_shard(i, s)
+    host = np.concatenate(shards)
+    ids = np.array([8192, 8999, 8500, 4095, 0], dtype=np.int32)
+    got = gather(g4, t, ids, g4.F32)
+    want = oracle.ple_gather(host, vocab, width, rps, ids)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    with pytest.raises(g4.G4Error):
+        t.upload_shard(2, shards[1])  # wrong size for the short shard
+    t.free()

@@ -1,0 +1,164 @@
+"""GPU parity of the W4A16 linear entry points against the oracle.
+
+Bar: dequantized weights bit-exact (FP32) and bit-exact to round-to-nearest-
+even of the exact value (BF16); matmul outputs within max-over-rows relative
+L2 error 1e-3 of the reference's FP32 dequant-then-matMul (the oracle), and
+of the binary64 product.
+"""
+import numpy as np
+import pytest
+
+import synthetic as syn
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-3  # max relative L2 error per output row
+
+# (out_dim, in_dim) of every W4A16 projection of Gemma-4-E2B
+# (gemma4-webgpu.js:65-95 layer schedule; hidden 1536).
+E2B_SHAPES = {
+    "q_sliding": (2048, 1536), "kv_sliding": (256, 1536), "o_sliding": (1536, 2048),
+    "gate_up_l0_14": (6144, 1536), "down_l0_14": (1536, 6144),
+    "q_full": (4096, 1536), "kv_full": (512, 1536), "o_full": (1536, 4096),
+    "gate_up_l15_34": (12288, 1536), "down_l15_34": (1536, 12288),
+    "ple_gate": (256, 1536), "ple_proj": (1536, 256), "top_proj": (8960, 1536),
+}
+
+
+def rel_l2_rows(y, ref):
+    y = np.asarray(y, dtype=np.float64).reshape(ref.shape)
+    num = np.linalg.norm(y - ref, axis=-1)
+    den = np.maximum(np.linalg.norm(ref, axis=-1), 1e-300)
+    return float((num / den).max())
+
+
+def dense(q, scales):
+    return q.astype(np.float64) * np.repeat(syn.bf16_to_f32(scales).astype(np.float64), 32, axis=1)
+
+
+def run_linear(g4, lin, x_bits, x_f32, rows, x_dtype, y_dtype=0):
+    if x_dtype == g4.BF16:
+        xb = g4.Buffer.from_array(x_bits)
+    else:
+        xb = g4.Buffer.from_array(x_f32.astype(np.float32))
+    ye = 4 if y_dtype == g4.F32 else 2
+    yb = g4.Buffer(rows * lin.out_dim * ye)
+    lin.linear(xb.ptr, x_dtype, rows, yb.ptr, y_dtype)
+    out = yb.download(np.float32 if y_dtype == g4.F32 else np.uint16)
+    return out.reshape(rows, lin.out_dim)
+
+
+def test_dequant_bit_exact(g4, oracle):
+    for seed, (n, k) in enumerate([(256, 1536), (96, 256), (130, 6144)]):
+        packed, scales, q = syn.w4_weights(100 + seed, n, k)
+        lin = g4.W4Linear(packed, scales)
+        out = g4.Buffer(n * k * 4)
+        lin.dequant(0, n, out.ptr, g4.F32)
+        got = out.download(np.float32).reshape(n, k)
+        rc, want = oracle.w4_dequant_rows(packed, syn.bf16_to_f32(scales), n, k, 0, n)
+        assert rc == 0
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+        # a sub-range, as BF16 (roundFloat32ToBF16 of the exact value)
+        r0, rc_ = n // 3, n // 2
+        outb = g4.Buffer(rc_ * k * 2)
+        lin.dequant(r0, rc_, outb.ptr, g4.BF16)
+        gotb = outb.download(np.uint16).reshape(rc_, k)
+        assert np.array_equal(gotb, oracle.f32_to_bf16_array(want[r0:r0 + rc_]).reshape(rc_, k))
+
+
+def test_gemv_config0_against_oracle(g4, oracle):
+    # M=1, K=1536, N=6144, BF16 activations, FP32 accumulate.
+    packed, scales, q = syn.w4_weights(0, 6144, 1536)
+    x_bits, x = syn.activations(0, 1, 1536)
+    lin = g4.W4Linear(packed, scales)
+    y_bf = run_linear(g4, lin, x_bits, x, 1, g4.BF16)
+    y_f32 = run_linear(g4, lin, x_bits, x, 1, g4.F32)
+    # the same values in either input dtype give the same arithmetic
+    assert np.array_equal(y_bf, y_f32)
+    ref32 = oracle.w4_linear(x, packed, scales)
+    ref64 = oracle.w4_linear_f64(x, packed, scales)
+    assert rel_l2_rows(y_bf, ref32.astype(np.float64)) <= TOL
+    assert rel_l2_rows(y_bf, ref64) <= TOL
+    # and far inside it: FP32 accumulation error only
+    assert rel_l2_rows(y_bf, ref64) < 1e-5
+
+
+@pytest.mark.parametrize("name", sorted(E2B_SHAPES))
+def test_gemv_e2b_shapes(g4, name):
+    n, k = E2B_SHAPES[name]
+    packed, scales, q = syn.w4_weights(len(name), n, k)
+    x_bits, x = syn.activations(len(name), 1, k)
+    lin = g4.W4Linear(packed, scales)
+    y = run_linear(g4, lin, x_bits, x, 1, g4.BF16)
+    ref = x.astype(np.float64) @ dense(q, scales).T
+    assert rel_l2_rows(y, ref) <= TOL
+
+
+@pytest.mark.parametrize("rows", [2, 3, 4, 5, 7, 9])
+def test_linear_few_rows(g4, oracle, rows):
+    packed, scales, q = syn.w4_weights(rows, 2048, 1536)
+    x_bits, x = syn.activations(rows, rows, 1536)
+    lin = g4.W4Linear(packed, scales)
+    y = run_linear(g4, lin, x_bits, x, rows, g4.F32)
+    ref = oracle.w4_linear(x, packed, scales).astype(np.float64)
+    assert rel_l2_rows(y, ref) <= TOL
+    ref64 = x.astype(np.float64) @ dense(q, scales).T
+    assert rel_l2_rows(y, ref64) < 1e-5
+
+
+def test_one_hot_input_returns_a_weight_column_exactly(g4):
+    n, k = 640, 1536
+    packed, scales, q = syn.w4_weights(77, n, k)
+    lin = g4.W4Linear(packed, scales)
+    w = (q.astype(np.float32) * np.repeat(syn.bf16_to_f32(scales).reshape(n, k // 32), 32, axis=1))
+    for col in (0, 31, 32, 700, k - 1):
+        x = np.zeros((1, k), dtype=np.float32)
+        x[0, col] = 1.0
+        y = run_linear(g4, lin, None, x, 1, g4.F32)
+        assert np.array_equal(y[0], w[:, col])
+
+
+def test_bf16_output_is_rne_of_fp32_output(g4, oracle):
+    packed, scales, q = syn.w4_weights(5, 1536, 2048)
+    x_bits, x = syn.activations(5, 1, 2048)
+    lin = g4.W4Linear(packed, scales)
+    y32 = run_linear(g4, lin, x_bits, x, 1, g4.BF16, g4.F32)
+    y16 = run_linear(g4, lin, x_bits, x, 1, g4.BF16, g4.BF16)
+    assert np.array_equal(y16.reshape(-1), oracle.f32_to_bf16_array(y32))
+
+
+def test_prefill_gemm_config3(g4, oracle):
+    # M=2048 tokens at both prefill shapes; checked against the binary64
+    # product everywhere and the FP32 oracle on a sample of rows.
+    for (n, k) in [(6144, 1536), (1536, 6144)]:
+        packed, scales, q = syn.w4_weights(3, n, k)
+        x_bits, x = syn.activations(3, 2048, k)
+        lin = g4.W4Linear(packed, scales)
+        y = run_linear(g4, lin, x_bits, x, 2048, g4.BF16)
+        ref = x.astype(np.float64) @ dense(q, scales).T
+        assert rel_l2_rows(y, ref) <= TOL
+        sample = np.array([0, 1, 777, 2047])
+        ref32 = oracle.w4_linear(x[sample], packed, scales).astype(np.float64)
+        assert rel_l2_rows(y[sample], ref32) <= TOL
+
+
+def test_errors_are_reported_not_faulted(g4):
+    packed, scales, _ = syn.w4_weights(1, 256, 512)
+    lin = g4.W4Linear(packed, scales)
+    x = g4.Buffer(512 * 4)
+    y_small = g4.Buffer(255 * 4)
+    with pytest.raises(g4.G4Error) as e:
+        lin.linear(x.ptr, g4.F32, 1, y_small.ptr, g4.F32)
+    assert e.value.code == g4.G4_E_RANGE
+    with pytest.raises(g4.G4Error) as e:
+        lin.linear(x.ptr, g4.F32, 2, g4.Buffer(512 * 4).ptr, g4.F32)  # x too short for 2 rows
+    assert e.value.code == g4.G4_E_RANGE
+    with pytest.raises(g4.G4Error) as e:
+        lin.linear(x.ptr, 7, 1, y_small.ptr, g4.F32)
+    assert e.value.code == g4.G4_E_ARG
+    with pytest.raises(g4.G4Error) as e:
+        g4.W4Linear(np.zeros((4, 5), np.uint32), np.zeros((4, 1), np.uint16))  # K=40
+    assert "divisible by groupSize" in str(e.value)
+    with pytest.raises(g4.G4Error) as e:
+        lin.dequant(200, 100, g4.Buffer(100 * 512 * 4).ptr)
+    assert e.value.code == g4.G4_E_RANGE
