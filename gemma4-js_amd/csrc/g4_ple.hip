@@ -35,68 +35,68 @@ namespace {
 
 using namespace g4;
 
-// One thread per (token, 32-column group): a 16-byte packed load, one scale,
-// 32 outputs.  Consecutive threads walk consecutive groups of a row, so the
-// packed reads and the output writes are both contiguous streams.
+// One thread per 16 bytes of output: EPT consecutive elements of one row
+// (4 for FP32, 8 for BF16), so every store instruction of a wave writes 1 KB
+// of consecutive output and the packed reads (EPT/2 bytes per lane) are
+// consecutive too.  The table is only read (1.32 GB, far beyond the caches);
+// the output is written once.
+template <bool BF16OUT>
 __global__ __launch_bounds__(256) void ple_gather_kernel(
     const uint8_t *__restrict__ table, const int32_t *__restrict__ ids, int n,
-    void *__restrict__ out, int out_bf16, int vocab, int width,
-    int rows_per_shard, size_t packed_row, size_t scale_row,
-    size_t full_shard_bytes) {
-  const int gpr = width >> 5;  // groups per row
+    void *__restrict__ out, int vocab, int width, int rows_per_shard, size_t packed_row,
+    size_t scale_row, size_t full_shard_bytes) {
+  constexpr int EPT = BF16OUT ? 8 : 4;
+  const int per_row = width / EPT;
   const size_t item = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (item >= (size_t)n * gpr) return;
-  const int j = (int)(item / gpr);
-  const int g = (int)(item - (size_t)j * gpr);
+  if (item >= (size_t)n * per_row) return;
+  const int j = (int)(item / per_row);
+  const int e0 = (int)(item - (size_t)j * per_row) * EPT;  // first element
   const int id = ids[j];
-  float v[32];
+  float v[EPT];
   if (id < 0 || id >= vocab) {
 #pragma unroll
-    for (int i = 0; i < 32; ++i) v[i] = __uint_as_float(0x7fc00000u);
+    for (int i = 0; i < EPT; ++i) v[i] = __uint_as_float(0x7fc00000u);
   } else {
     const int shard = id / rows_per_shard;
     const int local = id - shard * rows_per_shard;
     const int left = vocab - shard * rows_per_shard;
     const int rows_in_shard = left < rows_per_shard ? left : rows_per_shard;
     const uint8_t *base = table + (size_t)shard * full_shard_bytes;
-    const uint4 q = ld_nt(reinterpret_cast<const uint4 *>(base + (size_t)local * packed_row) + g);
+    const uint8_t *prow = base + (size_t)local * packed_row;
+    // two's-complement nibbles -> offset binary: n ^ 8 = q + 8
+    uint32_t w = BF16OUT ? *reinterpret_cast<const uint32_t *>(prow + e0 / 2)
+                         : (uint32_t)*reinterpret_cast<const uint16_t *>(prow + e0 / 2);
+    w ^= 0x88888888u;
     const uint16_t sb = reinterpret_cast<const uint16_t *>(
-        base + (size_t)rows_in_shard * packed_row + (size_t)local * scale_row)[g];
+        base + (size_t)rows_in_shard * packed_row + (size_t)local * scale_row)[e0 / 32];
     const float s = bf16_to_f32(sb);
-    const uint32_t w[4] = {q.x ^ 0x88888888u, q.y ^ 0x88888888u, q.z ^ 0x88888888u,
-                           q.w ^ 0x88888888u};
+#pragma unroll
+    for (int i = 0; i < EPT; ++i) v[i] = (float)((int)((w >> (4 * i)) & 15u) - 8) * s;
+  }
+  const size_t o = (size_t)j * width + e0;
+  if (BF16OUT) {
+    uint32_t p[4];
 #pragma unroll
     for (int k = 0; k < 4; ++k)
-#pragma unroll
-      for (int e = 0; e < 8; ++e)
-        v[8 * k + e] = (float)((int)((w[k] >> (4 * e)) & 15u) - 8) * s;
-  }
-  const size_t o = (size_t)j * width + (size_t)g * 32;
-  if (out_bf16) {
-    uint4 *dst = reinterpret_cast<uint4 *>(static_cast<uint16_t *>(out) + o);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      uint32_t p[4];
-#pragma unroll
-      for (int k = 0; k < 4; ++k)
-        p[k] = f32_to_bf16_rne(v[8 * i + 2 * k]) |
-               (f32_to_bf16_rne(v[8 * i + 2 * k + 1]) << 16);
-      st_nt(dst + i, make_uint4(p[0], p[1], p[2], p[3]));
-    }
+      p[k] = f32_to_bf16_rne(v[2 * k]) | (f32_to_bf16_rne(v[2 * k + 1]) << 16);
+    *reinterpret_cast<uint4 *>(static_cast<uint16_t *>(out) + o) = make_uint4(p[0], p[1], p[2], p[3]);
   } else {
-    float4 *dst = reinterpret_cast<float4 *>(static_cast<float *>(out) + o);
-#pragma unroll
-    for (int i = 0; i < 8; ++i)
-      st_nt(dst + i, make_float4(v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]));
+    *reinterpret_cast<float4 *>(static_cast<float *>(out) + o) = make_float4(v[0], v[1], v[2], v[3]);
   }
 }
 
 int launch_gather(const g4_ple *t, const int32_t *ids_dev, int n, void *out, int out_dtype) {
-  const size_t items = (size_t)n * (t->width / 32);
+  const bool bf = out_dtype == G4_BF16;
+  const size_t items = (size_t)n * (t->width / (bf ? 8 : 4));
   const unsigned blocks = (unsigned)((items + 255) / 256);
-  hipLaunchKernelGGL(ple_gather_kernel, dim3(blocks), dim3(256), 0, stream(), t->table,
-                     ids_dev, n, out, out_dtype == G4_BF16, t->vocab, t->width,
-                     t->rows_per_shard, t->packed_row, t->scale_row, t->full_shard_bytes);
+  if (bf)
+    hipLaunchKernelGGL(ple_gather_kernel<true>, dim3(blocks), dim3(256), 0, stream(), t->table,
+                       ids_dev, n, out, t->vocab, t->width, t->rows_per_shard, t->packed_row,
+                       t->scale_row, t->full_shard_bytes);
+  else
+    hipLaunchKernelGGL(ple_gather_kernel<false>, dim3(blocks), dim3(256), 0, stream(), t->table,
+                       ids_dev, n, out, t->vocab, t->width, t->rows_per_shard, t->packed_row,
+                       t->scale_row, t->full_shard_bytes);
   G4_LAUNCH_CHECK("ple_gather_kernel");
   return G4_OK;
 }

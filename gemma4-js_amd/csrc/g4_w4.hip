@@ -9,15 +9,11 @@
 // One group is exactly 16 packed bytes, so group g of row o is the 128-bit
 // word packed[o*G + g] (G = K/32): a lane that owns a group reads it with one
 // coalesced dwordx4 load.
-//
-// Arithmetic: per group the kernel forms d = sum_i x_i * n_i with the
-// unsigned nibble n_i = q_i + 8, then adds s * (d - 8 * sum_i x_i).  The sum
-// of x over a group is shared by every output row, so the -8 offset costs
-// one FMA per group instead of one per element.  Accumulation is FP32.
 #include "g4_internal.h"
 
 struct g4_w4 {
   int N, K, group, G;
+  uint8_t *mem;      // the one device allocation holding both arrays
   uint4 *packed;     // [N][G] 16-byte groups
   uint16_t *scales;  // [N][G] bf16 bits
   size_t bytes;
@@ -28,201 +24,460 @@ namespace {
 using namespace g4;
 
 // ---------------------------------------------------------------------------
-// Streaming GEMV (rows of x <= 4).
+// Streaming GEMV (decode: rows of x <= 4 per launch).
 //
-// A "team" of L lanes owns one output row at a time; lane t of a team handles
-// groups t, t+L, t+2L, ... of that row, holding the x values of those groups
-// in registers while it walks R rows.  L divides G, so no lane idles.  The
-// team's partial sums are combined with cross-lane shuffles at the end.
+// Work split: a "team" of L lanes owns one output row; lane t of the team
+// handles groups t, t+L, t+2L, ... (L is the largest power of two <= 64 that
+// divides G, so no lane idles).  Every lane issues the 128-bit loads of all
+// its groups before anything else, so the whole weight slab is in flight
+// while the block stages x.
+//
+// Arithmetic: v_dot2c_f32_bf16 on bf16 pairs.  A packed word w holds
+// nibbles n_0..n_7 (bits 4t..4t+3).  ((w >> 4t) & 0x000F000F) | 0x43004300 is
+// the bf16 pair (128 + n_t, 128 + n_{t+4}) - exact, one shift and one
+// v_and_or_b32 - so the activation pairs are staged in the matching order
+// (x[8c+t], x[8c+t+4]).  Per group d = sum x_i (128 + n_i) and
+// sum x_i q_i = d - 136 * sum x_i; the block stages 136 * sum x per group
+// once, shared by all rows.  FP32 activations are split into bf16 hi + lo
+// (x = hi + lo to 2^-17 relative), two dot2 chains; BF16 activations need
+// only hi.  Products are exact and accumulation is FP32.
+//
+// LDS image per activation row m (16-byte chunks, chunk c of group g at
+// [c * G + g] so a team's lanes read consecutive chunks, conflict-free):
+//   hi[4][G], lo[4][G] (FP32 input only), sx[G] = 136 * sum of the group.
 // ---------------------------------------------------------------------------
 
-template <typename XT>
-__device__ __forceinline__ void load_x_group(const XT *__restrict__ x, float (&v)[32]);
+typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2_t;
 
-template <>
-__device__ __forceinline__ void load_x_group<float>(const float *__restrict__ x,
-                                                    float (&v)[32]) {
-  const float4 *p = reinterpret_cast<const float4 *>(x);
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    float4 f = p[i];
-    v[4 * i + 0] = f.x;
-    v[4 * i + 1] = f.y;
-    v[4 * i + 2] = f.z;
-    v[4 * i + 3] = f.w;
-  }
+__device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a),
+                                         __builtin_bit_cast(bf16x2_t, b), c, false);
 }
 
-template <>
-__device__ __forceinline__ void load_x_group<uint16_t>(const uint16_t *__restrict__ x,
-                                                       float (&v)[32]) {
-  const uint4 *p = reinterpret_cast<const uint4 *>(x);
+constexpr uint32_t kPairMagic = 0x43004300u;  // bf16 pair (128, 128)
+constexpr float kPairBias = 136.f;            // (128 + n) - 136 = n - 8 = q
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, true));
+}
+
+// Sum over aligned teams of L lanes; every lane of the team gets the sum.
+template <int L>
+__device__ __forceinline__ float team_sum(float v) {
+  if (L >= 2) v += dpp_f32<0xB1>(v);   // quad_perm [1,0,3,2]
+  if (L >= 4) v += dpp_f32<0x4E>(v);   // quad_perm [2,3,0,1]
+  if (L >= 8) v += dpp_f32<0x141>(v);  // row_half_mirror
+  if (L >= 16) v += dpp_f32<0x140>(v); // row_mirror
+  if (L >= 32) v += __shfl_xor(v, 16, 64);
+  if (L >= 64) v += __shfl_xor(v, 32, 64);
+  return v;
+}
+
+__device__ __forceinline__ uint32_t bf16_pair(uint32_t lo16, uint32_t hi16) {
+  return (lo16 & 0xffffu) | (hi16 << 16);
+}
+
+// Stage group g of activation row m: 32 values -> hi/lo pair chunks + sum.
+template <bool F32X>
+__device__ __forceinline__ void stage_group(const void *__restrict__ xrow, int g, int G,
+                                            uint4 *__restrict__ hi, uint4 *__restrict__ lo,
+                                            float *__restrict__ sx) {
+  uint32_t h[32], l[32];
+  float sum = 0.f;
+  if (F32X) {
+    const float4 *p = reinterpret_cast<const float4 *>(static_cast<const float *>(xrow) + g * 32);
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    uint4 u = p[i];
-    uint32_t w[4] = {u.x, u.y, u.z, u.w};
+    for (int i = 0; i < 8; ++i) {
+      const float4 f = p[i];
+      const float v[4] = {f.x, f.y, f.z, f.w};
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      v[8 * i + 2 * j + 0] = __uint_as_float(w[j] << 16);
-      v[8 * i + 2 * j + 1] = __uint_as_float(w[j] & 0xffff0000u);
+      for (int e = 0; e < 4; ++e) {
+        const uint32_t hb = f32_to_bf16_rne(v[e]);
+        const float r = v[e] - bf16_to_f32(hb);
+        const uint32_t lb = f32_to_bf16_rne(r);
+        h[4 * i + e] = hb;
+        l[4 * i + e] = lb;
+        sum += bf16_to_f32(hb) + bf16_to_f32(lb);
+      }
+    }
+  } else {
+    const uint4 *p = reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(xrow) + g * 32);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint4 u = p[i];
+      const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        h[8 * i + 2 * e] = w[e] & 0xffffu;
+        h[8 * i + 2 * e + 1] = w[e] >> 16;
+        sum += bf16_to_f32(w[e] & 0xffffu) + bf16_to_f32(w[e] >> 16);
+      }
     }
   }
-}
-
-// sum_i x_i * n_i over one 16-byte group, n_i the unsigned nibble.
-__device__ __forceinline__ float group_dot(const uint4 q, const float (&x)[32]) {
-  const uint32_t w[4] = {q.x, q.y, q.z, q.w};
-  float d0 = 0.f, d1 = 0.f;
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const uint32_t lo = w[j] & 0x0f0f0f0fu;         // nibbles 0,2,4,6
-    const uint32_t hi = (w[j] >> 4) & 0x0f0f0f0fu;  // nibbles 1,3,5,7
-    const float *xj = x + 8 * j;
-    d0 = fmaf(xj[0], (float)(lo & 0xffu), d0);
-    d1 = fmaf(xj[1], (float)(hi & 0xffu), d1);
-    d0 = fmaf(xj[2], (float)((lo >> 8) & 0xffu), d0);
-    d1 = fmaf(xj[3], (float)((hi >> 8) & 0xffu), d1);
-    d0 = fmaf(xj[4], (float)((lo >> 16) & 0xffu), d0);
-    d1 = fmaf(xj[5], (float)((hi >> 16) & 0xffu), d1);
-    d0 = fmaf(xj[6], (float)(lo >> 24), d0);
-    d1 = fmaf(xj[7], (float)(hi >> 24), d1);
+  for (int c = 0; c < 4; ++c) {
+    hi[c * G + g] = make_uint4(bf16_pair(h[8 * c + 0], h[8 * c + 4]), bf16_pair(h[8 * c + 1], h[8 * c + 5]),
+                               bf16_pair(h[8 * c + 2], h[8 * c + 6]), bf16_pair(h[8 * c + 3], h[8 * c + 7]));
+    if (F32X)
+      lo[c * G + g] = make_uint4(bf16_pair(l[8 * c + 0], l[8 * c + 4]), bf16_pair(l[8 * c + 1], l[8 * c + 5]),
+                                 bf16_pair(l[8 * c + 2], l[8 * c + 6]), bf16_pair(l[8 * c + 3], l[8 * c + 7]));
   }
-  return d0 + d1;
+  sx[g] = kPairBias * sum;
 }
 
-template <int L, int C, int M, int R, typename XT>
+constexpr int kMaxGemvRows = 4;
+
+// B: groups per lane whose loads are issued together (divides G / L).
+// M: rows of x (1..4), uniform.
+template <int L, int B, bool F32X>
 __global__ __launch_bounds__(256) void w4_gemv_kernel(
-    const XT *__restrict__ x, const uint4 *__restrict__ wq,
-    const uint16_t *__restrict__ ws, void *__restrict__ y, int y_bf16, int K,
-    int N) {
-  constexpr int TPW = 64 / L;  // teams per wave
+    const void *__restrict__ x, const uint4 *__restrict__ wq, const uint16_t *__restrict__ ws,
+    void *__restrict__ y, int y_bf16, int K, int N, int M) {
+  extern __shared__ uint4 lds[];
+  constexpr int TPW = 64 / L;
   const int G = K >> 5;
-  const int GL = G / L;  // groups per lane per row
+  const int GL = G / L;
   const int lane = threadIdx.x & 63;
   const int tl = lane & (L - 1);
-  const int team = (blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6)) * TPW + lane / L;
-  const int row0 = team * R;
+  const int row = (blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6)) * TPW + lane / L;
+  // Lanes past the last row read the last row (no branch around the loads)
+  // and do not store.
+  const size_t rbase = (size_t)(row < N ? row : N - 1) * G + tl;
 
-  float acc[M][R];
+  // 1. weight loads of the first batch (HBM), all in flight together
+  uint4 q[B];
+  uint32_t s[B];
 #pragma unroll
-  for (int m = 0; m < M; ++m)
-#pragma unroll
-    for (int r = 0; r < R; ++r) acc[m][r] = 0.f;
+  for (int i = 0; i < B; ++i) {
+    q[i] = ld_nt(&wq[rbase + (size_t)L * i]);
+    s[i] = ws[rbase + (size_t)L * i];
+  }
 
-  for (int j0 = 0; j0 < GL; j0 += C) {
-    // Weight loads first: they come from HBM and take the longest.
-    uint4 q[R][C];
-    uint32_t s[R][C];
+  // 2. stage x (L2) into LDS
+  constexpr int CH = F32X ? 2 : 1;
+  uint4 *hi = lds;
+  uint4 *lo = lds + (size_t)M * 4 * G;
+  float *sx = reinterpret_cast<float *>(lds + (size_t)M * 4 * G * CH);
+  for (int g = threadIdx.x; g < G; g += blockDim.x)
 #pragma unroll
-    for (int r = 0; r < R; ++r) {
-      const int row = row0 + r;
+    for (int m = 0; m < kMaxGemvRows; ++m)
+      if (m < M)
+        stage_group<F32X>(F32X ? (const void *)(static_cast<const float *>(x) + (size_t)m * K)
+                               : (const void *)(static_cast<const uint16_t *>(x) + (size_t)m * K),
+                          g, G, hi + (size_t)m * 4 * G, lo + (size_t)m * 4 * G, sx + (size_t)m * G);
+  __syncthreads();
+
+  uint32_t mask = 0x000F000Fu;
+  asm volatile("" : "+v"(mask));  // keep the mask in a VGPR: lets v_and_or_b32 take the magic
+
+  float acc[kMaxGemvRows] = {0.f, 0.f, 0.f, 0.f};
+  for (int b0 = 0; b0 < GL; b0 += B) {
+    if (b0 > 0) {
 #pragma unroll
-      for (int c = 0; c < C; ++c) {
-        if (row < N) {
-          const size_t idx = (size_t)row * G + tl + L * (j0 + c);
-          q[r][c] = ld_nt(&wq[idx]);
-          s[r][c] = ws[idx];
-        } else {
-          q[r][c] = make_uint4(0, 0, 0, 0);
-          s[r][c] = 0;
-        }
+      for (int i = 0; i < B; ++i) {
+        q[i] = ld_nt(&wq[rbase + (size_t)L * (b0 + i)]);
+        s[i] = ws[rbase + (size_t)L * (b0 + i)];
       }
     }
 #pragma unroll
-    for (int c = 0; c < C; ++c) {
-      const int g = tl + L * (j0 + c);
+    for (int i = 0; i < B; ++i) {
+      const int g = tl + L * (b0 + i);
+      const uint32_t wd[4] = {q[i].x, q[i].y, q[i].z, q[i].w};
+      uint32_t wp[16];
 #pragma unroll
-      for (int m = 0; m < M; ++m) {
-        float xv[32];
-        load_x_group<XT>(x + (size_t)m * K + (size_t)g * 32, xv);
-        float sx = 0.f;
+      for (int c = 0; c < 4; ++c)
 #pragma unroll
-        for (int i = 0; i < 32; ++i) sx += xv[i];
-        const float off = -8.f * sx;
+        for (int t = 0; t < 4; ++t) wp[4 * c + t] = ((wd[c] >> (4 * t)) & mask) | kPairMagic;
+      const float sc = bf16_to_f32(s[i]);
 #pragma unroll
-        for (int r = 0; r < R; ++r) {
-          const float d = group_dot(q[r][c], xv) + off;
-          acc[m][r] = fmaf(bf16_to_f32(s[r][c]), d, acc[m][r]);
+      for (int m = 0; m < kMaxGemvRows; ++m) {
+        if (m >= M) break;
+        const uint4 *hm = hi + (size_t)m * 4 * G;
+        const uint4 *lm = lo + (size_t)m * 4 * G;
+        float d = 0.f;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const uint4 xp = hm[c * G + g];
+          d = dot2_bf16(xp.x, wp[4 * c + 0], d);
+          d = dot2_bf16(xp.y, wp[4 * c + 1], d);
+          d = dot2_bf16(xp.z, wp[4 * c + 2], d);
+          d = dot2_bf16(xp.w, wp[4 * c + 3], d);
+          if (F32X) {
+            const uint4 xl = lm[c * G + g];
+            d = dot2_bf16(xl.x, wp[4 * c + 0], d);
+            d = dot2_bf16(xl.y, wp[4 * c + 1], d);
+            d = dot2_bf16(xl.z, wp[4 * c + 2], d);
+            d = dot2_bf16(xl.w, wp[4 * c + 3], d);
+          }
         }
+        acc[m] = fmaf(sc, d - sx[(size_t)m * G + g], acc[m]);
       }
     }
   }
 
 #pragma unroll
-  for (int m = 0; m < M; ++m)
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      float v = acc[m][r];
-#pragma unroll
-      for (int o = L / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-      acc[m][r] = v;
-    }
+  for (int m = 0; m < kMaxGemvRows; ++m)
+    if (m < M) acc[m] = team_sum<L>(acc[m]);
 
-  if (tl == 0) {
+  if (tl == 0 && row < N) {
 #pragma unroll
-    for (int r = 0; r < R; ++r) {
-      const int row = row0 + r;
-      if (row >= N) continue;
-#pragma unroll
-      for (int m = 0; m < M; ++m) {
-        const size_t o = (size_t)m * N + row;
-        if (y_bf16)
-          static_cast<uint16_t *>(y)[o] = (uint16_t)f32_to_bf16_rne(acc[m][r]);
-        else
-          static_cast<float *>(y)[o] = acc[m][r];
-      }
+    for (int m = 0; m < kMaxGemvRows; ++m) {
+      if (m >= M) break;
+      const size_t o = (size_t)m * N + row;
+      if (y_bf16)
+        static_cast<uint16_t *>(y)[o] = (uint16_t)f32_to_bf16_rne(acc[m]);
+      else
+        static_cast<float *>(y)[o] = acc[m];
     }
   }
 }
 
-template <int L, int C, int M, int R, typename XT>
-int launch_gemv_lcmr(const g4_w4 *w, const XT *x, void *y, int y_bf16) {
+// LDS bytes the GEMV stages per activation row.
+size_t gemv_lds_per_row(int K, bool f32x) {
+  const size_t G = (size_t)K / 32;
+  return G * 4 * 16 * (f32x ? 2 : 1) + G * 4;
+}
+
+constexpr size_t kGemvLdsBudget = 64 * 1024;
+
+template <int L, int B, bool F32X>
+int launch_gemv_lb(const g4_w4 *w, const void *x, int M, void *y, int y_bf16) {
   constexpr int TPW = 64 / L;
-  const int teams = (w->N + R - 1) / R;
-  const int waves = (teams + TPW - 1) / TPW;
+  const int waves = (w->N + TPW - 1) / TPW;
   const int blocks = (waves + 3) / 4;
-  hipLaunchKernelGGL((w4_gemv_kernel<L, C, M, R, XT>), dim3(blocks), dim3(256), 0,
-                     stream(), x, w->packed, w->scales, y, y_bf16, w->K, w->N);
+  const size_t lds = gemv_lds_per_row(w->K, F32X) * M;
+  hipLaunchKernelGGL((w4_gemv_kernel<L, B, F32X>), dim3(blocks), dim3(256), lds, stream(), x,
+                     w->packed, w->scales, y, y_bf16, w->K, w->N, M);
   G4_LAUNCH_CHECK("w4_gemv_kernel");
   return G4_OK;
 }
 
-template <int L, int M, typename XT>
-int launch_gemv_lm(const g4_w4 *w, const XT *x, void *y, int y_bf16) {
+template <int L, bool F32X>
+int launch_gemv_l(const g4_w4 *w, const void *x, int M, void *y, int y_bf16) {
   const int GL = w->G / L;
-  if (M > 1) return launch_gemv_lcmr<L, 1, M, 1, XT>(w, x, y, y_bf16);
-  // Rows per team: keep >= ~1500 waves in flight on the 256 CUs.
-  constexpr int TPW = 64 / L;
-  const int waves1 = (w->N + TPW - 1) / TPW;
-  const int R = waves1 >= 8192 ? 4 : waves1 >= 4096 ? 2 : 1;
-  const int C = (GL % 3 == 0) ? 3 : (GL % 2 == 0) ? 2 : 1;
-#define G4_GEMV_CASE(CC, RR) \
-  if (C == CC && R == RR) return launch_gemv_lcmr<L, CC, 1, RR, XT>(w, x, y, y_bf16);
-  G4_GEMV_CASE(1, 1) G4_GEMV_CASE(1, 2) G4_GEMV_CASE(1, 4)
-  G4_GEMV_CASE(2, 1) G4_GEMV_CASE(2, 2) G4_GEMV_CASE(2, 4)
-  G4_GEMV_CASE(3, 1) G4_GEMV_CASE(3, 2) G4_GEMV_CASE(3, 4)
-#undef G4_GEMV_CASE
-  return fail(G4_E_ARG, "no GEMV variant for C=%d R=%d", C, R);
+  if (GL % 8 == 0) return launch_gemv_lb<L, 8, F32X>(w, x, M, y, y_bf16);
+  if (GL % 6 == 0) return launch_gemv_lb<L, 6, F32X>(w, x, M, y, y_bf16);
+  if (GL % 4 == 0) return launch_gemv_lb<L, 4, F32X>(w, x, M, y, y_bf16);
+  if (GL % 3 == 0) return launch_gemv_lb<L, 3, F32X>(w, x, M, y, y_bf16);
+  if (GL % 2 == 0) return launch_gemv_lb<L, 2, F32X>(w, x, M, y, y_bf16);
+  return launch_gemv_lb<L, 1, F32X>(w, x, M, y, y_bf16);
 }
 
-template <int M, typename XT>
-int launch_gemv_m(const g4_w4 *w, const XT *x, void *y, int y_bf16) {
+template <bool F32X>
+int launch_gemv(const g4_w4 *w, const void *x, int M, void *y, int y_bf16) {
+  if (M < 1 || M > kMaxGemvRows)
+    return fail(G4_E_ARG, "GEMV takes 1..%d rows per launch, got %d", kMaxGemvRows, M);
   const int G = w->G;
-  if (G % 64 == 0) return launch_gemv_lm<64, M, XT>(w, x, y, y_bf16);
-  if (G % 16 == 0) return launch_gemv_lm<16, M, XT>(w, x, y, y_bf16);
-  if (G % 8 == 0) return launch_gemv_lm<8, M, XT>(w, x, y, y_bf16);
-  return launch_gemv_lm<1, M, XT>(w, x, y, y_bf16);
+  if (G % 64 == 0) return launch_gemv_l<64, F32X>(w, x, M, y, y_bf16);
+  if (G % 32 == 0) return launch_gemv_l<32, F32X>(w, x, M, y, y_bf16);
+  if (G % 16 == 0) return launch_gemv_l<16, F32X>(w, x, M, y, y_bf16);
+  if (G % 8 == 0) return launch_gemv_l<8, F32X>(w, x, M, y, y_bf16);
+  return launch_gemv_l<1, F32X>(w, x, M, y, y_bf16);
 }
 
-template <typename XT>
-int launch_gemv(const g4_w4 *w, const XT *x, int rows, void *y, int y_bf16) {
-  switch (rows) {
-    case 1: return launch_gemv_m<1, XT>(w, x, y, y_bf16);
-    case 2: return launch_gemv_m<2, XT>(w, x, y, y_bf16);
-    case 3: return launch_gemv_m<3, XT>(w, x, y, y_bf16);
-    case 4: return launch_gemv_m<4, XT>(w, x, y, y_bf16);
+// Rows of x one GEMV launch takes: at most 4, and within the LDS budget.
+int gemv_rows_per_launch(int K, bool f32x) {
+  const size_t per = gemv_lds_per_row(K, f32x);
+  int m = (int)(kGemvLdsBudget / per);
+  return m < 1 ? 1 : m > kMaxGemvRows ? kMaxGemvRows : m;
+}
+
+// ---------------------------------------------------------------------------
+// Decode GEMV, one row of x (the M = 1 hot path).
+//
+// Flat work split: the weights of RB consecutive output rows are RB * G
+// 16-byte groups, contiguous in memory.  A block of T threads owns those RB
+// rows and thread t takes groups t, t + T, ..., t + (IPL-1) T of that slab, so
+// every load instruction of a wave reads 1 KB of consecutive bytes and every
+// lane does the same work (one or a few groups: many short waves keep all
+// four SIMDs of every CU busy when the data lands).  Each group's partial
+// s * (d - 136 * sum x) goes to LDS and 16 lanes per row add them up.
+//
+// x staging: each thread first loads its 8-element chunks of x - before any
+// weight load, because vmcnt retires loads in issue order and x must not wait
+// behind the HBM stream - turns each chunk into the 4 pair dwords of one
+// packed word and adds its 8 values into the group sum with a quad DPP
+// reduction.  Needs RB >= 4, which makes chunks per thread <= IPL.
+// ---------------------------------------------------------------------------
+template <int IPL, bool F32X>
+__global__ __launch_bounds__(1024) void w4_gemv1_kernel(
+    const void *__restrict__ x, const uint4 *__restrict__ wq, const uint16_t *__restrict__ ws,
+    void *__restrict__ y, int y_bf16, int K, int N, int RB) {
+  extern __shared__ uint4 lds[];
+  const int T = blockDim.x;
+  const int G = K >> 5;
+  const int nch = K >> 3;
+  const int t = threadIdx.x;
+
+  // 1. x chunks (L2-resident), issued first
+  uint4 xa[IPL], xb[IPL];
+#pragma unroll
+  for (int i = 0; i < IPL; ++i) {
+    const int ct = t + i * T;
+    const int cc = ct < nch ? ct : nch - 1;
+    if (F32X) {
+      xa[i] = reinterpret_cast<const uint4 *>(x)[2 * cc];
+      xb[i] = reinterpret_cast<const uint4 *>(x)[2 * cc + 1];
+    } else {
+      xa[i] = reinterpret_cast<const uint4 *>(x)[cc];
+    }
   }
-  return fail(G4_E_ARG, "GEMV supports 1..4 rows, got %d", rows);
+
+  // 2. weight groups (HBM); rows past N re-read the last group and are not stored
+  const size_t base = (size_t)blockIdx.x * RB * G;
+  const size_t last = (size_t)N * G - 1;
+  uint4 q[IPL];
+  uint32_t s[IPL];
+#pragma unroll
+  for (int i = 0; i < IPL; ++i) {
+    size_t it = base + t + (size_t)i * T;
+    it = it < last ? it : last;
+    q[i] = ld_nt(&wq[it]);
+    s[i] = ws[it];
+  }
+
+  // 3. stage x into LDS: hi[4][G], lo[4][G] (FP32 x), sx[G], then partials
+  constexpr int CH = F32X ? 2 : 1;
+  uint4 *hi = lds;
+  uint4 *lo = lds + 4 * G;
+  float *sx = reinterpret_cast<float *>(lds + 4 * G * CH);
+  float *part = sx + G;
+#pragma unroll
+  for (int i = 0; i < IPL; ++i) {
+    const int ct = t + i * T;
+    uint32_t h[8], l[8];
+    float sum = 0.f;
+    if (F32X) {
+      const float v[8] = {__uint_as_float(xa[i].x), __uint_as_float(xa[i].y),
+                          __uint_as_float(xa[i].z), __uint_as_float(xa[i].w),
+                          __uint_as_float(xb[i].x), __uint_as_float(xb[i].y),
+                          __uint_as_float(xb[i].z), __uint_as_float(xb[i].w)};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        h[e] = f32_to_bf16_rne(v[e]);
+        l[e] = f32_to_bf16_rne(v[e] - bf16_to_f32(h[e]));
+        sum += bf16_to_f32(h[e]) + bf16_to_f32(l[e]);
+      }
+    } else {
+      const uint32_t w[4] = {xa[i].x, xa[i].y, xa[i].z, xa[i].w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        h[2 * e] = w[e] & 0xffffu;
+        h[2 * e + 1] = w[e] >> 16;
+        sum += bf16_to_f32(h[2 * e]) + bf16_to_f32(h[2 * e + 1]);
+      }
+    }
+    // chunks 4g..4g+3 of a group sit in one lane quad
+    sum += dpp_f32<0xB1>(sum);
+    sum += dpp_f32<0x4E>(sum);
+    if (ct < nch) {
+      const int g = ct >> 2, c = ct & 3;
+      hi[c * G + g] = make_uint4(bf16_pair(h[0], h[4]), bf16_pair(h[1], h[5]),
+                                 bf16_pair(h[2], h[6]), bf16_pair(h[3], h[7]));
+      if (F32X)
+        lo[c * G + g] = make_uint4(bf16_pair(l[0], l[4]), bf16_pair(l[1], l[5]),
+                                   bf16_pair(l[2], l[6]), bf16_pair(l[3], l[7]));
+      if (c == 0) sx[g] = kPairBias * sum;
+    }
+  }
+  __syncthreads();
+
+  // 4. one partial per group
+  uint32_t mask = 0x000F000Fu;
+  asm volatile("" : "+v"(mask));  // keep the mask in a VGPR: lets v_and_or_b32 take the magic
+#pragma unroll
+  for (int i = 0; i < IPL; ++i) {
+    const int li = t + i * T;
+    const int g = li % G;
+    const uint32_t wd[4] = {q[i].x, q[i].y, q[i].z, q[i].w};
+    float d0 = 0.f, d1 = 0.f;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const uint32_t p0 = (wd[c] & mask) | kPairMagic;
+      const uint32_t p1 = ((wd[c] >> 4) & mask) | kPairMagic;
+      const uint32_t p2 = ((wd[c] >> 8) & mask) | kPairMagic;
+      const uint32_t p3 = ((wd[c] >> 12) & mask) | kPairMagic;
+      const uint4 xp = hi[c * G + g];
+      d0 = dot2_bf16(xp.x, p0, d0);
+      d1 = dot2_bf16(xp.y, p1, d1);
+      d0 = dot2_bf16(xp.z, p2, d0);
+      d1 = dot2_bf16(xp.w, p3, d1);
+      if (F32X) {
+        const uint4 xl = lo[c * G + g];
+        d0 = dot2_bf16(xl.x, p0, d0);
+        d1 = dot2_bf16(xl.y, p1, d1);
+        d0 = dot2_bf16(xl.z, p2, d0);
+        d1 = dot2_bf16(xl.w, p3, d1);
+      }
+    }
+    part[li] = bf16_to_f32(s[i]) * ((d0 + d1) - sx[g]);
+  }
+  __syncthreads();
+
+  // 5. 16 lanes per row sum the row's G partials
+  for (int b = 0; b < RB * 16; b += T) {
+    const int idx = b + t;
+    const int r = idx >> 4, j = idx & 15;
+    float v = 0.f;
+    if (r < RB)
+      for (int g = j; g < G; g += 16) v += part[r * G + g];
+    v = team_sum<16>(v);
+    const size_t row = (size_t)blockIdx.x * RB + r;
+    if (j == 0 && r < RB && row < (size_t)N) {
+      if (y_bf16)
+        static_cast<uint16_t *>(y)[row] = (uint16_t)f32_to_bf16_rne(v);
+      else
+        static_cast<float *>(y)[row] = v;
+    }
+  }
+}
+
+struct Gemv1Plan {
+  int T, IPL, RB;
+  size_t lds;
+};
+
+// Rows per block RB >= 4 (x staging amortised over >= 4 rows), RB * G = T * IPL
+// with T a multiple of 64 up to 1024 and IPL <= 4.
+bool plan_gemv1(int G, bool f32x, Gemv1Plan *p) {
+  for (int RB = 4; RB <= 256; RB *= 2) {
+    const long items = (long)RB * G;
+    if (items % 64) continue;
+    for (int ipl = 1; ipl <= 4; ++ipl) {
+      if (items % ipl) continue;
+      const long T = items / ipl;
+      if (T % 64 || T > 1024) continue;
+      p->T = (int)T;
+      p->IPL = ipl;
+      p->RB = RB;
+      p->lds = (size_t)G * 4 * 16 * (f32x ? 2 : 1) + (size_t)G * 4 + (size_t)RB * G * 4;
+      return p->lds <= 64 * 1024;
+    }
+  }
+  return false;
+}
+
+template <int IPL, bool F32X>
+int launch_gemv1_i(const g4_w4 *w, const Gemv1Plan &p, const void *x, void *y, int y_bf16) {
+  const int blocks = (w->N + p.RB - 1) / p.RB;
+  hipLaunchKernelGGL((w4_gemv1_kernel<IPL, F32X>), dim3(blocks), dim3(p.T), p.lds, stream(), x,
+                     w->packed, w->scales, y, y_bf16, w->K, w->N, p.RB);
+  G4_LAUNCH_CHECK("w4_gemv1_kernel");
+  return G4_OK;
+}
+
+template <bool F32X>
+int launch_gemv1(const g4_w4 *w, const void *x, void *y, int y_bf16) {
+  Gemv1Plan p;
+  if (!plan_gemv1(w->G, F32X, &p))
+    return fail(G4_E_ARG, "g4_w4_linear: no decode GEMV plan for in_dim %d", w->K);
+  switch (p.IPL) {
+    case 1: return launch_gemv1_i<1, F32X>(w, p, x, y, y_bf16);
+    case 2: return launch_gemv1_i<2, F32X>(w, p, x, y, y_bf16);
+    case 3: return launch_gemv1_i<3, F32X>(w, p, x, y, y_bf16);
+    default: return launch_gemv1_i<4, F32X>(w, p, x, y, y_bf16);
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -290,21 +545,22 @@ G4_API int g4_w4_load(const void *packed, const void *scales, int out_dim,
   w->G = in_dim / 32;
   const size_t qbytes = (size_t)out_dim * in_dim / 2;
   const size_t sbytes = (size_t)out_dim * w->G * 2;
-  int rc = device_alloc(qbytes, reinterpret_cast<void **>(&w->packed));
-  if (!rc) rc = device_alloc(sbytes, reinterpret_cast<void **>(&w->scales));
+  const size_t soff = (qbytes + 255) & ~size_t(255);
+  // One allocation: packed groups, then the scales.
+  int rc = device_alloc(soff + sbytes, reinterpret_cast<void **>(&w->mem));
   if (rc) {
-    device_free(w->packed);
     delete w;
     return rc;
   }
-  w->bytes = qbytes + sbytes;
+  w->packed = reinterpret_cast<uint4 *>(w->mem);
+  w->scales = reinterpret_cast<uint16_t *>(w->mem + soff);
+  w->bytes = soff + sbytes;
   hipError_t e = hipMemcpyAsync(w->packed, packed, qbytes, hipMemcpyHostToDevice, stream());
   if (e == hipSuccess)
     e = hipMemcpyAsync(w->scales, scales, sbytes, hipMemcpyHostToDevice, stream());
   if (e == hipSuccess) e = hipStreamSynchronize(stream());
   if (e != hipSuccess) {
-    device_free(w->packed);
-    device_free(w->scales);
+    device_free(w->mem);
     delete w;
     return fail(G4_E_HIP, "g4_w4_load: upload failed: %s", hipGetErrorString(e));
   }
@@ -316,10 +572,9 @@ G4_API int g4_w4_free(g4_w4 *w) {
   G4_CHECK_INIT();
   G4_CHECK_NOT_ENCODING();
   if (!w) return ok();
-  int rc = device_free(w->packed);
-  int rc2 = device_free(w->scales);
+  int rc = device_free(w->mem);
   delete w;
-  return rc ? rc : rc2 ? rc2 : ok();
+  return rc ? rc : ok();
 }
 
 G4_API int g4_w4_info(const g4_w4 *w, int *out_dim, int *in_dim, int *group,
@@ -347,16 +602,22 @@ G4_API int g4_w4_linear(const g4_w4 *w, const void *x, int x_dtype, int rows,
   if (rc) return rc;
   rc = check_device_range(y, (size_t)rows * w->N * ye, "g4_w4_linear y");
   if (rc) return rc;
-  // Rows are processed 4 at a time by the streaming kernel.
-  for (int r0 = 0; r0 < rows; r0 += 4) {
-    const int m = rows - r0 < 4 ? rows - r0 : 4;
+  const bool f32x = x_dtype == G4_F32;
+  if (gemv_lds_per_row(w->K, f32x) > kGemvLdsBudget)
+    return fail(G4_E_ARG, "g4_w4_linear: in_dim %d exceeds the GEMV staging limit (%s x)",
+                w->K, f32x ? "FP32" : "BF16");
+  if (rows == 1) {
+    rc = f32x ? launch_gemv1<true>(w, x, y, y_dtype == G4_BF16)
+              : launch_gemv1<false>(w, x, y, y_dtype == G4_BF16);
+    return rc ? rc : ok();
+  }
+  const int per = gemv_rows_per_launch(w->K, f32x);
+  for (int r0 = 0; r0 < rows; r0 += per) {
+    const int m = rows - r0 < per ? rows - r0 : per;
+    const void *xr = static_cast<const char *>(x) + (size_t)r0 * w->K * xe;
     void *yr = static_cast<char *>(y) + (size_t)r0 * w->N * ye;
-    if (x_dtype == G4_F32)
-      rc = launch_gemv<float>(w, static_cast<const float *>(x) + (size_t)r0 * w->K, m, yr,
-                              y_dtype == G4_BF16);
-    else
-      rc = launch_gemv<uint16_t>(w, static_cast<const uint16_t *>(x) + (size_t)r0 * w->K, m,
-                                 yr, y_dtype == G4_BF16);
+    rc = f32x ? launch_gemv<true>(w, xr, m, yr, y_dtype == G4_BF16)
+              : launch_gemv<false>(w, xr, m, yr, y_dtype == G4_BF16);
     if (rc) return rc;
   }
   return ok();
