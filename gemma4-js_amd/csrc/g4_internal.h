@@ -102,3 +102,18 @@ __device__ __forceinline__ uint32_t f32_to_bf16_rne(float v) {
 }
 
 }  // namespace g4
+
+// A W4A16 weight resident on the device (GPUW4Linear).
+struct g4_w4 {
+  int N, K, group, G;
+  uint8_t *mem;      // the one device allocation holding both arrays
+  uint4 *packed;     // [N][G] 16-byte groups, compressed-tensors order
+  uint16_t *scales;  // [N][G] bf16 bits
+  size_t bytes;
+  int shift;         // 2^shift * 8 * max|scale| <= 2^15 keeps every FP16 q*s exact
+};
+
+namespace g4 {
+// Prefill GEMM (rows >= 2): y[rows, N] = x[rows, K] . W^T, MFMA (g4_gemm.hip).
+int w4_gemm(const g4_w4 *w, const void *x, bool f32x, int rows, void *y, bool y_bf16);
+}  // namespace g4

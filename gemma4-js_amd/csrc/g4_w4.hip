@@ -11,14 +11,6 @@
 // coalesced dwordx4 load.
 #include "g4_internal.h"
 
-struct g4_w4 {
-  int N, K, group, G;
-  uint8_t *mem;      // the one device allocation holding both arrays
-  uint4 *packed;     // [N][G] 16-byte groups
-  uint16_t *scales;  // [N][G] bf16 bits
-  size_t bytes;
-};
-
 namespace {
 
 using namespace g4;
@@ -555,6 +547,26 @@ G4_API int g4_w4_load(const void *packed, const void *scales, int out_dim,
   w->packed = reinterpret_cast<uint4 *>(w->mem);
   w->scales = reinterpret_cast<uint16_t *>(w->mem + soff);
   w->bytes = soff + sbytes;
+  // Power-of-two shift for the FP16 path of the prefill GEMM: with
+  // 2^shift * 8 * max|s| <= 2^15 every q * s * 2^shift (<= 11 significant
+  // bits) stays an exact FP16 value unless a scale is 2^29 times smaller
+  // than the largest one.
+  {
+    const uint16_t *sb = static_cast<const uint16_t *>(scales);
+    uint32_t maxbits = 0;
+    for (size_t i = 0, n = (size_t)out_dim * w->G; i < n; ++i) {
+      const uint32_t a = sb[i] & 0x7fffu;
+      if (a < 0x7f80u && a > maxbits) maxbits = a;  // finite magnitudes only
+    }
+    int shift = 0;
+    if (maxbits) {
+      const int e = (int)(maxbits >> 7) - 127;  // floor(log2(max|s|)) for normal bf16
+      shift = 11 - e;                           // 8 * 2^(e+1) * 2^shift <= 2^15
+      if (shift > 60) shift = 60;
+      if (shift < -60) shift = -60;
+    }
+    w->shift = shift;
+  }
   hipError_t e = hipMemcpyAsync(w->packed, packed, qbytes, hipMemcpyHostToDevice, stream());
   if (e == hipSuccess)
     e = hipMemcpyAsync(w->scales, scales, sbytes, hipMemcpyHostToDevice, stream());
@@ -609,6 +621,10 @@ G4_API int g4_w4_linear(const g4_w4 *w, const void *x, int x_dtype, int rows,
   if (rows == 1) {
     rc = f32x ? launch_gemv1<true>(w, x, y, y_dtype == G4_BF16)
               : launch_gemv1<false>(w, x, y, y_dtype == G4_BF16);
+    return rc ? rc : ok();
+  }
+  if (rows > kMaxGemvRows) {
+    rc = w4_gemm(w, x, f32x, rows, y, y_dtype == G4_BF16);
     return rc ? rc : ok();
   }
   const int per = gemv_rows_per_launch(w->K, f32x);

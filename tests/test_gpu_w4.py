@@ -142,6 +142,44 @@ def test_prefill_gemm_config3(g4, oracle):
         assert rel_l2_rows(y[sample], ref32) <= TOL
 
 
+@pytest.mark.parametrize("x_dtype_name", ["f32", "bf16"])
+def test_gemm_ragged_shapes_and_activation_ranges(g4, x_dtype_name):
+    # Rows and columns that are not tile multiples, and activation rows far
+    # outside FP16's range (1e5..1e-7 scale factors): the per-row power-of-two
+    # rescale must keep every row inside the tolerance.
+    n, k, m = 200, 256, 130
+    packed, scales, q = syn.w4_weights(9, n, k)
+    rng = np.random.default_rng(9)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    factors = np.array([1e5, 3e4, 1.0, 1e-3, 1e-7, 7.0] * 22, dtype=np.float32)[:m]
+    x *= factors[:, None]
+    x[5] = 0.0  # an all-zero row
+    x_bits = syn.bf16_rne(x)
+    if x_dtype_name == "bf16":
+        x = syn.bf16_to_f32(x_bits).reshape(m, k)
+    lin = g4.W4Linear(packed, scales)
+    y = run_linear(g4, lin, x_bits, x, m, g4.BF16 if x_dtype_name == "bf16" else g4.F32)
+    ref = x.astype(np.float64) @ dense(q, scales).T
+    nz = np.ones(m, bool)
+    nz[5] = False
+    assert rel_l2_rows(y[nz], ref[nz]) <= TOL
+    assert np.all(y[5] == 0.0)
+
+
+def test_gemm_matches_gemv_path(g4):
+    # Rows 1..4 take the streaming GEMV, more rows the MFMA GEMM: the row a
+    # caller computes must not depend on how many rows come with it.
+    packed, scales, q = syn.w4_weights(13, 1536, 2048)
+    x_bits, x = syn.activations(13, 40, 2048)
+    lin = g4.W4Linear(packed, scales)
+    big = run_linear(g4, lin, x_bits, x, 40, g4.BF16)
+    ref = x.astype(np.float64) @ dense(q, scales).T
+    for r in (0, 17, 39):
+        one = run_linear(g4, lin, x_bits[r:r + 1], x[r:r + 1], 1, g4.BF16)
+        assert rel_l2_rows(one, ref[r:r + 1]) < 1e-4
+        assert rel_l2_rows(big[r:r + 1], ref[r:r + 1]) < 1e-4
+
+
 def test_errors_are_reported_not_faulted(g4):
     packed, scales, _ = syn.w4_weights(1, 256, 512)
     lin = g4.W4Linear(packed, scales)
