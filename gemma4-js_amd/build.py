@@ -80,7 +80,7 @@ def build_node_addon():
         return None
     tmp = ADDON + ".tmp"
     _run(["g++", "-O2", "-std=c++14", "-fPIC", "-shared", "-Wall",
-          "-DNAPI_VERSION=8", "-I", NODE_INCLUDE, "-I", INCLUDE, src,
+          "-DNAPI_VERSION=8", "-DNODE_GYP_MODULE_NAME=g4hip", "-I", NODE_INCLUDE, "-I", INCLUDE, src,
           "-o", tmp, "-L", LIBDIR, "-lg4hip", "-Wl,-rpath,$ORIGIN/../lib"])
     os.replace(tmp, ADDON)
     return ADDON

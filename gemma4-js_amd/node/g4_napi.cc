@@ -1,0 +1,763 @@
+// N-API binding of libg4hip (include/g4hip.h) for Node.
+//
+// This is the native half of the bridge that replaces the WebGPU buffer and
+// dispatch layer of custom-webgpu/gpu-runtime.js: device buffers become
+// DeviceBuffer objects, GPUW4Linear weights become W4Weight objects, the PLE
+// shard bundle becomes a PleTable, and every non-zero status from the C ABI is
+// thrown as a JS Error carrying g4_last_error() - the reference's own error
+// convention (synchronous throws for shape/range/capacity errors).
+//
+// Only plain pointers and sizes cross into the C ABI.  Objects own their
+// native handle; destroy() releases it and a finalizer is the backstop.
+#include <node_api.h>
+
+#include <stdint.h>
+#include <stdio.h>
+#include <string.h>
+
+#include "g4hip.h"
+
+namespace {
+
+#define NAPI_CALL(env, call)                                                   \
+  do {                                                                         \
+    napi_status s_ = (call);                                                   \
+    if (s_ != napi_ok) {                                                       \
+      const napi_extended_error_info *info_ = nullptr;                         \
+      napi_get_last_error_info((env), &info_);                                 \
+      bool pending_ = false;                                                   \
+      napi_is_exception_pending((env), &pending_);                             \
+      if (!pending_)                                                           \
+        napi_throw_error((env), nullptr,                                       \
+                         info_ && info_->error_message ? info_->error_message  \
+                                                       : "N-API call failed"); \
+      return nullptr;                                                          \
+    }                                                                          \
+  } while (0)
+
+// Throws the C ABI's error and returns nullptr from the calling function.
+#define G4_CALL(env, call)                                      \
+  do {                                                          \
+    int rc_ = (call);                                           \
+    if (rc_ != G4_OK) {                                         \
+      char code_[32];                                           \
+      snprintf(code_, sizeof code_, "G4_STATUS_%d", rc_);       \
+      napi_throw_error((env), code_, g4_last_error());          \
+      return nullptr;                                           \
+    }                                                           \
+  } while (0)
+
+napi_value undefined(napi_env env) {
+  napi_value u;
+  napi_get_undefined(env, &u);
+  return u;
+}
+
+bool get_args(napi_env env, napi_callback_info info, size_t want, napi_value *argv,
+              napi_value *self, void **data = nullptr) {
+  size_t argc = want;
+  if (napi_get_cb_info(env, info, &argc, argv, self, data) != napi_ok) return false;
+  for (size_t i = argc; i < want; ++i) napi_get_undefined(env, &argv[i]);
+  return true;
+}
+
+bool to_i64(napi_env env, napi_value v, int64_t *out, const char *what) {
+  napi_valuetype t;
+  napi_typeof(env, v, &t);
+  if (t != napi_number) {
+    char msg[128];
+    snprintf(msg, sizeof msg, "%s must be a number", what);
+    napi_throw_type_error(env, nullptr, msg);
+    return false;
+  }
+  double d;
+  napi_get_value_double(env, v, &d);
+  if (d != (double)(int64_t)d) {
+    char msg[128];
+    snprintf(msg, sizeof msg, "%s must be an integer", what);
+    napi_throw_range_error(env, nullptr, msg);
+    return false;
+  }
+  *out = (int64_t)d;
+  return true;
+}
+
+bool to_f64(napi_env env, napi_value v, double *out, const char *what) {
+  napi_valuetype t;
+  napi_typeof(env, v, &t);
+  if (t != napi_number) {
+    char msg[128];
+    snprintf(msg, sizeof msg, "%s must be a number", what);
+    napi_throw_type_error(env, nullptr, msg);
+    return false;
+  }
+  napi_get_value_double(env, v, out);
+  return true;
+}
+
+// Bytes of an ArrayBuffer, TypedArray, DataView or Buffer.
+bool host_bytes(napi_env env, napi_value v, void **data, size_t *len, const char *what) {
+  bool is;
+  napi_is_typedarray(env, v, &is);
+  if (is) {
+    napi_typedarray_type type;
+    size_t n, off;
+    napi_value ab;
+    void *p;
+    napi_get_typedarray_info(env, v, &type, &n, &p, &ab, &off);
+    size_t el = 1;
+    switch (type) {
+      case napi_int16_array: case napi_uint16_array: el = 2; break;
+      case napi_int32_array: case napi_uint32_array: case napi_float32_array: el = 4; break;
+      case napi_float64_array: case napi_bigint64_array: case napi_biguint64_array: el = 8; break;
+      default: el = 1;
+    }
+    *data = p;
+    *len = n * el;
+    return true;
+  }
+  napi_is_dataview(env, v, &is);
+  if (is) {
+    napi_value ab;
+    size_t off;
+    napi_get_dataview_info(env, v, len, data, &ab, &off);
+    return true;
+  }
+  napi_is_arraybuffer(env, v, &is);
+  if (is) {
+    napi_get_arraybuffer_info(env, v, data, len);
+    return true;
+  }
+  char msg[128];
+  snprintf(msg, sizeof msg, "%s must be an ArrayBuffer or a typed array", what);
+  napi_throw_type_error(env, nullptr, msg);
+  return false;
+}
+
+// ---- DeviceBuffer ------------------------------------------------------------
+
+struct DevBuf {
+  void *ptr;
+  size_t size;
+};
+
+napi_ref g_devbuf_ctor = nullptr;
+
+void devbuf_finalize(napi_env, void *data, void *) {
+  DevBuf *b = static_cast<DevBuf *>(data);
+  if (b->ptr) g4_free(b->ptr);
+  delete b;
+}
+
+DevBuf *unwrap_buf(napi_env env, napi_value v, const char *what) {
+  void *p = nullptr;
+  bool ok = false;
+  if (g_devbuf_ctor) {
+    napi_value ctor;
+    napi_get_reference_value(env, g_devbuf_ctor, &ctor);
+    napi_instanceof(env, v, ctor, &ok);
+  }
+  if (!ok || napi_unwrap(env, v, &p) != napi_ok || !p) {
+    char msg[128];
+    snprintf(msg, sizeof msg, "%s must be a DeviceBuffer", what);
+    napi_throw_type_error(env, nullptr, msg);
+    return nullptr;
+  }
+  DevBuf *b = static_cast<DevBuf *>(p);
+  if (!b->ptr) {
+    char msg[128];
+    snprintf(msg, sizeof msg, "%s was destroyed", what);
+    napi_throw_error(env, nullptr, msg);
+    return nullptr;
+  }
+  return b;
+}
+
+// Device address of byte `off` of a buffer; throws if off > size.
+bool buf_at(napi_env env, napi_value v, napi_value off_v, const char *what, void **out) {
+  DevBuf *b = unwrap_buf(env, v, what);
+  if (!b) return false;
+  int64_t off = 0;
+  napi_valuetype t;
+  napi_typeof(env, off_v, &t);
+  if (t != napi_undefined && !to_i64(env, off_v, &off, what)) return false;
+  if (off < 0 || (size_t)off > b->size) {
+    char msg[160];
+    snprintf(msg, sizeof msg, "%s: byte offset %lld outside the %zu-byte buffer", what,
+             (long long)off, b->size);
+    napi_throw_range_error(env, nullptr, msg);
+    return false;
+  }
+  *out = static_cast<char *>(b->ptr) + off;
+  return true;
+}
+
+// new DeviceBuffer(size)  - createBuffer (gpu-runtime.js:8-12)
+napi_value DevBuf_new(napi_env env, napi_callback_info info) {
+  napi_value argv[1], self;
+  if (!get_args(env, info, 1, argv, &self)) return nullptr;
+  int64_t size;
+  if (!to_i64(env, argv[0], &size, "size")) return nullptr;
+  if (size < 0) {
+    napi_throw_range_error(env, nullptr, "size must be >= 0");
+    return nullptr;
+  }
+  void *p = nullptr;
+  G4_CALL(env, g4_alloc((size_t)size, &p));
+  DevBuf *b = new DevBuf{p, size < 4 ? 4 : ((size_t)size + 3) & ~size_t(3)};
+  if (napi_wrap(env, self, b, devbuf_finalize, nullptr, nullptr) != napi_ok) {
+    g4_free(p);
+    delete b;
+    napi_throw_error(env, nullptr, "napi_wrap failed");
+    return nullptr;
+  }
+  return self;
+}
+
+napi_value DevBuf_size(napi_env env, napi_callback_info info) {
+  napi_value self;
+  if (!get_args(env, info, 0, nullptr, &self)) return nullptr;
+  void *p;
+  NAPI_CALL(env, napi_unwrap(env, self, &p));
+  napi_value r;
+  NAPI_CALL(env, napi_create_double(env, (double)static_cast<DevBuf *>(p)->size, &r));
+  return r;
+}
+
+// buffer.destroy()
+napi_value DevBuf_destroy(napi_env env, napi_callback_info info) {
+  napi_value self;
+  if (!get_args(env, info, 0, nullptr, &self)) return nullptr;
+  void *p;
+  NAPI_CALL(env, napi_unwrap(env, self, &p));
+  DevBuf *b = static_cast<DevBuf *>(p);
+  if (b->ptr) {
+    void *q = b->ptr;
+    b->ptr = nullptr;
+    G4_CALL(env, g4_free(q));
+  }
+  return undefined(env);
+}
+
+// buffer.write(bytes, byteOffset = 0)  - queue.writeBuffer
+napi_value DevBuf_write(napi_env env, napi_callback_info info) {
+  napi_value argv[2], self;
+  if (!get_args(env, info, 2, argv, &self)) return nullptr;
+  void *dst;
+  if (!buf_at(env, self, argv[1], "buffer", &dst)) return nullptr;
+  void *src;
+  size_t n;
+  if (!host_bytes(env, argv[0], &src, &n, "data")) return nullptr;
+  G4_CALL(env, g4_upload(dst, 0, src, n));
+  return undefined(env);
+}
+
+// buffer.read(byteOffset, byteLength) -> ArrayBuffer  (waits for the queue)
+napi_value DevBuf_read(napi_env env, napi_callback_info info) {
+  napi_value argv[2], self;
+  if (!get_args(env, info, 2, argv, &self)) return nullptr;
+  void *src;
+  if (!buf_at(env, self, argv[0], "buffer", &src)) return nullptr;
+  int64_t n;
+  if (!to_i64(env, argv[1], &n, "byteLength")) return nullptr;
+  if (n < 0) {
+    napi_throw_range_error(env, nullptr, "byteLength must be >= 0");
+    return nullptr;
+  }
+  void *data;
+  napi_value ab;
+  NAPI_CALL(env, napi_create_arraybuffer(env, (size_t)n, &data, &ab));
+  G4_CALL(env, g4_download(src, 0, data, (size_t)n));
+  return ab;
+}
+
+// ---- W4Weight (GPUW4Linear) ----------------------------------------------------
+
+struct W4 {
+  g4_w4 *h;
+  int out_dim, in_dim, group;
+};
+
+napi_ref g_w4_ctor = nullptr;
+
+void w4_finalize(napi_env, void *data, void *) {
+  W4 *w = static_cast<W4 *>(data);
+  if (w->h) g4_w4_free(w->h);
+  delete w;
+}
+
+W4 *unwrap_w4(napi_env env, napi_value self) {
+  void *p = nullptr;
+  if (napi_unwrap(env, self, &p) != napi_ok || !p) {
+    napi_throw_type_error(env, nullptr, "not a W4Weight");
+    return nullptr;
+  }
+  W4 *w = static_cast<W4 *>(p);
+  if (!w->h) {
+    napi_throw_error(env, nullptr, "W4Weight was disposed");
+    return nullptr;
+  }
+  return w;
+}
+
+// new W4Weight(packedBytes, scaleBytes, outDim, inDim, groupSize)
+napi_value W4_new(napi_env env, napi_callback_info info) {
+  napi_value argv[5], self;
+  if (!get_args(env, info, 5, argv, &self)) return nullptr;
+  void *pk, *sc;
+  size_t npk, nsc;
+  if (!host_bytes(env, argv[0], &pk, &npk, "packed")) return nullptr;
+  if (!host_bytes(env, argv[1], &sc, &nsc, "scales")) return nullptr;
+  int64_t out_dim, in_dim, group;
+  if (!to_i64(env, argv[2], &out_dim, "outDim") || !to_i64(env, argv[3], &in_dim, "inDim") ||
+      !to_i64(env, argv[4], &group, "groupSize"))
+    return nullptr;
+  if (out_dim <= 0 || in_dim <= 0 || group <= 0 || in_dim % 8 || in_dim % group) {
+    // the C ABI reports the precise message
+  } else if (npk != (size_t)(out_dim * (in_dim / 8) * 4)) {
+    napi_throw_error(env, nullptr, "packed weight length mismatch");
+    return nullptr;
+  } else if (nsc != (size_t)(out_dim * (in_dim / group) * 2)) {
+    napi_throw_error(env, nullptr, "scale length mismatch");
+    return nullptr;
+  }
+  g4_w4 *h = nullptr;
+  G4_CALL(env, g4_w4_load(pk, sc, (int)out_dim, (int)in_dim, (int)group, &h));
+  W4 *w = new W4{h, (int)out_dim, (int)in_dim, (int)group};
+  if (napi_wrap(env, self, w, w4_finalize, nullptr, nullptr) != napi_ok) {
+    g4_w4_free(h);
+    delete w;
+    napi_throw_error(env, nullptr, "napi_wrap failed");
+    return nullptr;
+  }
+  return self;
+}
+
+// w.linear(x, xDtype, rows, y, yDtype, xByteOffset = 0, yByteOffset = 0)
+napi_value W4_linear(napi_env env, napi_callback_info info) {
+  napi_value argv[7], self;
+  if (!get_args(env, info, 7, argv, &self)) return nullptr;
+  W4 *w = unwrap_w4(env, self);
+  if (!w) return nullptr;
+  void *x, *y;
+  if (!buf_at(env, argv[0], argv[5], "x", &x)) return nullptr;
+  if (!buf_at(env, argv[3], argv[6], "y", &y)) return nullptr;
+  int64_t xd, rows, yd;
+  if (!to_i64(env, argv[1], &xd, "xDtype") || !to_i64(env, argv[2], &rows, "rows") ||
+      !to_i64(env, argv[4], &yd, "yDtype"))
+    return nullptr;
+  G4_CALL(env, g4_w4_linear(w->h, x, (int)xd, (int)rows, y, (int)yd));
+  return undefined(env);
+}
+
+// w.dequant(rowStart, rowCount, out, dtype, outByteOffset = 0)
+napi_value W4_dequant(napi_env env, napi_callback_info info) {
+  napi_value argv[5], self;
+  if (!get_args(env, info, 5, argv, &self)) return nullptr;
+  W4 *w = unwrap_w4(env, self);
+  if (!w) return nullptr;
+  int64_t r0, rc, dt;
+  if (!to_i64(env, argv[0], &r0, "rowStart") || !to_i64(env, argv[1], &rc, "rowCount") ||
+      !to_i64(env, argv[3], &dt, "dtype"))
+    return nullptr;
+  void *out;
+  if (!buf_at(env, argv[2], argv[4], "out", &out)) return nullptr;
+  G4_CALL(env, g4_w4_dequant(w->h, (int)r0, (int)rc, out, (int)dt));
+  return undefined(env);
+}
+
+napi_value W4_dispose(napi_env env, napi_callback_info info) {
+  napi_value self;
+  if (!get_args(env, info, 0, nullptr, &self)) return nullptr;
+  void *p;
+  NAPI_CALL(env, napi_unwrap(env, self, &p));
+  W4 *w = static_cast<W4 *>(p);
+  if (w->h) {
+    g4_w4 *h = w->h;
+    w->h = nullptr;
+    G4_CALL(env, g4_w4_free(h));
+  }
+  return undefined(env);
+}
+
+napi_value W4_info(napi_env env, napi_callback_info info) {
+  napi_value self;
+  if (!get_args(env, info, 0, nullptr, &self)) return nullptr;
+  W4 *w = unwrap_w4(env, self);
+  if (!w) return nullptr;
+  int n, k, g;
+  size_t bytes;
+  G4_CALL(env, g4_w4_info(w->h, &n, &k, &g, &bytes));
+  napi_value o, v;
+  NAPI_CALL(env, napi_create_object(env, &o));
+  napi_create_int32(env, n, &v);
+  napi_set_named_property(env, o, "outDim", v);
+  napi_create_int32(env, k, &v);
+  napi_set_named_property(env, o, "inDim", v);
+  napi_create_int32(env, g, &v);
+  napi_set_named_property(env, o, "groupSize", v);
+  napi_create_double(env, (double)bytes, &v);
+  napi_set_named_property(env, o, "deviceBytes", v);
+  return o;
+}
+
+// ---- PleTable -----------------------------------------------------------------
+
+struct Ple {
+  g4_ple *h;
+};
+
+void ple_finalize(napi_env, void *data, void *) {
+  Ple *t = static_cast<Ple *>(data);
+  if (t->h) g4_ple_free(t->h);
+  delete t;
+}
+
+Ple *unwrap_ple(napi_env env, napi_value self) {
+  void *p = nullptr;
+  if (napi_unwrap(env, self, &p) != napi_ok || !p) {
+    napi_throw_type_error(env, nullptr, "not a PleTable");
+    return nullptr;
+  }
+  Ple *t = static_cast<Ple *>(p);
+  if (!t->h) {
+    napi_throw_error(env, nullptr, "PleTable was disposed");
+    return nullptr;
+  }
+  return t;
+}
+
+// new PleTable(vocab, width, groupSize, rowsPerShard)
+napi_value Ple_new(napi_env env, napi_callback_info info) {
+  napi_value argv[4], self;
+  if (!get_args(env, info, 4, argv, &self)) return nullptr;
+  int64_t vocab, width, group, rps;
+  if (!to_i64(env, argv[0], &vocab, "vocab") || !to_i64(env, argv[1], &width, "width") ||
+      !to_i64(env, argv[2], &group, "groupSize") || !to_i64(env, argv[3], &rps, "rowsPerShard"))
+    return nullptr;
+  g4_ple *h = nullptr;
+  G4_CALL(env, g4_ple_create((int)vocab, (int)width, (int)group, (int)rps, &h));
+  Ple *t = new Ple{h};
+  if (napi_wrap(env, self, t, ple_finalize, nullptr, nullptr) != napi_ok) {
+    g4_ple_free(h);
+    delete t;
+    napi_throw_error(env, nullptr, "napi_wrap failed");
+    return nullptr;
+  }
+  return self;
+}
+
+// t.shardBytes(i) -> number
+napi_value Ple_shardBytes(napi_env env, napi_callback_info info) {
+  napi_value argv[1], self;
+  if (!get_args(env, info, 1, argv, &self)) return nullptr;
+  Ple *t = unwrap_ple(env, self);
+  if (!t) return nullptr;
+  int64_t i;
+  if (!to_i64(env, argv[0], &i, "shard")) return nullptr;
+  size_t bytes;
+  int ns;
+  G4_CALL(env, g4_ple_shard_bytes(t->h, (int)i, &ns, &bytes));
+  napi_value r;
+  NAPI_CALL(env, napi_create_double(env, (double)bytes, &r));
+  return r;
+}
+
+// t.uploadShard(i, bytes)
+napi_value Ple_uploadShard(napi_env env, napi_callback_info info) {
+  napi_value argv[2], self;
+  if (!get_args(env, info, 2, argv, &self)) return nullptr;
+  Ple *t = unwrap_ple(env, self);
+  if (!t) return nullptr;
+  int64_t i;
+  if (!to_i64(env, argv[0], &i, "shard")) return nullptr;
+  void *p;
+  size_t n;
+  if (!host_bytes(env, argv[1], &p, &n, "shard bytes")) return nullptr;
+  G4_CALL(env, g4_ple_upload_shard(t->h, (int)i, p, n));
+  return undefined(env);
+}
+
+// t.gather(idsInt32Array, out, dtype, outByteOffset = 0)
+napi_value Ple_gather(napi_env env, napi_callback_info info) {
+  napi_value argv[4], self;
+  if (!get_args(env, info, 4, argv, &self)) return nullptr;
+  Ple *t = unwrap_ple(env, self);
+  if (!t) return nullptr;
+  bool is;
+  napi_is_typedarray(env, argv[0], &is);
+  napi_typedarray_type type = napi_uint8_array;
+  size_t n = 0;
+  void *ids = nullptr;
+  if (is) {
+    napi_value ab;
+    size_t off;
+    napi_get_typedarray_info(env, argv[0], &type, &n, &ids, &ab, &off);
+  }
+  if (!is || type != napi_int32_array) {
+    napi_throw_type_error(env, nullptr, "ids must be an Int32Array");
+    return nullptr;
+  }
+  void *out;
+  if (!buf_at(env, argv[1], argv[3], "out", &out)) return nullptr;
+  int64_t dt;
+  if (!to_i64(env, argv[2], &dt, "dtype")) return nullptr;
+  G4_CALL(env, g4_ple_gather(t->h, static_cast<const int32_t *>(ids), (int)n, out, (int)dt));
+  return undefined(env);
+}
+
+// t.gatherDev(idsBuffer, n, out, dtype, idsByteOffset = 0, outByteOffset = 0)
+napi_value Ple_gatherDev(napi_env env, napi_callback_info info) {
+  napi_value argv[6], self;
+  if (!get_args(env, info, 6, argv, &self)) return nullptr;
+  Ple *t = unwrap_ple(env, self);
+  if (!t) return nullptr;
+  void *ids, *out;
+  if (!buf_at(env, argv[0], argv[4], "ids", &ids)) return nullptr;
+  if (!buf_at(env, argv[2], argv[5], "out", &out)) return nullptr;
+  int64_t n, dt;
+  if (!to_i64(env, argv[1], &n, "n") || !to_i64(env, argv[3], &dt, "dtype")) return nullptr;
+  G4_CALL(env, g4_ple_gather_dev(t->h, static_cast<const int32_t *>(ids), (int)n, out, (int)dt));
+  return undefined(env);
+}
+
+napi_value Ple_dispose(napi_env env, napi_callback_info info) {
+  napi_value self;
+  if (!get_args(env, info, 0, nullptr, &self)) return nullptr;
+  void *p;
+  NAPI_CALL(env, napi_unwrap(env, self, &p));
+  Ple *t = static_cast<Ple *>(p);
+  if (t->h) {
+    g4_ple *h = t->h;
+    t->h = nullptr;
+    G4_CALL(env, g4_ple_free(h));
+  }
+  return undefined(env);
+}
+
+// ---- CommandBuffer (a finished encoder) ----------------------------------------------
+
+struct Cmd {
+  g4_cmdbuf *h;
+};
+
+void cmd_finalize(napi_env, void *data, void *) {
+  Cmd *c = static_cast<Cmd *>(data);
+  if (c->h) g4_cmdbuf_free(c->h);
+  delete c;
+}
+
+napi_ref g_cmd_ctor = nullptr;
+
+napi_value Cmd_new(napi_env env, napi_callback_info info) {
+  napi_value self;
+  if (!get_args(env, info, 0, nullptr, &self)) return nullptr;
+  Cmd *c = new Cmd{nullptr};
+  if (napi_wrap(env, self, c, cmd_finalize, nullptr, nullptr) != napi_ok) {
+    delete c;
+    napi_throw_error(env, nullptr, "napi_wrap failed");
+    return nullptr;
+  }
+  return self;
+}
+
+napi_value Cmd_submit(napi_env env, napi_callback_info info) {
+  napi_value self;
+  if (!get_args(env, info, 0, nullptr, &self)) return nullptr;
+  void *p;
+  NAPI_CALL(env, napi_unwrap(env, self, &p));
+  Cmd *c = static_cast<Cmd *>(p);
+  if (!c->h) {
+    napi_throw_error(env, nullptr, "CommandBuffer is empty or destroyed");
+    return nullptr;
+  }
+  G4_CALL(env, g4_submit(c->h));
+  return undefined(env);
+}
+
+napi_value Cmd_destroy(napi_env env, napi_callback_info info) {
+  napi_value self;
+  if (!get_args(env, info, 0, nullptr, &self)) return nullptr;
+  void *p;
+  NAPI_CALL(env, napi_unwrap(env, self, &p));
+  Cmd *c = static_cast<Cmd *>(p);
+  if (c->h) {
+    g4_cmdbuf *h = c->h;
+    c->h = nullptr;
+    G4_CALL(env, g4_cmdbuf_free(h));
+  }
+  return undefined(env);
+}
+
+// ---- free functions ------------------------------------------------------------
+
+napi_value F_init(napi_env env, napi_callback_info info) {
+  napi_value argv[1], self;
+  if (!get_args(env, info, 1, argv, &self)) return nullptr;
+  int64_t dev = 0;
+  napi_valuetype t;
+  napi_typeof(env, argv[0], &t);
+  if (t != napi_undefined && !to_i64(env, argv[0], &dev, "device")) return nullptr;
+  G4_CALL(env, g4_init((int)dev));
+  return undefined(env);
+}
+
+napi_value F_deviceInfo(napi_env env, napi_callback_info) {
+  char name[256];
+  int cu, clk;
+  size_t hbm;
+  G4_CALL(env, g4_device_info(name, sizeof name, &cu, &hbm, &clk));
+  napi_value o, v;
+  NAPI_CALL(env, napi_create_object(env, &o));
+  napi_create_string_utf8(env, name, NAPI_AUTO_LENGTH, &v);
+  napi_set_named_property(env, o, "name", v);
+  napi_create_int32(env, cu, &v);
+  napi_set_named_property(env, o, "cuCount", v);
+  napi_create_double(env, (double)hbm, &v);
+  napi_set_named_property(env, o, "hbmBytes", v);
+  napi_create_int32(env, clk, &v);
+  napi_set_named_property(env, o, "clockKHz", v);
+  return o;
+}
+
+napi_value F_sync(napi_env env, napi_callback_info) {
+  G4_CALL(env, g4_sync());
+  return undefined(env);
+}
+
+// copy(dst, dstOffset, src, srcOffset, byteLength)  - copyBufferToBuffer
+napi_value F_copy(napi_env env, napi_callback_info info) {
+  napi_value argv[5], self;
+  if (!get_args(env, info, 5, argv, &self)) return nullptr;
+  void *dst, *src;
+  if (!buf_at(env, argv[0], argv[1], "dst", &dst)) return nullptr;
+  if (!buf_at(env, argv[2], argv[3], "src", &src)) return nullptr;
+  int64_t n;
+  if (!to_i64(env, argv[4], &n, "byteLength")) return nullptr;
+  if (n < 0) {
+    napi_throw_range_error(env, nullptr, "byteLength must be >= 0");
+    return nullptr;
+  }
+  G4_CALL(env, g4_copy(dst, 0, src, 0, (size_t)n));
+  return undefined(env);
+}
+
+// bf16Head(x, E, rows, inDim, out, scale, softcap, eByteOffset = 0, outByteOffset = 0)
+napi_value F_bf16Head(napi_env env, napi_callback_info info) {
+  napi_value argv[9], self;
+  if (!get_args(env, info, 9, argv, &self)) return nullptr;
+  void *x, *E, *out;
+  napi_value zero;
+  napi_create_int32(env, 0, &zero);
+  if (!buf_at(env, argv[0], zero, "x", &x)) return nullptr;
+  if (!buf_at(env, argv[1], argv[7], "E", &E)) return nullptr;
+  if (!buf_at(env, argv[4], argv[8], "out", &out)) return nullptr;
+  int64_t rows, k;
+  double scale, softcap;
+  if (!to_i64(env, argv[2], &rows, "rows") || !to_i64(env, argv[3], &k, "inDim") ||
+      !to_f64(env, argv[5], &scale, "scale") || !to_f64(env, argv[6], &softcap, "softcap"))
+    return nullptr;
+  G4_CALL(env, g4_bf16_head(static_cast<const float *>(x), E, (int)rows, (int)k,
+                            static_cast<float *>(out), (float)scale, (float)softcap));
+  return undefined(env);
+}
+
+napi_value F_encoderBegin(napi_env env, napi_callback_info) {
+  G4_CALL(env, g4_encoder_begin());
+  return undefined(env);
+}
+
+// encoderFinish() -> CommandBuffer
+napi_value F_encoderFinish(napi_env env, napi_callback_info) {
+  g4_cmdbuf *h = nullptr;
+  G4_CALL(env, g4_encoder_finish(&h));
+  napi_value ctor, obj;
+  NAPI_CALL(env, napi_get_reference_value(env, g_cmd_ctor, &ctor));
+  NAPI_CALL(env, napi_new_instance(env, ctor, 0, nullptr, &obj));
+  void *p;
+  NAPI_CALL(env, napi_unwrap(env, obj, &p));
+  static_cast<Cmd *>(p)->h = h;
+  return obj;
+}
+
+// timeMs(fn): runs fn() between two stream events and returns the GPU ms.
+napi_value F_timeMs(napi_env env, napi_callback_info info) {
+  napi_value argv[1], self;
+  if (!get_args(env, info, 1, argv, &self)) return nullptr;
+  void *a = nullptr, *b = nullptr;
+  G4_CALL(env, g4_event_create(&a));
+  int rc = g4_event_create(&b);
+  if (rc) {
+    g4_event_destroy(a);
+    G4_CALL(env, rc);
+  }
+  napi_value r = nullptr;
+  float ms = 0.f;
+  rc = g4_event_record(a);
+  if (!rc) {
+    napi_value global, res;
+    napi_get_global(env, &global);
+    if (napi_call_function(env, global, argv[0], 0, nullptr, &res) != napi_ok) {
+      g4_event_destroy(a);
+      g4_event_destroy(b);
+      return nullptr;  // the JS exception propagates
+    }
+    rc = g4_event_record(b);
+  }
+  if (!rc) rc = g4_event_elapsed_ms(a, b, &ms);
+  g4_event_destroy(a);
+  g4_event_destroy(b);
+  G4_CALL(env, rc);
+  NAPI_CALL(env, napi_create_double(env, ms, &r));
+  return r;
+}
+
+napi_value define_class(napi_env env, napi_value exports, const char *name, napi_callback ctor,
+                        const napi_property_descriptor *props, size_t nprops, napi_ref *ref) {
+  napi_value cls;
+  NAPI_CALL(env, napi_define_class(env, name, NAPI_AUTO_LENGTH, ctor, nullptr, nprops, props, &cls));
+  NAPI_CALL(env, napi_create_reference(env, cls, 1, ref));
+  NAPI_CALL(env, napi_set_named_property(env, exports, name, cls));
+  return cls;
+}
+
+#define METHOD(name, fn) {name, nullptr, fn, nullptr, nullptr, nullptr, napi_default, nullptr}
+#define GETTER(name, fn) {name, nullptr, nullptr, fn, nullptr, nullptr, napi_default, nullptr}
+
+napi_value Init(napi_env env, napi_value exports) {
+  const napi_property_descriptor buf_props[] = {
+      GETTER("size", DevBuf_size), METHOD("destroy", DevBuf_destroy),
+      METHOD("write", DevBuf_write), METHOD("read", DevBuf_read)};
+  if (!define_class(env, exports, "DeviceBuffer", DevBuf_new, buf_props, 4, &g_devbuf_ctor))
+    return nullptr;
+  const napi_property_descriptor w4_props[] = {
+      METHOD("linear", W4_linear), METHOD("dequant", W4_dequant), METHOD("dispose", W4_dispose),
+      METHOD("info", W4_info)};
+  if (!define_class(env, exports, "W4Weight", W4_new, w4_props, 4, &g_w4_ctor)) return nullptr;
+  napi_ref ple_ref;
+  const napi_property_descriptor ple_props[] = {
+      METHOD("shardBytes", Ple_shardBytes), METHOD("uploadShard", Ple_uploadShard),
+      METHOD("gather", Ple_gather), METHOD("gatherDev", Ple_gatherDev),
+      METHOD("dispose", Ple_dispose)};
+  if (!define_class(env, exports, "PleTable", Ple_new, ple_props, 5, &ple_ref)) return nullptr;
+  const napi_property_descriptor cmd_props[] = {METHOD("submit", Cmd_submit),
+                                                METHOD("destroy", Cmd_destroy)};
+  if (!define_class(env, exports, "CommandBuffer", Cmd_new, cmd_props, 2, &g_cmd_ctor))
+    return nullptr;
+  const napi_property_descriptor fns[] = {
+      METHOD("init", F_init), METHOD("deviceInfo", F_deviceInfo), METHOD("sync", F_sync),
+      METHOD("copy", F_copy), METHOD("bf16Head", F_bf16Head),
+      METHOD("encoderBegin", F_encoderBegin), METHOD("encoderFinish", F_encoderFinish),
+      METHOD("timeMs", F_timeMs)};
+  NAPI_CALL(env, napi_define_properties(env, exports, sizeof fns / sizeof fns[0], fns));
+  napi_value v;
+  napi_create_int32(env, G4_F32, &v);
+  napi_set_named_property(env, exports, "F32", v);
+  napi_create_int32(env, G4_BF16, &v);
+  napi_set_named_property(env, exports, "BF16", v);
+  return exports;
+}
+
+}  // namespace
+
+NAPI_MODULE(NODE_GYP_MODULE_NAME, Init)
