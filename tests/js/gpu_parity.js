@@ -35,7 +35,9 @@ async function main() {
   device.queue.submit([enc.finish()]);
   writeF32File('y.f32', await rt.readF32(device, y, rows * lin.outDim));
 
-  // the same launch recorded once and replayed twice
+  // a one-row launch run eagerly, then recorded once and replayed twice
+  const y1 = ops.w4(device.createCommandEncoder(), lin, x, 1, garbage);
+  writeF32File('y_one.f32', await rt.readF32(device, y1, lin.outDim));
   const y2 = rt.createBuffer(device, rows * lin.outDim * 4, rt.GPUBufferUsage.STORAGE, 'y2');
   const rec = rt.HipCommandRecorder.record(() => lin.weight.linear(x, rt.F32, 1, y2, rt.F32));
   device.queue.submit([rec, rec]);
@@ -74,7 +76,7 @@ async function main() {
   writeF32File('logits.f32', logits);
   out.top10 = rt.topK(logits, 10).map(e => e.tokenId);
 
-  for (const b of [x, y, y2, h, logitsBuf, ple, ...chunks.map(c => c.buffer)]) b.destroy();
+  for (const b of [x, y, y1, y2, h, logitsBuf, ple, ...chunks.map(c => c.buffer)]) b.destroy();
   lin.dispose();
   bundle.dispose();
   reader.close();
