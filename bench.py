@@ -231,6 +231,14 @@ def main():
     g4hip.init(0)
     info = g4hip.device_info()
     log("device:", info)
+    # One 64 MiB device-to-device copy of known size before anything else:
+    # the reference point that scales the FETCH_SIZE / WRITE_SIZE counters
+    # when this command runs under `rocprofv3 --pmc`.
+    cal_a, cal_b = g4hip.Buffer(64 << 20), g4hip.Buffer(64 << 20)
+    g4hip.check(g4hip.lib().g4_copy(cal_b.ptr, 0, cal_a.ptr, 0, 64 << 20))
+    g4hip.sync()
+    cal_a.free()
+    cal_b.free()
     n, k = 6144, 1536
     log("GEMV M1 K%d N%d: %d steps (+%d warmup)" % (k, n, args.steps, args.warmup))
     g = bench_gemv(n, k, args.steps, args.warmup)

@@ -292,14 +292,17 @@ int gemv_rows_per_launch(int K, bool f32x) {
 // packed word and adds its 8 values into the group sum with a quad DPP
 // reduction.  Needs RB >= 4, which makes chunks per thread <= IPL.
 // ---------------------------------------------------------------------------
-template <int IPL, bool F32X>
-__global__ __launch_bounds__(1024) void w4_gemv1_kernel(
+// GC, TC: the group count and block size when known at compile time (0 =
+// taken from K and blockDim at run time); the E2B shapes use fixed ones.
+template <int GC, int TC, int IPL, bool F32X>
+__global__ __launch_bounds__(TC ? TC : 1024) void w4_gemv1_kernel(
     const void *__restrict__ x, const uint4 *__restrict__ wq, const uint16_t *__restrict__ ws,
-    void *__restrict__ y, int y_bf16, int K, int N, int RB) {
+    void *__restrict__ y, int y_bf16, int K, int N, int RB_) {
   extern __shared__ uint4 lds[];
-  const int T = blockDim.x;
-  const int G = K >> 5;
-  const int nch = K >> 3;
+  const int T = TC ? TC : (int)blockDim.x;
+  const int G = GC ? GC : K >> 5;
+  const int RB = GC ? TC * IPL / GC : RB_;
+  const int nch = 4 * G;
   const int t = threadIdx.x;
 
   // 1. x chunks (L2-resident), issued first
@@ -412,8 +415,14 @@ __global__ __launch_bounds__(1024) void w4_gemv1_kernel(
     const int idx = b + t;
     const int r = idx >> 4, j = idx & 15;
     float v = 0.f;
-    if (r < RB)
-      for (int g = j; g < G; g += 16) v += part[r * G + g];
+    if (r < RB) {
+      if (GC) {
+#pragma unroll
+        for (int g = j; g < GC; g += 16) v += part[r * GC + g];
+      } else {
+        for (int g = j; g < G; g += 16) v += part[r * G + g];
+      }
+    }
     v = team_sum<16>(v);
     const size_t row = (size_t)blockIdx.x * RB + r;
     if (j == 0 && r < RB && row < (size_t)N) {
@@ -450,11 +459,11 @@ bool plan_gemv1(int G, bool f32x, Gemv1Plan *p) {
   return false;
 }
 
-template <int IPL, bool F32X>
+template <int GC, int TC, int IPL, bool F32X>
 int launch_gemv1_i(const g4_w4 *w, const Gemv1Plan &p, const void *x, void *y, int y_bf16) {
   const int blocks = (w->N + p.RB - 1) / p.RB;
-  hipLaunchKernelGGL((w4_gemv1_kernel<IPL, F32X>), dim3(blocks), dim3(p.T), p.lds, stream(), x,
-                     w->packed, w->scales, y, y_bf16, w->K, w->N, p.RB);
+  hipLaunchKernelGGL((w4_gemv1_kernel<GC, TC, IPL, F32X>), dim3(blocks), dim3(p.T), p.lds,
+                     stream(), x, w->packed, w->scales, y, y_bf16, w->K, w->N, p.RB);
   G4_LAUNCH_CHECK("w4_gemv1_kernel");
   return G4_OK;
 }
@@ -464,11 +473,22 @@ int launch_gemv1(const g4_w4 *w, const void *x, void *y, int y_bf16) {
   Gemv1Plan p;
   if (!plan_gemv1(w->G, F32X, &p))
     return fail(G4_E_ARG, "g4_w4_linear: no decode GEMV plan for in_dim %d", w->K);
+  // compile-time variants for the plans of the Gemma-4-E2B projections
+#define G4_GEMV1_FIXED(GG, TT, II)                                      \
+  if (w->G == GG && p.T == TT && p.IPL == II)                           \
+    return launch_gemv1_i<GG, TT, II, F32X>(w, p, x, y, y_bf16);
+  G4_GEMV1_FIXED(48, 192, 1)    // K = 1536
+  G4_GEMV1_FIXED(64, 256, 1)    // K = 2048
+  G4_GEMV1_FIXED(128, 512, 1)   // K = 4096
+  G4_GEMV1_FIXED(192, 768, 1)   // K = 6144
+  G4_GEMV1_FIXED(384, 768, 2)   // K = 12288
+  G4_GEMV1_FIXED(8, 64, 1)      // K = 256
+#undef G4_GEMV1_FIXED
   switch (p.IPL) {
-    case 1: return launch_gemv1_i<1, F32X>(w, p, x, y, y_bf16);
-    case 2: return launch_gemv1_i<2, F32X>(w, p, x, y, y_bf16);
-    case 3: return launch_gemv1_i<3, F32X>(w, p, x, y, y_bf16);
-    default: return launch_gemv1_i<4, F32X>(w, p, x, y, y_bf16);
+    case 1: return launch_gemv1_i<0, 0, 1, F32X>(w, p, x, y, y_bf16);
+    case 2: return launch_gemv1_i<0, 0, 2, F32X>(w, p, x, y, y_bf16);
+    case 3: return launch_gemv1_i<0, 0, 3, F32X>(w, p, x, y, y_bf16);
+    default: return launch_gemv1_i<0, 0, 4, F32X>(w, p, x, y, y_bf16);
   }
 }
 
