@@ -267,18 +267,25 @@ def main():
         cpu = cpu_baseline(n, k, args.cpu_seconds)
         log("  ", cpu)
 
+    traffic, traffic_src = None, None
+    tpath = os.path.join(ROOT, "profiles", "w4_gemv_m1_k1536_n6144_traffic.json")
+    if os.path.exists(tpath):
+        with open(tpath) as f:
+            t = json.load(f)
+        traffic = t["hbm_bytes_per_launch"]
+        traffic_src = "profiles/w4_gemv_m1_k1536_n6144_traffic.json (rocprofv3 --pmc FETCH_SIZE, WRITE_SIZE)"
     line = {
         "metric": METRIC, "value": round(g["gbs"], 2), "unit": "GB/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": g["ms"] / args.steps,
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "fp32",
         "data": "synthetic (seeded int4 weights in [-7,7], bf16 scales |N|*0.02, bf16 N(0,1) x)",
-        "config": {"workload": "W4A16 decode GEMV M=1 K=1536 N=6144, cold (128 rotating weight "
-                               "copies), BF16 x, FP32 y", "M": 1, "K": k, "N": n,
+        "config": {"workload": "W4A16 decode GEMV M=1 K=1536 N=6144, cold (rotating weight "
+                               "copies, >= 640 MB), BF16 x, FP32 y", "M": 1, "K": k, "N": n,
                    "group": 32, "weight_copies": g["copies"], "device": info["name"],
                    "cu_count": info["cu_count"]},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "w4_gemv_kernel", "avg_launch_us": round(avg_us, 4),
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "traffic_source": traffic_src, "kernel": "w4_gemv1_kernel", "avg_launch_us": round(avg_us, 4),
                      "bytes_per_launch": g["bytes_per_step"]},
         "cpu_baseline": cpu,
         "extra": extra,
