@@ -15,18 +15,21 @@
 // only values 2^28 below the row maximum lose bits).  FP32 activations are
 // split as x' = hi + lo (two FP16 values, ~22 bits) and take two MFMAs.
 //
-// Structure.  A pre-pass (one block per row) finds e[m] and writes x' as
-// FP16 in "pair order": each 8-element chunk (x0..x7) is stored as
-// (x0,x4)(x1,x5)(x2,x6)(x3,x7), the order in which ((w >> 4t) & 0x000F000F)
-// | 0x64006400 unpacks a packed word into FP16 pairs (1024 + n_t,
-// 1024 + n_t+4).  The MFMA only needs A and B to share one k order inside
-// each group, so no lane shuffles are needed.
+// Pre-pass.  One block per 16 rows finds e[m] and writes x' as FP16 chunks
+// of 8 values in "pair order": chunk (x0..x7) is stored as (x0,x4)(x1,x5)
+// (x2,x6)(x3,x7), the order in which ((w >> 4t) & 0x000F000F) | 0x64006400
+// unpacks a packed word into FP16 pairs (1024 + n_t, 1024 + n_t+4).  The
+// MFMA only needs A and B to share one k order inside each 8-wide chunk, so
+// no lane shuffles are needed.  The chunks are laid out chunk-major,
+// xt[c][m] (16 bytes each, m padded to a multiple of 128), so the main
+// kernel's tile loads read whole contiguous runs of rows.
 //
-// Main kernel: 128x128 output tile per 256-thread block, 4 waves of 64x64
-// (4x4 MFMA tiles of 16x16), one 32-deep K step per group, double-buffered
-// LDS.  Per step each thread fetches two 16-byte chunks of x' and half a
-// packed group (8 bytes) plus its scale for the next step, runs its 16 MFMAs
-// on the current buffers, then dequantizes into the other buffer:
+// Main kernel: a 256-thread block (2 x 2 waves) computes a (32 TM) x (32 TN)
+// output tile, each wave (16 TM) x (16 TN) as TM x TN MFMA tiles of 16 x 16.
+// K advances KS groups (32 KS values) per stage through double-buffered LDS:
+// while the MFMAs of stage s run, the loads of stage s + 1 are in flight in
+// registers; afterwards they are stored to the other buffer, the weights
+// dequantized on the way:
 //   pair = ((w >> 4t) & 0x000F000F) | 0x64006400     (1024 + n, exact)
 //   pair = (pair - 1032) * s'                        (v_pk_add/mul_f16, exact)
 // LDS layout [chunk c][row] (16 B each) so the 16 lanes that read one MFMA
@@ -42,8 +45,8 @@ using namespace g4;
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 
-constexpr int BM = 128, BN = 128;
 constexpr int kThreads = 256;
+constexpr int kRowPad = 128;   // x' rows are padded to a multiple of the largest BM
 
 // ---- pre-pass: per-row exponent and FP16 x' in pair order ----------------
 
@@ -69,54 +72,86 @@ __device__ __forceinline__ uint32_t h2bits(_Float16 a, _Float16 b) {
   return (uint32_t)__builtin_bit_cast(uint16_t, a) | ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
 }
 
+// Row exponents: one wave per row.  e[m]: max |x[m]| * 2^-e in [2^13, 2^14);
+// all-zero or non-finite rows keep e = 0.  Grid: ceil(M / 4) blocks.
 template <bool F32X>
-__global__ __launch_bounds__(kThreads) void gemm_xprep_kernel(const void *__restrict__ x, int K,
-                                                              uint4 *__restrict__ xh,
-                                                              uint4 *__restrict__ xl,
-                                                              int *__restrict__ xe) {
-  __shared__ float red[kThreads / 64];
-  const int m = blockIdx.x;
+__global__ __launch_bounds__(kThreads) void gemm_xexp_kernel(const void *__restrict__ x, int M,
+                                                             int K, int *__restrict__ xe) {
+  const int lane = threadIdx.x & 63;
+  const int m = blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
+  if (m >= M) return;
   const int nch = K >> 3;
-  const size_t rowc = (size_t)m * nch;
   float mx = 0.f;
-  for (int c = threadIdx.x; c < nch; c += kThreads) {
+  for (int c = lane; c < nch; c += 64) {
     float v[8];
-    load8<F32X>(x, rowc + c, v);
+    load8<F32X>(x, (size_t)m * nch + c, v);
 #pragma unroll
     for (int e = 0; e < 8; ++e) mx = fmaxf(mx, fabsf(v[e]));
   }
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
-  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
-  __syncthreads();
-  mx = red[0];
-#pragma unroll
-  for (int i = 1; i < kThreads / 64; ++i) mx = fmaxf(mx, red[i]);
-  // e: max * 2^-e in [2^13, 2^14); all-zero or non-finite rows keep e = 0
   int e = 0;
   if (mx > 0.f && mx <= 3.4e38f) e = ilogbf(mx) - 13;
-  if (threadIdx.x == 0) xe[m] = e;
-  for (int c = threadIdx.x; c < nch; c += kThreads) {
-    float v[8];
-    load8<F32X>(x, rowc + c, v);
+  if (lane == 0) xe[m] = e;
+}
+
+// x' = x * 2^-e[m] as FP16 chunks in pair order, transposed to xt[c][m]
+// through LDS: a block converts a tile of 64 rows x 16 chunks, reading 256
+// contiguous bytes per row and writing 1 KB contiguous per chunk.  Rows
+// M <= m < Mp are written as zeros.  For FP32 x the low halves go to
+// xt[K/8 + c][m].  Grid: (Mp / 64, ceil(K / 128)).
+constexpr int kPrepTileM = 64, kPrepTileC = 16;
+template <bool F32X>
+__global__ __launch_bounds__(kThreads) void gemm_xprep_kernel(const void *__restrict__ x,
+                                                              const int *__restrict__ xe, int M,
+                                                              int Mp, int K,
+                                                              uint4 *__restrict__ xt) {
+  __shared__ uint4 hs[kPrepTileC][kPrepTileM + 1];
+  __shared__ uint4 ls[F32X ? kPrepTileC : 1][kPrepTileM + 1];
+  const int nch = K >> 3;
+  const int m0 = blockIdx.x * kPrepTileM, c0 = blockIdx.y * kPrepTileC;
+  const int t = threadIdx.x;
+#pragma unroll
+  for (int i = 0; i < kPrepTileM * kPrepTileC / kThreads; ++i) {
+    const int idx = t + i * kThreads;
+    const int r = idx / kPrepTileC, cc = idx % kPrepTileC;
+    const int m = m0 + r, c = c0 + cc;
+    float v[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    int e = 0;
+    if (m < M && c < nch) {
+      load8<F32X>(x, (size_t)m * nch + c, v);
+      e = xe[m];
+    }
     _Float16 h[8], l[8];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const float s = ldexpf(v[i], -e);
-      h[i] = (_Float16)s;
-      if (F32X) l[i] = (_Float16)(s - (float)h[i]);
+    for (int j = 0; j < 8; ++j) {
+      const float s = ldexpf(v[j], -e);
+      h[j] = (_Float16)s;
+      if (F32X) l[j] = (_Float16)(s - (float)h[j]);
     }
-    xh[rowc + c] = make_uint4(h2bits(h[0], h[4]), h2bits(h[1], h[5]), h2bits(h[2], h[6]),
-                              h2bits(h[3], h[7]));
+    hs[cc][r] = make_uint4(h2bits(h[0], h[4]), h2bits(h[1], h[5]), h2bits(h[2], h[6]),
+                           h2bits(h[3], h[7]));
     if (F32X)
-      xl[rowc + c] = make_uint4(h2bits(l[0], l[4]), h2bits(l[1], l[5]), h2bits(l[2], l[6]),
-                                h2bits(l[3], l[7]));
+      ls[cc][r] = make_uint4(h2bits(l[0], l[4]), h2bits(l[1], l[5]), h2bits(l[2], l[6]),
+                             h2bits(l[3], l[7]));
+  }
+  __syncthreads();
+  const size_t lo_plane = (size_t)nch * Mp;
+#pragma unroll
+  for (int i = 0; i < kPrepTileM * kPrepTileC / kThreads; ++i) {
+    const int idx = t + i * kThreads;
+    const int cc = idx / kPrepTileM, r = idx % kPrepTileM;
+    const int c = c0 + cc;
+    if (c >= nch) continue;
+    const size_t o = (size_t)c * Mp + m0 + r;
+    xt[o] = hs[cc][r];
+    if (F32X) xt[lo_plane + o] = ls[cc][r];
   }
 }
 
 // ---- main kernel -------------------------------------------------------------
 
-__device__ __forceinline__ f16x8 as_f16x8(uint4 u) { return __builtin_bit_cast(f16x8, u); }
+__device__ __forceinline__ f16x8 as_f16x8(u32x4 u) { return __builtin_bit_cast(f16x8, u); }
 
 __device__ __forceinline__ uint32_t deq_pair(uint32_t w, int t, f16x2 s2) {
   const uint32_t u = ((w >> (4 * t)) & 0x000F000Fu) | 0x64006400u;
@@ -126,107 +161,171 @@ __device__ __forceinline__ uint32_t deq_pair(uint32_t w, int t, f16x2 s2) {
   return __builtin_bit_cast(uint32_t, h);
 }
 
-template <int NX>
-__global__ __launch_bounds__(kThreads) void w4_gemm_kernel(
-    const uint4 *__restrict__ xh, const uint4 *__restrict__ xl, const int *__restrict__ xe,
-    const uint4 *__restrict__ wq, const uint16_t *__restrict__ ws, int shift,
-    void *__restrict__ y, int y_bf16, int M, int N, int K) {
-  // [buf][chunk][row] 16-byte entries
-  __shared__ uint4 As[2][NX][4][BM];
-  __shared__ uint4 Bs[2][4][BN];
+// Requires Mp a multiple of BM and (K / 32) a multiple of KS (the launcher
+// checks both).
+template <int TM, int TN, int NX, int KS, int P>
+__global__ __launch_bounds__(kThreads, 2) void w4_gemm_kernel(
+    const u32x4 *__restrict__ xt, const int *__restrict__ xe, const u32x4 *__restrict__ wq,
+    const uint16_t *__restrict__ ws, int shift, void *__restrict__ y, int y_bf16, int M, int Mp,
+    int N, int K, int xcd_map) {
+  constexpr int BM = 32 * TM, BN = 32 * TN;
+  constexpr int KC = 4 * KS;              // 16-byte chunks per row per stage
+  constexpr int AE = BM * KC / kThreads;  // x' chunks per thread per stage (per plane)
+  constexpr int BG = BN * KS;             // weight groups per stage
+  constexpr int BE = (BG + kThreads - 1) / kThreads;
+  static_assert(BM * KC % kThreads == 0, "A tile must split evenly over the block");
+  __shared__ u32x4 As[2][NX][KC][BM];
+  __shared__ u32x4 Bs[2][KC][BN];
 
   const int G = K >> 5;
-  const int nch = K >> 3;
+  const int S = G / KS;
   const int t = threadIdx.x;
   const int lane = t & 63, wave = t >> 6;
   const int wm = wave >> 1, wn = wave & 1;
-  const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
 
-  // A fetch: entries idx = t, t + 256 of the 512 (row, chunk) pairs
-  int a_row[2], a_c[2];
-  size_t a_src[2];
-#pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const int idx = t + i * kThreads;
-    a_row[i] = idx >> 2;
-    a_c[i] = idx & 3;
-    const int gm = m0 + a_row[i] < M ? m0 + a_row[i] : M - 1;
-    a_src[i] = (size_t)gm * nch + a_c[i];
+  // block -> (m tile, n tile); with xcd_map, all n tiles of one m band run on
+  // one XCD (blocks are dealt to the 8 XCDs round-robin), so its L2 holds
+  // that band of x' for every one of them.
+  const int nn = (N + BN - 1) / BN;
+  int mt, ntile;
+  if (xcd_map) {
+    const int b = blockIdx.x, xcd = b & 7, j = b >> 3;
+    mt = xcd + 8 * (j / nn);
+    ntile = j - (j / nn) * nn;
+  } else {
+    mt = blockIdx.x / nn;
+    ntile = blockIdx.x - mt * nn;
   }
-  // B fetch: row n = t >> 1 of the tile, words 2h, 2h+1 of the group
-  const int b_row = t >> 1, b_h = t & 1;
-  const int gn = n0 + b_row < N ? n0 + b_row : N - 1;
-  const uint2 *bsrc = reinterpret_cast<const uint2 *>(wq + (size_t)gn * G) + b_h;
-  const uint16_t *ssrc = ws + (size_t)gn * G;
+  const int m0 = mt * BM, n0 = ntile * BN;
 
-  uint4 ra[NX][2];
-  uint2 rb;
-  uint32_t rs;
-  auto fetch = [&](int g) {
+  // A: entry i of this thread is chunk a_c[i] of tile row a_row[i]
+  const size_t a_stage = (size_t)KC * Mp;  // xt entries per stage
+  const size_t lo_plane = (size_t)(K >> 3) * Mp;
+  int a_row[AE], a_c[AE];
+  const u32x4 *a_src[AE];
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      ra[0][i] = xh[a_src[i] + (size_t)g * 4];
-      if (NX == 2) ra[NX - 1][i] = xl[a_src[i] + (size_t)g * 4];
+  for (int i = 0; i < AE; ++i) {
+    const int idx = t + i * kThreads;
+    a_c[i] = idx / BM;
+    a_row[i] = idx % BM;
+    a_src[i] = xt + (size_t)a_c[i] * Mp + m0 + a_row[i];
+  }
+  // B: entry i is group b_kk[i] of the stage for tile row b_row[i]
+  int b_row[BE], b_kk[BE];
+  bool b_live[BE];
+  // Scales: with an even KS, one aligned 32-bit load brings the scales of
+  // groups kk & ~1 and kk | 1 (G is even then); the half is picked at store.
+  constexpr int SW = KS % 2 == 0 ? 2 : 1;  // scales per scale load
+  const u32x4 *b_src[BE];
+  const uint16_t *s_src[BE];
+#pragma unroll
+  for (int i = 0; i < BE; ++i) {
+    const int idx = t + i * kThreads;
+    b_live[i] = idx < BG;  // idle entries load group 0 of row 0 and store nothing
+    const int id = b_live[i] ? idx : 0;
+    b_row[i] = id / KS;
+    b_kk[i] = id % KS;
+    const int gn = n0 + b_row[i] < N ? n0 + b_row[i] : N - 1;
+    b_src[i] = wq + (size_t)gn * G + b_kk[i];
+    s_src[i] = ws + (size_t)gn * G + (b_kk[i] & ~(SW - 1));
+  }
+
+  // Ring of P register slots: stage j is loaded into slot j % P, P - 1
+  // stages ahead of the MFMAs that use it.  Loads past the last stage re-read
+  // it (in bounds, never used), so every step issues the same loads.
+  u32x4 ra[P][NX][AE];
+  u32x4 rb[P][BE];
+  uint32_t rs[P][BE];
+  auto fetch = [&](int st, int slot) {
+    const int sc = st < S ? st : S - 1;
+#pragma unroll
+    for (int i = 0; i < AE; ++i) {
+      ra[slot][0][i] = a_src[i][sc * a_stage];
+      if (NX == 2) ra[slot][NX - 1][i] = a_src[i][lo_plane + sc * a_stage];
     }
-    rb = bsrc[(size_t)g * 2];
-    rs = ssrc[g];
+#pragma unroll
+    for (int i = 0; i < BE; ++i) {
+      rb[slot][i] = b_src[i][sc * KS];
+      if (SW == 2)
+        rs[slot][i] = *reinterpret_cast<const uint32_t *>(s_src[i] + sc * KS);
+      else
+        rs[slot][i] = s_src[i][sc * KS];
+    }
   };
-  auto stage = [&](int buf) {
+  auto store = [&](int slot, int buf) {
 #pragma unroll
     for (int x = 0; x < NX; ++x)
 #pragma unroll
-      for (int i = 0; i < 2; ++i) As[buf][x][a_c[i]][a_row[i]] = ra[x][i];
-    const _Float16 sh = (_Float16)ldexpf(bf16_to_f32(rs), shift);
-    const f16x2 s2 = {sh, sh};
-    const uint32_t w2[2] = {rb.x, rb.y};
+      for (int i = 0; i < AE; ++i) As[buf][x][a_c[i]][a_row[i]] = ra[slot][x][i];
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
-      Bs[buf][2 * b_h + j][b_row] =
-          make_uint4(deq_pair(w2[j], 0, s2), deq_pair(w2[j], 1, s2), deq_pair(w2[j], 2, s2),
-                     deq_pair(w2[j], 3, s2));
-  };
-
-  f32x4 acc[4][4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
-
-  fetch(0);
-  stage(0);
-  __syncthreads();
-
-  const int lr = lane & 15, lc = lane >> 4;  // operand row/col within a 16-tile, k chunk
-  for (int g = 0; g < G; ++g) {
-    const int buf = g & 1;
-    if (g + 1 < G) fetch(g + 1);
-    f16x8 bop[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) bop[j] = as_f16x8(Bs[buf][lc][wn * 64 + j * 16 + lr]);
-#pragma unroll
-    for (int x = 0; x < NX; ++x)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const f16x8 aop = as_f16x8(As[buf][x][lc][wm * 64 + i * 16 + lr]);
+    for (int i = 0; i < BE; ++i)
+      if (b_live[i]) {
+        const uint32_t sbits = SW == 2 && (b_kk[i] & 1) ? rs[slot][i] >> 16 : rs[slot][i] & 0xffffu;
+        const _Float16 sh = (_Float16)ldexpf(bf16_to_f32(sbits), shift);
+        const f16x2 s2 = {sh, sh};
+        const u32x4 w = rb[slot][i];
 #pragma unroll
         for (int j = 0; j < 4; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(aop, bop[j], acc[i][j], 0, 0, 0);
+          Bs[buf][4 * b_kk[i] + j][b_row[i]] =
+              (u32x4){deq_pair(w[j], 0, s2), deq_pair(w[j], 1, s2), deq_pair(w[j], 2, s2),
+                      deq_pair(w[j], 3, s2)};
       }
-    if (g + 1 < G) stage(buf ^ 1);
-    __syncthreads();
+  };
+
+  f32x4 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) acc[i][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
+
+  const int lr = lane & 15, lc = lane >> 4;  // operand row within a 16-tile, k chunk
+  auto compute = [&](int buf) {
+#pragma unroll
+    for (int kk = 0; kk < KS; ++kk) {
+      f16x8 bop[TN];
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+        bop[j] = as_f16x8(Bs[buf][4 * kk + lc][wn * 16 * TN + j * 16 + lr]);
+#pragma unroll
+      for (int x = 0; x < NX; ++x)
+#pragma unroll
+        for (int i = 0; i < TM; ++i) {
+          const f16x8 aop = as_f16x8(As[buf][x][4 * kk + lc][wm * 16 * TM + i * 16 + lr]);
+#pragma unroll
+          for (int j = 0; j < TN; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(aop, bop[j], acc[i][j], 0, 0, 0);
+        }
+    }
+  };
+
+#pragma unroll
+  for (int s = 0; s < P - 1; ++s) fetch(s, s);
+  store(0, 0);
+  __syncthreads();
+  // unrolled by P, so the ring slot of every step is a constant
+  for (int st0 = 0; st0 < S; st0 += P) {
+#pragma unroll
+    for (int s = 0; s < P; ++s) {
+      const int st = st0 + s;
+      if (st >= S) break;
+      fetch(st + P - 1, (s + P - 1) % P);  // the slot of stage st - 1, already in LDS
+      compute(st & 1);
+      if (st + 1 < S) store((s + 1) % P, (st + 1) & 1);
+      __syncthreads();
+    }
   }
 
   // epilogue: lane holds rows 4*lc + r (r = 0..3) of column lr of each tile
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
+  for (int i = 0; i < TM; ++i) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const int m = m0 + wm * 64 + i * 16 + 4 * lc + r;
+      const int m = m0 + wm * 16 * TM + i * 16 + 4 * lc + r;
       if (m >= M) continue;
       const int sc = xe[m] - shift;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int n = n0 + wn * 64 + j * 16 + lr;
+      for (int j = 0; j < TN; ++j) {
+        const int n = n0 + wn * 16 * TN + j * 16 + lr;
         if (n >= N) continue;
         const float v = ldexpf(acc[i][j][r], sc);
         const size_t o = (size_t)m * N + n;
@@ -237,6 +336,44 @@ __global__ __launch_bounds__(kThreads) void w4_gemm_kernel(
       }
     }
   }
+}
+
+template <int TM, int TN, int NX, int KS, int P>
+int launch_gemm(const g4_w4 *w, const uint4 *xt, const int *xe, int rows, int Mp, void *y,
+                bool y_bf16) {
+  constexpr int BM = 32 * TM, BN = 32 * TN;
+  if (Mp % BM != 0 || w->G % KS != 0)
+    return fail(G4_E_ARG, "w4_gemm: tile %dx%d (KS %d) does not fit rows %d, K %d", BM, BN, KS,
+                rows, w->K);
+  const int nm = (rows + BM - 1) / BM, nn = (w->N + BN - 1) / BN;
+  const int xcd_map = nm % 8 == 0;
+  hipLaunchKernelGGL((w4_gemm_kernel<TM, TN, NX, KS, P>), dim3(nm * nn), dim3(kThreads), 0,
+                     stream(), reinterpret_cast<const u32x4 *>(xt), xe,
+                     reinterpret_cast<const u32x4 *>(w->packed), w->scales, w->shift, y,
+                     (int)y_bf16, rows, Mp, w->N, w->K, xcd_map);
+  G4_LAUNCH_CHECK("w4_gemm_kernel");
+  return G4_OK;
+}
+
+// Tile choice: the largest tile (128 x 128) unless that leaves CUs idle or a
+// ragged last wave; then 64-row tiles, and 96-column tiles when those divide
+// N into a multiple of the CU count (e.g. M 2048, N 1536 -> 32 x 16 = 512).
+// Two groups per stage unless the group count is odd.
+template <int NX>
+int launch_gemm_auto(const g4_w4 *w, const uint4 *xt, const int *xe, int rows, int Mp, void *y,
+                     bool y_bf16) {
+  constexpr int P = 4;
+  if (w->G % 2 != 0) return launch_gemm<2, 2, NX, 1, P>(w, xt, xe, rows, Mp, y, y_bf16);
+  const int cus = cu_count() > 0 ? cu_count() : 256;
+  auto blocks = [&](int bm, int bn) {
+    return (long)((rows + bm - 1) / bm) * ((w->N + bn - 1) / bn);
+  };
+  if (blocks(128, 128) >= 2L * cus)
+    return launch_gemm<4, 4, NX, 2, P>(w, xt, xe, rows, Mp, y, y_bf16);
+  if (w->N % 96 == 0 && blocks(64, 96) % cus == 0)
+    return launch_gemm<2, 3, NX, 2, P>(w, xt, xe, rows, Mp, y, y_bf16);
+  if (blocks(64, 128) >= cus) return launch_gemm<2, 4, NX, 2, P>(w, xt, xe, rows, Mp, y, y_bf16);
+  return launch_gemm<2, 2, NX, 2, P>(w, xt, xe, rows, Mp, y, y_bf16);
 }
 
 // Workspace for x' (and its low half) and the row exponents; grows on demand
@@ -274,31 +411,30 @@ int workspace(size_t need, void **p) {
 namespace g4 {
 
 int w4_gemm(const g4_w4 *w, const void *x, bool f32x, int rows, void *y, bool y_bf16) {
-  const size_t xbytes = (size_t)rows * w->K * 2;  // FP16 x' per half
-  const size_t xoff_l = (xbytes + 255) & ~size_t(255);
-  const size_t eoff = xoff_l + (f32x ? xoff_l : 0);
+  const int Mp = (rows + kRowPad - 1) / kRowPad * kRowPad;
+  const size_t xt_bytes = (size_t)Mp * w->K * 2 * (f32x ? 2 : 1);  // FP16 x' (hi [+ lo])
+  const size_t eoff = (xt_bytes + 255) & ~size_t(255);
   void *ws = nullptr;
   int rc = workspace(eoff + (size_t)rows * 4, &ws);
   if (rc) return rc;
-  uint4 *xh = static_cast<uint4 *>(ws);
-  uint4 *xl = reinterpret_cast<uint4 *>(static_cast<char *>(ws) + xoff_l);
+  uint4 *xt = static_cast<uint4 *>(ws);
   int *xe = reinterpret_cast<int *>(static_cast<char *>(ws) + eoff);
-  if (f32x)
-    hipLaunchKernelGGL(gemm_xprep_kernel<true>, dim3(rows), dim3(kThreads), 0, stream(), x, w->K,
-                       xh, xl, xe);
-  else
-    hipLaunchKernelGGL(gemm_xprep_kernel<false>, dim3(rows), dim3(kThreads), 0, stream(), x,
-                       w->K, xh, xl, xe);
+  const dim3 egrid((rows + kThreads / 64 - 1) / (kThreads / 64));
+  const dim3 pgrid(Mp / kPrepTileM, (w->K / 8 + kPrepTileC - 1) / kPrepTileC);
+  if (f32x) {
+    hipLaunchKernelGGL(gemm_xexp_kernel<true>, egrid, dim3(kThreads), 0, stream(), x, rows, w->K,
+                       xe);
+    hipLaunchKernelGGL(gemm_xprep_kernel<true>, pgrid, dim3(kThreads), 0, stream(), x, xe, rows,
+                       Mp, w->K, xt);
+  } else {
+    hipLaunchKernelGGL(gemm_xexp_kernel<false>, egrid, dim3(kThreads), 0, stream(), x, rows,
+                       w->K, xe);
+    hipLaunchKernelGGL(gemm_xprep_kernel<false>, pgrid, dim3(kThreads), 0, stream(), x, xe, rows,
+                       Mp, w->K, xt);
+  }
   G4_LAUNCH_CHECK("gemm_xprep_kernel");
-  const dim3 grid((w->N + BN - 1) / BN, (rows + BM - 1) / BM);
-  if (f32x)
-    hipLaunchKernelGGL(w4_gemm_kernel<2>, grid, dim3(kThreads), 0, stream(), xh, xl, xe,
-                       w->packed, w->scales, w->shift, y, (int)y_bf16, rows, w->N, w->K);
-  else
-    hipLaunchKernelGGL(w4_gemm_kernel<1>, grid, dim3(kThreads), 0, stream(), xh, xl, xe,
-                       w->packed, w->scales, w->shift, y, (int)y_bf16, rows, w->N, w->K);
-  G4_LAUNCH_CHECK("w4_gemm_kernel");
-  return G4_OK;
+  return f32x ? launch_gemm_auto<2>(w, xt, xe, rows, Mp, y, y_bf16)
+              : launch_gemm_auto<1>(w, xt, xe, rows, Mp, y, y_bf16);
 }
 
 }  // namespace g4
