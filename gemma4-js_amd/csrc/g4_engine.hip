@@ -1,0 +1,631 @@
+// Decoder engine: Gemma4WebGPU (custom-webgpu/gemma4-webgpu.js:139-502) on the
+// HIP kernels of this library.  The forward pass is the reference's op
+// sequence (encodeLayer 215-301, forward 303-402, logits 404-431, greedy
+// 441-481) with one MI355X-first change: the token position and the next
+// token live in device memory.  Kernels read the position from there, and
+// the last kernel of a step (argmax over the head partials) writes the next
+// token and advances the position, so one recorded decode step (a HIP graph)
+// is replayed for every generated token without a host round trip.
+//
+// Weights are borrowed (g4_w4 / g4_ple handles and the BF16 embedding stay
+// owned by the caller); norm vectors are copied in.  Activation buffers and
+// KV caches are allocated once, sized for max_seq positions.
+#include <math.h>
+#include <string.h>
+
+#include <vector>
+
+#include "g4_internal.h"
+#include "g4_ops.h"
+
+namespace {
+
+using namespace g4;
+
+constexpr int kNorms = 7;  // input, post_attn, pre_ffw, post_ffw, post_ple, q, k
+constexpr int kProjs = 9;  // q, k, v, o, gate, up, down, ple_gate, ple_proj
+
+struct Layer {
+  int hd = 0, inter = 0, full = 0, kv_src = -1, rope_angles = 0;
+  float rope_base = 0.f;
+  const g4_w4 *w[kProjs] = {};
+  float *norm[kNorms] = {};
+  float skip = 1.f;
+  float *kc = nullptr, *vc = nullptr;  // own caches [max_seq, hd]
+};
+
+// One split attention pass needs this many keys per split (decode: small
+// splits over many blocks; prefill: larger ones).
+int kpw_for(int rows) { return rows <= 4 ? 4 : 64; }
+
+// Final argmax reduction + advance: ids[0] = token, gen[pos + rows] = token,
+// pos += rows.  One block.
+__global__ __launch_bounds__(256) void advance_kernel(const float2 *__restrict__ partials,
+                                                      int nparts, int rows, int *__restrict__ ids,
+                                                      int *__restrict__ pos,
+                                                      int *__restrict__ gen, int gen_cap) {
+  __shared__ float sv[4];
+  __shared__ int si[4];
+  float bv = -INFINITY;
+  int bi = 0x7fffffff;
+  for (int i = threadIdx.x; i < nparts; i += 256) {
+    const float2 p = partials[i];
+    const float v = p.x;
+    const int ix = __float_as_int(p.y);
+    if (v > bv || (v == bv && ix < bi)) {
+      bv = v;
+      bi = ix;
+    }
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const float ov = __shfl_xor(bv, o, 64);
+    const int oi = __shfl_xor(bi, o, 64);
+    if (ov > bv || (ov == bv && oi < bi)) {
+      bv = ov;
+      bi = oi;
+    }
+  }
+  if ((threadIdx.x & 63) == 0) {
+    sv[threadIdx.x >> 6] = bv;
+    si[threadIdx.x >> 6] = bi;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int w = 1; w < 4; ++w)
+      if (sv[w] > bv || (sv[w] == bv && si[w] < bi)) {
+        bv = sv[w];
+        bi = si[w];
+      }
+    const int tok = bi == 0x7fffffff ? -1 : bi;
+    const int p = *pos + rows;
+    ids[0] = tok;
+    if (p < gen_cap) gen[p] = tok;
+    *pos = p;
+  }
+}
+
+}  // namespace
+
+struct g4_gemma {
+  g4_gemma_config cfg;
+  std::vector<Layer> L;
+  const g4_w4 *top = nullptr;
+  float *ple_norm = nullptr, *final_norm = nullptr;
+  const uint16_t *E = nullptr;
+  const g4_ple *ple = nullptr;
+  int max_rows = 0, hd_max = 0, inter_max = 0, ple_total = 0;
+  int cache_len = 0;  // host mirror of the KV length (KVCache.length)
+  // device state
+  int *ids = nullptr, *pos = nullptr, *gen = nullptr;
+  float *h[2] = {}, *pre = nullptr, *qraw = nullptr, *q = nullptr, *kraw = nullptr,
+        *vraw = nullptr, *ctx = nullptr, *attn = nullptr, *an = nullptr, *ares = nullptr,
+        *pf = nullptr, *gate = nullptr, *up = nullptr, *act = nullptr, *down = nullptr,
+        *fn = nullptr, *fres = nullptr, *pg = nullptr, *pm = nullptr, *pp = nullptr,
+        *pn = nullptr, *tokple = nullptr, *proj = nullptr, *projs = nullptr,
+        *perlayer = nullptr, *last = nullptr, *logits = nullptr, *part = nullptr;
+  float2 *hpart = nullptr;
+  size_t part_floats = 0;
+  std::vector<void *> allocs;
+  g4_cmdbuf *step = nullptr;  // recorded one-token decode step
+};
+
+namespace {
+
+int galloc(g4_gemma *m, size_t bytes, void **p) {
+  int rc = device_alloc(bytes, p);
+  if (!rc) m->allocs.push_back(*p);
+  return rc;
+}
+
+template <typename T>
+int galloc_n(g4_gemma *m, size_t n, T **p) {
+  return galloc(m, n * sizeof(T), reinterpret_cast<void **>(p));
+}
+
+void drop_step(g4_gemma *m) {
+  if (m->step) {
+    g4_cmdbuf_free(m->step);
+    m->step = nullptr;
+  }
+}
+
+int check_ready(const g4_gemma *m) {
+  const g4_gemma_config &c = m->cfg;
+  if (!m->top || !m->ple_norm || !m->final_norm || !m->E || !m->ple)
+    return fail(G4_E_STATE, "g4_gemma: top-level weights are not set (embedding, PLE table, "
+                            "per-layer projection, PLE norm, final norm)");
+  for (int i = 0; i < c.layers; ++i) {
+    const Layer &l = m->L[i];
+    for (int p = 0; p < kProjs; ++p) {
+      const bool needed = !((p == G4_PROJ_K || p == G4_PROJ_V) && l.kv_src >= 0);
+      if (needed && !l.w[p])
+        return fail(G4_E_STATE, "g4_gemma: layer %d projection %d is not set", i, p);
+    }
+    for (int n = 0; n < kNorms; ++n) {
+      const bool needed = !(n == G4_NORM_K && l.kv_src >= 0);
+      if (needed && !l.norm[n])
+        return fail(G4_E_STATE, "g4_gemma: layer %d norm %d is not set", i, n);
+    }
+  }
+  return G4_OK;
+}
+
+// Enqueue the forward of `rows` tokens whose ids are in m->ids and whose first
+// position is *m->pos; leaves the final-norm last row in m->last.
+int run_layers(g4_gemma *m, int rows, bool graph) {
+  const g4_gemma_config &c = m->cfg;
+  const int H = c.hidden, P = c.ple_dim, NL = c.layers;
+  const float eps = c.eps;
+  int rc;
+  // Top level (gemma4-webgpu.js:316-323): scaled embedding, PLE rows,
+  // per-layer projection, pleMix.
+  if ((rc = launch_embed(m->E, c.vocab, H, m->ids, rows, (float)sqrt((double)H), m->h[0])))
+    return rc;
+  if ((rc = g4_ple_gather_dev(m->ple, m->ids, rows, m->tokple, G4_F32))) return rc;
+  if ((rc = g4_w4_linear(m->top, m->h[0], G4_F32, rows, m->proj, G4_F32))) return rc;
+  if ((rc = launch_scale(m->proj, (size_t)rows * NL * P, (float)(1.0 / sqrt((double)H)),
+                         m->projs)))
+    return rc;
+  if ((rc = launch_ple_mix(m->projs, m->ple_norm, m->tokple, rows, P, NL, 1e-6f, 16.f,
+                           0.7071067811865476f, m->perlayer)))
+    return rc;
+
+  const int keylen_host = m->cache_len + rows;  // prefill calls know it; graphs read *pos
+  const int max_keylen = graph ? c.max_seq : keylen_host;
+  const int kpw = kpw_for(rows);
+  int cur = 0;
+  for (int i = 0; i < NL; ++i) {
+    const Layer &l = m->L[i];
+    float *hid = m->h[cur], *out = m->h[cur ^ 1];
+    const int HD = c.heads * l.hd;
+    // encodeLayer (gemma4-webgpu.js:215-301)
+    if ((rc = launch_rms(hid, rows, H, l.norm[G4_NORM_INPUT], eps, m->pre, nullptr))) return rc;
+    if ((rc = g4_w4_linear(l.w[G4_PROJ_Q], m->pre, G4_F32, rows, m->qraw, G4_F32))) return rc;
+    if ((rc = launch_norm_rope(m->qraw, rows, c.heads, l.hd, 0, m->pos, l.norm[G4_NORM_Q],
+                               l.rope_angles, l.rope_base, eps, m->q, false)))
+      return rc;
+    const Layer &src = l.kv_src >= 0 ? m->L[l.kv_src] : l;
+    if (l.kv_src < 0) {
+      if ((rc = g4_w4_linear(l.w[G4_PROJ_K], m->pre, G4_F32, rows, m->kraw, G4_F32))) return rc;
+      if ((rc = g4_w4_linear(l.w[G4_PROJ_V], m->pre, G4_F32, rows, m->vraw, G4_F32))) return rc;
+      // KVCache.append: rows go straight to positions pos .. pos + rows - 1
+      if ((rc = launch_norm_rope(m->kraw, rows, 1, l.hd, 0, m->pos, l.norm[G4_NORM_K],
+                                 l.rope_angles, l.rope_base, eps, l.kc, true)))
+        return rc;
+      if ((rc = launch_rms(m->vraw, rows, l.hd, nullptr, eps, l.vc, m->pos))) return rc;
+    }
+    if ((rc = launch_attention(m->q, src.kc, src.vc, rows, c.heads, l.hd, keylen_host, 0, m->pos,
+                               max_keylen, !l.full, c.window, kpw, m->part, m->ctx)))
+      return rc;
+    if ((rc = g4_w4_linear(l.w[G4_PROJ_O], m->ctx, G4_F32, rows, m->attn, G4_F32))) return rc;
+    if ((rc = launch_rms(m->attn, rows, H, l.norm[G4_NORM_POST_ATTN], eps, m->an, nullptr)))
+      return rc;
+    if ((rc = launch_add_scale(hid, m->an, (size_t)rows * H, 1.f, m->ares))) return rc;
+    if ((rc = launch_rms(m->ares, rows, H, l.norm[G4_NORM_PRE_FFW], eps, m->pf, nullptr)))
+      return rc;
+    if ((rc = g4_w4_linear(l.w[G4_PROJ_GATE], m->pf, G4_F32, rows, m->gate, G4_F32))) return rc;
+    if ((rc = g4_w4_linear(l.w[G4_PROJ_UP], m->pf, G4_F32, rows, m->up, G4_F32))) return rc;
+    if ((rc = launch_gelu_mul(m->gate, m->up, (size_t)rows * l.inter, m->act))) return rc;
+    if ((rc = g4_w4_linear(l.w[G4_PROJ_DOWN], m->act, G4_F32, rows, m->down, G4_F32))) return rc;
+    if ((rc = launch_rms(m->down, rows, H, l.norm[G4_NORM_POST_FFW], eps, m->fn, nullptr)))
+      return rc;
+    if ((rc = launch_add_scale(m->ares, m->fn, (size_t)rows * H, 1.f, m->fres))) return rc;
+    if ((rc = g4_w4_linear(l.w[G4_PROJ_PLE_GATE], m->fres, G4_F32, rows, m->pg, G4_F32)))
+      return rc;
+    if ((rc = launch_gelu_ple(m->pg, m->perlayer, rows, i, P, NL, m->pm))) return rc;
+    if ((rc = g4_w4_linear(l.w[G4_PROJ_PLE_PROJ], m->pm, G4_F32, rows, m->pp, G4_F32)))
+      return rc;
+    if ((rc = launch_rms(m->pp, rows, H, l.norm[G4_NORM_POST_PLE], eps, m->pn, nullptr)))
+      return rc;
+    if ((rc = launch_add_scale(m->fres, m->pn, (size_t)rows * H, l.skip, out))) return rc;
+    (void)HD;
+    cur ^= 1;
+  }
+  // final norm of the last row (gemma4-webgpu.js:394-400)
+  return launch_rms(m->h[cur] + (size_t)(rows - 1) * H, 1, H, m->final_norm, eps, m->last,
+                    nullptr);
+}
+
+// Head over the whole vocabulary with per-block argmax partials, then the
+// advance kernel (token -> ids[0], gen[pos + rows]; pos += rows).
+int run_head(g4_gemma *m, int rows) {
+  const g4_gemma_config &c = m->cfg;
+  int rc = launch_bf16_head(m->last, m->E, c.vocab, c.hidden, m->logits, 1.f, c.softcap,
+                            m->hpart);
+  if (rc) return rc;
+  const int nparts = (int)head_argmax_blocks(c.vocab);
+  hipLaunchKernelGGL(advance_kernel, dim3(1), dim3(256), 0, stream(), m->hpart, nparts, rows,
+                     m->ids, m->pos, m->gen, c.max_seq + 1);
+  G4_LAUNCH_CHECK("advance_kernel");
+  return G4_OK;
+}
+
+int stage_ids(g4_gemma *m, const int32_t *ids, int n, int start_pos) {
+  const g4_gemma_config &c = m->cfg;
+  if (n <= 0) return fail(G4_E_ARG, "g4_gemma: token count must be positive, got %d", n);
+  if (n > m->max_rows) return fail(G4_E_ARG, "g4_gemma: %d tokens exceed max_seq %d", n, m->max_rows);
+  // KVCache.append checks (gemma4-webgpu.js:128-130)
+  if (start_pos != m->cache_len)
+    return fail(G4_E_ARG, "KV append position %d != cache length %d", start_pos, m->cache_len);
+  if (start_pos + n > c.max_seq)
+    return fail(G4_E_RANGE, "KV cache capacity %d exceeded", c.max_seq);
+  for (int i = 0; i < n; ++i)
+    if (ids[i] < 0 || ids[i] >= c.vocab)
+      return fail(G4_E_RANGE, "token id %d out of range [0, %d)", ids[i], c.vocab);
+  G4_HIP_TRY(hipMemcpyAsync(m->ids, ids, (size_t)n * 4, hipMemcpyHostToDevice, stream()));
+  G4_HIP_TRY(hipMemcpyAsync(m->pos, &start_pos, 4, hipMemcpyHostToDevice, stream()));
+  // the host buffers above may be pageable stack/heap memory: wait for the copies
+  G4_HIP_TRY(hipStreamSynchronize(stream()));
+  return G4_OK;
+}
+
+int upload_f32(g4_gemma *m, float **dst, const float *src, int n) {
+  if (!src) return fail(G4_E_ARG, "g4_gemma: null norm vector");
+  if (!*dst) {
+    int rc = galloc_n(m, (size_t)n, dst);
+    if (rc) return rc;
+  }
+  G4_HIP_TRY(hipMemcpyAsync(*dst, src, (size_t)n * 4, hipMemcpyHostToDevice, stream()));
+  G4_HIP_TRY(hipStreamSynchronize(stream()));
+  return G4_OK;
+}
+
+}  // namespace
+
+// ---- C ABI ---------------------------------------------------------------------
+
+G4_API int g4_gemma_e2b_config(int max_seq, g4_gemma_config *c) {
+  if (!c) return fail(G4_E_ARG, "g4_gemma_e2b_config: null config");
+  memset(c, 0, sizeof *c);
+  // gemma4-webgpu.js:12 (HIDDEN, PLE, LAYERS, HEADS) and spec(i) (65-77)
+  c->hidden = 1536;
+  c->heads = 8;
+  c->ple_dim = 256;
+  c->vocab = 262144;
+  c->layers = 35;
+  c->max_seq = max_seq;
+  c->window = 512;
+  c->eps = 1e-6f;
+  c->softcap = 30.f;
+  for (int i = 0; i < 35; ++i) {
+    const bool full = (i + 1) % 5 == 0;
+    c->head_dim[i] = full ? 512 : 256;
+    c->intermediate[i] = i < 15 ? 6144 : 12288;
+    c->full[i] = full ? 1 : 0;
+    // layers >= 15 read the cache of layer 13 (sliding) or 14 (full)
+    c->kv_source[i] = i < 15 ? -1 : (full ? 14 : 13);
+    c->rope_base[i] = full ? 1000000.f : 10000.f;
+    c->rope_prop[i] = full ? 0.25f : 1.f;
+  }
+  return ok();
+}
+
+G4_API int g4_gemma_create(const g4_gemma_config *cfg, g4_gemma **out) {
+  G4_CHECK_INIT();
+  G4_CHECK_NOT_ENCODING();
+  if (!cfg || !out) return fail(G4_E_ARG, "g4_gemma_create: null argument");
+  *out = nullptr;
+  const g4_gemma_config &c = *cfg;
+  if (c.layers <= 0 || c.layers > G4_GEMMA_MAX_LAYERS || c.hidden <= 0 || c.hidden % 32 != 0 ||
+      c.hidden > 4096 || c.heads <= 0 || c.heads > 8 || c.ple_dim <= 0 || c.ple_dim % 32 != 0 ||
+      c.vocab <= 0 || c.max_seq <= 0 || c.window <= 0)
+    return fail(G4_E_ARG,
+                "g4_gemma_create: bad config (layers %d <= %d, hidden %d multiple of 32 <= "
+                "4096, heads %d <= 8, ple_dim %d multiple of 32, vocab %d, max_seq %d)",
+                c.layers, G4_GEMMA_MAX_LAYERS, c.hidden, c.heads, c.ple_dim, c.vocab, c.max_seq);
+  for (int i = 0; i < c.layers; ++i) {
+    const int hd = c.head_dim[i];
+    if (hd != 64 && hd != 128 && hd != 256 && hd != 512)
+      return fail(G4_E_ARG, "g4_gemma_create: layer %d head_dim %d (64, 128, 256 or 512)", i, hd);
+    if (c.intermediate[i] <= 0 || c.intermediate[i] % 32 != 0)
+      return fail(G4_E_ARG, "g4_gemma_create: layer %d intermediate %d", i, c.intermediate[i]);
+    const int s = c.kv_source[i];
+    if (s >= i || s < -1 || (s >= 0 && (c.kv_source[s] != -1 || c.head_dim[s] != hd)))
+      return fail(G4_E_ARG,
+                  "g4_gemma_create: layer %d kv_source %d must be an earlier layer with its own "
+                  "cache and the same head_dim",
+                  i, s);
+    if (c.rope_prop[i] < 0.f || c.rope_prop[i] > 1.f || !(c.rope_base[i] > 0.f))
+      return fail(G4_E_ARG, "g4_gemma_create: layer %d rope base %g / proportion %g", i,
+                  c.rope_base[i], c.rope_prop[i]);
+  }
+  g4_gemma *m = new g4_gemma();
+  m->cfg = c;
+  m->L.resize(c.layers);
+  m->max_rows = c.max_seq;
+  m->ple_total = c.layers * c.ple_dim;
+  for (int i = 0; i < c.layers; ++i) {
+    Layer &l = m->L[i];
+    l.hd = c.head_dim[i];
+    l.inter = c.intermediate[i];
+    l.full = c.full[i];
+    l.kv_src = c.kv_source[i];
+    l.rope_base = c.rope_base[i];
+    // normRope passes floor(ropeProp * hd / 2) (gpu-runtime.js:1352)
+    l.rope_angles = (int)floorf(c.rope_prop[i] * (float)l.hd / 2.f);
+    if (l.hd > m->hd_max) m->hd_max = l.hd;
+    if (l.inter > m->inter_max) m->inter_max = l.inter;
+  }
+  const size_t R = (size_t)m->max_rows, H = c.hidden;
+  const size_t QD = (size_t)c.heads * m->hd_max;
+  int rc = G4_OK;
+  auto A = [&](float **p, size_t n) {
+    if (!rc) rc = galloc_n(m, n, p);
+  };
+  if (!rc) rc = galloc_n(m, R, &m->ids);
+  if (!rc) rc = galloc_n(m, 1, &m->pos);
+  if (!rc) rc = galloc_n(m, (size_t)c.max_seq + 1, &m->gen);
+  A(&m->h[0], R * H);
+  A(&m->h[1], R * H);
+  A(&m->pre, R * H);
+  A(&m->qraw, R * QD);
+  A(&m->q, R * QD);
+  A(&m->kraw, R * m->hd_max);
+  A(&m->vraw, R * m->hd_max);
+  A(&m->ctx, R * QD);
+  A(&m->attn, R * H);
+  A(&m->an, R * H);
+  A(&m->ares, R * H);
+  A(&m->pf, R * H);
+  A(&m->gate, R * m->inter_max);
+  A(&m->up, R * m->inter_max);
+  A(&m->act, R * m->inter_max);
+  A(&m->down, R * H);
+  A(&m->fn, R * H);
+  A(&m->fres, R * H);
+  A(&m->pg, R * c.ple_dim);
+  A(&m->pm, R * c.ple_dim);
+  A(&m->pp, R * H);
+  A(&m->pn, R * H);
+  A(&m->tokple, R * m->ple_total);
+  A(&m->proj, R * m->ple_total);
+  A(&m->projs, R * m->ple_total);
+  A(&m->perlayer, R * m->ple_total);
+  A(&m->last, H);
+  A(&m->logits, (size_t)c.vocab);
+  {
+    const int small = m->max_rows < 4 ? m->max_rows : 4;  // row counts that use kpw_for(1)
+    const size_t a = attention_part_floats(small, c.heads, m->hd_max, c.max_seq, kpw_for(1));
+    const size_t b = attention_part_floats(m->max_rows, c.heads, m->hd_max, c.max_seq,
+                                           kpw_for(m->max_rows));
+    m->part_floats = a > b ? a : b;
+    A(&m->part, m->part_floats);
+  }
+  if (!rc) rc = galloc_n(m, head_argmax_blocks(c.vocab), &m->hpart);
+  for (int i = 0; i < c.layers && !rc; ++i) {
+    Layer &l = m->L[i];
+    if (l.kv_src < 0) {
+      A(&l.kc, (size_t)c.max_seq * l.hd);
+      A(&l.vc, (size_t)c.max_seq * l.hd);
+    }
+  }
+  if (rc) {
+    for (void *p : m->allocs) device_free(p);
+    delete m;
+    return rc;
+  }
+  *out = m;
+  return ok();
+}
+
+G4_API int g4_gemma_free(g4_gemma *m) {
+  G4_CHECK_INIT();
+  G4_CHECK_NOT_ENCODING();
+  if (!m) return ok();
+  drop_step(m);
+  int rc = G4_OK;
+  for (void *p : m->allocs) {
+    int r = device_free(p);
+    if (r && !rc) rc = r;
+  }
+  delete m;
+  return rc ? rc : ok();
+}
+
+G4_API int g4_gemma_set_linear(g4_gemma *m, int layer, int which, const g4_w4 *w) {
+  G4_CHECK_INIT();
+  G4_CHECK_NOT_ENCODING();
+  if (!m || !w) return fail(G4_E_ARG, "g4_gemma_set_linear: null argument");
+  const g4_gemma_config &c = m->cfg;
+  int N = 0, K = 0;
+  g4_w4_info(w, &N, &K, nullptr, nullptr);
+  if (layer == -1) {
+    if (which != G4_PROJ_TOP)
+      return fail(G4_E_ARG, "g4_gemma_set_linear: layer -1 takes G4_PROJ_TOP only");
+    if (N != c.layers * c.ple_dim || K != c.hidden)
+      return fail(G4_E_ARG, "per_layer_model_projection must be [%d, %d], got [%d, %d]",
+                  c.layers * c.ple_dim, c.hidden, N, K);
+    m->top = w;
+    drop_step(m);
+    return ok();
+  }
+  if (layer < 0 || layer >= c.layers || which < 0 || which >= kProjs)
+    return fail(G4_E_ARG, "g4_gemma_set_linear: layer %d / projection %d out of range", layer,
+                which);
+  Layer &l = m->L[layer];
+  if ((which == G4_PROJ_K || which == G4_PROJ_V) && l.kv_src >= 0)
+    return fail(G4_E_ARG, "g4_gemma_set_linear: layer %d shares layer %d's KV (no k/v proj)",
+                layer, l.kv_src);
+  const int H = c.hidden, QD = c.heads * l.hd, P = c.ple_dim;
+  static const char *names[kProjs] = {"q_proj", "k_proj", "v_proj", "o_proj", "gate_proj",
+                                      "up_proj", "down_proj", "per_layer_input_gate",
+                                      "per_layer_projection"};
+  const int want[kProjs][2] = {{QD, H}, {l.hd, H}, {l.hd, H}, {H, QD}, {l.inter, H},
+                               {l.inter, H}, {H, l.inter}, {P, H}, {H, P}};
+  if (N != want[which][0] || K != want[which][1])
+    return fail(G4_E_ARG, "layer %d %s must be [%d, %d], got [%d, %d]", layer, names[which],
+                want[which][0], want[which][1], N, K);
+  l.w[which] = w;
+  drop_step(m);
+  return ok();
+}
+
+G4_API int g4_gemma_set_norm(g4_gemma *m, int layer, int which, const float *v, int n) {
+  G4_CHECK_INIT();
+  G4_CHECK_NOT_ENCODING();
+  if (!m) return fail(G4_E_ARG, "g4_gemma_set_norm: null model");
+  const g4_gemma_config &c = m->cfg;
+  if (layer == -1) {
+    if (which == G4_NORM_PLE_PROJECTION) {
+      if (n != c.ple_dim) return fail(G4_E_ARG, "per_layer_projection_norm needs %d values", c.ple_dim);
+      return upload_f32(m, &m->ple_norm, v, n) ?: ok();
+    }
+    if (which == G4_NORM_FINAL) {
+      if (n != c.hidden) return fail(G4_E_ARG, "final norm needs %d values", c.hidden);
+      return upload_f32(m, &m->final_norm, v, n) ?: ok();
+    }
+    return fail(G4_E_ARG, "g4_gemma_set_norm: layer -1 takes the PLE projection or final norm");
+  }
+  if (layer < 0 || layer >= c.layers || which < 0 || which >= kNorms)
+    return fail(G4_E_ARG, "g4_gemma_set_norm: layer %d / norm %d out of range", layer, which);
+  Layer &l = m->L[layer];
+  if (which == G4_NORM_K && l.kv_src >= 0)
+    return fail(G4_E_ARG, "g4_gemma_set_norm: layer %d has no k_norm (shared KV)", layer);
+  const int want = (which == G4_NORM_Q || which == G4_NORM_K) ? l.hd : c.hidden;
+  if (n != want)
+    return fail(G4_E_ARG, "layer %d norm %d needs %d values, got %d", layer, which, want, n);
+  return upload_f32(m, &l.norm[which], v, n) ?: ok();
+}
+
+G4_API int g4_gemma_set_layer_scalar(g4_gemma *m, int layer, float s) {
+  if (!m || layer < 0 || layer >= m->cfg.layers)
+    return fail(G4_E_ARG, "g4_gemma_set_layer_scalar: bad layer %d", layer);
+  m->L[layer].skip = s;
+  drop_step(m);
+  return ok();
+}
+
+G4_API int g4_gemma_set_embedding(g4_gemma *m, const void *E_dev) {
+  G4_CHECK_INIT();
+  if (!m) return fail(G4_E_ARG, "g4_gemma_set_embedding: null model");
+  int rc = check_device_range(E_dev, (size_t)m->cfg.vocab * m->cfg.hidden * 2,
+                              "g4_gemma_set_embedding E");
+  if (rc) return rc;
+  if ((reinterpret_cast<uintptr_t>(E_dev) & 15u) != 0)
+    return fail(G4_E_ARG, "g4_gemma_set_embedding: E must be 16-byte aligned");
+  m->E = static_cast<const uint16_t *>(E_dev);
+  drop_step(m);
+  return ok();
+}
+
+G4_API int g4_gemma_set_ple(g4_gemma *m, const g4_ple *t) {
+  if (!m || !t) return fail(G4_E_ARG, "g4_gemma_set_ple: null argument");
+  int vocab = 0, width = 0;
+  ple_geometry(t, &vocab, &width);
+  // the table must cover the vocabulary with layers * ple_dim columns
+  if (vocab < m->cfg.vocab || width != m->cfg.layers * m->cfg.ple_dim)
+    return fail(G4_E_ARG, "g4_gemma_set_ple: table [%d, %d] does not match vocab %d x %d",
+                vocab, width, m->cfg.vocab, m->cfg.layers * m->cfg.ple_dim);
+  m->ple = t;
+  drop_step(m);
+  return ok();
+}
+
+G4_API int g4_gemma_reset(g4_gemma *m) {
+  if (!m) return fail(G4_E_ARG, "g4_gemma_reset: null model");
+  m->cache_len = 0;  // resetCache (gemma4-webgpu.js:191-194)
+  return ok();
+}
+
+G4_API int g4_gemma_cache_length(const g4_gemma *m, int *len) {
+  if (!m || !len) return fail(G4_E_ARG, "g4_gemma_cache_length: null argument");
+  *len = m->cache_len;
+  return ok();
+}
+
+G4_API int g4_gemma_forward(g4_gemma *m, const int32_t *ids, int n, int start_pos,
+                            float *last_hidden) {
+  G4_CHECK_INIT();
+  G4_CHECK_NOT_ENCODING();
+  if (!m || !ids) return fail(G4_E_ARG, "g4_gemma_forward: null argument");
+  int rc = check_ready(m);
+  if (!rc && last_hidden) rc = check_device_range(last_hidden, (size_t)m->cfg.hidden * 4,
+                                                  "g4_gemma_forward last_hidden");
+  if (!rc) rc = stage_ids(m, ids, n, start_pos);
+  if (!rc) rc = run_layers(m, n, false);
+  if (rc) return rc;
+  m->cache_len += n;
+  if (last_hidden)
+    G4_HIP_TRY(hipMemcpyAsync(last_hidden, m->last, (size_t)m->cfg.hidden * 4,
+                              hipMemcpyDeviceToDevice, stream()));
+  return ok();
+}
+
+G4_API int g4_gemma_logits(g4_gemma *m, const float *last_hidden, float *logits) {
+  G4_CHECK_INIT();
+  if (!m || !last_hidden || !logits) return fail(G4_E_ARG, "g4_gemma_logits: null argument");
+  if (!m->E) return fail(G4_E_STATE, "g4_gemma_logits: embedding not set");
+  const g4_gemma_config &c = m->cfg;
+  int rc = check_device_range(last_hidden, (size_t)c.hidden * 4, "g4_gemma_logits last_hidden");
+  if (!rc) rc = check_device_range(logits, (size_t)c.vocab * 4, "g4_gemma_logits logits");
+  if (!rc)
+    rc = launch_bf16_head(last_hidden, m->E, c.vocab, c.hidden, logits, 1.f, c.softcap, nullptr);
+  return rc ? rc : ok();
+}
+
+G4_API int g4_gemma_greedy(g4_gemma *m, const int32_t *ids, int n, int start_pos,
+                           int32_t *next_token, float *logits) {
+  G4_CHECK_INIT();
+  G4_CHECK_NOT_ENCODING();
+  if (!m || !ids || !next_token) return fail(G4_E_ARG, "g4_gemma_greedy: null argument");
+  int rc = check_ready(m);
+  if (!rc && logits)
+    rc = check_device_range(logits, (size_t)m->cfg.vocab * 4, "g4_gemma_greedy logits");
+  if (!rc) rc = stage_ids(m, ids, n, start_pos);
+  if (!rc) rc = run_layers(m, n, false);
+  if (!rc) rc = run_head(m, n);
+  if (rc) return rc;
+  m->cache_len += n;
+  if (logits)
+    G4_HIP_TRY(hipMemcpyAsync(logits, m->logits, (size_t)m->cfg.vocab * 4,
+                              hipMemcpyDeviceToDevice, stream()));
+  int32_t tok = -1;
+  G4_HIP_TRY(hipMemcpyAsync(&tok, m->ids, 4, hipMemcpyDeviceToHost, stream()));
+  G4_HIP_TRY(hipStreamSynchronize(stream()));
+  if (tok < 0) return fail(G4_E_STATE, "topK(): no finite logits.");
+  *next_token = tok;
+  return ok();
+}
+
+G4_API int g4_gemma_decode(g4_gemma *m, int steps, int32_t *tokens) {
+  G4_CHECK_INIT();
+  G4_CHECK_NOT_ENCODING();
+  if (!m || steps < 0) return fail(G4_E_ARG, "g4_gemma_decode: bad argument");
+  if (steps == 0) return ok();
+  int rc = check_ready(m);
+  if (rc) return rc;
+  if (m->cache_len == 0)
+    return fail(G4_E_STATE, "g4_gemma_decode: run g4_gemma_greedy on a prompt first");
+  if (m->cache_len + steps > m->cfg.max_seq)
+    return fail(G4_E_RANGE, "KV cache capacity %d exceeded", m->cfg.max_seq);
+  if (!m->step) {
+    // record one token: ids[0] and *pos come from the previous step's advance
+    if ((rc = g4_encoder_begin())) return rc;
+    rc = run_layers(m, 1, true);
+    if (!rc) rc = run_head(m, 1);
+    g4_cmdbuf *cb = nullptr;
+    const int rc2 = g4_encoder_finish(&cb);
+    if (rc) {
+      if (cb) g4_cmdbuf_free(cb);
+      return rc;
+    }
+    if (rc2) return rc2;
+    m->step = cb;
+  }
+  const int first = m->cache_len;
+  for (int s = 0; s < steps; ++s) {
+    rc = g4_submit(m->step);
+    if (rc) return rc;
+  }
+  m->cache_len += steps;
+  if (tokens) {
+    // gen[p] holds the token chosen for position p; step s fills first + 1 + s
+    G4_HIP_TRY(hipMemcpyAsync(tokens, m->gen + first + 1, (size_t)steps * 4,
+                              hipMemcpyDeviceToHost, stream()));
+    G4_HIP_TRY(hipStreamSynchronize(stream()));
+    for (int s = 0; s < steps; ++s)
+      if (tokens[s] < 0) return fail(G4_E_STATE, "topK(): no finite logits.");
+  }
+  return ok();
+}

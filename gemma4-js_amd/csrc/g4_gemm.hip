@@ -376,35 +376,8 @@ int launch_gemm_auto(const g4_w4 *w, const uint4 *xt, const int *xe, int rows, i
   return launch_gemm<2, 2, NX, 2, P>(w, xt, xe, rows, Mp, y, y_bf16);
 }
 
-// Workspace for x' (and its low half) and the row exponents; grows on demand
-// outside command encoders, reused by every later call.
-struct Workspace {
-  void *mem = nullptr;
-  size_t bytes = 0;
-};
+// x' (and its low half) and the row exponents, reused by every later call.
 Workspace g_ws;
-
-int workspace(size_t need, void **p) {
-  if (need <= g_ws.bytes) {
-    *p = g_ws.mem;
-    return G4_OK;
-  }
-  if (encoding())
-    return fail(G4_E_STATE,
-                "g4_w4_linear: the prefill workspace must grow (%zu bytes); make one call with "
-                "this row count outside a command encoder first", need);
-  if (g_ws.mem) {
-    int rc = device_free(g_ws.mem);
-    if (rc) return rc;
-    g_ws.mem = nullptr;
-    g_ws.bytes = 0;
-  }
-  int rc = device_alloc(need, &g_ws.mem);
-  if (rc) return rc;
-  g_ws.bytes = need;
-  *p = g_ws.mem;
-  return G4_OK;
-}
 
 }  // namespace
 
@@ -415,7 +388,7 @@ int w4_gemm(const g4_w4 *w, const void *x, bool f32x, int rows, void *y, bool y_
   const size_t xt_bytes = (size_t)Mp * w->K * 2 * (f32x ? 2 : 1);  // FP16 x' (hi [+ lo])
   const size_t eoff = (xt_bytes + 255) & ~size_t(255);
   void *ws = nullptr;
-  int rc = workspace(eoff + (size_t)rows * 4, &ws);
+  int rc = g_ws.get(eoff + (size_t)rows * 4, &ws, "g4_w4_linear (prefill)");
   if (rc) return rc;
   uint4 *xt = static_cast<uint4 *>(ws);
   int *xe = reinterpret_cast<int *>(static_cast<char *>(ws) + eoff);

@@ -5,23 +5,60 @@
 // 64 dispatches of 4096 rows; here a wave owns a few rows at a time and the
 // whole [rows, K] slab streams through with 16-byte loads.
 #include "g4_internal.h"
+#include "g4_ops.h"
 
+namespace g4 {
 namespace {
 
-using namespace g4;
-
 constexpr int kRowsPerWave = 8;
+constexpr int kNoIndex = 0x7fffffff;
+
+// Greedy selection keeps the first index of the largest finite logit: topK
+// (gpu-runtime.js:1396-1425) skips non-finite values and, with a stable sort,
+// ranks equal values by index.
+__device__ __forceinline__ void arg_better(float v, int i, float &bv, int &bi) {
+  if (v > bv || (v == bv && i < bi)) {
+    bv = v;
+    bi = i;
+  }
+}
+
+__device__ __forceinline__ void wave_argmax(float &bv, int &bi) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const float ov = __shfl_xor(bv, o, 64);
+    const int oi = __shfl_xor(bi, o, 64);
+    arg_better(ov, oi, bv, bi);
+  }
+}
+
+// Block-wide (max, first index); thread 0 writes it to partials[blockIdx.x].
+__device__ __forceinline__ void block_argmax_store(float bv, int bi, float2 *partials) {
+  __shared__ float sv[4];
+  __shared__ int si[4];
+  wave_argmax(bv, bi);
+  if ((threadIdx.x & 63) == 0) {
+    sv[threadIdx.x >> 6] = bv;
+    si[threadIdx.x >> 6] = bi;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int w = 1; w < (int)(blockDim.x >> 6); ++w) arg_better(sv[w], si[w], bv, bi);
+    partials[blockIdx.x] = make_float2(bv, __int_as_float(bi));
+  }
+}
 
 // Lane l holds x for the 8-element chunks l, l+64, ... (CPL chunks) and
 // reads the same chunks of every row it visits.
 template <int CPL>
 __global__ __launch_bounds__(256) void bf16_head_kernel(
     const float *__restrict__ x, const uint16_t *__restrict__ E, int rows, int K,
-    float *__restrict__ out, float scale, float softcap) {
+    float *__restrict__ out, float scale, float softcap, float2 *__restrict__ partials) {
   const int lane = threadIdx.x & 63;
   const int wave = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
   const int row0 = wave * kRowsPerWave;
-  if (row0 >= rows) return;
+  // waves past the end still take part in the block's argmax
+  if (row0 >= rows && !partials) return;
   const int chunks = K >> 3;
 
   float xv[CPL][8];
@@ -70,24 +107,112 @@ __global__ __launch_bounds__(256) void bf16_head_kernel(
   for (int r = 0; r < kRowsPerWave; ++r)
     if (lane == r) mine = acc[r];
   const int row = row0 + lane;
+  float bv = -INFINITY;
+  int bi = kNoIndex;
   if (lane < kRowsPerWave && row < rows) {
     const float raw = mine * scale;
-    out[row] = softcap > 0.f ? tanhf(raw / softcap) * softcap : raw;
+    const float v = softcap > 0.f ? tanhf(raw / softcap) * softcap : raw;
+    out[row] = v;
+    if (isfinite(v)) {
+      bv = v;
+      bi = row;
+    }
+  }
+  if (partials) block_argmax_store(bv, bi, partials);
+}
+
+// Plain argmax over x[0, n): per-block partials, then argmax_final_kernel.
+__global__ __launch_bounds__(256) void argmax_blocks_kernel(const float *__restrict__ x, int n,
+                                                            float2 *__restrict__ partials) {
+  float bv = -INFINITY;
+  int bi = kNoIndex;
+  const int per = (n + gridDim.x - 1) / gridDim.x;
+  const int i0 = blockIdx.x * per, i1 = i0 + per < n ? i0 + per : n;
+  for (int i = i0 + threadIdx.x; i < i1; i += blockDim.x) {
+    const float v = x[i];
+    if (isfinite(v)) arg_better(v, i, bv, bi);
+  }
+  block_argmax_store(bv, bi, partials);
+}
+
+// One block reduces the partials; out_idx gets -1 when no value was finite
+// (topK throws "no finite logits" in that case).
+__global__ __launch_bounds__(256) void argmax_final_kernel(const float2 *__restrict__ partials,
+                                                           int nparts, int *__restrict__ out_idx) {
+  __shared__ float sv[4];
+  __shared__ int si[4];
+  float bv = -INFINITY;
+  int bi = kNoIndex;
+  for (int i = threadIdx.x; i < nparts; i += blockDim.x) {
+    const float2 p = partials[i];
+    arg_better(p.x, __float_as_int(p.y), bv, bi);
+  }
+  wave_argmax(bv, bi);
+  if ((threadIdx.x & 63) == 0) {
+    sv[threadIdx.x >> 6] = bv;
+    si[threadIdx.x >> 6] = bi;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int w = 1; w < 4; ++w) arg_better(sv[w], si[w], bv, bi);
+    *out_idx = bi == kNoIndex ? -1 : bi;
   }
 }
 
 template <int CPL>
 int launch_head(const float *x, const uint16_t *E, int rows, int K, float *out, float scale,
-                float softcap) {
-  const int waves = (rows + kRowsPerWave - 1) / kRowsPerWave;
-  const int blocks = (waves + 3) / 4;
-  hipLaunchKernelGGL(bf16_head_kernel<CPL>, dim3(blocks), dim3(256), 0, stream(), x, E, rows,
-                     K, out, scale, softcap);
+                float softcap, float2 *partials) {
+  hipLaunchKernelGGL(bf16_head_kernel<CPL>, dim3(head_argmax_blocks(rows)), dim3(256), 0,
+                     stream(), x, E, rows, K, out, scale, softcap, partials);
   G4_LAUNCH_CHECK("bf16_head_kernel");
   return G4_OK;
 }
 
 }  // namespace
+
+size_t head_argmax_blocks(int rows) {
+  const int waves = (rows + kRowsPerWave - 1) / kRowsPerWave;
+  return (size_t)(waves + 3) / 4;
+}
+
+int launch_bf16_head(const float *x, const uint16_t *E, int rows, int K, float *out, float scale,
+                     float softcap, float2 *partials) {
+  if (rows == 0) return G4_OK;
+  switch ((K / 8 + 63) / 64) {
+    case 1: return launch_head<1>(x, E, rows, K, out, scale, softcap, partials);
+    case 2: return launch_head<2>(x, E, rows, K, out, scale, softcap, partials);
+    case 3: return launch_head<3>(x, E, rows, K, out, scale, softcap, partials);
+    case 4: return launch_head<4>(x, E, rows, K, out, scale, softcap, partials);
+    case 5: return launch_head<5>(x, E, rows, K, out, scale, softcap, partials);
+    case 6: return launch_head<6>(x, E, rows, K, out, scale, softcap, partials);
+    case 7: return launch_head<7>(x, E, rows, K, out, scale, softcap, partials);
+    default: return launch_head<8>(x, E, rows, K, out, scale, softcap, partials);
+  }
+}
+
+int launch_argmax_partials(const float2 *partials, int nparts, int *out_idx) {
+  hipLaunchKernelGGL(argmax_final_kernel, dim3(1), dim3(256), 0, stream(), partials, nparts,
+                     out_idx);
+  G4_LAUNCH_CHECK("argmax_final_kernel");
+  return G4_OK;
+}
+
+size_t argmax_blocks(int n) {
+  const int b = (n + 4095) / 4096;
+  return (size_t)(b < 1 ? 1 : b > 1024 ? 1024 : b);
+}
+
+int launch_argmax(const float *x, int n, float2 *partials, int *out_idx) {
+  const int blocks = (int)argmax_blocks(n);
+  hipLaunchKernelGGL(argmax_blocks_kernel, dim3(blocks), dim3(256), 0, stream(), x, n,
+                     partials);
+  G4_LAUNCH_CHECK("argmax_blocks_kernel");
+  return launch_argmax_partials(partials, blocks, out_idx);
+}
+
+}  // namespace g4
+
+using namespace g4;
 
 G4_API int g4_bf16_head(const float *x, const void *E, int rows, int in_dim, float *out,
                         float scale, float softcap) {
@@ -103,17 +228,7 @@ G4_API int g4_bf16_head(const float *x, const void *E, int rows, int in_dim, flo
   if (!rc) rc = check_device_range(E, (size_t)rows * in_dim * 2, "g4_bf16_head E");
   if (!rc) rc = check_device_range(out, (size_t)rows * 4, "g4_bf16_head out");
   if (rc) return rc;
-  const uint16_t *e = static_cast<const uint16_t *>(E);
-  const int cpl = (in_dim / 8 + 63) / 64;
-  switch (cpl) {
-    case 1: rc = launch_head<1>(x, e, rows, in_dim, out, scale, softcap); break;
-    case 2: rc = launch_head<2>(x, e, rows, in_dim, out, scale, softcap); break;
-    case 3: rc = launch_head<3>(x, e, rows, in_dim, out, scale, softcap); break;
-    case 4: rc = launch_head<4>(x, e, rows, in_dim, out, scale, softcap); break;
-    case 5: rc = launch_head<5>(x, e, rows, in_dim, out, scale, softcap); break;
-    case 6: rc = launch_head<6>(x, e, rows, in_dim, out, scale, softcap); break;
-    case 7: rc = launch_head<7>(x, e, rows, in_dim, out, scale, softcap); break;
-    default: rc = launch_head<8>(x, e, rows, in_dim, out, scale, softcap); break;
-  }
+  rc = launch_bf16_head(x, static_cast<const uint16_t *>(E), rows, in_dim, out, scale, softcap,
+                        nullptr);
   return rc ? rc : ok();
 }

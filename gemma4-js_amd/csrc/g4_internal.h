@@ -33,6 +33,16 @@ int device_free(void *p);
 // Device attribute cache.
 int cu_count();
 
+// Scratch memory that grows on demand.  Growing allocates, which a command
+// encoder cannot record: inside an encoder a request beyond the current size
+// fails with G4_E_STATE and `who` in the message (make one call of that size
+// outside the encoder first).  Contents are not preserved across growth.
+struct Workspace {
+  void *mem = nullptr;
+  size_t bytes = 0;
+  int get(size_t need, void **p, const char *who);
+};
+
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
@@ -116,4 +126,10 @@ struct g4_w4 {
 namespace g4 {
 // Prefill GEMM (rows >= 2): y[rows, N] = x[rows, K] . W^T, MFMA (g4_gemm.hip).
 int w4_gemm(const g4_w4 *w, const void *x, bool f32x, int rows, void *y, bool y_bf16);
+}  // namespace g4
+
+struct g4_ple;
+namespace g4 {
+// Rows and columns of a PLE table (g4_ple.hip).
+void ple_geometry(const g4_ple *t, int *vocab, int *width);
 }  // namespace g4

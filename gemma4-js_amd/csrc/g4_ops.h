@@ -1,0 +1,39 @@
+// Launchers of the GPUOps kernels (g4_ops.hip) and of the fused head/argmax
+// (g4_head.hip), shared by the C ABI and the model engine.  They enqueue on
+// the library stream and do no operand checking: callers validate first.
+#pragma once
+
+#include <stddef.h>
+#include <stdint.h>
+
+namespace g4 {
+
+int launch_rms(const float *x, int rows, int width, const float *scale, float eps, float *y,
+               const int *pos_dev);
+int launch_add_scale(const float *a, const float *b, size_t n, float s, float *y);
+int launch_scale(const float *a, size_t n, float s, float *y);
+int launch_gelu_mul(const float *gate, const float *up, size_t n, float *y);
+int launch_gelu_ple(const float *gate, const float *ple, int rows, int layer, int width,
+                    int layers, float *y);
+int launch_norm_rope(const float *x, int rows, int heads, int hd, int pos0, const int *pos_dev,
+                     const float *scale, int rope_angles, float base, float eps, float *y,
+                     bool at_pos);
+// Floats of split scratch that launch_attention needs for up to max_keylen keys.
+size_t attention_part_floats(int qrows, int heads, int hd, int max_keylen, int kpw);
+int launch_attention(const float *q, const float *k, const float *v, int qrows, int heads,
+                     int hd, int keylen, int qpos0, const int *pos_dev, int max_keylen,
+                     bool sliding, int window, int kpw, float *part, float *out);
+int launch_ple_mix(const float *proj, const float *norm_scale, const float *token_ple, int rows,
+                   int width, int layers, float eps, float ple_scale, float out_scale, float *y);
+int launch_embed(const uint16_t *E, int vocab, int width, const int *ids_dev, int n, float scale,
+                 float *y);
+
+// Head partials for the device argmax: per block (max value, first index).
+size_t head_argmax_blocks(int rows);
+int launch_bf16_head(const float *x, const uint16_t *E, int rows, int K, float *out, float scale,
+                     float softcap, float2 *partials);
+int launch_argmax_partials(const float2 *partials, int nparts, int *out_idx);
+int launch_argmax(const float *x, int n, float2 *partials, int *out_idx);
+size_t argmax_blocks(int n);
+
+}  // namespace g4

@@ -1,0 +1,580 @@
+// The element-wise, normalisation and attention ops of GPUOps
+// (custom-webgpu/gpu-runtime.js:1104-1263 shaders, 1325-1369 methods) and the
+// embedding lookup of Gemma4WebGPU.inputBuffers/forward
+// (gemma4-webgpu.js:198-215, 318-320), as gfx950 kernels.
+//
+// All activations are FP32 as in the reference.  Reductions (RMS sums,
+// softmax) are tree-shaped here instead of the shaders' serial loops, so
+// results agree with the reference to FP32 rounding, not bit for bit.
+//
+// Kernels that a captured decode step replays read the token position from
+// device memory when `pos_dev` is non-null (the host value is then ignored),
+// so one recorded step serves every position.
+#include <math.h>
+
+#include "g4_internal.h"
+#include "g4_ops.h"
+
+namespace g4 {
+
+namespace {
+
+constexpr int kBlock = 256;
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+// Sum over a 256-thread block; every thread gets the total.
+__device__ __forceinline__ float block_sum(float v, float *red) {
+  v = wave_sum(v);
+  __syncthreads();  // red may still be read by a previous call
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  return red[0] + red[1] + red[2] + red[3];
+}
+
+// GELU, tanh form with the shader's clamp (gpu-runtime.js:1148-1155).
+__device__ __forceinline__ float gelu_tanh(float x) {
+  const float c = 0.7978845608028654f;
+  const float z = c * (x + 0.044715f * x * x * x);
+  const float t = tanhf(fminf(fmaxf(z, -10.f), 10.f));
+  return 0.5f * x * (1.f + t);
+}
+
+__device__ __forceinline__ float inv_rms(float ss, int width, float eps) {
+  return 1.f / sqrtf(ss / (float)width + eps);
+}
+
+// ---- RMS_SHADER (gpu-runtime.js:1104-1118) ----------------------------------
+// One block per row.  y row index = row (+ *pos_dev when given: the row goes
+// to that position of a cache).
+__global__ __launch_bounds__(kBlock) void rms_kernel(const float *__restrict__ x, int width,
+                                                     const float *__restrict__ scale, float eps,
+                                                     float *__restrict__ y,
+                                                     const int *__restrict__ pos_dev) {
+  __shared__ float red[4];
+  const int row = blockIdx.x;
+  const float *xr = x + (size_t)row * width;
+  float ss = 0.f;
+  for (int i = threadIdx.x; i < width; i += kBlock) ss += xr[i] * xr[i];
+  const float inv = inv_rms(block_sum(ss, red), width, eps);
+  const int orow = row + (pos_dev ? *pos_dev : 0);
+  float *yr = y + (size_t)orow * width;
+  for (int i = threadIdx.x; i < width; i += kBlock)
+    yr[i] = xr[i] * inv * (scale ? scale[i] : 1.f);
+}
+
+// ---- ADD_SCALE_SHADER / SCALE_SHADER / GELU_MUL_SHADER ----------------------
+__global__ __launch_bounds__(kBlock) void add_scale_kernel(const float *__restrict__ a,
+                                                           const float *__restrict__ b,
+                                                           size_t n, float s,
+                                                           float *__restrict__ y) {
+  const size_t i = (size_t)blockIdx.x * kBlock + threadIdx.x;
+  if (i < n) y[i] = (a[i] + b[i]) * s;
+}
+
+__global__ __launch_bounds__(kBlock) void scale_kernel(const float *__restrict__ a, size_t n,
+                                                       float s, float *__restrict__ y) {
+  const size_t i = (size_t)blockIdx.x * kBlock + threadIdx.x;
+  if (i < n) y[i] = a[i] * s;
+}
+
+__global__ __launch_bounds__(kBlock) void gelu_mul_kernel(const float *__restrict__ gate,
+                                                          const float *__restrict__ up, size_t n,
+                                                          float *__restrict__ y) {
+  const size_t i = (size_t)blockIdx.x * kBlock + threadIdx.x;
+  if (i < n) y[i] = gelu_tanh(gate[i]) * up[i];
+}
+
+// ---- GELU_PLE_SHADER (gpu-runtime.js:1159-1173) -----------------------------
+// y[r, d] = gelu(gate[r, d]) * ple[r, layer, d], ple laid out [rows][layers][width].
+__global__ __launch_bounds__(kBlock) void gelu_ple_kernel(const float *__restrict__ gate,
+                                                          const float *__restrict__ ple,
+                                                          int rows, int layer, int width,
+                                                          int layers, float *__restrict__ y) {
+  const int i = blockIdx.x * kBlock + threadIdx.x;
+  if (i >= rows * width) return;
+  const int r = i / width, d = i - r * width;
+  y[i] = gelu_tanh(gate[i]) * ple[((size_t)r * layers + layer) * width + d];
+}
+
+// ---- NORM_ROPE_SHADER (gpu-runtime.js:1175-1202) ----------------------------
+// One block per (row, head); thread t < hd/2 owns the rotate-half pair
+// (t, t + hd/2).  Output row index is row, or *pos_dev + row when pos_dev is
+// given and `at_pos` is set (appending k straight into a cache).
+__global__ __launch_bounds__(kBlock) void norm_rope_kernel(
+    const float *__restrict__ x, int heads, int hd, int pos0, const int *__restrict__ pos_dev,
+    const float *__restrict__ scale, int rope_angles, float base, float eps,
+    float *__restrict__ y, int at_pos) {
+  __shared__ float red[4];
+  const int rh = blockIdx.x;
+  const int row = rh / heads, h = rh - row * heads;
+  const float *xv = x + (size_t)rh * hd;
+  const int half = hd >> 1, t = threadIdx.x;
+  float a = 0.f, b = 0.f;
+  if (t < half) {
+    a = xv[t];
+    b = xv[t + half];
+  }
+  const float inv = inv_rms(block_sum(a * a + b * b, red), hd, eps);
+  const int pos = (pos_dev ? *pos_dev : pos0) + row;
+  if (t < half) {
+    const float an = a * inv * scale[t], bn = b * inv * scale[t + half];
+    float sn = 0.f, cs = 1.f;
+    if (t < rope_angles) {
+      const float ex = 2.f * (float)t / (float)hd;
+      const float theta = (float)pos / powf(base, ex);
+      sn = sinf(theta);
+      cs = cosf(theta);
+    }
+    const size_t orow = at_pos ? (size_t)pos : (size_t)row;
+    float *yv = y + (orow * heads + h) * hd;
+    yv[t] = an * cs - bn * sn;
+    yv[t + half] = bn * cs + an * sn;
+  }
+}
+
+// ---- attention: QK_SHADER + SOFTMAX_SHADER + ATTN_OUT_SHADER ----------------
+// (gpu-runtime.js:1204-1248), split over keys (flash decoding).
+//
+// Block = one wave; it owns `kpw` consecutive keys of one query row for all
+// heads (the k/v rows are shared by every head).  Lane l holds dims
+// [DPL*l, DPL*l + DPL) of q and of the output for each head.  Per key: the
+// H partial dots are reduced across the wave, an online softmax updates the
+// running max / sum per head, and p * v[key] accumulates.  The block writes
+// (max, sum, unnormalised output) per head; attn_combine_kernel merges the
+// splits.  Masked keys (key > qpos, or outside the sliding window) are
+// skipped: the shader gives them logit -1e30, i.e. weight exactly 0.
+constexpr int kMaxHeads = 8;
+
+struct AttnArgs {
+  const float *q;       // [qrows, H, hd]
+  const float *k, *v;   // [keylen, hd] cache rows
+  float *part;          // [qrows, nsplit, H, hd + 2]
+  int H, hd, keylen, qpos0, sliding, window, kpw, nsplit;
+  const int *pos_dev;   // if set: qpos0 = *pos_dev and keylen = *pos_dev + qrows
+  int qrows;
+};
+
+template <int DPL>
+__global__ __launch_bounds__(64) void attn_split_kernel(AttnArgs a) {
+  const int lane = threadIdx.x;
+  const int split = blockIdx.x, qr = blockIdx.y;
+  const int H = a.H, hd = a.hd;
+  const int qpos0 = a.pos_dev ? *a.pos_dev : a.qpos0;
+  const int keylen = a.pos_dev ? *a.pos_dev + a.qrows : a.keylen;
+  const int qpos = qpos0 + qr;
+  if (split * a.kpw >= keylen) return;  // past the keys of this call: not combined
+  int k0 = split * a.kpw, k1 = k0 + a.kpw;
+  if (k1 > keylen) k1 = keylen;
+  if (k1 > qpos + 1) k1 = qpos + 1;                       // key <= qpos
+  if (a.sliding && k0 < qpos - a.window + 1) k0 = qpos - a.window + 1;  // key + window > qpos
+  if (k0 < 0) k0 = 0;
+
+  float q[kMaxHeads][DPL], o[kMaxHeads][DPL], m[kMaxHeads], l[kMaxHeads];
+  const int d0 = lane * DPL;
+  const bool live = d0 < hd;
+#pragma unroll
+  for (int h = 0; h < kMaxHeads; ++h) {
+    m[h] = -1e30f;
+    l[h] = 0.f;
+#pragma unroll
+    for (int j = 0; j < DPL; ++j) {
+      q[h][j] = (h < H && live) ? a.q[((size_t)qr * H + h) * hd + d0 + j] : 0.f;
+      o[h][j] = 0.f;
+    }
+  }
+  for (int key = k0; key < k1; ++key) {
+    float kv[DPL], vv[DPL];
+#pragma unroll
+    for (int j = 0; j < DPL; ++j) {
+      kv[j] = live ? a.k[(size_t)key * hd + d0 + j] : 0.f;
+      vv[j] = live ? a.v[(size_t)key * hd + d0 + j] : 0.f;
+    }
+#pragma unroll
+    for (int h = 0; h < kMaxHeads; ++h) {
+      if (h >= H) break;
+      float s = 0.f;
+#pragma unroll
+      for (int j = 0; j < DPL; ++j) s = fmaf(q[h][j], kv[j], s);
+      s = wave_sum(s);
+      const float mn = fmaxf(m[h], s);
+      const float c = expf(m[h] - mn), p = expf(s - mn);
+      l[h] = l[h] * c + p;
+#pragma unroll
+      for (int j = 0; j < DPL; ++j) o[h][j] = fmaf(p, vv[j], o[h][j] * c);
+      m[h] = mn;
+    }
+  }
+  const size_t stride = (size_t)hd + 2;
+  float *pp = a.part + ((size_t)qr * a.nsplit + split) * H * stride;
+#pragma unroll
+  for (int h = 0; h < kMaxHeads; ++h) {
+    if (h >= H) break;
+    float *ph = pp + h * stride;
+    if (live)
+#pragma unroll
+      for (int j = 0; j < DPL; ++j) ph[2 + d0 + j] = o[h][j];
+    if (lane == 0) {
+      ph[0] = m[h];
+      ph[1] = l[h];
+    }
+  }
+}
+
+// One block per (query row, head): out = sum_s e^(m_s - M) o_s / sum_s e^(m_s - M) l_s.
+__global__ __launch_bounds__(kBlock) void attn_combine_kernel(const float *__restrict__ part,
+                                                              int H, int hd, int kpw,
+                                                              int nsplit, int keylen,
+                                                              const int *__restrict__ pos_dev,
+                                                              int qrows, float *__restrict__ out) {
+  const int qr = blockIdx.x / H, h = blockIdx.x - qr * H;
+  const int kl = pos_dev ? *pos_dev + qrows : keylen;
+  const int ns = (kl + kpw - 1) / kpw < nsplit ? (kl + kpw - 1) / kpw : nsplit;
+  const size_t stride = (size_t)hd + 2;
+  const float *pb = part + ((size_t)qr * nsplit * H + h) * stride;
+  float M = -3.4e38f;
+  for (int s = 0; s < ns; ++s) M = fmaxf(M, pb[(size_t)s * H * stride]);
+  float L = 0.f;
+  for (int s = 0; s < ns; ++s) {
+    const float *ps = pb + (size_t)s * H * stride;
+    L += expf(ps[0] - M) * ps[1];
+  }
+  const float invL = 1.f / L;
+  for (int d = threadIdx.x; d < hd; d += kBlock) {
+    float acc = 0.f;
+    for (int s = 0; s < ns; ++s) {
+      const float *ps = pb + (size_t)s * H * stride;
+      acc += expf(ps[0] - M) * ps[2 + d];
+    }
+    out[((size_t)qr * H + h) * hd + d] = acc * invL;
+  }
+}
+
+// ---- PLE_MIX_SHADER (gpu-runtime.js:1250-1263) ------------------------------
+// One block per (row, layer) chunk of `width` values.
+__global__ __launch_bounds__(kBlock) void ple_mix_kernel(const float *__restrict__ proj,
+                                                         const float *__restrict__ norm_scale,
+                                                         const float *__restrict__ token_ple,
+                                                         int width, float eps, float ple_scale,
+                                                         float out_scale,
+                                                         float *__restrict__ y) {
+  __shared__ float red[4];
+  const size_t base = (size_t)blockIdx.x * width;
+  float ss = 0.f;
+  for (int d = threadIdx.x; d < width; d += kBlock) ss += proj[base + d] * proj[base + d];
+  const float inv = inv_rms(block_sum(ss, red), width, eps);
+  for (int d = threadIdx.x; d < width; d += kBlock) {
+    const float n = proj[base + d] * inv * norm_scale[d];
+    y[base + d] = (n + token_ple[base + d] * ple_scale) * out_scale;
+  }
+}
+
+// ---- embedding rows: bf16Rows(embed_tokens, ids) then ops.scale -------------
+// y[r, i] = float(E[ids[r], i]) * scale.  An id outside [0, vocab) gives a
+// NaN row and touches no table memory.
+__global__ __launch_bounds__(kBlock) void embed_kernel(const uint16_t *__restrict__ E, int vocab,
+                                                       int width, const int *__restrict__ ids,
+                                                       float scale, float *__restrict__ y) {
+  const int r = blockIdx.x;
+  const int id = ids[r];
+  const bool ok = id >= 0 && id < vocab;
+  for (int i = threadIdx.x; i < width; i += kBlock)
+    y[(size_t)r * width + i] =
+        ok ? bf16_to_f32(E[(size_t)id * width + i]) * scale : __int_as_float(0x7fc00000);
+}
+
+int grid1(size_t n, dim3 *g) {
+  const size_t b = (n + kBlock - 1) / kBlock;
+  if (b > 0x7fffffffu) return fail(G4_E_ARG, "element count %zu too large", n);
+  *g = dim3((unsigned)b);
+  return G4_OK;
+}
+
+}  // namespace
+
+// ---- launchers shared with the engine ---------------------------------------
+
+int launch_rms(const float *x, int rows, int width, const float *scale, float eps, float *y,
+               const int *pos_dev) {
+  if (rows == 0) return G4_OK;
+  hipLaunchKernelGGL(rms_kernel, dim3(rows), dim3(kBlock), 0, stream(), x, width, scale, eps, y,
+                     pos_dev);
+  G4_LAUNCH_CHECK("rms_kernel");
+  return G4_OK;
+}
+
+int launch_add_scale(const float *a, const float *b, size_t n, float s, float *y) {
+  if (n == 0) return G4_OK;
+  dim3 g;
+  if (int rc = grid1(n, &g)) return rc;
+  hipLaunchKernelGGL(add_scale_kernel, g, dim3(kBlock), 0, stream(), a, b, n, s, y);
+  G4_LAUNCH_CHECK("add_scale_kernel");
+  return G4_OK;
+}
+
+int launch_scale(const float *a, size_t n, float s, float *y) {
+  if (n == 0) return G4_OK;
+  dim3 g;
+  if (int rc = grid1(n, &g)) return rc;
+  hipLaunchKernelGGL(scale_kernel, g, dim3(kBlock), 0, stream(), a, n, s, y);
+  G4_LAUNCH_CHECK("scale_kernel");
+  return G4_OK;
+}
+
+int launch_gelu_mul(const float *gate, const float *up, size_t n, float *y) {
+  if (n == 0) return G4_OK;
+  dim3 g;
+  if (int rc = grid1(n, &g)) return rc;
+  hipLaunchKernelGGL(gelu_mul_kernel, g, dim3(kBlock), 0, stream(), gate, up, n, y);
+  G4_LAUNCH_CHECK("gelu_mul_kernel");
+  return G4_OK;
+}
+
+int launch_gelu_ple(const float *gate, const float *ple, int rows, int layer, int width,
+                    int layers, float *y) {
+  if (rows == 0) return G4_OK;
+  dim3 g;
+  if (int rc = grid1((size_t)rows * width, &g)) return rc;
+  hipLaunchKernelGGL(gelu_ple_kernel, g, dim3(kBlock), 0, stream(), gate, ple, rows, layer,
+                     width, layers, y);
+  G4_LAUNCH_CHECK("gelu_ple_kernel");
+  return G4_OK;
+}
+
+int launch_norm_rope(const float *x, int rows, int heads, int hd, int pos0, const int *pos_dev,
+                     const float *scale, int rope_angles, float base, float eps, float *y,
+                     bool at_pos) {
+  if (rows == 0) return G4_OK;
+  hipLaunchKernelGGL(norm_rope_kernel, dim3(rows * heads), dim3(kBlock), 0, stream(), x, heads,
+                     hd, pos0, pos_dev, scale, rope_angles, base, eps, y, (int)at_pos);
+  G4_LAUNCH_CHECK("norm_rope_kernel");
+  return G4_OK;
+}
+
+size_t attention_part_floats(int qrows, int heads, int hd, int max_keylen, int kpw) {
+  const int nsplit = (max_keylen + kpw - 1) / kpw;
+  return (size_t)qrows * nsplit * heads * ((size_t)hd + 2);
+}
+
+int launch_attention(const float *q, const float *k, const float *v, int qrows, int heads,
+                     int hd, int keylen, int qpos0, const int *pos_dev, int max_keylen,
+                     bool sliding, int window, int kpw, float *part, float *out) {
+  if (qrows == 0) return G4_OK;
+  AttnArgs a;
+  a.q = q;
+  a.k = k;
+  a.v = v;
+  a.part = part;
+  a.H = heads;
+  a.hd = hd;
+  a.keylen = keylen;
+  a.qpos0 = qpos0;
+  a.sliding = sliding ? 1 : 0;
+  a.window = window;
+  a.kpw = kpw;
+  a.nsplit = (max_keylen + kpw - 1) / kpw;
+  a.pos_dev = pos_dev;
+  a.qrows = qrows;
+  const dim3 grid(a.nsplit, qrows);
+  switch (hd / 64) {
+    case 1: hipLaunchKernelGGL(attn_split_kernel<1>, grid, dim3(64), 0, stream(), a); break;
+    case 2: hipLaunchKernelGGL(attn_split_kernel<2>, grid, dim3(64), 0, stream(), a); break;
+    case 4: hipLaunchKernelGGL(attn_split_kernel<4>, grid, dim3(64), 0, stream(), a); break;
+    case 8: hipLaunchKernelGGL(attn_split_kernel<8>, grid, dim3(64), 0, stream(), a); break;
+    default: return fail(G4_E_ARG, "attention: head_dim %d must be 64, 128, 256 or 512", hd);
+  }
+  G4_LAUNCH_CHECK("attn_split_kernel");
+  hipLaunchKernelGGL(attn_combine_kernel, dim3(qrows * heads), dim3(kBlock), 0, stream(), part,
+                     heads, hd, kpw, a.nsplit, keylen, pos_dev, qrows, out);
+  G4_LAUNCH_CHECK("attn_combine_kernel");
+  return G4_OK;
+}
+
+int launch_ple_mix(const float *proj, const float *norm_scale, const float *token_ple, int rows,
+                   int width, int layers, float eps, float ple_scale, float out_scale,
+                   float *y) {
+  if (rows == 0) return G4_OK;
+  hipLaunchKernelGGL(ple_mix_kernel, dim3(rows * layers), dim3(kBlock), 0, stream(), proj,
+                     norm_scale, token_ple, width, eps, ple_scale, out_scale, y);
+  G4_LAUNCH_CHECK("ple_mix_kernel");
+  return G4_OK;
+}
+
+int launch_embed(const uint16_t *E, int vocab, int width, const int *ids_dev, int n, float scale,
+                 float *y) {
+  if (n == 0) return G4_OK;
+  hipLaunchKernelGGL(embed_kernel, dim3(n), dim3(kBlock), 0, stream(), E, vocab, width, ids_dev,
+                     scale, y);
+  G4_LAUNCH_CHECK("embed_kernel");
+  return G4_OK;
+}
+
+}  // namespace g4
+
+// ---- C ABI ---------------------------------------------------------------------
+
+namespace {
+using namespace g4;
+
+Workspace g_attn_ws, g_argmax_ws;
+
+int check_f32(const float *p, size_t n, const char *what) {
+  return check_device_range(p, n * 4, what);
+}
+
+// Keys per split of the attention kernel: a few for decode (many small
+// blocks), more when many query rows already fill the GPU.
+int attn_kpw(int qrows) { return qrows <= 4 ? 4 : 32; }
+
+}  // namespace
+
+G4_API int g4_rms(const float *x, int rows, int width, const float *scale, float eps, float *y) {
+  G4_CHECK_INIT();
+  if (rows < 0 || width <= 0) return fail(G4_E_ARG, "g4_rms: rows %d, width %d", rows, width);
+  if (rows == 0) return ok();
+  const size_t n = (size_t)rows * width;
+  int rc = check_f32(x, n, "g4_rms x");
+  if (!rc && scale) rc = check_f32(scale, width, "g4_rms scale");
+  if (!rc) rc = check_f32(y, n, "g4_rms y");
+  if (!rc) rc = launch_rms(x, rows, width, scale, eps, y, nullptr);
+  return rc ? rc : ok();
+}
+
+G4_API int g4_add_scale(const float *a, const float *b, size_t n, float scale, float *y) {
+  G4_CHECK_INIT();
+  if (n == 0) return ok();
+  int rc = check_f32(a, n, "g4_add_scale a");
+  if (!rc) rc = check_f32(b, n, "g4_add_scale b");
+  if (!rc) rc = check_f32(y, n, "g4_add_scale y");
+  if (!rc) rc = launch_add_scale(a, b, n, scale, y);
+  return rc ? rc : ok();
+}
+
+G4_API int g4_scale(const float *a, size_t n, float scale, float *y) {
+  G4_CHECK_INIT();
+  if (n == 0) return ok();
+  int rc = check_f32(a, n, "g4_scale a");
+  if (!rc) rc = check_f32(y, n, "g4_scale y");
+  if (!rc) rc = launch_scale(a, n, scale, y);
+  return rc ? rc : ok();
+}
+
+G4_API int g4_gelu_mul(const float *gate, const float *up, size_t n, float *y) {
+  G4_CHECK_INIT();
+  if (n == 0) return ok();
+  int rc = check_f32(gate, n, "g4_gelu_mul gate");
+  if (!rc) rc = check_f32(up, n, "g4_gelu_mul up");
+  if (!rc) rc = check_f32(y, n, "g4_gelu_mul y");
+  if (!rc) rc = launch_gelu_mul(gate, up, n, y);
+  return rc ? rc : ok();
+}
+
+G4_API int g4_gelu_ple(const float *gate, const float *ple, int rows, int layer, int width,
+                       int layers, float *y) {
+  G4_CHECK_INIT();
+  if (rows < 0 || width <= 0 || layers <= 0 || layer < 0 || layer >= layers)
+    return fail(G4_E_ARG, "g4_gelu_ple: rows %d, layer %d of %d, width %d", rows, layer, layers,
+                width);
+  if (rows == 0) return ok();
+  const size_t n = (size_t)rows * width;
+  int rc = check_f32(gate, n, "g4_gelu_ple gate");
+  if (!rc) rc = check_f32(ple, n * layers, "g4_gelu_ple ple");
+  if (!rc) rc = check_f32(y, n, "g4_gelu_ple y");
+  if (!rc) rc = launch_gelu_ple(gate, ple, rows, layer, width, layers, y);
+  return rc ? rc : ok();
+}
+
+G4_API int g4_norm_rope(const float *x, int rows, int heads, int head_dim, int pos0,
+                        const float *scale, int rope_angles, float base, float eps, float *y) {
+  G4_CHECK_INIT();
+  if (rows < 0 || heads <= 0 || head_dim <= 0 || head_dim % 2 != 0 || head_dim > 512 ||
+      pos0 < 0 || rope_angles < 0 || rope_angles > head_dim / 2)
+    return fail(G4_E_ARG,
+                "g4_norm_rope: rows %d, heads %d, head_dim %d (even, <= 512), pos0 %d, "
+                "rope_angles %d",
+                rows, heads, head_dim, pos0, rope_angles);
+  if (rows == 0) return ok();
+  const size_t n = (size_t)rows * heads * head_dim;
+  int rc = check_f32(x, n, "g4_norm_rope x");
+  if (!rc) rc = check_f32(scale, head_dim, "g4_norm_rope scale");
+  if (!rc) rc = check_f32(y, n, "g4_norm_rope y");
+  if (!rc)
+    rc = launch_norm_rope(x, rows, heads, head_dim, pos0, nullptr, scale, rope_angles, base, eps,
+                          y, false);
+  return rc ? rc : ok();
+}
+
+G4_API int g4_attention(const float *q, const float *k, const float *v, int qrows, int heads,
+                        int head_dim, int keylen, int qpos0, int sliding, int window, float *y) {
+  G4_CHECK_INIT();
+  if (qrows < 0 || heads <= 0 || heads > 8 ||
+      (head_dim != 64 && head_dim != 128 && head_dim != 256 && head_dim != 512))
+    return fail(G4_E_ARG, "g4_attention: qrows %d, heads %d (<= 8), head_dim %d (64..512)",
+                qrows, heads, head_dim);
+  if (qrows == 0) return ok();
+  if (qpos0 < 0 || keylen < qpos0 + qrows || (sliding && window <= 0))
+    return fail(G4_E_ARG,
+                "g4_attention: keylen %d must cover query positions %d..%d (window %d)", keylen,
+                qpos0, qpos0 + qrows - 1, window);
+  const size_t qn = (size_t)qrows * heads * head_dim;
+  int rc = check_f32(q, qn, "g4_attention q");
+  if (!rc) rc = check_f32(k, (size_t)keylen * head_dim, "g4_attention k");
+  if (!rc) rc = check_f32(v, (size_t)keylen * head_dim, "g4_attention v");
+  if (!rc) rc = check_f32(y, qn, "g4_attention y");
+  if (rc) return rc;
+  const int kpw = attn_kpw(qrows);
+  void *part = nullptr;
+  rc = g_attn_ws.get(attention_part_floats(qrows, heads, head_dim, keylen, kpw) * 4, &part,
+                     "g4_attention");
+  if (!rc)
+    rc = launch_attention(q, k, v, qrows, heads, head_dim, keylen, qpos0, nullptr, keylen,
+                          sliding != 0, window, kpw, static_cast<float *>(part), y);
+  return rc ? rc : ok();
+}
+
+G4_API int g4_ple_mix(const float *proj, const float *norm_scale, const float *token_ple,
+                      int rows, int width, int layers, float *y) {
+  G4_CHECK_INIT();
+  if (rows < 0 || width <= 0 || layers <= 0)
+    return fail(G4_E_ARG, "g4_ple_mix: rows %d, width %d, layers %d", rows, width, layers);
+  if (rows == 0) return ok();
+  const size_t n = (size_t)rows * layers * width;
+  int rc = check_f32(proj, n, "g4_ple_mix proj");
+  if (!rc) rc = check_f32(norm_scale, width, "g4_ple_mix norm_scale");
+  if (!rc) rc = check_f32(token_ple, n, "g4_ple_mix token_ple");
+  if (!rc) rc = check_f32(y, n, "g4_ple_mix y");
+  // PLE_MIX_SHADER constants: eps 1e-6, token rows * 16 (= sqrt(256)), * 1/sqrt(2)
+  if (!rc)
+    rc = launch_ple_mix(proj, norm_scale, token_ple, rows, width, layers, 1e-6f, 16.f,
+                        0.7071067811865476f, y);
+  return rc ? rc : ok();
+}
+
+G4_API int g4_embed(const void *E, int vocab, int width, const int32_t *ids_dev, int n,
+                    float scale, float *y) {
+  G4_CHECK_INIT();
+  if (vocab <= 0 || width <= 0 || n < 0)
+    return fail(G4_E_ARG, "g4_embed: vocab %d, width %d, n %d", vocab, width, n);
+  if (n == 0) return ok();
+  int rc = check_device_range(E, (size_t)vocab * width * 2, "g4_embed E");
+  if (!rc) rc = check_device_range(ids_dev, (size_t)n * 4, "g4_embed ids");
+  if (!rc) rc = check_f32(y, (size_t)n * width, "g4_embed y");
+  if (!rc)
+    rc = launch_embed(static_cast<const uint16_t *>(E), vocab, width, ids_dev, n, scale, y);
+  return rc ? rc : ok();
+}
+
+G4_API int g4_argmax(const float *x, int n, int32_t *out_dev) {
+  G4_CHECK_INIT();
+  if (n <= 0) return fail(G4_E_ARG, "g4_argmax: n %d", n);
+  int rc = check_f32(x, n, "g4_argmax x");
+  if (!rc) rc = check_device_range(out_dev, 4, "g4_argmax out");
+  void *part = nullptr;
+  if (!rc) rc = g_argmax_ws.get(argmax_blocks(n) * sizeof(float2), &part, "g4_argmax");
+  if (!rc) rc = launch_argmax(x, n, static_cast<float2 *>(part), out_dev);
+  return rc ? rc : ok();
+}

@@ -183,6 +183,28 @@ G4_API int g4_ple_upload_shard(g4_ple *t, int shard, const void *bytes, size_t n
   return ok();
 }
 
+namespace g4 {
+void ple_geometry(const g4_ple *t, int *vocab, int *width) {
+  *vocab = t->vocab;
+  *width = t->width;
+}
+}  // namespace g4
+
+G4_API int g4_ple_upload_shard_dev(g4_ple *t, int shard, const void *bytes_dev, size_t n) {
+  G4_CHECK_INIT();
+  G4_CHECK_NOT_ENCODING();
+  size_t want = 0;
+  int rc = g4_ple_shard_bytes(t, shard, nullptr, &want);
+  if (rc) return rc;
+  if (n != want)
+    return fail(G4_E_ARG, "PLE shard %d has %zu bytes, expected %zu", shard, n, want);
+  rc = check_device_range(bytes_dev, n, "g4_ple_upload_shard_dev bytes");
+  if (rc) return rc;
+  G4_HIP_TRY(hipMemcpyAsync(t->table + (size_t)shard * t->full_shard_bytes, bytes_dev, n,
+                            hipMemcpyDeviceToDevice, stream()));
+  return ok();
+}
+
 G4_API int g4_ple_free(g4_ple *t) {
   G4_CHECK_INIT();
   G4_CHECK_NOT_ENCODING();

@@ -22,10 +22,45 @@ bool g_encoding = false;
 int g_device = -1;
 int g_cu_count = 0;
 
-// Live device allocations: base -> size.  Used to bounds-check operands
-// before a kernel is launched.
+// Live device allocations: base -> requested size (align4).  Used to
+// bounds-check operands before a kernel is launched.
 std::mutex g_mu;
 std::map<uintptr_t, size_t> g_allocs;
+
+// Caching allocator.  The reference creates a buffer per op output and
+// destroys it right after submit (gemma4-webgpu.js:216-301, 357-381); doing a
+// hipMalloc/hipFree per op would serialise the queue.  Because every use of
+// device memory is ordered on the one library stream, a block freed after its
+// last use was enqueued can serve a later allocation at once: the stream runs
+// the old reader before the new writer.  Blocks are kept per capacity class.
+std::map<uintptr_t, size_t> g_capacity;    // live and cached block -> capacity
+std::multimap<size_t, void *> g_free;      // capacity -> cached block
+size_t g_cached_bytes = 0;
+constexpr size_t kCacheLimit = size_t(16) << 30;
+
+size_t capacity_class(size_t n) {
+  if (n <= (size_t(64) << 10)) {
+    size_t c = 256;
+    while (c < n) c <<= 1;
+    return c;
+  }
+  const size_t g = size_t(64) << 10;
+  return (n + g - 1) / g * g;
+}
+
+// Gives every cached block back to HIP (after the stream is idle).
+int release_cache_locked() {
+  if (g_free.empty()) return G4_OK;
+  hipError_t e = hipStreamSynchronize(g_stream);
+  if (e != hipSuccess) return fail(G4_E_HIP, "hipStreamSynchronize: %s", hipGetErrorString(e));
+  for (auto &kv : g_free) {
+    g_capacity.erase(reinterpret_cast<uintptr_t>(kv.second));
+    (void)hipFree(kv.second);
+  }
+  g_free.clear();
+  g_cached_bytes = 0;
+  return G4_OK;
+}
 
 }  // namespace
 
@@ -63,6 +98,12 @@ int check_device_range(const void *p, size_t bytes, const char *what) {
         return G4_OK;
       }
     }
+    auto ct = g_capacity.upper_bound(a);
+    if (ct != g_capacity.begin()) {
+      --ct;
+      if (a < ct->first + ct->second)
+        return fail(G4_E_STATE, "%s: %p points into a buffer that was freed", what, p);
+    }
   }
   // Not one of ours: ask the HIP runtime for the allocation's extent.
   hipDeviceptr_t base = nullptr;
@@ -82,15 +123,40 @@ int check_device_range(const void *p, size_t bytes, const char *what) {
 int device_alloc(size_t bytes, void **p) {
   if (!p) return fail(G4_E_ARG, "device_alloc: null output pointer");
   size_t n = bytes < 4 ? 4 : (bytes + 3) & ~size_t(3);  // align4 (gpu-runtime.js:7)
+  const size_t cap = capacity_class(n);
   void *d = nullptr;
-  hipError_t e = hipMalloc(&d, n);
-  if (e != hipSuccess) {
-    (void)hipGetLastError();
-    return fail(G4_E_NOMEM, "hipMalloc(%zu) failed: %s", n, hipGetErrorString(e));
+  {
+    std::lock_guard<std::mutex> lk(g_mu);
+    auto it = g_free.find(cap);
+    if (it != g_free.end()) {
+      d = it->second;
+      g_free.erase(it);
+      g_cached_bytes -= cap;
+    }
   }
-  e = hipMemsetAsync(d, 0, n, g_stream);
+  if (!d) {
+    hipError_t e = hipMalloc(&d, cap);
+    if (e != hipSuccess) {
+      (void)hipGetLastError();
+      // retry once with the cache given back
+      std::lock_guard<std::mutex> lk(g_mu);
+      int rc = release_cache_locked();
+      if (rc) return rc;
+      e = hipMalloc(&d, cap);
+      if (e != hipSuccess) {
+        (void)hipGetLastError();
+        return fail(G4_E_NOMEM, "hipMalloc(%zu) failed: %s", cap, hipGetErrorString(e));
+      }
+    }
+    std::lock_guard<std::mutex> lk(g_mu);
+    g_capacity[reinterpret_cast<uintptr_t>(d)] = cap;
+  }
+  // WebGPU buffers start zeroed; stream-ordered after any earlier user.
+  hipError_t e = hipMemsetAsync(d, 0, n, g_stream);
   if (e != hipSuccess) {
-    (void)hipFree(d);
+    std::lock_guard<std::mutex> lk(g_mu);
+    g_free.emplace(cap, d);
+    g_cached_bytes += cap;
     return fail(G4_E_HIP, "hipMemsetAsync failed: %s", hipGetErrorString(e));
   }
   {
@@ -103,17 +169,40 @@ int device_alloc(size_t bytes, void **p) {
 
 int device_free(void *p) {
   if (!p) return G4_OK;
-  {
-    std::lock_guard<std::mutex> lk(g_mu);
-    auto it = g_allocs.find(reinterpret_cast<uintptr_t>(p));
-    if (it == g_allocs.end())
-      return fail(G4_E_ARG, "g4_free: %p was not allocated by g4_alloc", p);
-    g_allocs.erase(it);
+  std::lock_guard<std::mutex> lk(g_mu);
+  auto it = g_allocs.find(reinterpret_cast<uintptr_t>(p));
+  if (it == g_allocs.end())
+    return fail(G4_E_ARG, "g4_free: %p was not allocated by g4_alloc", p);
+  g_allocs.erase(it);
+  // Stream-ordered reuse: work already queued that reads the block runs
+  // before any later writer (WebGPU's destroy() likewise waits for submitted
+  // work).  Past the cache limit the cached blocks go back to HIP.
+  const size_t cap = g_capacity[reinterpret_cast<uintptr_t>(p)];
+  g_free.emplace(cap, p);
+  g_cached_bytes += cap;
+  if (g_cached_bytes > kCacheLimit) return release_cache_locked();
+  return G4_OK;
+}
+
+int Workspace::get(size_t need, void **p, const char *who) {
+  if (need <= bytes) {
+    *p = mem;
+    return G4_OK;
   }
-  // Work already queued may still read the buffer: drain the queue first
-  // (WebGPU's destroy() is likewise deferred until submitted work is done).
-  G4_HIP_TRY(hipStreamSynchronize(g_stream));
-  G4_HIP_TRY(hipFree(p));
+  if (g_encoding)
+    return fail(G4_E_STATE,
+                "%s: scratch must grow to %zu bytes; make one call of this size outside a "
+                "command encoder first", who, need);
+  if (mem) {
+    int rc = device_free(mem);
+    if (rc) return rc;
+    mem = nullptr;
+    bytes = 0;
+  }
+  int rc = device_alloc(need, &mem);
+  if (rc) return rc;
+  bytes = need;
+  *p = mem;
   return G4_OK;
 }
 

@@ -600,6 +600,95 @@ G4_API int g4_w4_load(const void *packed, const void *scales, int out_dim,
   return ok();
 }
 
+namespace {
+
+// Largest finite |scale| as bf16 magnitude bits, one block.
+__global__ __launch_bounds__(1024) void scale_maxbits_kernel(const uint16_t *__restrict__ s,
+                                                             size_t n, uint32_t *__restrict__ out) {
+  __shared__ uint32_t red[16];
+  uint32_t m = 0;
+  for (size_t i = threadIdx.x; i < n; i += 1024) {
+    const uint32_t a = s[i] & 0x7fffu;
+    if (a < 0x7f80u && a > m) m = a;
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const uint32_t v = __shfl_xor(m, o, 64);
+    m = v > m ? v : m;
+  }
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int i = 1; i < 16; ++i) m = red[i] > m ? red[i] : m;
+    *out = m;
+  }
+}
+
+}  // namespace
+
+G4_API int g4_w4_load_dev(const void *packed_dev, const void *scales_dev, int out_dim,
+                          int in_dim, int group, g4_w4 **out) {
+  G4_CHECK_INIT();
+  G4_CHECK_NOT_ENCODING();
+  if (!out) return fail(G4_E_ARG, "g4_w4_load_dev: null output handle");
+  *out = nullptr;
+  if (out_dim <= 0 || in_dim <= 0)
+    return fail(G4_E_ARG, "g4_w4_load_dev: bad shape [%d, %d]", out_dim, in_dim);
+  if (in_dim % 8 != 0) return fail(G4_E_ARG, "inDim must be divisible by 8.");
+  if (group <= 0 || in_dim % group != 0)
+    return fail(G4_E_ARG, "inDim must be divisible by groupSize.");
+  if (group != 32)
+    return fail(G4_E_ARG, "g4_w4_load_dev: group size %d unsupported (the checkpoint uses 32)",
+                group);
+  const int G = in_dim / 32;
+  const size_t qbytes = (size_t)out_dim * in_dim / 2;
+  const size_t sbytes = (size_t)out_dim * G * 2;
+  int rc = check_device_range(packed_dev, qbytes, "g4_w4_load_dev packed");
+  if (!rc) rc = check_device_range(scales_dev, sbytes, "g4_w4_load_dev scales");
+  if (rc) return rc;
+  g4_w4 *w = new g4_w4();
+  w->N = out_dim;
+  w->K = in_dim;
+  w->group = group;
+  w->G = G;
+  const size_t soff = (qbytes + 255) & ~size_t(255);
+  rc = device_alloc(soff + sbytes + 256, reinterpret_cast<void **>(&w->mem));
+  if (rc) {
+    delete w;
+    return rc;
+  }
+  w->packed = reinterpret_cast<uint4 *>(w->mem);
+  w->scales = reinterpret_cast<uint16_t *>(w->mem + soff);
+  w->bytes = soff + sbytes;
+  uint32_t *maxbits_dev = reinterpret_cast<uint32_t *>(w->mem + ((soff + sbytes + 255) & ~size_t(255)));
+  uint32_t maxbits = 0;
+  hipError_t e = hipMemcpyAsync(w->packed, packed_dev, qbytes, hipMemcpyDeviceToDevice, stream());
+  if (e == hipSuccess)
+    e = hipMemcpyAsync(w->scales, scales_dev, sbytes, hipMemcpyDeviceToDevice, stream());
+  if (e == hipSuccess) {
+    hipLaunchKernelGGL(scale_maxbits_kernel, dim3(1), dim3(1024), 0, stream(), w->scales,
+                       (size_t)out_dim * G, maxbits_dev);
+    e = hipGetLastError();
+  }
+  if (e == hipSuccess)
+    e = hipMemcpyAsync(&maxbits, maxbits_dev, 4, hipMemcpyDeviceToHost, stream());
+  if (e == hipSuccess) e = hipStreamSynchronize(stream());
+  if (e != hipSuccess) {
+    device_free(w->mem);
+    delete w;
+    return fail(G4_E_HIP, "g4_w4_load_dev: copy failed: %s", hipGetErrorString(e));
+  }
+  int shift = 0;  // the same rule as g4_w4_load
+  if (maxbits) {
+    shift = 11 - ((int)(maxbits >> 7) - 127);
+    if (shift > 60) shift = 60;
+    if (shift < -60) shift = -60;
+  }
+  w->shift = shift;
+  *out = w;
+  return ok();
+}
+
 G4_API int g4_w4_free(g4_w4 *w) {
   G4_CHECK_INIT();
   G4_CHECK_NOT_ENCODING();

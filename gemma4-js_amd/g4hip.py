@@ -59,7 +59,52 @@ SIGNATURES = {
     "g4_ple_gather": (_int, [_vp, _vp, _int, _vp, _int]),
     "g4_ple_gather_dev": (_int, [_vp, _vp, _int, _vp, _int]),
     "g4_bf16_head": (_int, [_vp, _vp, _int, _int, _vp, _c.c_float, _c.c_float]),
+    "g4_rms": (_int, [_vp, _int, _int, _vp, _c.c_float, _vp]),
+    "g4_add_scale": (_int, [_vp, _vp, _sz, _c.c_float, _vp]),
+    "g4_scale": (_int, [_vp, _sz, _c.c_float, _vp]),
+    "g4_gelu_mul": (_int, [_vp, _vp, _sz, _vp]),
+    "g4_gelu_ple": (_int, [_vp, _vp, _int, _int, _int, _int, _vp]),
+    "g4_norm_rope": (_int, [_vp, _int, _int, _int, _int, _vp, _int, _c.c_float, _c.c_float, _vp]),
+    "g4_attention": (_int, [_vp, _vp, _vp, _int, _int, _int, _int, _int, _int, _int, _vp]),
+    "g4_ple_mix": (_int, [_vp, _vp, _vp, _int, _int, _int, _vp]),
+    "g4_embed": (_int, [_vp, _int, _int, _vp, _int, _c.c_float, _vp]),
+    "g4_argmax": (_int, [_vp, _int, _vp]),
+    "g4_w4_load_dev": (_int, [_vp, _vp, _int, _int, _int, _c.POINTER(_vp)]),
+    "g4_ple_upload_shard_dev": (_int, [_vp, _int, _vp, _sz]),
+    "g4_fill_random": (_int, [_vp, _sz, _int, _c.c_uint64, _c.c_float]),
+    "g4_gemma_e2b_config": (_int, [_int, _vp]),
+    "g4_gemma_create": (_int, [_vp, _c.POINTER(_vp)]),
+    "g4_gemma_free": (_int, [_vp]),
+    "g4_gemma_set_linear": (_int, [_vp, _int, _int, _vp]),
+    "g4_gemma_set_norm": (_int, [_vp, _int, _int, _vp, _int]),
+    "g4_gemma_set_layer_scalar": (_int, [_vp, _int, _c.c_float]),
+    "g4_gemma_set_embedding": (_int, [_vp, _vp]),
+    "g4_gemma_set_ple": (_int, [_vp, _vp]),
+    "g4_gemma_reset": (_int, [_vp]),
+    "g4_gemma_cache_length": (_int, [_vp, _c.POINTER(_int)]),
+    "g4_gemma_forward": (_int, [_vp, _vp, _int, _int, _vp]),
+    "g4_gemma_logits": (_int, [_vp, _vp, _vp]),
+    "g4_gemma_greedy": (_int, [_vp, _vp, _int, _int, _c.POINTER(_c.c_int32), _vp]),
+    "g4_gemma_decode": (_int, [_vp, _int, _vp]),
 }
+
+# g4_fill_random kinds
+RAND_W4_PACKED, RAND_PLE_PACKED, RAND_BF16_ABS_NORMAL, RAND_BF16_NORMAL, RAND_F32_NORMAL = range(5)
+# g4_gemma projections and norms
+PROJ = dict(q=0, k=1, v=2, o=3, gate=4, up=5, down=6, ple_gate=7, ple_proj=8, top=9)
+NORM = dict(input=0, post_attn=1, pre_ffw=2, post_ffw=3, post_ple=4, q=5, k=6,
+            ple_projection=7, final=8)
+GEMMA_MAX_LAYERS = 64
+
+
+class GemmaConfig(_c.Structure):
+    _fields_ = [("hidden", _int), ("heads", _int), ("ple_dim", _int), ("vocab", _int),
+                ("layers", _int), ("max_seq", _int), ("window", _int), ("eps", _c.c_float),
+                ("softcap", _c.c_float),
+                ("head_dim", _int * GEMMA_MAX_LAYERS), ("intermediate", _int * GEMMA_MAX_LAYERS),
+                ("full", _int * GEMMA_MAX_LAYERS), ("kv_source", _int * GEMMA_MAX_LAYERS),
+                ("rope_base", _c.c_float * GEMMA_MAX_LAYERS),
+                ("rope_prop", _c.c_float * GEMMA_MAX_LAYERS)]
 
 
 class G4Error(RuntimeError):
@@ -231,6 +276,12 @@ class W4Linear:
                                self.in_dim, group, ctypes.byref(h)))
         self.h = h.value
 
+    @classmethod
+    def _from_handle(cls, h, out_dim, in_dim, group=32):
+        self = cls.__new__(cls)
+        self.h, self.out_dim, self.in_dim, self.group = h, out_dim, in_dim, group
+        return self
+
     def info(self):
         n, k, g, b = _int(), _int(), _int(), _sz()
         check(lib().g4_w4_info(self.h, ctypes.byref(n), ctypes.byref(k), ctypes.byref(g),
@@ -300,6 +351,146 @@ class PleTable:
 
 def bf16_head(x_ptr, E_ptr, rows, in_dim, out_ptr, scale=1.0, softcap=30.0):
     check(lib().g4_bf16_head(x_ptr, E_ptr, rows, in_dim, out_ptr, scale, softcap))
+
+
+def _f(p):
+    return p if p is None or isinstance(p, int) else p.ptr
+
+
+def rms(x, rows, width, scale, y, eps=1e-6):
+    check(lib().g4_rms(_f(x), rows, width, _f(scale), eps, _f(y)))
+
+
+def add_scale(a, b, n, s, y):
+    check(lib().g4_add_scale(_f(a), _f(b), n, s, _f(y)))
+
+
+def scale(a, n, s, y):
+    check(lib().g4_scale(_f(a), n, s, _f(y)))
+
+
+def gelu_mul(gate, up, n, y):
+    check(lib().g4_gelu_mul(_f(gate), _f(up), n, _f(y)))
+
+
+def gelu_ple(gate, ple, rows, layer, width, layers, y):
+    check(lib().g4_gelu_ple(_f(gate), _f(ple), rows, layer, width, layers, _f(y)))
+
+
+def norm_rope(x, rows, heads, hd, pos0, scale_, rope_angles, base, y, eps=1e-6):
+    check(lib().g4_norm_rope(_f(x), rows, heads, hd, pos0, _f(scale_), rope_angles, base, eps,
+                             _f(y)))
+
+
+def attention(q, k, v, qrows, heads, hd, keylen, qpos0, sliding, window, y):
+    check(lib().g4_attention(_f(q), _f(k), _f(v), qrows, heads, hd, keylen, qpos0,
+                             1 if sliding else 0, window, _f(y)))
+
+
+def ple_mix(proj, norm_scale, token_ple, rows, width, layers, y):
+    check(lib().g4_ple_mix(_f(proj), _f(norm_scale), _f(token_ple), rows, width, layers, _f(y)))
+
+
+def embed(E, vocab, width, ids, n, s, y):
+    check(lib().g4_embed(_f(E), vocab, width, _f(ids), n, s, _f(y)))
+
+
+def argmax(x, n, out):
+    check(lib().g4_argmax(_f(x), n, _f(out)))
+
+
+def fill_random(buf, count, kind, seed, sigma=1.0):
+    check(lib().g4_fill_random(_f(buf), count, kind, seed, sigma))
+
+
+def w4_random(n, k, seed, scale_sigma=0.02):
+    """A W4Linear of random weights generated on the device (config-style
+    distributions: q uniform in [-7, 7], scales bf16 |N(0,1)| * sigma)."""
+    packed = Buffer(n * k // 2)
+    scales = Buffer(n * (k // 32) * 2)
+    fill_random(packed, n * k // 8, RAND_W4_PACKED, seed)
+    fill_random(scales, n * (k // 32), RAND_BF16_ABS_NORMAL, seed ^ 0x5CA1E, scale_sigma)
+    h = _vp()
+    check(lib().g4_w4_load_dev(packed.ptr, scales.ptr, n, k, 32, ctypes.byref(h)))
+    packed.free()
+    scales.free()
+    return W4Linear._from_handle(h.value, n, k)
+
+
+def e2b_config(max_seq):
+    c = GemmaConfig()
+    check(lib().g4_gemma_e2b_config(max_seq, ctypes.byref(c)))
+    return c
+
+
+class Gemma:
+    """Gemma4WebGPU on the device engine (g4_gemma_*)."""
+
+    def __init__(self, cfg):
+        h = _vp()
+        check(lib().g4_gemma_create(ctypes.byref(cfg), ctypes.byref(h)))
+        self.h = h.value
+        self.cfg = cfg
+        self._keep = []  # borrowed handles must outlive the model
+
+    def set_linear(self, layer, which, w):
+        check(lib().g4_gemma_set_linear(self.h, layer, PROJ[which], w.h))
+        self._keep.append(w)
+
+    def set_norm(self, layer, which, v):
+        v = np.ascontiguousarray(v, dtype=np.float32)
+        check(lib().g4_gemma_set_norm(self.h, layer, NORM[which], v.ctypes.data, v.size))
+
+    def set_layer_scalar(self, layer, s):
+        check(lib().g4_gemma_set_layer_scalar(self.h, layer, s))
+
+    def set_embedding(self, E):
+        check(lib().g4_gemma_set_embedding(self.h, _f(E)))
+        self._keep.append(E)
+
+    def set_ple(self, t):
+        check(lib().g4_gemma_set_ple(self.h, t.h))
+        self._keep.append(t)
+
+    def reset(self):
+        check(lib().g4_gemma_reset(self.h))
+
+    def cache_length(self):
+        n = _int()
+        check(lib().g4_gemma_cache_length(self.h, ctypes.byref(n)))
+        return n.value
+
+    def forward(self, ids, start_pos, last_hidden=None):
+        ids = np.ascontiguousarray(ids, dtype=np.int32)
+        check(lib().g4_gemma_forward(self.h, ids.ctypes.data, ids.size, start_pos,
+                                     _f(last_hidden)))
+
+    def logits(self, last_hidden, out):
+        check(lib().g4_gemma_logits(self.h, _f(last_hidden), _f(out)))
+
+    def greedy(self, ids, start_pos, logits=None):
+        ids = np.ascontiguousarray(ids, dtype=np.int32)
+        tok = ctypes.c_int32()
+        check(lib().g4_gemma_greedy(self.h, ids.ctypes.data, ids.size, start_pos,
+                                    ctypes.byref(tok), _f(logits)))
+        return tok.value
+
+    def decode(self, steps, want_tokens=True):
+        out = np.zeros(max(steps, 1), dtype=np.int32)
+        check(lib().g4_gemma_decode(self.h, steps, out.ctypes.data if want_tokens else None))
+        return out[:steps] if want_tokens else None
+
+    def free(self):
+        if self.h:
+            check(lib().g4_gemma_free(self.h))
+            self.h = None
+
+    def __del__(self):
+        try:
+            if self.h and _lib is not None:
+                _lib.g4_gemma_free(self.h)
+        except Exception:
+            pass
 
 
 def exported_symbols():

@@ -126,6 +126,11 @@ typedef struct g4_w4 g4_w4;
 int g4_w4_load(const void *packed, const void *scales, int out_dim, int in_dim,
                int group, g4_w4 **out);
 
+/* g4_w4_load from DEVICE memory (same layouts): for weights produced on the
+ * device, e.g. by g4_fill_random, or already staged there.  Synchronises. */
+int g4_w4_load_dev(const void *packed_dev, const void *scales_dev, int out_dim,
+                   int in_dim, int group, g4_w4 **out);
+
 /* GPUW4Linear.dispose(). */
 int g4_w4_free(g4_w4 *w);
 
@@ -165,6 +170,10 @@ int g4_ple_create(int vocab, int width, int group, int rows_per_shard,
 /* Copy the bytes of one shard file (exact builder layout) into the table. */
 int g4_ple_upload_shard(g4_ple *t, int shard, const void *bytes, size_t n);
 
+/* g4_ple_upload_shard from DEVICE memory (stream-ordered, no wait). */
+int g4_ple_upload_shard_dev(g4_ple *t, int shard, const void *bytes_dev,
+                            size_t n);
+
 /* Number of shards and the byte size of shard `shard`. */
 int g4_ple_shard_bytes(const g4_ple *t, int shard, int *num_shards,
                        size_t *bytes);
@@ -198,6 +207,196 @@ int g4_ple_gather_dev(const g4_ple *t, const int32_t *ids_dev, int n,
  * softcap <= 0 disables the cap. */
 int g4_bf16_head(const float *x, const void *E, int rows, int in_dim,
                  float *out, float scale, float softcap);
+
+/* ---- remaining GPUOps of a decoder layer ---------------------------------
+ * FP32 device buffers throughout, as every activation of the reference.  The
+ * caller allocates the output (the reference's ops allocate it and hand it
+ * back; the Node binding does that part).  Reductions are tree-shaped, so
+ * results match the shaders to FP32 rounding rather than bit for bit. */
+
+/* GPUOps.rms / RMS_SHADER (gpu-runtime.js:1104-1118, 1325-1332):
+ *   y[r, i] = x[r, i] / sqrt(mean_k x[r, k]^2 + eps) * (scale ? scale[i] : 1)
+ * scale may be NULL (the shader's has_scale = 0).  The reference uses eps 1e-6. */
+int g4_rms(const float *x, int rows, int width, const float *scale, float eps,
+           float *y);
+
+/* GPUOps.addScale / ADD_SCALE_SHADER (gpu-runtime.js:1120-1128, 1333-1336):
+ * y[i] = (a[i] + b[i]) * scale. */
+int g4_add_scale(const float *a, const float *b, size_t n, float scale, float *y);
+
+/* GPUOps.scale / SCALE_SHADER (gpu-runtime.js:1130-1137, 1337-1340):
+ * y[i] = a[i] * scale. */
+int g4_scale(const float *a, size_t n, float scale, float *y);
+
+/* GPUOps.geluMul / GELU_MUL_SHADER (gpu-runtime.js:1139-1157, 1341-1344):
+ * y[i] = gelu_tanh(gate[i]) * up[i], the tanh argument clamped to [-10, 10]. */
+int g4_gelu_mul(const float *gate, const float *up, size_t n, float *y);
+
+/* GPUOps.geluPle / GELU_PLE_SHADER (gpu-runtime.js:1159-1173, 1345-1348):
+ * y[r, d] = gelu_tanh(gate[r, d]) * ple[r, layer, d]; ple is [rows, layers,
+ * width] (the reference: width 256, layers 35). */
+int g4_gelu_ple(const float *gate, const float *ple, int rows, int layer,
+                int width, int layers, float *y);
+
+/* GPUOps.normRope / NORM_ROPE_SHADER (gpu-runtime.js:1175-1202, 1349-1356):
+ * per (row, head) RMS norm with scale[head_dim], then rotate-half RoPE of the
+ * first rope_angles pairs (d, d + head_dim/2) at position pos0 + row with
+ * theta = pos / base^(2 pair / head_dim).  The reference passes
+ * rope_angles = floor(ropeProp * head_dim / 2) and eps 1e-6.
+ * head_dim even and <= 512. */
+int g4_norm_rope(const float *x, int rows, int heads, int head_dim, int pos0,
+                 const float *scale, int rope_angles, float base, float eps,
+                 float *y);
+
+/* GPUOps.attention (gpu-runtime.js:1357-1365): QK_SHADER, SOFTMAX_SHADER and
+ * ATTN_OUT_SHADER (1204-1248) as one split-key pass plus a merge.
+ *   q [qrows, heads, head_dim]; k, v [keylen, head_dim] (one KV head shared
+ *   by all query heads); y [qrows, heads, head_dim].
+ * Query row r sits at position qpos0 + r and sees keys key <= qpos0 + r, and
+ * with `sliding` only those with key + window > qpos0 + r.  No 1/sqrt(d)
+ * factor (the shader has none).  heads <= 8; head_dim 64, 128, 256 or 512. */
+int g4_attention(const float *q, const float *k, const float *v, int qrows,
+                 int heads, int head_dim, int keylen, int qpos0, int sliding,
+                 int window, float *y);
+
+/* GPUOps.pleMix / PLE_MIX_SHADER (gpu-runtime.js:1250-1263, 1366-1369):
+ * for each [width] chunk c of proj ([rows, layers, width]):
+ *   y = (rms(proj_c) * norm_scale + token_ple_c * 16) / sqrt(2). */
+int g4_ple_mix(const float *proj, const float *norm_scale,
+               const float *token_ple, int rows, int width, int layers,
+               float *y);
+
+/* Embedding rows (Gemma4WebGPU.inputBuffers + ops.scale,
+ * gemma4-webgpu.js:198-215, 318): y[r, i] = float(E[ids[r], i]) * scale.
+ * E: device BF16 [vocab, width]; ids: DEVICE int32 [n].  An id outside
+ * [0, vocab) yields a NaN row (no table memory is read). */
+int g4_embed(const void *E, int vocab, int width, const int32_t *ids_dev,
+             int n, float scale, float *y);
+
+/* Greedy pick of Gemma4WebGPU.greedy (gemma4-webgpu.js:441-481) with topK
+ * (gpu-runtime.js:1396-1425) done on the device: out_dev[0] = the first
+ * index of the largest finite x[i], or -1 if none is finite (topK throws). */
+int g4_argmax(const float *x, int n, int32_t *out_dev);
+
+/* ---- synthetic data (random-init models) ----------------------------------
+ * No reference counterpart: the benchmarks run random-init weights of the
+ * checkpoint's shapes, generated on the device.  Fills `count` elements of
+ * `kind` at dst with a counter-based generator (reproducible per seed):
+ *   G4_RAND_W4_PACKED        uint32 words, 8 nibbles uniform in [1, 15]
+ *                            (q = nibble - 8 in [-7, 7]); sigma unused
+ *   G4_RAND_PLE_PACKED       bytes, 2 two's-complement nibbles in [-7, 7]
+ *   G4_RAND_BF16_ABS_NORMAL  bf16 |N(0,1)| * sigma (group scales)
+ *   G4_RAND_BF16_NORMAL      bf16 N(0,1) * sigma (embeddings)
+ *   G4_RAND_F32_NORMAL       float N(0,1) * sigma */
+#define G4_RAND_W4_PACKED 0
+#define G4_RAND_PLE_PACKED 1
+#define G4_RAND_BF16_ABS_NORMAL 2
+#define G4_RAND_BF16_NORMAL 3
+#define G4_RAND_F32_NORMAL 4
+int g4_fill_random(void *dst, size_t count, int kind, uint64_t seed,
+                   float sigma);
+
+/* ---- decoder engine ----------------------------------------------------------
+ * Gemma4WebGPU (custom-webgpu/gemma4-webgpu.js:139-502) on the kernels above:
+ * load/forward/logits/greedy with the reference's op sequence (encodeLayer
+ * 215-301), KV caches per non-shared layer (KVCache, 117-137) and the same
+ * append/capacity errors.  Token position and the chosen token stay in device
+ * memory; g4_gemma_decode replays one recorded decode step (a HIP graph) per
+ * token.  Weights are borrowed: the g4_w4 / g4_ple handles and the BF16
+ * embedding must outlive the model.  Norm vectors are copied in. */
+#define G4_GEMMA_MAX_LAYERS 64
+
+typedef struct {
+  int hidden;                          /* 1536 (HIDDEN)                       */
+  int heads;                           /* query heads, <= 8; one KV head      */
+  int ple_dim;                         /* 256 (PLE)                           */
+  int vocab;                           /* 262144                              */
+  int layers;                          /* 35 (LAYERS)                         */
+  int max_seq;                         /* KV capacity in positions (maxSeq)   */
+  int window;                          /* sliding window, 512                 */
+  float eps;                           /* RMS epsilon, 1e-6                   */
+  float softcap;                       /* final logit softcap, 30             */
+  int head_dim[G4_GEMMA_MAX_LAYERS];   /* spec(i).headDim: 256 or 512         */
+  int intermediate[G4_GEMMA_MAX_LAYERS];
+  int full[G4_GEMMA_MAX_LAYERS];       /* 1: global attention, 0: sliding     */
+  int kv_source[G4_GEMMA_MAX_LAYERS];  /* -1: own k/v; else the earlier layer
+                                          whose cache is reused (spec.shared) */
+  float rope_base[G4_GEMMA_MAX_LAYERS];
+  float rope_prop[G4_GEMMA_MAX_LAYERS];
+} g4_gemma_config;
+
+/* Fills the Gemma-4-E2B schedule of spec(i) (gemma4-webgpu.js:12, 65-77):
+ * every 5th layer global with head_dim 512 and RoPE (1e6, 0.25), the rest
+ * sliding with head_dim 256 and RoPE (1e4, 1.0); intermediate 6144 for
+ * layers 0-14 and 12288 after; layers 15-34 reuse the caches of layer 13
+ * (sliding) and 14 (global). */
+int g4_gemma_e2b_config(int max_seq, g4_gemma_config *cfg);
+
+typedef struct g4_gemma g4_gemma;
+int g4_gemma_create(const g4_gemma_config *cfg, g4_gemma **out);
+int g4_gemma_free(g4_gemma *m);
+
+/* Projections of linearsForLayer (gemma4-webgpu.js:79-96); layer -1 with
+ * G4_PROJ_TOP is per_layer_model_projection.  Shapes are checked. */
+#define G4_PROJ_Q 0
+#define G4_PROJ_K 1
+#define G4_PROJ_V 2
+#define G4_PROJ_O 3
+#define G4_PROJ_GATE 4
+#define G4_PROJ_UP 5
+#define G4_PROJ_DOWN 6
+#define G4_PROJ_PLE_GATE 7
+#define G4_PROJ_PLE_PROJ 8
+#define G4_PROJ_TOP 9
+int g4_gemma_set_linear(g4_gemma *m, int layer, int which, const g4_w4 *w);
+
+/* Norm weights of loadLayer (gemma4-webgpu.js:104-113) as FP32 host arrays;
+ * layer -1 takes per_layer_projection_norm and the final norm (151-156). */
+#define G4_NORM_INPUT 0
+#define G4_NORM_POST_ATTN 1
+#define G4_NORM_PRE_FFW 2
+#define G4_NORM_POST_FFW 3
+#define G4_NORM_POST_PLE 4
+#define G4_NORM_Q 5
+#define G4_NORM_K 6
+#define G4_NORM_PLE_PROJECTION 7
+#define G4_NORM_FINAL 8
+int g4_gemma_set_norm(g4_gemma *m, int layer, int which, const float *v, int n);
+/* layer_scalar (skipScale, gemma4-webgpu.js:114). */
+int g4_gemma_set_layer_scalar(g4_gemma *m, int layer, float s);
+/* The tied BF16 embedding [vocab, hidden] in device memory (embed_tokens and
+ * the LM head, gemma4-webgpu.js:170-188). */
+int g4_gemma_set_embedding(g4_gemma *m, const void *E_dev);
+/* The W4 PLE table of pleRowsToGpu (width layers * ple_dim). */
+int g4_gemma_set_ple(g4_gemma *m, const g4_ple *t);
+
+/* resetCache (gemma4-webgpu.js:190-194) and the current KV length. */
+int g4_gemma_reset(g4_gemma *m);
+int g4_gemma_cache_length(const g4_gemma *m, int *len);
+
+/* forward(tokenIds, startPos) (gemma4-webgpu.js:303-402): runs n host token
+ * ids at positions start_pos.. and, if last_hidden (device [hidden]) is not
+ * NULL, stores the final-norm hidden state of the last token there.
+ * start_pos must equal the cache length ("KV append position ... != cache
+ * length ...") and start_pos + n <= max_seq ("KV cache capacity ...
+ * exceeded"). */
+int g4_gemma_forward(g4_gemma *m, const int32_t *ids, int n, int start_pos,
+                     float *last_hidden);
+
+/* logits(lastHidden) (gemma4-webgpu.js:404-431) into device [vocab]. */
+int g4_gemma_logits(g4_gemma *m, const float *last_hidden, float *logits);
+
+/* greedy(tokenIds, startPos) (gemma4-webgpu.js:441-481): forward, logits and
+ * the first index of the largest finite logit (topK's top-1).  logits
+ * (device [vocab]) may be NULL. */
+int g4_gemma_greedy(g4_gemma *m, const int32_t *ids, int n, int start_pos,
+                    int32_t *next_token, float *logits);
+
+/* `steps` further greedy tokens, each fed back as the next input (the
+ * generation loop of custom-webgpu/main.js), from the state a g4_gemma_greedy
+ * call left.  tokens (host [steps]) may be NULL.  The first call records the
+ * decode step; later calls replay it. */
+int g4_gemma_decode(g4_gemma *m, int steps, int32_t *tokens);
 
 #ifdef __cplusplus
 }

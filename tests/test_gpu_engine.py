@@ -1,0 +1,238 @@
+"""The decoder engine (g4_gemma_*) against the oracle model, and its
+size-independent properties at the real Gemma-4-E2B shapes.
+
+Tiny model: 5 layers covering the E2B schedule's features (sliding and
+global layers, two head sizes, partial RoPE, layers that reuse an earlier
+layer's KV cache, a sliding window shorter than the sequence), host weights
+shared with the oracle.  Logits and last hidden states are compared with
+relative L2 <= 1e-3 (the W4 projections' tolerance); greedy tokens must match
+unless the oracle's top two logits are within 1e-3 of each other.
+
+E2B shapes (random device weights, 35 layers, vocab 262144): the recorded
+decode step (HIP graph) must choose exactly the tokens of eager one-token
+calls, and a prefill of a sequence must agree with the same sequence fed in
+two parts."""
+import math
+
+import numpy as np
+import pytest
+
+import layer_oracle as lo
+import synthetic as syn
+
+pytestmark = pytest.mark.gpu
+
+TINY = dict(hidden=128, heads=2, ple_dim=32, vocab=512, window=8, layers=[
+    dict(head_dim=64, full=0, kv_source=-1, intermediate=256, rope_base=1e4, rope_prop=1.0),
+    dict(head_dim=128, full=1, kv_source=-1, intermediate=256, rope_base=1e6, rope_prop=0.25),
+    dict(head_dim=64, full=0, kv_source=0, intermediate=512, rope_base=1e4, rope_prop=1.0),
+    dict(head_dim=128, full=1, kv_source=1, intermediate=512, rope_base=1e6, rope_prop=0.25),
+    dict(head_dim=64, full=0, kv_source=0, intermediate=512, rope_base=1e4, rope_prop=1.0),
+])
+RPS = 64  # PLE rows per shard
+
+
+def rel(a, b):
+    a = np.asarray(a, np.float64).ravel()
+    b = np.asarray(b, np.float64).ravel()
+    return np.linalg.norm(a - b) / np.linalg.norm(b)
+
+
+def tiny_config(g4, max_seq=40):
+    c = g4.GemmaConfig()
+    c.hidden, c.heads, c.ple_dim, c.vocab = TINY["hidden"], TINY["heads"], TINY["ple_dim"], TINY["vocab"]
+    c.layers, c.max_seq, c.window, c.eps, c.softcap = len(TINY["layers"]), max_seq, TINY["window"], 1e-6, 30.0
+    for i, L in enumerate(TINY["layers"]):
+        c.head_dim[i], c.intermediate[i], c.full[i] = L["head_dim"], L["intermediate"], L["full"]
+        c.kv_source[i], c.rope_base[i], c.rope_prop[i] = L["kv_source"], L["rope_base"], L["rope_prop"]
+    return c
+
+
+@pytest.fixture(scope="module")
+def tiny(g4):
+    H, heads, P, V = TINY["hidden"], TINY["heads"], TINY["ple_dim"], TINY["vocab"]
+    NL = len(TINY["layers"])
+    rng = np.random.default_rng(2024)
+    E = syn.bf16_rne(rng.standard_normal((V, H), dtype=np.float32) * np.float32(0.05))
+    shards = [syn.ple_shard(7, s, RPS, NL * P) for s in range(V // RPS)]
+    table = np.concatenate(shards)
+
+    def w(seed, n, k):
+        packed, scales, _ = syn.w4_weights(seed, n, k)
+        return packed, scales
+
+    top = w(1, NL * P, H)
+    layers = []
+    seed = 10
+    for i, L in enumerate(TINY["layers"]):
+        hd, inter, shared = L["head_dim"], L["intermediate"], L["kv_source"] >= 0
+        shapes = dict(q=(heads * hd, H), o=(H, heads * hd), gate=(inter, H), up=(inter, H),
+                      down=(H, inter), ple_gate=(P, H), ple_proj=(H, P))
+        if not shared:
+            shapes.update(k=(hd, H), v=(hd, H))
+        lin = {}
+        for name, (n, k) in shapes.items():
+            seed += 1
+            lin[name] = w(seed, n, k)
+        norm = {n: rng.uniform(0.8, 1.2, H).astype(np.float32)
+                for n in ("input", "post_attn", "pre_ffw", "post_ffw", "post_ple")}
+        norm["q"] = rng.uniform(0.8, 1.2, hd).astype(np.float32)
+        if not shared:
+            norm["k"] = rng.uniform(0.8, 1.2, hd).astype(np.float32)
+        layers.append(dict(L, linear=lin, norm=norm, skip=float(rng.uniform(0.9, 1.1))))
+    ple_norm = rng.uniform(0.8, 1.2, P).astype(np.float32)
+    final_norm = rng.uniform(0.8, 1.2, H).astype(np.float32)
+
+    def ple_rows(ids):
+        import g4oracle
+        return g4oracle.ple_gather(table, V, NL * P, RPS, ids)
+
+    ref = lo.Model(H, heads, P, V, layers, E, ple_rows, top, ple_norm, final_norm,
+                   window=TINY["window"])
+
+    def make_engine(max_seq=40):
+        m = g4.Gemma(tiny_config(g4, max_seq))
+        Eb = g4.Buffer.from_array(E)
+        m.set_embedding(Eb)
+        t = g4.PleTable(V, NL * P, 32, RPS)
+        for s, data in enumerate(shards):
+            t.upload_shard(s, data)
+        m.set_ple(t)
+        m.set_linear(-1, "top", g4.W4Linear(*top))
+        m.set_norm(-1, "ple_projection", ple_norm)
+        m.set_norm(-1, "final", final_norm)
+        for i, L in enumerate(layers):
+            for name, (packed, scales) in L["linear"].items():
+                m.set_linear(i, name, g4.W4Linear(packed, scales))
+            for name, v in L["norm"].items():
+                m.set_norm(i, name, v)
+            m.set_layer_scalar(i, L["skip"])
+        return m
+
+    return ref, make_engine
+
+
+def near_tie(logits, tok, tol=1e-3):
+    return float(np.max(logits) - logits[tok]) <= tol
+
+
+def test_tiny_prefill_greedy_matches_oracle(g4, tiny):
+    ref, make = tiny
+    m = make()
+    ids = syn.token_ids(3, 12, TINY["vocab"])
+    lg = g4.Buffer(TINY["vocab"] * 4)
+    tok = m.greedy(ids, 0, lg)
+    ref.reset()
+    want_tok, want_lg = ref.greedy(ids, 0)
+    got_lg = lg.download(np.float32)
+    assert rel(got_lg, want_lg) < 1e-3
+    assert tok == want_tok or near_tie(want_lg, tok)
+    assert m.cache_length() == 12
+
+
+def test_tiny_decode_matches_oracle_step_by_step(g4, tiny):
+    ref, make = tiny
+    m = make()
+    ids = syn.token_ids(4, 10, TINY["vocab"])  # > window 8: sliding masks are exercised
+    t0 = m.greedy(ids, 0)
+    toks = m.decode(8)
+    ref.reset()
+    want0, lg = ref.greedy(ids, 0)
+    assert t0 == want0 or near_tie(lg, t0)
+    prev, pos = t0, len(ids)
+    for t in toks:
+        want, lg = ref.greedy([prev], pos)  # feed the engine's token: no divergence
+        assert t == want or near_tie(lg, int(t)), (pos, t, want)
+        prev, pos = int(t), pos + 1
+    assert m.cache_length() == len(ids) + 8
+
+
+def test_tiny_forward_and_logits_entry_points(g4, tiny):
+    ref, make = tiny
+    m = make()
+    ids = syn.token_ids(5, 6, TINY["vocab"])
+    h = g4.Buffer(TINY["hidden"] * 4)
+    m.forward(ids, 0, h)
+    ref.reset()
+    want_h = ref.forward(ids, 0)
+    assert rel(h.download(np.float32), want_h) < 1e-3
+    lg = g4.Buffer(TINY["vocab"] * 4)
+    m.logits(h, lg)
+    assert rel(lg.download(np.float32), ref.logits(want_h)) < 1e-3
+
+
+def test_tiny_graph_decode_equals_eager_steps(g4, tiny):
+    _, make = tiny
+    ids = syn.token_ids(6, 9, TINY["vocab"])
+    a = make()
+    t0 = a.greedy(ids, 0)
+    graph = a.decode(12)
+    b = make()
+    assert b.greedy(ids, 0) == t0
+    eager, prev = [], t0
+    for s in range(12):
+        prev = b.greedy([prev], len(ids) + s)
+        eager.append(prev)
+    np.testing.assert_array_equal(graph, np.array(eager, np.int32))
+
+
+def test_tiny_kv_errors_and_reset(g4, tiny):
+    _, make = tiny
+    m = make(max_seq=16)
+    ids = syn.token_ids(8, 10, TINY["vocab"])
+    m.greedy(ids, 0)
+    with pytest.raises(g4.G4Error, match="KV append position 3 != cache length 10"):
+        m.forward([1], 3)
+    with pytest.raises(g4.G4Error, match="KV cache capacity 16 exceeded"):
+        m.forward(syn.token_ids(9, 7, TINY["vocab"]), 10)
+    with pytest.raises(g4.G4Error, match="KV cache capacity 16 exceeded"):
+        m.decode(7)
+    with pytest.raises(g4.G4Error, match="out of range"):
+        m.forward([TINY["vocab"]], 10)
+    m.reset()
+    assert m.cache_length() == 0
+    m.greedy(ids, 0)
+
+
+def test_unset_weights_are_reported(g4):
+    m = g4.Gemma(tiny_config(g4))
+    with pytest.raises(g4.G4Error, match="not set"):
+        m.greedy([1, 2], 0)
+
+
+@pytest.fixture(scope="module")
+def e2b(g4):
+    import e2b
+    cfg = g4.e2b_config(96)
+    return e2b.build(cfg, seed=1), cfg
+
+
+def test_e2b_graph_decode_equals_eager(g4, e2b):
+    m, cfg = e2b
+    ids = syn.token_ids(11, 24, cfg.vocab)
+    m.reset()
+    t0 = m.greedy(ids, 0)
+    graph = m.decode(8)
+    assert t0 >= 0 and np.all(graph >= 0)
+    m.reset()
+    assert m.greedy(ids, 0) == t0
+    prev, eager = t0, []
+    for s in range(8):
+        prev = m.greedy([prev], len(ids) + s)
+        eager.append(prev)
+    np.testing.assert_array_equal(graph, np.array(eager, np.int32))
+
+
+def test_e2b_prefill_equals_two_part_prefill(g4, e2b):
+    m, cfg = e2b
+    ids = syn.token_ids(12, 40, cfg.vocab)
+    h1 = g4.Buffer(cfg.hidden * 4)
+    h2 = g4.Buffer(cfg.hidden * 4)
+    m.reset()
+    m.forward(ids, 0, h1)
+    m.reset()
+    m.forward(ids[:29], 0)
+    m.forward(ids[29:], 29, h2)
+    a, b = h1.download(np.float32), h2.download(np.float32)
+    assert np.all(np.isfinite(a))
+    assert rel(b, a) < 1e-3

@@ -1,0 +1,187 @@
+"""Pins the decoder-layer oracle (oracle/layer_oracle.py) with closed forms,
+invariants and brute force, so a dropped term, a wrong sign or a swapped
+index in the restatement fails here before it is used as the checker."""
+import math
+
+import numpy as np
+import pytest
+
+import layer_oracle as lo
+
+
+def test_rms_constant_vector_closed_form():
+    # x = c everywhere: y = c / sqrt(c^2 + eps) * scale
+    c, w, eps = 3.0, 64, 1e-6
+    s = np.linspace(0.5, 2.0, w).astype(np.float32)
+    y = lo.rms(np.full((2, w), c, np.float32), w, s, eps)
+    want = c / math.sqrt(c * c + eps) * s
+    np.testing.assert_allclose(y[0], want, rtol=1e-6)
+    np.testing.assert_allclose(y[1], want, rtol=1e-6)
+
+
+def test_rms_unit_mean_square_and_no_scale():
+    rng = np.random.default_rng(1)
+    x = rng.standard_normal((3, 100)).astype(np.float32) * 7
+    y = lo.rms(x, 100, None, 0.0).astype(np.float64)
+    np.testing.assert_allclose((y * y).mean(axis=1), 1.0, rtol=1e-6)
+    # direction is kept: y is a positive multiple of x
+    assert np.all(np.sign(y) == np.sign(x))
+
+
+def test_add_scale_and_scale():
+    a = np.array([1, -2, 3.5], np.float32)
+    b = np.array([0.5, 2, -1], np.float32)
+    np.testing.assert_array_equal(lo.add_scale(a, b, 2.0), np.array([3, 0, 5], np.float32))
+    np.testing.assert_array_equal(lo.scale(a, -0.5), np.array([-0.5, 1, -1.75], np.float32))
+
+
+def test_gelu_known_values_and_limits():
+    # tanh-form GELU: gelu(0) = 0, gelu(1) = 0.5 * (1 + tanh(0.79788456 * 1.044715))
+    g = lo.gelu_tanh(np.array([0.0, 1.0, -1.0, 20.0, -20.0], np.float32))
+    t1 = math.tanh(0.7978845608028654 * 1.044715)
+    np.testing.assert_allclose(g[:3], [0.0, 0.5 * (1 + t1), -0.5 * (1 - t1)], rtol=1e-12)
+    # the clamp at |z| = 10 leaves the asymptotes: x and 0
+    np.testing.assert_allclose(g[3], 20.0 * 0.5 * (1 + math.tanh(10.0)), rtol=1e-12)
+    assert abs(g[4]) < 1e-6
+    # gelu(x) - gelu(-x) = x (odd part of 0.5 x (1 + tanh))
+    x = np.linspace(-3, 3, 13).astype(np.float32)
+    np.testing.assert_allclose(lo.gelu_tanh(x) - lo.gelu_tanh(-x), x, atol=1e-7)
+
+
+def test_gelu_mul_and_gelu_ple_index_layer_and_width():
+    rows, width, layers = 2, 4, 3
+    gate = np.arange(rows * width, dtype=np.float32).reshape(rows, width) / 4
+    ple = np.arange(rows * layers * width, dtype=np.float32).reshape(rows, layers, width)
+    y = lo.gelu_ple(gate, ple, rows, 1, width, layers)
+    want = lo.gelu_tanh(gate) * ple[:, 1, :]
+    np.testing.assert_allclose(y, want, rtol=1e-6)
+    np.testing.assert_allclose(lo.gelu_mul(gate, 2 * np.ones_like(gate)), 2 * lo.gelu_tanh(gate),
+                               rtol=1e-6)
+
+
+def test_norm_rope_position_zero_is_plain_norm():
+    rng = np.random.default_rng(2)
+    x = rng.standard_normal((1, 2 * 8)).astype(np.float32)
+    s = rng.uniform(0.5, 1.5, 8).astype(np.float32)
+    y = lo.norm_rope(x, 1, 2, 8, 0, s, 4, 10000.0)
+    np.testing.assert_allclose(y.reshape(2, 8), lo.rms(x.reshape(2, 8), 8, s), rtol=1e-6)
+
+
+def test_norm_rope_rotation_known_angle_and_norm():
+    # hd 4, pair 0 at position 1 rotates by exactly 1 rad; pair 1 by 1/base^(1/2)
+    x = np.array([[1.0, 2.0, 3.0, 4.0]], np.float32)
+    s = np.ones(4, np.float32)
+    base = 100.0
+    y = lo.norm_rope(x, 1, 1, 4, 1, s, 2, base, eps=0.0)[0].astype(np.float64)
+    n = x[0] / math.sqrt((x[0] ** 2).mean())
+    th0, th1 = 1.0, float(np.float32(1.0) / np.float32(math.sqrt(base)))
+    want = [n[0] * math.cos(th0) - n[2] * math.sin(th0), n[1] * math.cos(th1) - n[3] * math.sin(th1),
+            n[2] * math.cos(th0) + n[0] * math.sin(th0), n[3] * math.cos(th1) + n[1] * math.sin(th1)]
+    np.testing.assert_allclose(y, want, rtol=1e-6)
+    # pairs beyond rope_angles are not rotated
+    y1 = lo.norm_rope(x, 1, 1, 4, 5, s, 1, base, eps=0.0)[0]
+    np.testing.assert_allclose([y1[1], y1[3]], [n[1], n[3]], rtol=1e-6)
+
+
+def test_norm_rope_rows_advance_position():
+    rng = np.random.default_rng(3)
+    x = rng.standard_normal((3, 16)).astype(np.float32)
+    s = np.ones(16, np.float32)
+    y = lo.norm_rope(x, 3, 1, 16, 7, s, 8, 10000.0)
+    for r in range(3):
+        np.testing.assert_allclose(y[r], lo.norm_rope(x[r:r + 1], 1, 1, 16, 7 + r, s, 8, 10000.0)[0],
+                                   rtol=1e-7)
+
+
+def test_attention_single_visible_key_returns_its_value():
+    rng = np.random.default_rng(4)
+    hd, heads = 8, 2
+    k = rng.standard_normal((5, hd)).astype(np.float32)
+    v = rng.standard_normal((5, hd)).astype(np.float32)
+    q = rng.standard_normal((1, heads * hd)).astype(np.float32)
+    # query at position 0 sees only key 0
+    y = lo.attention(q, k, v, 1, heads, hd, 1, 0, False, 512)
+    np.testing.assert_allclose(y.reshape(heads, hd), np.stack([v[0], v[0]]), rtol=1e-6)
+
+
+def test_attention_uniform_logits_average_visible_values():
+    rng = np.random.default_rng(5)
+    hd, heads = 4, 1
+    k = rng.standard_normal((10, hd)).astype(np.float32)
+    v = rng.standard_normal((10, hd)).astype(np.float32)
+    q = np.zeros((2, hd), np.float32)  # all logits 0
+    # query rows at positions 8 and 9, sliding window 3: keys 6..8 and 7..9
+    y = lo.attention(q, k, v, 2, heads, hd, 10, 8, True, 3)
+    np.testing.assert_allclose(y[0], v[6:9].mean(axis=0), rtol=1e-6)
+    np.testing.assert_allclose(y[1], v[7:10].mean(axis=0), rtol=1e-6)
+    # global: all keys up to the position
+    y = lo.attention(q, k, v, 2, heads, hd, 10, 8, False, 3)
+    np.testing.assert_allclose(y[0], v[:9].mean(axis=0), rtol=1e-6)
+
+
+def test_attention_matches_brute_force_loops():
+    rng = np.random.default_rng(6)
+    qrows, heads, hd, keylen, qpos0, window = 3, 2, 4, 7, 4, 2
+    q = rng.standard_normal((qrows, heads * hd)).astype(np.float32)
+    k = rng.standard_normal((keylen, hd)).astype(np.float32)
+    v = rng.standard_normal((keylen, hd)).astype(np.float32)
+    for sliding in (False, True):
+        y = lo.attention(q, k, v, qrows, heads, hd, keylen, qpos0, sliding, window)
+        for r in range(qrows):
+            qp = qpos0 + r
+            for h in range(heads):
+                qv = q[r, h * hd:(h + 1) * hd].astype(np.float64)
+                logits = []
+                for key in range(keylen):
+                    ok = key <= qp and (not sliding or key + window > qp)
+                    logits.append(float(qv @ k[key]) if ok else -1e30)
+                m = max(logits)
+                e = [math.exp(t - m) for t in logits]
+                out = sum(ei * v[i].astype(np.float64) for i, ei in enumerate(e)) / sum(e)
+                np.testing.assert_allclose(y[r, h * hd:(h + 1) * hd], out, rtol=1e-6, atol=1e-7)
+
+
+def test_ple_mix_closed_forms():
+    rows, width, layers = 1, 8, 2
+    s = np.linspace(1, 2, width).astype(np.float32)
+    tok = np.arange(rows * layers * width, dtype=np.float32).reshape(rows, layers * width) / 10
+    # zero projection: the token rows alone, times 16 / sqrt(2)
+    y = lo.ple_mix(np.zeros_like(tok), s, tok, rows, width, layers)
+    np.testing.assert_allclose(y, tok * 16 / math.sqrt(2), rtol=1e-6)
+    # constant projection c, zero token rows: c / sqrt(c^2 + 1e-6) * s / sqrt(2)
+    c = 2.0
+    y = lo.ple_mix(np.full_like(tok, c), s, np.zeros_like(tok), rows, width, layers)
+    want = np.tile(c / math.sqrt(c * c + 1e-6) * s / math.sqrt(2), layers)
+    np.testing.assert_allclose(y[0], want, rtol=1e-6)
+
+
+def test_embed_is_exact_bf16_times_scale():
+    E = np.array([[0x3F80, 0xC000], [0x4040, 0x0000]], np.uint16)  # 1, -2, 3, 0
+    y = lo.embed(E, [1, 0], np.float32(math.sqrt(1536)))
+    s = np.float32(math.sqrt(1536))
+    np.testing.assert_array_equal(y, np.array([[3 * s, 0], [s, -2 * s]], np.float32))
+
+
+def test_e2b_spec_schedule():
+    full = [i for i in range(35) if lo.e2b_spec(i)["full"]]
+    assert full == [4, 9, 14, 19, 24, 29, 34]
+    assert lo.e2b_spec(14)["head_dim"] == 512 and lo.e2b_spec(13)["head_dim"] == 256
+    assert [lo.e2b_spec(i)["intermediate"] for i in (14, 15)] == [6144, 12288]
+    assert not lo.e2b_spec(14)["shared"] and lo.e2b_spec(15)["shared"]
+    assert lo.e2b_spec(13)["store_shared"] and lo.e2b_spec(14)["store_shared"]
+
+
+@pytest.mark.parametrize("plant", [None, "no_window"])
+def test_attention_window_planted_mistake_is_caught(plant):
+    # A restatement that forgets the sliding window must disagree with the
+    # uniform-logit closed form; this guards the check itself.
+    rng = np.random.default_rng(7)
+    k = rng.standard_normal((6, 2)).astype(np.float32)
+    v = rng.standard_normal((6, 2)).astype(np.float32)
+    q = np.zeros((1, 2), np.float32)
+    y = lo.attention(q, k, v, 1, 1, 2, 6, 5, plant is None, 2)
+    want = v[4:6].mean(axis=0)
+    if plant is None:
+        np.testing.assert_allclose(y[0], want, rtol=1e-6)
+    else:
+        assert not np.allclose(y[0], want, rtol=1e-3)
