@@ -1,0 +1,74 @@
+// Device helpers of the bf16-pair dot-product GEMVs (g4_w4.hip, g4_fused.hip)
+// and the launch planner of the one-row decode GEMV.
+#pragma once
+
+#include "g4_internal.h"
+
+namespace g4 {
+
+typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2_t;
+
+__device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a),
+                                         __builtin_bit_cast(bf16x2_t, b), c, false);
+}
+
+constexpr uint32_t kPairMagic = 0x43004300u;  // bf16 pair (128, 128)
+constexpr float kPairBias = 136.f;            // (128 + n) - 136 = n - 8 = q
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, true));
+}
+
+// Sum over aligned teams of L lanes; every lane of the team gets the sum.
+template <int L>
+__device__ __forceinline__ float team_sum(float v) {
+  if (L >= 2) v += dpp_f32<0xB1>(v);   // quad_perm [1,0,3,2]
+  if (L >= 4) v += dpp_f32<0x4E>(v);   // quad_perm [2,3,0,1]
+  if (L >= 8) v += dpp_f32<0x141>(v);  // row_half_mirror
+  if (L >= 16) v += dpp_f32<0x140>(v); // row_mirror
+  if (L >= 32) v += __shfl_xor(v, 16, 64);
+  if (L >= 64) v += __shfl_xor(v, 32, 64);
+  return v;
+}
+
+__device__ __forceinline__ uint32_t bf16_pair(uint32_t lo16, uint32_t hi16) {
+  return (lo16 & 0xffffu) | (hi16 << 16);
+}
+
+// GELU, tanh form with the clamp of GELU_MUL_SHADER (gpu-runtime.js:1148-1155).
+__device__ __forceinline__ float gelu_tanh(float x) {
+  const float c = 0.7978845608028654f;
+  const float z = c * (x + 0.044715f * x * x * x);
+  const float t = tanhf(fminf(fmaxf(z, -10.f), 10.f));
+  return 0.5f * x * (1.f + t);
+}
+
+struct Gemv1Plan {
+  int T, IPL, RB;
+  size_t lds;
+};
+
+// Rows per block RB >= min_rb (>= 4: x staging amortised over >= 4 rows),
+// RB * G = T * IPL with T a multiple of 64 up to 1024 and IPL <= 4.  A larger
+// min_rb trades blocks for less re-reading of x per weight byte.
+inline bool plan_gemv1(int G, bool f32x, Gemv1Plan *p, int min_rb = 4) {
+  for (int RB = min_rb; RB <= 256; RB *= 2) {
+    const long items = (long)RB * G;
+    if (items % 64) continue;
+    for (int ipl = 1; ipl <= 4; ++ipl) {
+      if (items % ipl) continue;
+      const long T = items / ipl;
+      if (T % 64 || T > 1024) continue;
+      p->T = (int)T;
+      p->IPL = ipl;
+      p->RB = RB;
+      p->lds = (size_t)G * 4 * 16 * (f32x ? 2 : 1) + (size_t)G * 4 + (size_t)RB * G * 4;
+      return p->lds <= 64 * 1024;
+    }
+  }
+  return false;
+}
+
+}  // namespace g4

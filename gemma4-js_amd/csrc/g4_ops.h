@@ -6,6 +6,8 @@
 #include <stddef.h>
 #include <stdint.h>
 
+struct g4_w4;
+
 namespace g4 {
 
 int launch_rms(const float *x, int rows, int width, const float *scale, float eps, float *y,
@@ -27,6 +29,23 @@ int launch_ple_mix(const float *proj, const float *norm_scale, const float *toke
                    int width, int layers, float eps, float ple_scale, float out_scale, float *y);
 int launch_embed(const uint16_t *E, int vocab, int width, const int *ids_dev, int n, float scale,
                  float *y);
+
+// Fused one-token kernels (g4_fused.hip).  Inputs and r_out must not alias.
+int fused_norm_linear(const float *a, const float *w1, float eps, const g4_w4 *const *w,
+                      float *const *y, int n);
+int fused_res_norm_linear(const float *a, const float *h, const float *w1, float c,
+                          const float *w2, float eps, float *r_out, const g4_w4 *const *w,
+                          float *const *y, int n);
+int fused_res_norm_gate_up(const float *a, const float *h, const float *w1, float c,
+                           const float *w2, float eps, float *r_out, const g4_w4 *gate,
+                           const g4_w4 *up, float *act);
+int fused_res_linear_gelu_mul(const float *a, const float *h, const float *w1, float eps,
+                              float *r_out, const g4_w4 *w, const float *mul, float *y);
+int launch_rope_qkv(const float *qraw, const float *kraw, const float *vraw, int heads, int hd,
+                    const int *pos_dev, const float *qnorm, const float *knorm, int rope_angles,
+                    float base, float eps, float *q, float *kc, float *vc, bool own_kv);
+int launch_norm_chain(const float *a, const float *h, const float *w1, const float *w2, float c,
+                      float eps, int rows, int width, float *r_out, float *x_out);
 
 // Head partials for the device argmax: per block (max value, first index).
 size_t head_argmax_blocks(int rows);

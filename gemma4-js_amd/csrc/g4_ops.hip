@@ -12,6 +12,7 @@
 // so one recorded step serves every position.
 #include <math.h>
 
+#include "g4_gemv.h"
 #include "g4_internal.h"
 #include "g4_ops.h"
 
@@ -225,32 +226,218 @@ __global__ __launch_bounds__(64) void attn_split_kernel(AttnArgs a) {
   }
 }
 
-// One block per (query row, head): out = sum_s e^(m_s - M) o_s / sum_s e^(m_s - M) l_s.
+// Single-query attention (a decode step): the visible keys [lo, keylen) are
+// split evenly over the grid (at most kDecMaxKeys per block).  Block = 4
+// waves.  Phase 1: each wave takes every 4th key of the block; lane l holds
+// dims [DPL*l, DPL*l + DPL) of q for all heads, and the 8 per-head partial
+// dots of a key are reduced across the wave by a reduce-scatter (10 shuffles
+// instead of 8 full reductions), leaving head (l >> 3) & 7 in lane group
+// l >> 3.  Phase 2: per head (32 threads) the block's max, exp and sum.
+// Phase 3: per head, 32 threads each accumulate hd/32 output dims over the
+// block's keys.  Every block writes (max, sum, output) per head, an empty
+// block (max -1e30, sum 0): attn_combine_kernel merges them.
+constexpr int kDecMaxKeys = 16;
+constexpr int kMaxSplits = 1024;
+
+__device__ __forceinline__ float xor_shfl(float v, int m) { return __shfl_xor(v, m, 64); }
+
+template <int DPL>
+__global__ __launch_bounds__(kBlock) void attn_dec_kernel(const float *__restrict__ q,
+                                                          const float *__restrict__ k,
+                                                          const float *__restrict__ v,
+                                                          float *__restrict__ part, int H,
+                                                          int keylen_host,
+                                                          const int *__restrict__ pos_dev,
+                                                          int sliding, int window) {
+  constexpr int HD = 64 * DPL;
+  constexpr int D32 = HD / 32;                            // q dims per lane (32 lanes / head)
+  constexpr int DPT = HD / kBlock > 0 ? HD / kBlock : 1;  // output dims per thread
+  __shared__ float4 ks[kDecMaxKeys * HD / 4];
+  __shared__ __align__(16) float ps[kDecMaxKeys][kMaxHeads];
+  __shared__ float mh[kMaxHeads], lh[kMaxHeads];
+  const int t = threadIdx.x;
+  const int keylen = pos_dev ? *pos_dev + 1 : keylen_host;
+  const int qpos = keylen - 1;
+  int lo = 0;
+  if (sliding && qpos - window + 1 > 0) lo = qpos - window + 1;
+  const int per = (keylen - lo + (int)gridDim.x - 1) / (int)gridDim.x;
+  const int k0 = lo + blockIdx.x * per;
+  const int n = k0 < keylen ? (keylen - k0 < per ? keylen - k0 : per) : 0;
+  const int h = t >> 5, ds = t & 31;
+  const bool dlive = t < HD;
+
+  // all global loads first: q slice of head h, the block's K rows (to LDS),
+  // the V elements of this thread's output dims
+  // (loads are unconditional from clamped in-bounds addresses, so no branch
+  // separates them; keys >= n and dims >= HD are loaded but never used)
+  const float hq = h < H ? 1.f : 0.f;
+  const float *qh = q + (h < H ? h : 0) * HD + ds * D32;
+  float qv[D32];
+#pragma unroll
+  for (int j = 0; j < D32; ++j) qv[j] = qh[j] * hq;
+  auto row = [&](int kl) { return (size_t)(k0 + kl < keylen ? k0 + kl : keylen - 1) * HD; };
+  float4 kr[DPL];
+#pragma unroll
+  for (int i = 0; i < DPL; ++i) {
+    const int idx = t + i * kBlock;  // float4 index in the 16 x HD tile
+    const int kl = idx / (HD / 4);
+    kr[i] = reinterpret_cast<const float4 *>(k + row(kl))[idx % (HD / 4)];  // rows >= n unused
+  }
+  const int td = dlive ? t : 0;
+  float vv[kDecMaxKeys][DPT];
+#pragma unroll
+  for (int kl = 0; kl < kDecMaxKeys; ++kl)
+#pragma unroll
+    for (int i = 0; i < DPT; ++i) vv[kl][i] = v[row(kl) + td + i * kBlock];  // kl >= n unused
+#pragma unroll
+  for (int i = 0; i < DPL; ++i) ks[t + i * kBlock] = kr[i];
+  __syncthreads();
+
+  // QK of head h (32 lanes, lane ds holds dims [ds*D32, ds*D32 + D32)): the
+  // 16 partial dots first, then one reduce-scatter over the 32 lanes (xor 16,
+  // then the DPP row mirror, half-row mirror and quad swaps) leaves the logit
+  // of key 8 b4 + 4 b3 + 2 b2 + b1 in lanes ds and ds ^ 1 (b = bits of ds).
+  const float *ksf = reinterpret_cast<const float *>(ks);
+  float dv[kDecMaxKeys];
+#pragma unroll
+  for (int kl = 0; kl < kDecMaxKeys; ++kl) {
+    float a = 0.f;
+#pragma unroll
+    for (int j = 0; j < D32; ++j) a = fmaf(qv[j], ksf[kl * HD + ds * D32 + j], a);
+    dv[kl] = a;  // rows >= n hold finite data of a clamped row: discarded below
+  }
+  const bool b4 = ds & 16, b3 = ds & 8, b2 = ds & 4, b1 = ds & 2;
+  float a8[8], a4[4], a2[2];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const float keep = b4 ? dv[8 + i] : dv[i], send = b4 ? dv[i] : dv[8 + i];
+    a8[i] = keep + __shfl_xor(send, 16, 64);
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float keep = b3 ? a8[4 + i] : a8[i], send = b3 ? a8[i] : a8[4 + i];
+    a4[i] = keep + dpp_f32<0x140>(send);  // row_mirror: lane i <-> 15 - i
+  }
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const float keep = b2 ? a4[2 + i] : a4[i], send = b2 ? a4[i] : a4[2 + i];
+    a2[i] = keep + dpp_f32<0x141>(send);  // row_half_mirror: lane i <-> 7 - i
+  }
+  float sk = (b1 ? a2[1] : a2[0]) + dpp_f32<0x4E>(b1 ? a2[0] : a2[1]);  // quad swap pairs
+  sk += dpp_f32<0xB1>(sk);
+  const int key = (b4 ? 8 : 0) + (b3 ? 4 : 0) + (b2 ? 2 : 0) + (b1 ? 1 : 0);
+  const bool kvalid = key < n;
+  // softmax over the block's keys (each key sits in two lanes)
+  float m = kvalid ? sk : -1e30f;
+#pragma unroll
+  for (int o = 16; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+  const float p = kvalid ? expf(sk - m) : 0.f;
+  const float l = team_sum<32>((ds & 1) ? 0.f : p);
+  if (!(ds & 1) && h < H && key < kDecMaxKeys) ps[key][h] = p;
+  if (ds == 0 && h < H) {
+    mh[h] = m;
+    lh[h] = l;
+  }
+  __syncthreads();
+
+  // PV: thread t owns dims t, t + 256, ... of every head
+  float acc[kMaxHeads][DPT];
+#pragma unroll
+  for (int hh = 0; hh < kMaxHeads; ++hh)
+#pragma unroll
+    for (int i = 0; i < DPT; ++i) acc[hh][i] = 0.f;
+#pragma unroll
+  for (int kl = 0; kl < kDecMaxKeys; ++kl) {
+    if (kl >= n) break;
+    const float4 p0 = reinterpret_cast<const float4 *>(ps[kl])[0];
+    const float4 p1 = reinterpret_cast<const float4 *>(ps[kl])[1];
+    const float pk[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
+#pragma unroll
+    for (int hh = 0; hh < kMaxHeads; ++hh)
+#pragma unroll
+      for (int i = 0; i < DPT; ++i) acc[hh][i] = fmaf(pk[hh], vv[kl][i], acc[hh][i]);
+  }
+  if (dlive) {
+#pragma unroll
+    for (int hh = 0; hh < kMaxHeads; ++hh) {
+      if (hh >= H) break;
+      float *pp = part + ((size_t)blockIdx.x * H + hh) * (HD + 2);
+#pragma unroll
+      for (int i = 0; i < DPT; ++i) pp[2 + t + i * kBlock] = acc[hh][i];
+      if (t == 0) {
+        pp[0] = mh[hh];
+        pp[1] = lh[hh];
+      }
+    }
+  }
+}
+
+// Merges split partials:
+//   out = sum_s e^(m_s - M) o_s / sum_s e^(m_s - M) l_s.
+// Block (query row, head, 64-dim slice).  Each thread issues the loads of the
+// first 16 of its splits (s = wave + 4 i) before anything else; the 4 waves'
+// sums meet in LDS.  Splits beyond the keys of this call (kpw > 0:
+// ceil(keylen / kpw) splits) were not written.
 __global__ __launch_bounds__(kBlock) void attn_combine_kernel(const float *__restrict__ part,
                                                               int H, int hd, int kpw,
                                                               int nsplit, int keylen,
                                                               const int *__restrict__ pos_dev,
                                                               int qrows, float *__restrict__ out) {
-  const int qr = blockIdx.x / H, h = blockIdx.x - qr * H;
+  constexpr int U = 16;
+  __shared__ float red[4];
+  __shared__ float accs[4][64];
+  __shared__ float ls4[4];
+  const int dslices = hd >> 6;
+  const int b = blockIdx.x;
+  const int dsl = b % dslices, qh = b / dslices;
+  const int qr = qh / H, h = qh - qr * H;
   const int kl = pos_dev ? *pos_dev + qrows : keylen;
-  const int ns = (kl + kpw - 1) / kpw < nsplit ? (kl + kpw - 1) / kpw : nsplit;
-  const size_t stride = (size_t)hd + 2;
+  int ns = nsplit;
+  if (kpw > 0 && (kl + kpw - 1) / kpw < ns) ns = (kl + kpw - 1) / kpw;
+  const size_t stride = (size_t)hd + 2, sstep = (size_t)H * stride;
   const float *pb = part + ((size_t)qr * nsplit * H + h) * stride;
-  float M = -3.4e38f;
-  for (int s = 0; s < ns; ++s) M = fmaxf(M, pb[(size_t)s * H * stride]);
-  float L = 0.f;
-  for (int s = 0; s < ns; ++s) {
-    const float *ps = pb + (size_t)s * H * stride;
-    L += expf(ps[0] - M) * ps[1];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int d = dsl * 64 + lane;
+  float mv[U], lv[U], ov[U];
+#pragma unroll
+  for (int i = 0; i < U; ++i) {
+    const int sp = wave + 4 * i;
+    const float *ps = pb + (size_t)(sp < ns ? sp : 0) * sstep;  // clamped: no branch
+    const float m0 = ps[0], l0 = ps[1], o0 = ps[2 + d];
+    mv[i] = sp < ns ? m0 : -3.4e38f;
+    lv[i] = sp < ns ? l0 : 0.f;
+    ov[i] = sp < ns ? o0 : 0.f;
   }
-  const float invL = 1.f / L;
-  for (int d = threadIdx.x; d < hd; d += kBlock) {
-    float acc = 0.f;
-    for (int s = 0; s < ns; ++s) {
-      const float *ps = pb + (size_t)s * H * stride;
-      acc += expf(ps[0] - M) * ps[2 + d];
-    }
-    out[((size_t)qr * H + h) * hd + d] = acc * invL;
+  // block max of all split maxima (splits past 4U are read again below)
+  float mx = -3.4e38f;
+#pragma unroll
+  for (int i = 0; i < U; ++i) mx = fmaxf(mx, mv[i]);
+  for (int sp = wave + 4 * U; sp < ns; sp += 4) mx = fmaxf(mx, pb[(size_t)sp * sstep]);
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+  if (lane == 0) red[wave] = mx;
+  __syncthreads();
+  const float M = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  float acc = 0.f, lsum = 0.f;
+#pragma unroll
+  for (int i = 0; i < U; ++i) {
+    const float w = expf(mv[i] - M);
+    acc = fmaf(w, ov[i], acc);
+    lsum = fmaf(w, lv[i], lsum);
+  }
+  for (int sp = wave + 4 * U; sp < ns; sp += 4) {
+    const float *ps = pb + (size_t)sp * sstep;
+    const float w = expf(ps[0] - M);
+    acc = fmaf(w, ps[2 + d], acc);
+    lsum = fmaf(w, ps[1], lsum);
+  }
+  accs[wave][lane] = acc;
+  if (lane == 0) ls4[wave] = lsum;
+  __syncthreads();
+  if (wave == 0) {
+    const float L = ls4[0] + ls4[1] + ls4[2] + ls4[3];
+    out[((size_t)qr * H + h) * hd + d] =
+        (accs[0][lane] + accs[1][lane] + accs[2][lane] + accs[3][lane]) / L;
   }
 }
 
@@ -355,15 +542,52 @@ int launch_norm_rope(const float *x, int rows, int heads, int hd, int pos0, cons
   return G4_OK;
 }
 
+// Splits of the single-query kernel for up to max_keylen keys.
+int dec_splits(int max_keylen) {
+  const int need = (max_keylen + kDecMaxKeys - 1) / kDecMaxKeys;
+  return need > 64 ? need : 64;
+}
+
+// Keys per split for the multi-query kernel such that the split count stays
+// within the combine's limit.
+int split_kpw(int kpw, int max_keylen) {
+  const int min_kpw = (max_keylen + kMaxSplits - 1) / kMaxSplits;
+  return kpw > min_kpw ? kpw : min_kpw;
+}
+
 size_t attention_part_floats(int qrows, int heads, int hd, int max_keylen, int kpw) {
-  const int nsplit = (max_keylen + kpw - 1) / kpw;
-  return (size_t)qrows * nsplit * heads * ((size_t)hd + 2);
+  const size_t multi = (size_t)qrows * ((max_keylen + split_kpw(kpw, max_keylen) - 1) /
+                                        split_kpw(kpw, max_keylen));
+  const size_t single = (size_t)dec_splits(max_keylen);
+  return (multi > single ? multi : single) * heads * ((size_t)hd + 2);
 }
 
 int launch_attention(const float *q, const float *k, const float *v, int qrows, int heads,
                      int hd, int keylen, int qpos0, const int *pos_dev, int max_keylen,
                      bool sliding, int window, int kpw, float *part, float *out) {
   if (qrows == 0) return G4_OK;
+  if (max_keylen > kDecMaxKeys * kMaxSplits)
+    return fail(G4_E_ARG, "attention: %d keys exceed the supported %d", max_keylen,
+                kDecMaxKeys * kMaxSplits);
+  if (qrows == 1) {
+    // one query row: position keylen - 1 (or *pos_dev), keys split over the grid
+    const int ns = dec_splits(max_keylen);
+    const dim3 grid(ns);
+    const int sl = sliding ? 1 : 0;
+    switch (hd / 64) {
+      case 1: hipLaunchKernelGGL(attn_dec_kernel<1>, grid, dim3(kBlock), 0, stream(), q, k, v, part, heads, keylen, pos_dev, sl, window); break;
+      case 2: hipLaunchKernelGGL(attn_dec_kernel<2>, grid, dim3(kBlock), 0, stream(), q, k, v, part, heads, keylen, pos_dev, sl, window); break;
+      case 4: hipLaunchKernelGGL(attn_dec_kernel<4>, grid, dim3(kBlock), 0, stream(), q, k, v, part, heads, keylen, pos_dev, sl, window); break;
+      case 8: hipLaunchKernelGGL(attn_dec_kernel<8>, grid, dim3(kBlock), 0, stream(), q, k, v, part, heads, keylen, pos_dev, sl, window); break;
+      default: return fail(G4_E_ARG, "attention: head_dim %d must be 64, 128, 256 or 512", hd);
+    }
+    G4_LAUNCH_CHECK("attn_dec_kernel");
+    hipLaunchKernelGGL(attn_combine_kernel, dim3(heads * (hd / 64)), dim3(kBlock), 0, stream(),
+                       part, heads, hd, 0, ns, keylen, pos_dev, qrows, out);
+    G4_LAUNCH_CHECK("attn_combine_kernel");
+    return G4_OK;
+  }
+  kpw = split_kpw(kpw, max_keylen);
   AttnArgs a;
   a.q = q;
   a.k = k;
@@ -388,8 +612,8 @@ int launch_attention(const float *q, const float *k, const float *v, int qrows, 
     default: return fail(G4_E_ARG, "attention: head_dim %d must be 64, 128, 256 or 512", hd);
   }
   G4_LAUNCH_CHECK("attn_split_kernel");
-  hipLaunchKernelGGL(attn_combine_kernel, dim3(qrows * heads), dim3(kBlock), 0, stream(), part,
-                     heads, hd, kpw, a.nsplit, keylen, pos_dev, qrows, out);
+  hipLaunchKernelGGL(attn_combine_kernel, dim3(qrows * heads * (hd / 64)), dim3(kBlock), 0,
+                     stream(), part, heads, hd, kpw, a.nsplit, keylen, pos_dev, qrows, out);
   G4_LAUNCH_CHECK("attn_combine_kernel");
   return G4_OK;
 }

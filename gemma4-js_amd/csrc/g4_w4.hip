@@ -10,6 +10,7 @@
 // word packed[o*G + g] (G = K/32): a lane that owns a group reads it with one
 // coalesced dwordx4 load.
 #include "g4_internal.h"
+#include "g4_gemv.h"
 
 namespace {
 
@@ -38,37 +39,6 @@ using namespace g4;
 // [c * G + g] so a team's lanes read consecutive chunks, conflict-free):
 //   hi[4][G], lo[4][G] (FP32 input only), sx[G] = 136 * sum of the group.
 // ---------------------------------------------------------------------------
-
-typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2_t;
-
-__device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
-  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a),
-                                         __builtin_bit_cast(bf16x2_t, b), c, false);
-}
-
-constexpr uint32_t kPairMagic = 0x43004300u;  // bf16 pair (128, 128)
-constexpr float kPairBias = 136.f;            // (128 + n) - 136 = n - 8 = q
-
-template <int CTRL>
-__device__ __forceinline__ float dpp_f32(float v) {
-  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, true));
-}
-
-// Sum over aligned teams of L lanes; every lane of the team gets the sum.
-template <int L>
-__device__ __forceinline__ float team_sum(float v) {
-  if (L >= 2) v += dpp_f32<0xB1>(v);   // quad_perm [1,0,3,2]
-  if (L >= 4) v += dpp_f32<0x4E>(v);   // quad_perm [2,3,0,1]
-  if (L >= 8) v += dpp_f32<0x141>(v);  // row_half_mirror
-  if (L >= 16) v += dpp_f32<0x140>(v); // row_mirror
-  if (L >= 32) v += __shfl_xor(v, 16, 64);
-  if (L >= 64) v += __shfl_xor(v, 32, 64);
-  return v;
-}
-
-__device__ __forceinline__ uint32_t bf16_pair(uint32_t lo16, uint32_t hi16) {
-  return (lo16 & 0xffffu) | (hi16 << 16);
-}
 
 // Stage group g of activation row m: 32 values -> hi/lo pair chunks + sum.
 template <bool F32X>
@@ -434,31 +404,6 @@ __global__ __launch_bounds__(TC ? TC : 1024) void w4_gemv1_kernel(
   }
 }
 
-struct Gemv1Plan {
-  int T, IPL, RB;
-  size_t lds;
-};
-
-// Rows per block RB >= 4 (x staging amortised over >= 4 rows), RB * G = T * IPL
-// with T a multiple of 64 up to 1024 and IPL <= 4.
-bool plan_gemv1(int G, bool f32x, Gemv1Plan *p) {
-  for (int RB = 4; RB <= 256; RB *= 2) {
-    const long items = (long)RB * G;
-    if (items % 64) continue;
-    for (int ipl = 1; ipl <= 4; ++ipl) {
-      if (items % ipl) continue;
-      const long T = items / ipl;
-      if (T % 64 || T > 1024) continue;
-      p->T = (int)T;
-      p->IPL = ipl;
-      p->RB = RB;
-      p->lds = (size_t)G * 4 * 16 * (f32x ? 2 : 1) + (size_t)G * 4 + (size_t)RB * G * 4;
-      return p->lds <= 64 * 1024;
-    }
-  }
-  return false;
-}
-
 template <int GC, int TC, int IPL, bool F32X>
 int launch_gemv1_i(const g4_w4 *w, const Gemv1Plan &p, const void *x, void *y, int y_bf16) {
   const int blocks = (w->N + p.RB - 1) / p.RB;
@@ -470,8 +415,11 @@ int launch_gemv1_i(const g4_w4 *w, const Gemv1Plan &p, const void *x, void *y, i
 
 template <bool F32X>
 int launch_gemv1(const g4_w4 *w, const void *x, void *y, int y_bf16) {
+  // FP32 x of a long row is 4 K bytes per block against 4 rows * K / 2 bytes of
+  // weights: from K = 4096 on, 8 rows per block halve that re-read.
   Gemv1Plan p;
-  if (!plan_gemv1(w->G, F32X, &p))
+  const int min_rb = F32X && w->K >= 4096 ? 8 : 4;
+  if (!plan_gemv1(w->G, F32X, &p, min_rb) && !plan_gemv1(w->G, F32X, &p))
     return fail(G4_E_ARG, "g4_w4_linear: no decode GEMV plan for in_dim %d", w->K);
   // compile-time variants for the plans of the Gemma-4-E2B projections
 #define G4_GEMV1_FIXED(GG, TT, II)                                      \
@@ -483,6 +431,9 @@ int launch_gemv1(const g4_w4 *w, const void *x, void *y, int y_bf16) {
   G4_GEMV1_FIXED(192, 768, 1)   // K = 6144
   G4_GEMV1_FIXED(384, 768, 2)   // K = 12288
   G4_GEMV1_FIXED(8, 64, 1)      // K = 256
+  G4_GEMV1_FIXED(128, 1024, 1)  // K = 4096, FP32 x: 8 rows
+  G4_GEMV1_FIXED(192, 768, 2)   // K = 6144, FP32 x: 8 rows
+  G4_GEMV1_FIXED(384, 1024, 3)  // K = 12288, FP32 x: 8 rows
 #undef G4_GEMV1_FIXED
   switch (p.IPL) {
     case 1: return launch_gemv1_i<0, 0, 1, F32X>(w, p, x, y, y_bf16);
