@@ -16,8 +16,10 @@ Algorithmic bytes per GEMV = N*K/2 packed + N*(K/32)*2 scales + K*2 x (BF16)
 
 Extras (same JSON line, "extra"): one E2B sliding decoder layer of 7 GEMVs
 (aggregate GB/s), PLE gather of 1 and 2048 ids over the full [262144, 8960]
-table, the tied BF16 LM head over 262144 rows, and the prefill GEMM
-(M=2048) at both shapes in TFLOP/s.
+table, the tied BF16 LM head over 262144 rows, the prefill GEMM (M=2048) at
+both shapes in TFLOP/s, and the full random-init Gemma-4-E2B decode (prompt
+of 512 random ids, then 256 greedy steps, max_seq 1024): decode tokens/s,
+also reported as "decode_tok_s" on the line, and prefill tokens/s.
 
 cpu_baseline: the oracle's TF.js-semantics FP32 dequant + matMul
 restatement (single-threaded C, the reference's CPU path is single-threaded
@@ -194,6 +196,40 @@ def bench_gemm(reps=3, seed=3):
     return res
 
 
+def bench_decode(prompt=512, steps=256, max_seq=1024, seed=4):
+    """Config 4: random-init Gemma-4-E2B (35 layers, vocab 262144, W4 projections,
+    W4 PLE table, BF16 tied head) - a prompt of random ids, then greedy decode
+    steps, each a replay of the recorded one-token step."""
+    import e2b
+    cfg = g4hip.e2b_config(max_seq)
+    m = e2b.build(cfg, seed)
+    ids = syn.token_ids(seed, prompt, cfg.vocab)
+    m.reset()
+    m.greedy(ids, 0)
+    m.decode(4, want_tokens=False)  # records the decode step
+    g4hip.sync()
+    m.reset()
+    a, b, c = g4hip.Event(), g4hip.Event(), g4hip.Event()
+    a.record()
+    first = m.greedy(ids, 0)  # prefill: forward + head + argmax (synchronises)
+    b.record()
+    m.decode(steps, want_tokens=False)
+    c.record()
+    g4hip.sync()
+    pre_ms, dec_ms = a.elapsed_ms(b), b.elapsed_ms(c)
+    w4 = e2b.w4_bytes(cfg)
+    head = cfg.vocab * cfg.hidden * 2
+    per_token = w4 + head
+    m.free()
+    return {"prompt": prompt, "steps": steps, "max_seq": max_seq,
+            "prefill_ms": pre_ms, "prefill_tok_s": prompt / (pre_ms * 1e-3),
+            "decode_ms": dec_ms, "ms_per_token": dec_ms / steps,
+            "decode_tok_s": steps / (dec_ms * 1e-3),
+            "weight_bytes_per_token": per_token,
+            "weight_gbs": per_token * steps / (dec_ms * 1e-3) / 1e9,
+            "first_token": int(first)}
+
+
 def cpu_baseline(n, k, budget_s=10.0, seed=0):
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import g4oracle
@@ -260,6 +296,9 @@ def main():
         log("prefill GEMM (config 3) ...")
         extra["gemm_prefill"] = bench_gemm()
         log("  ", extra["gemm_prefill"])
+        log("E2B decode (config 4): prompt 512, 256 greedy steps ...")
+        extra["decode_e2b"] = bench_decode()
+        log("  ", extra["decode_e2b"])
 
     cpu = None
     if not args.no_cpu:
@@ -288,6 +327,7 @@ def main():
                      "traffic_source": traffic_src, "kernel": "w4_gemv1_kernel", "avg_launch_us": round(avg_us, 4),
                      "bytes_per_launch": g["bytes_per_step"]},
         "cpu_baseline": cpu,
+        "decode_tok_s": round(extra["decode_e2b"]["decode_tok_s"], 1) if "decode_e2b" in extra else None,
         "extra": extra,
     }
     print(json.dumps(line), flush=True)
