@@ -302,7 +302,7 @@ __global__ __launch_bounds__(TC ? TC : 1024) void fused_gemv_kernel(FusedArgs A,
 
 template <int GC, int TC, int IPL, int PRO, int EPI>
 int launch_fused_i(const FusedArgs &a, const Gemv1Plan &p, int ngroups, size_t lds) {
-  const int cap = 2 * (cu_count() > 0 ? cu_count() : 256);
+  const int cap = cu_count() > 0 ? cu_count() : 256;
   const int blocks = ngroups < cap ? ngroups : cap;
   hipLaunchKernelGGL((fused_gemv_kernel<GC, TC, IPL, PRO, EPI>), dim3(blocks), dim3(p.T), lds,
                      stream(), a, p.RB, ngroups);
@@ -310,27 +310,27 @@ int launch_fused_i(const FusedArgs &a, const Gemv1Plan &p, int ngroups, size_t l
   return G4_OK;
 }
 
-// Rows per block: enough that ~2 blocks per CU cover all rows with every
-// weight load in flight at once (up to 4 groups per thread); at least 8.
+// Rows per block: the largest power of two (at least 8) not above
+// rows / (2 CUs), every weight load of a row group issued at once (up to 4
+// groups per thread); launched with one block per CU looping over the groups
+// (measured best for the E2B gate/up shapes: 16 and 32 rows).
 bool plan_fused(int G, int total_rows, Gemv1Plan *p) {
   const int cus = cu_count() > 0 ? cu_count() : 256;
   const int target = (total_rows + 2 * cus - 1) / (2 * cus);
-  int best = 0;
+  bool found = false;
   for (int RB = 8; RB <= 256; RB *= 2) {
+    if (found && RB > target) break;
     for (int ipl = 1; ipl <= 4; ++ipl) {
       const long items = (long)RB * G;
       if (items % ipl || (items / ipl) % 64 || items / ipl > 1024) continue;
-      if (!best || RB <= target || RB == 8) {
-        best = RB;
-        p->T = (int)(items / ipl);
-        p->IPL = ipl;
-        p->RB = RB;
-      }
+      found = true;
+      p->T = (int)(items / ipl);
+      p->IPL = ipl;
+      p->RB = RB;
       break;
     }
-    if (best && RB >= target) break;
   }
-  if (!best) return plan_gemv1(G, true, p, 4);
+  if (!found) return plan_gemv1(G, true, p, 4);
   p->lds = (size_t)G * 4 * 16 * 2 + (size_t)G * 4 + (size_t)p->RB * G * 4;
   return p->lds <= 64 * 1024;
 }
@@ -362,6 +362,7 @@ int launch_fused(FusedArgs a) {
     if (p.T == 768 && p.IPL == 1) return launch_fused_i<48, 768, 1, PRO, EPI>(a, p, groups, lds);
     if (p.T == 768 && p.IPL == 2) return launch_fused_i<48, 768, 2, PRO, EPI>(a, p, groups, lds);
     if (p.T == 768 && p.IPL == 4) return launch_fused_i<48, 768, 4, PRO, EPI>(a, p, groups, lds);
+    if (p.T == 1024 && p.IPL == 3) return launch_fused_i<48, 1024, 3, PRO, EPI>(a, p, groups, lds);
   }
   switch (p.IPL) {
     case 1: return launch_fused_i<0, 0, 1, PRO, EPI>(a, p, groups, lds);
