@@ -712,6 +712,172 @@ napi_value F_timeMs(napi_env env, napi_callback_info info) {
   return r;
 }
 
+// ---- remaining GPUOps (gpu-runtime.js:1325-1369) ----------------------------------
+// Each takes DeviceBuffers (whole-buffer pointers) and plain numbers and
+// enqueues one C-ABI op; the JS GPUOps allocates the outputs.
+
+bool dev(napi_env env, napi_value v, const char *what, void **out) {
+  napi_value no_offset;
+  napi_get_undefined(env, &no_offset);
+  return buf_at(env, v, no_offset, what, out);
+}
+
+bool dev_or_null(napi_env env, napi_value v, const char *what, void **out) {
+  napi_valuetype t;
+  napi_typeof(env, v, &t);
+  if (t == napi_null || t == napi_undefined) {
+    *out = nullptr;
+    return true;
+  }
+  return dev(env, v, what, out);
+}
+
+bool ints(napi_env env, napi_value *argv, const int *idx, int64_t *out, int n,
+          const char *const *names) {
+  for (int i = 0; i < n; ++i)
+    if (!to_i64(env, argv[idx[i]], &out[i], names[i])) return false;
+  return true;
+}
+
+// rms(x, rows, width, scale | null, eps, y)
+napi_value F_rms(napi_env env, napi_callback_info info) {
+  napi_value a[6], self;
+  if (!get_args(env, info, 6, a, &self)) return nullptr;
+  void *x, *sc, *y;
+  int64_t rows, width;
+  double eps;
+  if (!dev(env, a[0], "x", &x) || !to_i64(env, a[1], &rows, "rows") ||
+      !to_i64(env, a[2], &width, "width") || !dev_or_null(env, a[3], "scale", &sc) ||
+      !to_f64(env, a[4], &eps, "eps") || !dev(env, a[5], "y", &y))
+    return nullptr;
+  G4_CALL(env, g4_rms((const float *)x, (int)rows, (int)width, (const float *)sc, (float)eps,
+                      (float *)y));
+  return undefined(env);
+}
+
+// addScale(a, b, n, scale, y)
+napi_value F_addScale(napi_env env, napi_callback_info info) {
+  napi_value a[5], self;
+  if (!get_args(env, info, 5, a, &self)) return nullptr;
+  void *x, *z, *y;
+  int64_t n;
+  double s;
+  if (!dev(env, a[0], "a", &x) || !dev(env, a[1], "b", &z) || !to_i64(env, a[2], &n, "n") ||
+      !to_f64(env, a[3], &s, "scale") || !dev(env, a[4], "y", &y))
+    return nullptr;
+  G4_CALL(env, g4_add_scale((const float *)x, (const float *)z, (size_t)n, (float)s, (float *)y));
+  return undefined(env);
+}
+
+// scale(a, n, s, y)
+napi_value F_scale(napi_env env, napi_callback_info info) {
+  napi_value a[4], self;
+  if (!get_args(env, info, 4, a, &self)) return nullptr;
+  void *x, *y;
+  int64_t n;
+  double s;
+  if (!dev(env, a[0], "a", &x) || !to_i64(env, a[1], &n, "n") ||
+      !to_f64(env, a[2], &s, "scale") || !dev(env, a[3], "y", &y))
+    return nullptr;
+  G4_CALL(env, g4_scale((const float *)x, (size_t)n, (float)s, (float *)y));
+  return undefined(env);
+}
+
+// geluMul(gate, up, n, y)
+napi_value F_geluMul(napi_env env, napi_callback_info info) {
+  napi_value a[4], self;
+  if (!get_args(env, info, 4, a, &self)) return nullptr;
+  void *g, *u, *y;
+  int64_t n;
+  if (!dev(env, a[0], "gate", &g) || !dev(env, a[1], "up", &u) || !to_i64(env, a[2], &n, "n") ||
+      !dev(env, a[3], "y", &y))
+    return nullptr;
+  G4_CALL(env, g4_gelu_mul((const float *)g, (const float *)u, (size_t)n, (float *)y));
+  return undefined(env);
+}
+
+// geluPle(gate, ple, rows, layer, width, layers, y)
+napi_value F_geluPle(napi_env env, napi_callback_info info) {
+  napi_value a[7], self;
+  if (!get_args(env, info, 7, a, &self)) return nullptr;
+  void *g, *p, *y;
+  int64_t v[4];
+  static const int idx[4] = {2, 3, 4, 5};
+  static const char *const names[4] = {"rows", "layer", "width", "layers"};
+  if (!dev(env, a[0], "gate", &g) || !dev(env, a[1], "ple", &p) || !ints(env, a, idx, v, 4, names) ||
+      !dev(env, a[6], "y", &y))
+    return nullptr;
+  G4_CALL(env, g4_gelu_ple((const float *)g, (const float *)p, (int)v[0], (int)v[1], (int)v[2],
+                           (int)v[3], (float *)y));
+  return undefined(env);
+}
+
+// normRope(x, rows, heads, hd, pos0, scale, ropeAngles, base, eps, y)
+napi_value F_normRope(napi_env env, napi_callback_info info) {
+  napi_value a[10], self;
+  if (!get_args(env, info, 10, a, &self)) return nullptr;
+  void *x, *sc, *y;
+  int64_t v[4], angles;
+  double base, eps;
+  static const int idx[4] = {1, 2, 3, 4};
+  static const char *const names[4] = {"rows", "heads", "hd", "pos0"};
+  if (!dev(env, a[0], "x", &x) || !ints(env, a, idx, v, 4, names) ||
+      !dev(env, a[5], "scale", &sc) || !to_i64(env, a[6], &angles, "ropeAngles") ||
+      !to_f64(env, a[7], &base, "base") || !to_f64(env, a[8], &eps, "eps") ||
+      !dev(env, a[9], "y", &y))
+    return nullptr;
+  G4_CALL(env, g4_norm_rope((const float *)x, (int)v[0], (int)v[1], (int)v[2], (int)v[3],
+                            (const float *)sc, (int)angles, (float)base, (float)eps, (float *)y));
+  return undefined(env);
+}
+
+// attention(q, k, v, qrows, heads, hd, keylen, qpos0, sliding, window, y)
+napi_value F_attention(napi_env env, napi_callback_info info) {
+  napi_value a[11], self;
+  if (!get_args(env, info, 11, a, &self)) return nullptr;
+  void *q, *k, *vv, *y;
+  int64_t v[7];
+  static const int idx[7] = {3, 4, 5, 6, 7, 8, 9};
+  static const char *const names[7] = {"qrows", "heads", "hd", "keylen", "qpos0", "sliding",
+                                       "window"};
+  if (!dev(env, a[0], "q", &q) || !dev(env, a[1], "k", &k) || !dev(env, a[2], "v", &vv) ||
+      !ints(env, a, idx, v, 7, names) || !dev(env, a[10], "y", &y))
+    return nullptr;
+  G4_CALL(env, g4_attention((const float *)q, (const float *)k, (const float *)vv, (int)v[0],
+                            (int)v[1], (int)v[2], (int)v[3], (int)v[4], (int)v[5], (int)v[6],
+                            (float *)y));
+  return undefined(env);
+}
+
+// pleMix(proj, normScale, tokenPle, rows, width, layers, y)
+napi_value F_pleMix(napi_env env, napi_callback_info info) {
+  napi_value a[7], self;
+  if (!get_args(env, info, 7, a, &self)) return nullptr;
+  void *p, *ns, *tp, *y;
+  int64_t v[3];
+  static const int idx[3] = {3, 4, 5};
+  static const char *const names[3] = {"rows", "width", "layers"};
+  if (!dev(env, a[0], "proj", &p) || !dev(env, a[1], "normScale", &ns) ||
+      !dev(env, a[2], "tokenPle", &tp) || !ints(env, a, idx, v, 3, names) ||
+      !dev(env, a[6], "y", &y))
+    return nullptr;
+  G4_CALL(env, g4_ple_mix((const float *)p, (const float *)ns, (const float *)tp, (int)v[0],
+                          (int)v[1], (int)v[2], (float *)y));
+  return undefined(env);
+}
+
+// argmax(x, n, out): out[0] = first index of the largest finite x, or -1
+napi_value F_argmax(napi_env env, napi_callback_info info) {
+  napi_value a[3], self;
+  if (!get_args(env, info, 3, a, &self)) return nullptr;
+  void *x, *o;
+  int64_t n;
+  if (!dev(env, a[0], "x", &x) || !to_i64(env, a[1], &n, "n") || !dev(env, a[2], "out", &o))
+    return nullptr;
+  G4_CALL(env, g4_argmax((const float *)x, (int)n, (int32_t *)o));
+  return undefined(env);
+}
+
 napi_value define_class(napi_env env, napi_value exports, const char *name, napi_callback ctor,
                         const napi_property_descriptor *props, size_t nprops, napi_ref *ref) {
   napi_value cls;
@@ -748,7 +914,10 @@ napi_value Init(napi_env env, napi_value exports) {
       METHOD("init", F_init), METHOD("deviceInfo", F_deviceInfo), METHOD("sync", F_sync),
       METHOD("copy", F_copy), METHOD("bf16Head", F_bf16Head),
       METHOD("encoderBegin", F_encoderBegin), METHOD("encoderFinish", F_encoderFinish),
-      METHOD("timeMs", F_timeMs)};
+      METHOD("timeMs", F_timeMs), METHOD("rms", F_rms), METHOD("addScale", F_addScale),
+      METHOD("scale", F_scale), METHOD("geluMul", F_geluMul), METHOD("geluPle", F_geluPle),
+      METHOD("normRope", F_normRope), METHOD("attention", F_attention),
+      METHOD("pleMix", F_pleMix), METHOD("argmax", F_argmax)};
   NAPI_CALL(env, napi_define_properties(env, exports, sizeof fns / sizeof fns[0], fns));
   napi_value v;
   napi_create_int32(env, G4_F32, &v);

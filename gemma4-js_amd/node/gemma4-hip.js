@@ -1,0 +1,283 @@
+'use strict';
+// Gemma4WebGPU (custom-webgpu/gemma4-webgpu.js:139-502) for Node 12 on the HIP
+// path: the same load / forward / logits / greedy surface and the same op
+// sequence per layer (encodeLayer, gemma4-webgpu.js:215-301), driven through
+// hip-runtime.js's GPUOps instead of WebGPU.  The reference module cannot be
+// loaded by Node 12 (ES modules, optional chaining), so the driver is
+// restated here; the checkpoint reader, PLE bundle and ops keep the
+// reference's interfaces.
+//
+// Geometry: the reference fixes HIDDEN 1536, PLE 256, LAYERS 35, HEADS 8 and
+// the E2B layer schedule spec(i) (gemma4-webgpu.js:12, 65-77).  They are the
+// defaults here; options override them (used to run small checkpoints of the
+// same layout).
+
+const rt = require('./hip-runtime.js');
+
+const U = rt.GPUBufferUsage;
+
+// spec(i) of gemma4-webgpu.js:65-77: every 5th layer global (head_dim 512,
+// RoPE base 1e6 on a quarter of the pairs), intermediate 12288 from layer 15,
+// layers >= 15 reuse the KV caches of layers 13 (sliding) and 14 (global).
+function e2bSpec(i) {
+  const full = (i + 1) % 5 === 0;
+  return {
+    full,
+    headDim: full ? 512 : 256,
+    intermediate: i < 15 ? 6144 : 12288,
+    shared: i >= 15,
+    storeShared: i === 13 || i === 14,
+    attentionType: full ? 'full' : 'sliding',
+    ropeBase: full ? 1000000 : 10000,
+    ropeProp: full ? 0.25 : 1.0,
+  };
+}
+
+function layerNames(i, s) {
+  const root = `model.language_model.layers.${i}`;
+  const names = {
+    q: `${root}.self_attn.q_proj`, o: `${root}.self_attn.o_proj`,
+    gate: `${root}.mlp.gate_proj`, up: `${root}.mlp.up_proj`, down: `${root}.mlp.down_proj`,
+    pleGate: `${root}.per_layer_input_gate`, pleProj: `${root}.per_layer_projection`,
+  };
+  if (!s.shared) {
+    names.k = `${root}.self_attn.k_proj`;
+    names.v = `${root}.self_attn.v_proj`;
+  }
+  return names;
+}
+
+async function scaleBuffer(device, reader, name) {
+  return rt.uploadF32(device, await reader.bf16(name), U.STORAGE, name);
+}
+
+// KVCache (gemma4-webgpu.js:117-137): appends with copyBufferToBuffer.
+class KVCache {
+  constructor(device, headDim, maxSeq, label) {
+    this.headDim = headDim;
+    this.maxSeq = maxSeq;
+    this.length = 0;
+    this.k = rt.createBuffer(device, maxSeq * headDim * 4, U.STORAGE | U.COPY_DST | U.COPY_SRC, `${label}:k`);
+    this.v = rt.createBuffer(device, maxSeq * headDim * 4, U.STORAGE | U.COPY_DST | U.COPY_SRC, `${label}:v`);
+  }
+  append(encoder, kNew, vNew, rows, startPos) {
+    if (startPos !== this.length) throw new Error(`KV append position ${startPos} != cache length ${this.length}`);
+    if (startPos + rows > this.maxSeq) throw new Error(`KV cache capacity ${this.maxSeq} exceeded`);
+    const off = startPos * this.headDim * 4, bytes = rows * this.headDim * 4;
+    encoder.copyBufferToBuffer(kNew, 0, this.k, off, bytes);
+    encoder.copyBufferToBuffer(vNew, 0, this.v, off, bytes);
+    this.length += rows;
+  }
+  dispose() { this.k.destroy(); this.v.destroy(); }
+}
+
+class Gemma4Hip {
+  // reader: SafeFileReader over the CORE checkpoint (plus pleRowsToGpu when a
+  // W4 PLE bundle is attached, as the distribution reader has).
+  constructor(device, reader, opts = {}) {
+    this.device = device;
+    this.reader = reader;
+    this.maxSeq = opts.maxSeq || 512;
+    this.lmChunkRows = opts.lmChunkRows || 4096;
+    this.log = opts.log || (() => {});
+    this.hidden = opts.hidden || 1536;
+    this.pleDim = opts.pleDim || 256;
+    this.numLayers = opts.layers || 35;
+    this.heads = opts.heads || 8;
+    this.window = opts.window || 512;
+    this.spec = opts.spec || e2bSpec;
+    this.ops = new rt.GPUOps(device, { pleWidth: this.pleDim, pleLayers: this.numLayers });
+    this.layers = [];
+    this.caches = [];
+    this.shared = {};
+    this.lmChunks = [];
+    this.loaded = false;
+  }
+
+  async loadLayer(i) {
+    const root = `model.language_model.layers.${i}`, s = this.spec(i), reader = this.reader;
+    const linear = {};
+    const names = layerNames(i, s);
+    for (const key of Object.keys(names)) {
+      linear[key] = await rt.GPUW4Linear.load(this.device, reader, names[key]);
+    }
+    const norm = {
+      input: await scaleBuffer(this.device, reader, `${root}.input_layernorm.weight`),
+      postAttn: await scaleBuffer(this.device, reader, `${root}.post_attention_layernorm.weight`),
+      preFfw: await scaleBuffer(this.device, reader, `${root}.pre_feedforward_layernorm.weight`),
+      postFfw: await scaleBuffer(this.device, reader, `${root}.post_feedforward_layernorm.weight`),
+      postPle: await scaleBuffer(this.device, reader, `${root}.post_per_layer_input_norm.weight`),
+      q: await scaleBuffer(this.device, reader, `${root}.self_attn.q_norm.weight`),
+      k: s.shared ? null : await scaleBuffer(this.device, reader, `${root}.self_attn.k_norm.weight`),
+    };
+    const skipScale = await reader.scalarBF16(`${root}.layer_scalar`);
+    return { i, s, linear, norm, skipScale };
+  }
+
+  // load() (gemma4-webgpu.js:150-189)
+  async load() {
+    this.log('Loading top-level W4A16 projection...');
+    this.topProj = await rt.GPUW4Linear.load(this.device, this.reader, 'model.language_model.per_layer_model_projection');
+    this.pleNorm = await scaleBuffer(this.device, this.reader, 'model.language_model.per_layer_projection_norm.weight');
+    this.finalNorm = await scaleBuffer(this.device, this.reader, 'model.language_model.norm.weight');
+    this.log(`Loading ${this.numLayers} quantized transformer layers...`);
+    for (let i = 0; i < this.numLayers; i++) {
+      const layer = await this.loadLayer(i);
+      this.layers.push(layer);
+      this.caches[i] = layer.s.shared ? null : new KVCache(this.device, layer.s.headDim, this.maxSeq, `layer${i}`);
+    }
+    this.log('Loading tied BF16 LM-head embedding in device chunks...');
+    const info = this.reader.info('model.language_model.embed_tokens.weight');
+    this.vocab = info.shape[0];
+    const width = info.shape[1], rowBytes = width * 2;
+    if (width !== this.hidden) throw new Error(`embedding width ${width} != hidden ${this.hidden}`);
+    for (let start = 0; start < this.vocab; start += this.lmChunkRows) {
+      const rows = Math.min(this.lmChunkRows, this.vocab - start);
+      const ab = await this.reader.rangeInTensor('model.language_model.embed_tokens.weight', start * rowBytes, rows * rowBytes);
+      this.lmChunks.push({ start, rows, buffer: rt.uploadBytes(this.device, new Uint8Array(ab), U.STORAGE | U.COPY_DST, `lm-head:${start}`) });
+    }
+    this.loaded = true;
+    this.log('Device model preload complete.');
+  }
+
+  resetCache() {
+    for (const c of this.caches) if (c) c.length = 0;
+    this.shared = {};
+  }
+
+  // inputBuffers (gemma4-webgpu.js:198-215)
+  async inputBuffers(tokenIds) {
+    const embed = await this.reader.bf16Rows('model.language_model.embed_tokens.weight', tokenIds);
+    let ple;
+    if (typeof this.reader.pleRowsToGpu === 'function') {
+      ple = await this.reader.pleRowsToGpu(this.device, tokenIds);
+    } else {
+      ple = rt.uploadF32(this.device, await this.reader.bf16Rows('model.language_model.embed_tokens_per_layer.weight', tokenIds), U.STORAGE, 'token-ple');
+    }
+    return { embed: rt.uploadF32(this.device, embed, U.STORAGE, 'token-embed'), ple };
+  }
+
+  // encodeLayer (gemma4-webgpu.js:215-301): one decoder layer, every op output
+  // a fresh buffer that goes on `garbage` once consumed.
+  encodeLayer(encoder, layer, hidden, perLayer, rows, startPos, garbage) {
+    const ops = this.ops, s = layer.s, L = layer.linear, N = layer.norm, H = this.hidden;
+    const nHidden = rows * H;
+    const trash = (x) => { if (x) garbage.push(x); return x; };
+    const pre = ops.rms(encoder, hidden, rows, H, N.input, garbage);
+    const q = ops.normRope(encoder, trash(ops.w4(encoder, L.q, pre, rows, garbage)), rows, this.heads, s.headDim, startPos, N.q, s.ropeProp, s.ropeBase, garbage);
+    let cache;
+    if (s.shared) {
+      cache = this.shared[s.attentionType];
+      if (!cache) throw new Error(`Missing shared ${s.attentionType} KV cache at layer ${layer.i}`);
+    } else {
+      const k = ops.normRope(encoder, trash(ops.w4(encoder, L.k, pre, rows, garbage)), rows, 1, s.headDim, startPos, N.k, s.ropeProp, s.ropeBase, garbage);
+      const v = ops.rms(encoder, trash(ops.w4(encoder, L.v, pre, rows, garbage)), rows, s.headDim, null, garbage);
+      cache = this.caches[layer.i];
+      cache.append(encoder, k, v, rows, startPos);
+      trash(k);
+      trash(v);
+      if (s.storeShared) this.shared[s.attentionType] = cache;
+    }
+    trash(pre);
+    const context = trash(ops.attention(encoder, q, cache.k, cache.v, rows, this.heads, s.headDim, startPos + rows, startPos, !s.full, this.window, garbage));
+    trash(q);
+    const attnNorm = trash(ops.rms(encoder, trash(ops.w4(encoder, L.o, context, rows, garbage)), rows, H, N.postAttn, garbage));
+    const attnResidual = ops.addScale(encoder, hidden, attnNorm, nHidden, 1, garbage);
+    trash(hidden);
+    const preFfw = trash(ops.rms(encoder, attnResidual, rows, H, N.preFfw, garbage));
+    const gate = trash(ops.w4(encoder, L.gate, preFfw, rows, garbage));
+    const up = trash(ops.w4(encoder, L.up, preFfw, rows, garbage));
+    const act = trash(ops.geluMul(encoder, gate, up, rows * s.intermediate, garbage));
+    const ffwNorm = trash(ops.rms(encoder, trash(ops.w4(encoder, L.down, act, rows, garbage)), rows, H, N.postFfw, garbage));
+    const ffwResidual = trash(ops.addScale(encoder, attnResidual, ffwNorm, nHidden, 1, garbage));
+    trash(attnResidual);
+    const pm = trash(ops.geluPle(encoder, trash(ops.w4(encoder, L.pleGate, ffwResidual, rows, garbage)), perLayer, rows, layer.i, garbage));
+    const pn = trash(ops.rms(encoder, trash(ops.w4(encoder, L.pleProj, pm, rows, garbage)), rows, H, N.postPle, garbage));
+    return ops.addScale(encoder, ffwResidual, pn, nHidden, layer.skipScale, garbage);
+  }
+
+  // forward (gemma4-webgpu.js:303-402); returns the final-norm last row [hidden]
+  async forward(tokenIds, startPos) {
+    if (!this.loaded) throw new Error('Model not loaded.');
+    const rows = tokenIds.length, H = this.hidden, P = this.pleDim, NL = this.numLayers;
+    const inp = await this.inputBuffers(tokenIds);
+    let encoder = this.device.createCommandEncoder();
+    let garbage = [];
+    let hidden = this.ops.scale(encoder, inp.embed, rows * H, Math.sqrt(H), garbage);
+    const projected = this.ops.w4(encoder, this.topProj, hidden, rows, garbage);
+    const projectedScaled = this.ops.scale(encoder, projected, rows * NL * P, 1 / Math.sqrt(H), garbage);
+    const perLayer = this.ops.pleMix(encoder, projectedScaled, this.pleNorm, inp.ple, rows, garbage);
+    garbage.push(inp.embed, inp.ple, projected, projectedScaled);
+    this.device.queue.submit([encoder.finish()]);
+    for (const b of garbage) b.destroy();
+    for (const layer of this.layers) {
+      encoder = this.device.createCommandEncoder();
+      garbage = [];
+      hidden = this.encodeLayer(encoder, layer, hidden, perLayer, rows, startPos, garbage);
+      this.device.queue.submit([encoder.finish()]);
+      for (const b of garbage) b.destroy();
+    }
+    perLayer.destroy();
+    encoder = this.device.createCommandEncoder();
+    garbage = [];
+    const final = this.ops.rms(encoder, hidden, rows, H, this.finalNorm, garbage);
+    const last = this.ops.emptyF32(H, 'last-hidden');
+    encoder.copyBufferToBuffer(final, (rows - 1) * H * 4, last, 0, H * 4);
+    garbage.push(hidden, final);
+    this.device.queue.submit([encoder.finish()]);
+    for (const b of garbage) b.destroy();
+    return last;
+  }
+
+  // logits (gemma4-webgpu.js:404-431)
+  async logits(lastHidden) {
+    const logits = this.ops.emptyF32(this.vocab, 'logits');
+    const encoder = this.device.createCommandEncoder();
+    for (const c of this.lmChunks) this.ops.headChunk(encoder, lastHidden, c.buffer, logits, c.start, c.rows, null, this.hidden);
+    this.device.queue.submit([encoder.finish()]);
+    const out = await rt.readF32(this.device, logits, this.vocab);
+    logits.destroy();
+    return out;
+  }
+
+  // greedy (gemma4-webgpu.js:441-481)
+  async greedy(tokenIds, startPos) {
+    const h = await this.forward(tokenIds, startPos);
+    const l = await this.logits(h);
+    h.destroy();
+    let finite = 0;
+    for (let i = 0; i < l.length; i++) if (Number.isFinite(l[i])) finite++;
+    if (finite !== l.length) throw new Error(`Non-finite logits: ${l.length - finite}/${l.length}`);
+    const top10 = rt.topK(l, 10);
+    return { logits: l, top10, nextTokenId: top10[0].tokenId };
+  }
+
+  cacheSummary() {
+    let bytes = 0, caches = 0;
+    for (const c of this.caches) if (c) { caches++; bytes += c.length * c.headDim * 4 * 2; }
+    return { caches, bytes };
+  }
+
+  dispose() {
+    if (this.topProj) this.topProj.dispose();
+    if (this.pleNorm) this.pleNorm.destroy();
+    if (this.finalNorm) this.finalNorm.destroy();
+    for (const l of this.layers) {
+      for (const x of Object.values(l.linear)) x.dispose();
+      for (const x of Object.values(l.norm)) if (x) x.destroy();
+    }
+    for (const c of this.caches) if (c) c.dispose();
+    for (const c of this.lmChunks) c.buffer.destroy();
+    this.ops.dispose();
+  }
+}
+
+// The distribution reader: the CORE safetensors reader plus pleRowsToGpu from
+// a device-resident W4 PLE bundle (gpu-runtime.js:905-907, 993-995).
+function withPleBundle(reader, bundle) {
+  const r = Object.create(reader);
+  r.pleRowsToGpu = (device, ids) => bundle.rowsToGpu(device, ids);
+  return r;
+}
+
+module.exports = { Gemma4Hip, KVCache, e2bSpec, withPleBundle };

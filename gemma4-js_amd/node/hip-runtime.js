@@ -222,21 +222,71 @@ class GPUW4Linear {
 
 // ---- ops (gpu-runtime.js:1295-1378) ---------------------------------------------------
 
-function notOnHipPath(name) {
-  return function () {
-    throw new Error(`GPUOps.${name} is not implemented on the HIP path; only the W4A16 linear, ` +
-      'the PLE gather and the tied BF16 head are');
-  };
-}
+// The reference's PLE geometry (gpu-runtime.js:1344-1347, 1366-1369: 256-wide
+// rows for 35 layers); a GPUOps built for another model passes its own.
+const PLE_WIDTH = 256, PLE_LAYERS = 35, RMS_EPS = 1e-6;
 
 class GPUOps {
-  constructor(device) { this.device = device; }
+  constructor(device, { pleWidth = PLE_WIDTH, pleLayers = PLE_LAYERS } = {}) {
+    this.device = device;
+    this.pleWidth = pleWidth;
+    this.pleLayers = pleLayers;
+  }
   track(garbage, buffer) { if (garbage) garbage.push(buffer); return buffer; }
   emptyF32(n, label = '') { return createBuffer(this.device, n * 4, U.STORAGE | U.COPY_SRC | U.COPY_DST, label); }
   // y[rows, outDim] = x[rows, inDim] . W^T, FP32 in and out (gpu-runtime.js:1316-1324)
   w4(encoder, linear, x, rows, garbage = null) {
     const y = this.emptyF32(rows * linear.outDim, `${linear.name}:out`);
     linear.weight.linear(x, F32, rows, y, F32);
+    return y;
+  }
+  // RMS_SHADER (gpu-runtime.js:1325-1332): y = x / rms(x) * (scale or 1), eps 1e-6
+  rms(encoder, x, rows, width, scale = null, garbage = null) {
+    const y = this.emptyF32(rows * width, 'rms-out');
+    native.rms(x, rows, width, scale, RMS_EPS, y);
+    return y;
+  }
+  // ADD_SCALE_SHADER (gpu-runtime.js:1333-1336): y = (a + b) * scale
+  addScale(encoder, a, b, n, scale = 1, garbage = null) {
+    const y = this.emptyF32(n, 'add-out');
+    native.addScale(a, b, n, scale, y);
+    return y;
+  }
+  // SCALE_SHADER (gpu-runtime.js:1337-1340): y = a * s
+  scale(encoder, a, n, s, garbage = null) {
+    const y = this.emptyF32(n, 'scale-out');
+    native.scale(a, n, s, y);
+    return y;
+  }
+  // GELU_MUL_SHADER (gpu-runtime.js:1341-1344): y = gelu(gate) * up
+  geluMul(encoder, gate, up, n, garbage = null) {
+    const y = this.emptyF32(n, 'gelu-mul');
+    native.geluMul(gate, up, n, y);
+    return y;
+  }
+  // GELU_PLE_SHADER (gpu-runtime.js:1345-1348): y = gelu(gate) * ple[row, layer]
+  geluPle(encoder, gate, ple, rows, layer, garbage = null) {
+    const y = this.emptyF32(rows * this.pleWidth, 'gelu-ple');
+    native.geluPle(gate, ple, rows, layer, this.pleWidth, this.pleLayers, y);
+    return y;
+  }
+  // NORM_ROPE_SHADER (gpu-runtime.js:1349-1356): per-head RMS norm, rotate-half
+  // RoPE of floor(ropeProp * hd / 2) pairs at positions pos0 + row
+  normRope(encoder, x, rows, heads, hd, pos0, scale, ropeProp, base, garbage = null) {
+    const y = this.emptyF32(rows * heads * hd, 'rope-out');
+    native.normRope(x, rows, heads, hd, pos0, scale, Math.floor(ropeProp * hd / 2), base, RMS_EPS, y);
+    return y;
+  }
+  // QK_SHADER + SOFTMAX_SHADER + ATTN_OUT_SHADER (gpu-runtime.js:1357-1365)
+  attention(encoder, q, kcache, vcache, qrows, heads, hd, keylen, qpos0, sliding, window, garbage = null) {
+    const out = this.emptyF32(qrows * heads * hd, 'attn-out');
+    native.attention(q, kcache, vcache, qrows, heads, hd, keylen, qpos0, sliding ? 1 : 0, window, out);
+    return out;
+  }
+  // PLE_MIX_SHADER (gpu-runtime.js:1366-1369)
+  pleMix(encoder, proj, normScale, tokenPle, rows, garbage = null) {
+    const y = this.emptyF32(rows * this.pleLayers * this.pleWidth, 'ple-mix');
+    native.pleMix(proj, normScale, tokenPle, rows, this.pleWidth, this.pleLayers, y);
     return y;
   }
   // out[outOffset + r] = 30 * tanh((x . E[r]) / 30) over a chunk of rows
@@ -246,9 +296,6 @@ class GPUOps {
     native.bf16Head(x, weightChunk, rows, inDim, out, 1.0, 30.0, 0, outOffset * 4);
   }
   dispose() {}
-}
-for (const name of ['rms', 'addScale', 'scale', 'geluMul', 'geluPle', 'normRope', 'attention', 'pleMix']) {
-  GPUOps.prototype[name] = notOnHipPath(name);
 }
 
 // ---- PLE W4 shard bundle, resident on the device (gpu-runtime.js:413-527) ---------------

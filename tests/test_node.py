@@ -117,3 +117,109 @@ def test_js_surface_on_gpu_matches_oracle(tmp_path, oracle):
     want_l = oracle.bf16_head(h, E, 1.0, 30.0)
     assert np.allclose(logits, want_l, rtol=1e-4, atol=1e-4)
     assert res["top10"][0] == int(oracle.topk(want_l, 10)[0][0])
+
+
+def _bf16_bytes(a):
+    return syn.bf16_rne(np.asarray(a, np.float32)).astype(np.uint16).tobytes()
+
+
+@pytest.mark.gpu
+def test_js_model_driver_matches_oracle(tmp_path, oracle):
+    """Gemma4Hip (gemma4-hip.js: Gemma4WebGPU's load/forward/logits/greedy on the
+    HIP GPUOps) on a 5-layer checkpoint in the reference's tensor layout - W4
+    projections, BF16 norms and layer scalars, tied BF16 embedding, dense BF16
+    per-layer embeddings - against the oracle model.  Logits of the prompt
+    within relative L2 1e-3; greedy tokens equal unless the oracle's top two
+    are within 1e-3."""
+    import layer_oracle as lo
+    H, heads, P, V, window = 128, 2, 32, 512, 8
+    specs = [  # sliding/global, own or shared KV, as spec(i) describes E2B layers
+        dict(full=False, headDim=64, intermediate=256, shared=False, storeShared=True,
+             attentionType="sliding", ropeBase=10000, ropeProp=1.0),
+        dict(full=True, headDim=128, intermediate=256, shared=False, storeShared=True,
+             attentionType="full", ropeBase=1000000, ropeProp=0.25),
+        dict(full=False, headDim=64, intermediate=512, shared=True, storeShared=False,
+             attentionType="sliding", ropeBase=10000, ropeProp=1.0),
+        dict(full=True, headDim=128, intermediate=512, shared=True, storeShared=False,
+             attentionType="full", ropeBase=1000000, ropeProp=0.25),
+        dict(full=False, headDim=64, intermediate=512, shared=True, storeShared=False,
+             attentionType="sliding", ropeBase=10000, ropeProp=1.0),
+    ]
+    NL = len(specs)
+    rng = np.random.default_rng(77)
+    T = {}
+    E = syn.bf16_rne(rng.standard_normal((V, H)).astype(np.float32) * np.float32(0.05))
+    T["model.language_model.embed_tokens.weight"] = ("BF16", (V, H), E.tobytes())
+    ple_dense = syn.bf16_rne(rng.standard_normal((V, NL * P)).astype(np.float32) * np.float32(0.05))
+    T["model.language_model.embed_tokens_per_layer.weight"] = ("BF16", (V, NL * P), ple_dense.tobytes())
+    seed = [100]
+
+    def lin(name, n, k):
+        seed[0] += 1
+        packed, scales, _ = syn.w4_weights(seed[0], n, k)
+        T[name + ".weight_packed"] = ("I32", (n, k // 8), packed.astype(np.uint32).tobytes())
+        T[name + ".weight_scale"] = ("BF16", (n, k // 32), scales.astype(np.uint16).tobytes())
+        return packed, scales
+
+    def norm(name, n):
+        bits = syn.bf16_rne(rng.uniform(0.8, 1.2, n).astype(np.float32))
+        T[name] = ("BF16", (n,), bits.tobytes())
+        return syn.bf16_to_f32(bits).astype(np.float32)
+
+    top = lin("model.language_model.per_layer_model_projection", NL * P, H)
+    ple_norm = norm("model.language_model.per_layer_projection_norm.weight", P)
+    final_norm = norm("model.language_model.norm.weight", H)
+    layers = []
+    for i, s in enumerate(specs):
+        root = "model.language_model.layers.%d" % i
+        hd, inter = s["headDim"], s["intermediate"]
+        L = dict(head_dim=hd, intermediate=inter, full=s["full"],
+                 kv_source=-1 if not s["shared"] else (1 if s["full"] else 0),
+                 rope_base=float(s["ropeBase"]), rope_prop=s["ropeProp"], linear={}, norm={})
+        shapes = [("q", "self_attn.q_proj", heads * hd, H), ("o", "self_attn.o_proj", H, heads * hd),
+                  ("gate", "mlp.gate_proj", inter, H), ("up", "mlp.up_proj", inter, H),
+                  ("down", "mlp.down_proj", H, inter), ("ple_gate", "per_layer_input_gate", P, H),
+                  ("ple_proj", "per_layer_projection", H, P)]
+        if not s["shared"]:
+            shapes += [("k", "self_attn.k_proj", hd, H), ("v", "self_attn.v_proj", hd, H)]
+        for key, name, n, k in shapes:
+            L["linear"][key] = lin(root + "." + name, n, k)
+        for key, name, n in [("input", "input_layernorm", H), ("post_attn", "post_attention_layernorm", H),
+                             ("pre_ffw", "pre_feedforward_layernorm", H),
+                             ("post_ffw", "post_feedforward_layernorm", H),
+                             ("post_ple", "post_per_layer_input_norm", H), ("q", "self_attn.q_norm", hd)]:
+            L["norm"][key] = norm(root + "." + name + ".weight", n)
+        if not s["shared"]:
+            L["norm"]["k"] = norm(root + ".self_attn.k_norm.weight", hd)
+        sk = syn.bf16_rne(np.array([rng.uniform(0.9, 1.1)], np.float32))
+        T[root + ".layer_scalar"] = ("BF16", (1,), sk.tobytes())
+        L["skip"] = float(syn.bf16_to_f32(sk)[0])
+        layers.append(L)
+    ckpt = tmp_path / "core.safetensors"
+    write_safetensors(str(ckpt), T)
+    prompt = [int(t) for t in syn.token_ids(21, 11, V)]
+    steps = 4
+    cfg = dict(hidden=H, heads=heads, pleDim=P, window=window, maxSeq=32, lmChunkRows=200,
+               specs=specs, prompt=prompt, steps=steps)
+    (tmp_path / "cfg.json").write_text(json.dumps(cfg))
+    res = run_node("model_parity.js", str(ckpt), str(tmp_path / "cfg.json"), timeout=300)
+
+    ple_f32 = syn.bf16_to_f32(ple_dense).reshape(V, NL * P)
+    ref = lo.Model(H, heads, P, V, layers, E, lambda ids: ple_f32[np.asarray(ids)], top, ple_norm,
+                   final_norm, window=window)
+    want_tok, want_lg = ref.greedy(prompt, 0)
+    got_lg = np.asarray(res["logits0"], np.float64)
+    assert np.linalg.norm(got_lg - want_lg) / np.linalg.norm(want_lg) < 1e-3
+    toks = res["tokens"]
+
+    def near_tie(lg, tok):
+        return float(np.max(lg) - lg[tok]) <= 1e-3
+
+    assert toks[0] == want_tok or near_tie(want_lg, toks[0])
+    pos = len(prompt)
+    for t_prev, t in zip(toks[:-1], toks[1:]):
+        w, lg = ref.greedy([t_prev], pos)
+        assert t == w or near_tie(lg, t), (pos, t, w)
+        pos += 1
+    assert res["cache"]["caches"] == 2 and res["cache"]["bytes"] == pos * (64 + 128) * 4 * 2
+    assert res["appendError"] == "KV append position %d != cache length %d" % (pos + 5, pos)
