@@ -230,6 +230,23 @@ def bench_decode(prompt=512, steps=256, max_seq=1024, seed=4):
             "first_token": int(first)}
 
 
+def bench_decode_eager(steps, prompt=512, max_seq=1024, seed=4):
+    """The E2B prompt, then `steps` one-token greedy calls launched one by one
+    (each a host round trip): the decode step's kernels without graph replay."""
+    import e2b
+    cfg = g4hip.e2b_config(max_seq)
+    m = e2b.build(cfg, seed)
+    ids = syn.token_ids(seed, prompt, cfg.vocab)
+    m.reset()
+    tok = m.greedy(ids, 0)
+    t0 = time.perf_counter()
+    for s in range(steps):
+        tok = m.greedy([tok], prompt + s)
+    el = time.perf_counter() - t0
+    m.free()
+    return {"steps": steps, "host_ms_per_token": el * 1e3 / steps, "last_token": int(tok)}
+
+
 def cpu_baseline(n, k, budget_s=10.0, seed=0):
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import g4oracle
@@ -258,6 +275,11 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--skip-decode", action="store_true",
+                    help="leave out the E2B decode extra")
+    ap.add_argument("--decode-eager", type=int, default=0, metavar="STEPS",
+                    help="only run the E2B prompt and STEPS one-token greedy calls without "
+                         "graph replay (for kernel profiles), then exit")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py runs on one GPU: --gpus %d is not supported (the path is measured on a "
@@ -267,6 +289,9 @@ def main():
     g4hip.init(0)
     info = g4hip.device_info()
     log("device:", info)
+    if args.decode_eager:
+        print(json.dumps({"decode_eager": bench_decode_eager(args.decode_eager)}), flush=True)
+        return
     # One 64 MiB device-to-device copy of known size before anything else:
     # the reference point that scales the FETCH_SIZE / WRITE_SIZE counters
     # when this command runs under `rocprofv3 --pmc`.
@@ -296,9 +321,10 @@ def main():
         log("prefill GEMM (config 3) ...")
         extra["gemm_prefill"] = bench_gemm()
         log("  ", extra["gemm_prefill"])
-        log("E2B decode (config 4): prompt 512, 256 greedy steps ...")
-        extra["decode_e2b"] = bench_decode()
-        log("  ", extra["decode_e2b"])
+        if not args.skip_decode:
+            log("E2B decode (config 4): prompt 512, 256 greedy steps ...")
+            extra["decode_e2b"] = bench_decode()
+            log("  ", extra["decode_e2b"])
 
     cpu = None
     if not args.no_cpu:
@@ -306,12 +332,13 @@ def main():
         cpu = cpu_baseline(n, k, args.cpu_seconds)
         log("  ", cpu)
 
-    traffic, traffic_src = None, None
+    traffic, traffic_src, kname = None, None, "w4_gemv1_kernel"
     tpath = os.path.join(ROOT, "profiles", "w4_gemv_m1_k1536_n6144_traffic.json")
     if os.path.exists(tpath):
         with open(tpath) as f:
             t = json.load(f)
         traffic = t["hbm_bytes_per_launch"]
+        kname = t.get("kernel", kname)
         traffic_src = "profiles/w4_gemv_m1_k1536_n6144_traffic.json (rocprofv3 --pmc FETCH_SIZE, WRITE_SIZE)"
     line = {
         "metric": METRIC, "value": round(g["gbs"], 2), "unit": "GB/s", "n_gpus": 1,
@@ -324,7 +351,7 @@ def main():
                    "cu_count": info["cu_count"]},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
-                     "traffic_source": traffic_src, "kernel": "w4_gemv1_kernel", "avg_launch_us": round(avg_us, 4),
+                     "traffic_source": traffic_src, "kernel": kname, "avg_launch_us": round(avg_us, 4),
                      "bytes_per_launch": g["bytes_per_step"]},
         "cpu_baseline": cpu,
         "decode_tok_s": round(extra["decode_e2b"]["decode_tok_s"], 1) if "decode_e2b" in extra else None,
