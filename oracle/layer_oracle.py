@@ -14,8 +14,11 @@ float32 multiply of an exact bf16 value).
 Pinning (tests/test_oracle_layers.py): closed forms and invariants for each
 op (constant-vector RMS, GELU values and limits, RoPE at position 0 and as a
 rotation, single-key and uniform attention, masks against brute force,
-pleMix with zero inputs), plus the model forward checked against itself
-(prefill of a sequence vs token-by-token decode).
+pleMix with zero inputs).  The model forward is pinned by two invariants:
+with every projection zero each layer only scales the residual stream by its
+skip scalar (closed form; a dropped residual add fails it), and a sequence
+fed whole equals the same sequence fed in parts (positions, causal mask,
+KV append and KV sharing).
 """
 import numpy as np
 

@@ -185,3 +185,97 @@ def test_attention_window_planted_mistake_is_caught(plant):
         np.testing.assert_allclose(y[0], want, rtol=1e-6)
     else:
         assert not np.allclose(y[0], want, rtol=1e-3)
+
+
+# ---------------------------------------------------------------------------
+# Model-level pins (Model.forward composes the ops above in the order of
+# gemma4-webgpu.js encodeLayer 215-301 / forward 303-402).
+
+def _tiny_layers(rng, H, heads, P, zero):
+    import synthetic as syn
+    spec = [dict(head_dim=16, full=0, kv_source=-1, intermediate=32, rope_base=1e4, rope_prop=1.0),
+            dict(head_dim=32, full=1, kv_source=-1, intermediate=32, rope_base=1e6, rope_prop=0.25),
+            dict(head_dim=16, full=0, kv_source=0, intermediate=64, rope_base=1e4, rope_prop=1.0)]
+    layers, seed = [], 100
+    for L in spec:
+        hd, inter = L["head_dim"], L["intermediate"]
+        shapes = dict(q=(heads * hd, H), o=(H, heads * hd), gate=(inter, H), up=(inter, H),
+                      down=(H, inter), ple_gate=(P, H), ple_proj=(H, P))
+        if L["kv_source"] < 0:
+            shapes.update(k=(hd, H), v=(hd, H))
+        lin = {}
+        for name, (n, k) in shapes.items():
+            seed += 1
+            if zero:  # q = 0 everywhere: every projection outputs exactly 0
+                lin[name] = (syn.pack_w4(np.zeros((n, k), np.int8)),
+                             syn.bf16_rne(np.ones((n, k // 32), np.float32)))
+            else:
+                packed, scales, _ = syn.w4_weights(seed, n, k, 0.1)
+                lin[name] = (packed, scales)
+        norm = {n: rng.uniform(0.8, 1.2, H).astype(np.float32)
+                for n in ("input", "post_attn", "pre_ffw", "post_ffw", "post_ple")}
+        norm["q"] = rng.uniform(0.8, 1.2, hd).astype(np.float32)
+        norm["k"] = rng.uniform(0.8, 1.2, hd).astype(np.float32)
+        layers.append(dict(L, linear=lin, norm=norm, skip=float(rng.uniform(0.5, 2.0))))
+    return layers
+
+
+def _tiny_model(seed, zero=False, window=4):
+    import synthetic as syn
+    H, heads, P, V = 64, 2, 32, 32
+    rng = np.random.default_rng(seed)
+    E = syn.bf16_rne(rng.standard_normal((V, H), dtype=np.float32))
+    layers = _tiny_layers(rng, H, heads, P, zero)
+    NL = len(layers)
+    ple = rng.standard_normal((V, NL * P)).astype(np.float32)
+    top = syn.w4_weights(seed + 1, NL * P, H, 0.1)[:2]
+    m = lo.Model(H, heads, P, V, layers, E, lambda ids: ple[np.asarray(ids)], top,
+                 rng.uniform(0.8, 1.2, P).astype(np.float32),
+                 rng.uniform(0.8, 1.2, H).astype(np.float32), window=window)
+    return m, E
+
+
+def test_model_zero_projections_leave_the_residual_stream():
+    # Every projection 0: attention, MLP and PLE branches add exactly 0, so
+    # each layer maps hidden -> hidden * skip and the output is the final norm
+    # of the scaled embedding row.  A dropped residual add fails this.
+    m, E = _tiny_model(3, zero=True)
+    ids = [5, 17, 2, 30]
+    got = m.forward(ids, 0)
+    skip = np.prod([L["skip"] for L in m.layers])
+    h = lo.embed(E, ids, np.float32(math.sqrt(m.hidden))).astype(np.float64)[-1:] * skip
+    want = lo.rms(h.astype(np.float32), m.hidden, m.final_norm)[0]
+    np.testing.assert_allclose(got, want, rtol=1e-6)
+
+
+def test_model_zero_projections_planted_residual_drop_is_caught(monkeypatch):
+    m, E = _tiny_model(3, zero=True)
+    real = lo.add_scale
+    monkeypatch.setattr(lo, "add_scale", lambda a, b, s: real(np.zeros_like(a), b, s))
+    got = m.forward([5, 17, 2, 30], 0)
+    h = lo.embed(E, [30], np.float32(math.sqrt(m.hidden)))
+    want = lo.rms(h, m.hidden, m.final_norm)[0]
+    assert not np.allclose(got, want, rtol=1e-3)
+
+
+@pytest.mark.parametrize("split", [1, 3, 6])
+def test_model_prefill_equals_incremental_forward(split):
+    # Causal masking, the sliding window (4 < 9 tokens), KV sharing and the
+    # position offsets of a later call: a sequence fed whole and fed in two
+    # parts (then one token at a time) must give the same last hidden state.
+    ids = [3, 9, 27, 1, 14, 22, 8, 31, 0]
+    m, _ = _tiny_model(4)
+    whole = m.forward(ids, 0)
+    m.reset()
+    m.forward(ids[:split], 0)
+    for p in range(split, len(ids)):
+        part = m.forward(ids[p:p + 1], p)
+    np.testing.assert_allclose(part, whole, rtol=1e-9, atol=1e-12)
+    assert m.length == len(ids)
+
+
+def test_model_rejects_wrong_append_position():
+    m, _ = _tiny_model(5)
+    m.forward([1, 2], 0)
+    with pytest.raises(ValueError, match="KV append position 1 != cache length 2"):
+        m.forward([3], 1)
