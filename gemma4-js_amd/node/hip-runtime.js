@@ -10,9 +10,11 @@
 // runs them at queue.submit() in submission order (gpu-runtime.js:328-332,
 // gemma4-webgpu.js:339-358).  Here every op is enqueued on the library's one
 // HIP stream as it is encoded, so device order equals encode order, which is
-// the order the reference submits in; submit() is therefore a no-op and
-// buffer.destroy() waits for queued work first.  Recording for replay is
-// available separately through HipCommandRecorder (HIP graphs).
+// the order the reference submits in; submit() is therefore a no-op.
+// buffer.destroy() returns the memory to the library's stream-ordered cache:
+// only work enqueued after the destroy can reuse it, so nothing waits, as
+// WebGPU defers the release until submitted work is done.  Recording for
+// replay is available separately through HipCommandRecorder (HIP graphs).
 
 const fs = require('fs');
 const path = require('path');
