@@ -94,6 +94,7 @@ struct g4_gemma {
   float *ple_norm = nullptr, *final_norm = nullptr;
   const uint16_t *E = nullptr;
   const g4_ple *ple = nullptr;
+  const uint16_t *ple_dense = nullptr;  // BF16 [vocab, layers * ple_dim], when no W4 table
   int max_rows = 0, hd_max = 0, inter_max = 0, ple_total = 0;
   int cache_len = 0;  // host mirror of the KV length (KVCache.length)
   // device state
@@ -132,7 +133,7 @@ void drop_step(g4_gemma *m) {
 
 int check_ready(const g4_gemma *m) {
   const g4_gemma_config &c = m->cfg;
-  if (!m->top || !m->ple_norm || !m->final_norm || !m->E || !m->ple)
+  if (!m->top || !m->ple_norm || !m->final_norm || !m->E || (!m->ple && !m->ple_dense))
     return fail(G4_E_STATE, "g4_gemma: top-level weights are not set (embedding, PLE table, "
                             "per-layer projection, PLE norm, final norm)");
   for (int i = 0; i < c.layers; ++i) {
@@ -151,6 +152,16 @@ int check_ready(const g4_gemma *m) {
   return G4_OK;
 }
 
+// The token rows of the per-layer embeddings into m->tokple (FP32): gathered
+// and dequantized from the W4 table (reader.pleRowsToGpu), or, for a
+// checkpoint with a dense BF16 embed_tokens_per_layer, its rows widened
+// (bf16Rows + uploadF32; gemma4-webgpu.js:198-215).
+int token_ple(g4_gemma *m, int rows) {
+  const g4_gemma_config &c = m->cfg;
+  if (m->ple) return g4_ple_gather_dev(m->ple, m->ids, rows, m->tokple, G4_F32);
+  return launch_embed(m->ple_dense, c.vocab, c.layers * c.ple_dim, m->ids, rows, 1.f, m->tokple);
+}
+
 // One token (a decode step) on the fused kernels: per layer q/k/v GEMV with
 // the norm chain of the previous layer's end in its prologue, one RoPE/cache
 // kernel, attention, o GEMV, gate/up GEMV with the post-attention chain in its
@@ -164,7 +175,7 @@ int run_token(g4_gemma *m, bool graph) {
   int rc;
   if ((rc = launch_embed(m->E, c.vocab, H, m->ids, 1, (float)sqrt((double)H), m->h[0])))
     return rc;
-  if ((rc = g4_ple_gather_dev(m->ple, m->ids, 1, m->tokple, G4_F32))) return rc;
+  if ((rc = token_ple(m, 1))) return rc;
   if ((rc = g4_w4_linear(m->top, m->h[0], G4_F32, 1, m->proj, G4_F32))) return rc;
   if ((rc = launch_scale(m->proj, (size_t)NL * P, (float)(1.0 / sqrt((double)H)), m->projs)))
     return rc;
@@ -229,7 +240,7 @@ int run_layers(g4_gemma *m, int rows, bool graph) {
   // per-layer projection, pleMix.
   if ((rc = launch_embed(m->E, c.vocab, H, m->ids, rows, (float)sqrt((double)H), m->h[0])))
     return rc;
-  if ((rc = g4_ple_gather_dev(m->ple, m->ids, rows, m->tokple, G4_F32))) return rc;
+  if ((rc = token_ple(m, rows))) return rc;
   if ((rc = g4_w4_linear(m->top, m->h[0], G4_F32, rows, m->proj, G4_F32))) return rc;
   if ((rc = launch_scale(m->proj, (size_t)rows * NL * P, (float)(1.0 / sqrt((double)H)),
                          m->projs)))
@@ -585,6 +596,20 @@ G4_API int g4_gemma_set_ple(g4_gemma *m, const g4_ple *t) {
     return fail(G4_E_ARG, "g4_gemma_set_ple: table [%d, %d] does not match vocab %d x %d",
                 vocab, width, m->cfg.vocab, m->cfg.layers * m->cfg.ple_dim);
   m->ple = t;
+  m->ple_dense = nullptr;
+  drop_step(m);
+  return ok();
+}
+
+G4_API int g4_gemma_set_ple_dense(g4_gemma *m, const void *rows_dev) {
+  G4_CHECK_INIT();
+  if (!m) return fail(G4_E_ARG, "g4_gemma_set_ple_dense: null model");
+  const g4_gemma_config &c = m->cfg;
+  int rc = check_device_range(rows_dev, (size_t)c.vocab * c.layers * c.ple_dim * 2,
+                              "g4_gemma_set_ple_dense rows");
+  if (rc) return rc;
+  m->ple_dense = static_cast<const uint16_t *>(rows_dev);
+  m->ple = nullptr;
   drop_step(m);
   return ok();
 }

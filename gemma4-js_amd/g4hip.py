@@ -80,6 +80,7 @@ SIGNATURES = {
     "g4_gemma_set_layer_scalar": (_int, [_vp, _int, _c.c_float]),
     "g4_gemma_set_embedding": (_int, [_vp, _vp]),
     "g4_gemma_set_ple": (_int, [_vp, _vp]),
+    "g4_gemma_set_ple_dense": (_int, [_vp, _vp]),
     "g4_gemma_reset": (_int, [_vp]),
     "g4_gemma_cache_length": (_int, [_vp, _c.POINTER(_int)]),
     "g4_gemma_forward": (_int, [_vp, _vp, _int, _int, _vp]),
@@ -451,6 +452,11 @@ class Gemma:
     def set_ple(self, t):
         check(lib().g4_gemma_set_ple(self.h, t.h))
         self._keep.append(t)
+
+    def set_ple_dense(self, rows):
+        """Dense BF16 per-layer embeddings [vocab, layers * ple_dim] (a Buffer)."""
+        check(lib().g4_gemma_set_ple_dense(self.h, rows.ptr))
+        self._keep.append(rows)
 
     def reset(self):
         check(lib().g4_gemma_reset(self.h))

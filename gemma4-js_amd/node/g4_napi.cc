@@ -15,6 +15,8 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <vector>
+
 #include "g4hip.h"
 
 namespace {
@@ -60,6 +62,21 @@ bool get_args(napi_env env, napi_callback_info info, size_t want, napi_value *ar
   for (size_t i = argc; i < want; ++i) napi_get_undefined(env, &argv[i]);
   return true;
 }
+
+// True when v was made by the class whose constructor `ctor` refers to.
+bool is_instance(napi_env env, napi_value v, napi_ref ctor) {
+  bool ok = false;
+  napi_valuetype t;
+  napi_typeof(env, v, &t);
+  if (!ctor || t != napi_object) return false;
+  napi_value c;
+  napi_get_reference_value(env, ctor, &c);
+  napi_instanceof(env, v, c, &ok);
+  return ok;
+}
+
+napi_ref g_devbuf_ctor = nullptr, g_w4_ctor = nullptr, g_ple_ctor = nullptr,
+         g_cmd_ctor = nullptr, g_engine_ctor = nullptr;
 
 bool to_i64(napi_env env, napi_value v, int64_t *out, const char *what) {
   napi_valuetype t;
@@ -141,8 +158,6 @@ struct DevBuf {
   size_t size;
 };
 
-napi_ref g_devbuf_ctor = nullptr;
-
 void devbuf_finalize(napi_env, void *data, void *) {
   DevBuf *b = static_cast<DevBuf *>(data);
   if (b->ptr) g4_free(b->ptr);
@@ -151,13 +166,7 @@ void devbuf_finalize(napi_env, void *data, void *) {
 
 DevBuf *unwrap_buf(napi_env env, napi_value v, const char *what) {
   void *p = nullptr;
-  bool ok = false;
-  if (g_devbuf_ctor) {
-    napi_value ctor;
-    napi_get_reference_value(env, g_devbuf_ctor, &ctor);
-    napi_instanceof(env, v, ctor, &ok);
-  }
-  if (!ok || napi_unwrap(env, v, &p) != napi_ok || !p) {
+  if (!is_instance(env, v, g_devbuf_ctor) || napi_unwrap(env, v, &p) != napi_ok || !p) {
     char msg[128];
     snprintf(msg, sizeof msg, "%s must be a DeviceBuffer", what);
     napi_throw_type_error(env, nullptr, msg);
@@ -278,8 +287,6 @@ struct W4 {
   int out_dim, in_dim, group;
 };
 
-napi_ref g_w4_ctor = nullptr;
-
 void w4_finalize(napi_env, void *data, void *) {
   W4 *w = static_cast<W4 *>(data);
   if (w->h) g4_w4_free(w->h);
@@ -288,7 +295,7 @@ void w4_finalize(napi_env, void *data, void *) {
 
 W4 *unwrap_w4(napi_env env, napi_value self) {
   void *p = nullptr;
-  if (napi_unwrap(env, self, &p) != napi_ok || !p) {
+  if (!is_instance(env, self, g_w4_ctor) || napi_unwrap(env, self, &p) != napi_ok || !p) {
     napi_throw_type_error(env, nullptr, "not a W4Weight");
     return nullptr;
   }
@@ -415,7 +422,7 @@ void ple_finalize(napi_env, void *data, void *) {
 
 Ple *unwrap_ple(napi_env env, napi_value self) {
   void *p = nullptr;
-  if (napi_unwrap(env, self, &p) != napi_ok || !p) {
+  if (!is_instance(env, self, g_ple_ctor) || napi_unwrap(env, self, &p) != napi_ok || !p) {
     napi_throw_type_error(env, nullptr, "not a PleTable");
     return nullptr;
   }
@@ -547,8 +554,6 @@ void cmd_finalize(napi_env, void *data, void *) {
   delete c;
 }
 
-napi_ref g_cmd_ctor = nullptr;
-
 napi_value Cmd_new(napi_env env, napi_callback_info info) {
   napi_value self;
   if (!get_args(env, info, 0, nullptr, &self)) return nullptr;
@@ -564,8 +569,11 @@ napi_value Cmd_new(napi_env env, napi_callback_info info) {
 napi_value Cmd_submit(napi_env env, napi_callback_info info) {
   napi_value self;
   if (!get_args(env, info, 0, nullptr, &self)) return nullptr;
-  void *p;
-  NAPI_CALL(env, napi_unwrap(env, self, &p));
+  void *p = nullptr;
+  if (!is_instance(env, self, g_cmd_ctor) || napi_unwrap(env, self, &p) != napi_ok || !p) {
+    napi_throw_type_error(env, nullptr, "not a CommandBuffer");
+    return nullptr;
+  }
   Cmd *c = static_cast<Cmd *>(p);
   if (!c->h) {
     napi_throw_error(env, nullptr, "CommandBuffer is empty or destroyed");
@@ -578,8 +586,11 @@ napi_value Cmd_submit(napi_env env, napi_callback_info info) {
 napi_value Cmd_destroy(napi_env env, napi_callback_info info) {
   napi_value self;
   if (!get_args(env, info, 0, nullptr, &self)) return nullptr;
-  void *p;
-  NAPI_CALL(env, napi_unwrap(env, self, &p));
+  void *p = nullptr;
+  if (!is_instance(env, self, g_cmd_ctor) || napi_unwrap(env, self, &p) != napi_ok || !p) {
+    napi_throw_type_error(env, nullptr, "not a CommandBuffer");
+    return nullptr;
+  }
   Cmd *c = static_cast<Cmd *>(p);
   if (c->h) {
     g4_cmdbuf *h = c->h;
@@ -878,6 +889,399 @@ napi_value F_argmax(napi_env env, napi_callback_info info) {
   return undefined(env);
 }
 
+// ---- GemmaEngine (g4_gemma_*) ---------------------------------------------------
+// The native decoder engine behind Gemma4WebGPU's load/forward/logits/greedy
+// surface (gemma4-webgpu.js:139-481), plus decode(steps) on a recorded step.
+// The engine borrows the W4Weight / PleTable / DeviceBuffer objects it is
+// given; the JS object holds references to them so they outlive it.
+
+struct Engine {
+  g4_gemma *h;
+};
+
+void engine_finalize(napi_env, void *data, void *) {
+  Engine *e = static_cast<Engine *>(data);
+  if (e->h) g4_gemma_free(e->h);
+  delete e;
+}
+
+Engine *unwrap_engine(napi_env env, napi_value self) {
+  void *p = nullptr;
+  if (!is_instance(env, self, g_engine_ctor) || napi_unwrap(env, self, &p) != napi_ok || !p) {
+    napi_throw_type_error(env, nullptr, "not a GemmaEngine");
+    return nullptr;
+  }
+  Engine *e = static_cast<Engine *>(p);
+  if (!e->h) {
+    napi_throw_error(env, nullptr, "GemmaEngine was disposed");
+    return nullptr;
+  }
+  return e;
+}
+
+bool get_prop(napi_env env, napi_value obj, const char *name, napi_value *out) {
+  bool has = false;
+  napi_has_named_property(env, obj, name, &has);
+  if (!has) {
+    char msg[128];
+    snprintf(msg, sizeof msg, "config.%s is missing", name);
+    napi_throw_type_error(env, nullptr, msg);
+    return false;
+  }
+  return napi_get_named_property(env, obj, name, out) == napi_ok;
+}
+
+bool prop_int(napi_env env, napi_value obj, const char *name, int *out) {
+  napi_value v;
+  int64_t x;
+  if (!get_prop(env, obj, name, &v) || !to_i64(env, v, &x, name)) return false;
+  if (x < INT32_MIN || x > INT32_MAX) {
+    napi_throw_range_error(env, nullptr, "config value out of int range");
+    return false;
+  }
+  *out = (int)x;
+  return true;
+}
+
+bool prop_float(napi_env env, napi_value obj, const char *name, float *out) {
+  napi_value v;
+  double x;
+  if (!get_prop(env, obj, name, &v) || !to_f64(env, v, &x, name)) return false;
+  *out = (float)x;
+  return true;
+}
+
+// Token ids from an Array of numbers or an Int32Array / Uint32Array.
+bool id_list(napi_env env, napi_value v, std::vector<int32_t> *ids) {
+  bool is = false;
+  napi_is_typedarray(env, v, &is);
+  if (is) {
+    napi_typedarray_type type;
+    size_t n, off;
+    napi_value ab;
+    void *p;
+    napi_get_typedarray_info(env, v, &type, &n, &p, &ab, &off);
+    if (type != napi_int32_array && type != napi_uint32_array) {
+      napi_throw_type_error(env, nullptr, "token ids must be an Array, Int32Array or Uint32Array");
+      return false;
+    }
+    const int32_t *q = static_cast<const int32_t *>(p);
+    ids->assign(q, q + n);
+    return true;
+  }
+  napi_is_array(env, v, &is);
+  if (!is) {
+    napi_throw_type_error(env, nullptr, "token ids must be an Array, Int32Array or Uint32Array");
+    return false;
+  }
+  uint32_t n = 0;
+  napi_get_array_length(env, v, &n);
+  ids->resize(n);
+  for (uint32_t i = 0; i < n; ++i) {
+    napi_value x;
+    int64_t id;
+    napi_get_element(env, v, i, &x);
+    if (!to_i64(env, x, &id, "token id")) return false;
+    if (id < INT32_MIN || id > INT32_MAX) {
+      napi_throw_range_error(env, nullptr, "token id out of int range");
+      return false;
+    }
+    (*ids)[i] = (int32_t)id;
+  }
+  return true;
+}
+
+napi_value config_object(napi_env env, const g4_gemma_config &c) {
+  napi_value o, v, layers;
+  NAPI_CALL(env, napi_create_object(env, &o));
+#define SET_NUM(key, val)                                \
+  NAPI_CALL(env, napi_create_double(env, (double)(val), &v)); \
+  NAPI_CALL(env, napi_set_named_property(env, o, key, v));
+  SET_NUM("hidden", c.hidden);
+  SET_NUM("heads", c.heads);
+  SET_NUM("pleDim", c.ple_dim);
+  SET_NUM("vocab", c.vocab);
+  SET_NUM("maxSeq", c.max_seq);
+  SET_NUM("window", c.window);
+  SET_NUM("eps", c.eps);
+  SET_NUM("softcap", c.softcap);
+#undef SET_NUM
+  NAPI_CALL(env, napi_create_array_with_length(env, c.layers, &layers));
+  for (int i = 0; i < c.layers; ++i) {
+    napi_value L;
+    NAPI_CALL(env, napi_create_object(env, &L));
+#define SET_L(key, val)                                  \
+  NAPI_CALL(env, napi_create_double(env, (double)(val), &v)); \
+  NAPI_CALL(env, napi_set_named_property(env, L, key, v));
+    SET_L("headDim", c.head_dim[i]);
+    SET_L("intermediate", c.intermediate[i]);
+    SET_L("full", c.full[i]);
+    SET_L("kvSource", c.kv_source[i]);
+    SET_L("ropeBase", c.rope_base[i]);
+    SET_L("ropeProp", c.rope_prop[i]);
+#undef SET_L
+    NAPI_CALL(env, napi_set_element(env, layers, i, L));
+  }
+  NAPI_CALL(env, napi_set_named_property(env, o, "layers", layers));
+  return o;
+}
+
+// e2bConfig(maxSeq) -> the Gemma-4-E2B geometry (gemma4-webgpu.js:12, 65-77)
+napi_value F_e2bConfig(napi_env env, napi_callback_info info) {
+  napi_value a[1], self;
+  if (!get_args(env, info, 1, a, &self)) return nullptr;
+  int64_t max_seq;
+  if (!to_i64(env, a[0], &max_seq, "maxSeq")) return nullptr;
+  g4_gemma_config c;
+  G4_CALL(env, g4_gemma_e2b_config((int)max_seq, &c));
+  return config_object(env, c);
+}
+
+// new GemmaEngine({hidden, heads, pleDim, vocab, maxSeq, window, eps, softcap,
+//                  layers: [{headDim, intermediate, full, kvSource, ropeBase, ropeProp}]})
+napi_value Engine_new(napi_env env, napi_callback_info info) {
+  napi_value a[1], self;
+  if (!get_args(env, info, 1, a, &self)) return nullptr;
+  napi_valuetype t;
+  napi_typeof(env, a[0], &t);
+  if (t != napi_object) {
+    napi_throw_type_error(env, nullptr, "GemmaEngine needs a config object");
+    return nullptr;
+  }
+  g4_gemma_config c;
+  memset(&c, 0, sizeof c);
+  if (!prop_int(env, a[0], "hidden", &c.hidden) || !prop_int(env, a[0], "heads", &c.heads) ||
+      !prop_int(env, a[0], "pleDim", &c.ple_dim) || !prop_int(env, a[0], "vocab", &c.vocab) ||
+      !prop_int(env, a[0], "maxSeq", &c.max_seq) || !prop_int(env, a[0], "window", &c.window) ||
+      !prop_float(env, a[0], "eps", &c.eps) || !prop_float(env, a[0], "softcap", &c.softcap))
+    return nullptr;
+  napi_value layers;
+  bool is_array = false;
+  if (!get_prop(env, a[0], "layers", &layers)) return nullptr;
+  napi_is_array(env, layers, &is_array);
+  uint32_t n = 0;
+  if (is_array) napi_get_array_length(env, layers, &n);
+  if (!is_array || n == 0 || n > G4_GEMMA_MAX_LAYERS) {
+    napi_throw_range_error(env, nullptr, "config.layers must be an array of 1-64 layer specs");
+    return nullptr;
+  }
+  c.layers = (int)n;
+  for (uint32_t i = 0; i < n; ++i) {
+    napi_value L;
+    napi_get_element(env, layers, i, &L);
+    if (!prop_int(env, L, "headDim", &c.head_dim[i]) ||
+        !prop_int(env, L, "intermediate", &c.intermediate[i]) ||
+        !prop_int(env, L, "full", &c.full[i]) || !prop_int(env, L, "kvSource", &c.kv_source[i]) ||
+        !prop_float(env, L, "ropeBase", &c.rope_base[i]) ||
+        !prop_float(env, L, "ropeProp", &c.rope_prop[i]))
+      return nullptr;
+  }
+  g4_gemma *h = nullptr;
+  G4_CALL(env, g4_gemma_create(&c, &h));
+  Engine *e = new Engine{h};
+  if (napi_wrap(env, self, e, engine_finalize, nullptr, nullptr) != napi_ok) {
+    g4_gemma_free(h);
+    delete e;
+    napi_throw_error(env, nullptr, "napi_wrap failed");
+    return nullptr;
+  }
+  return self;
+}
+
+// e.setLinear(layer, which, w4Weight)   (layer -1: the per-layer model projection)
+napi_value Engine_setLinear(napi_env env, napi_callback_info info) {
+  napi_value a[3], self;
+  if (!get_args(env, info, 3, a, &self)) return nullptr;
+  Engine *e = unwrap_engine(env, self);
+  int64_t layer, which;
+  if (!e || !to_i64(env, a[0], &layer, "layer") || !to_i64(env, a[1], &which, "which"))
+    return nullptr;
+  W4 *w = unwrap_w4(env, a[2]);
+  if (!w) return nullptr;
+  G4_CALL(env, g4_gemma_set_linear(e->h, (int)layer, (int)which, w->h));
+  return undefined(env);
+}
+
+// e.setNorm(layer, which, Float32Array)
+napi_value Engine_setNorm(napi_env env, napi_callback_info info) {
+  napi_value a[3], self;
+  if (!get_args(env, info, 3, a, &self)) return nullptr;
+  Engine *e = unwrap_engine(env, self);
+  int64_t layer, which;
+  if (!e || !to_i64(env, a[0], &layer, "layer") || !to_i64(env, a[1], &which, "which"))
+    return nullptr;
+  bool is = false;
+  napi_is_typedarray(env, a[2], &is);
+  napi_typedarray_type type = napi_int8_array;
+  size_t n = 0, off;
+  void *p = nullptr;
+  napi_value ab;
+  if (is) napi_get_typedarray_info(env, a[2], &type, &n, &p, &ab, &off);
+  if (!is || type != napi_float32_array) {
+    napi_throw_type_error(env, nullptr, "norm weights must be a Float32Array");
+    return nullptr;
+  }
+  G4_CALL(env, g4_gemma_set_norm(e->h, (int)layer, (int)which, static_cast<const float *>(p),
+                                 (int)n));
+  return undefined(env);
+}
+
+// e.setLayerScalar(layer, s)
+napi_value Engine_setLayerScalar(napi_env env, napi_callback_info info) {
+  napi_value a[2], self;
+  if (!get_args(env, info, 2, a, &self)) return nullptr;
+  Engine *e = unwrap_engine(env, self);
+  int64_t layer;
+  double s;
+  if (!e || !to_i64(env, a[0], &layer, "layer") || !to_f64(env, a[1], &s, "scalar"))
+    return nullptr;
+  G4_CALL(env, g4_gemma_set_layer_scalar(e->h, (int)layer, (float)s));
+  return undefined(env);
+}
+
+// e.setEmbedding(deviceBuffer)   BF16 [vocab, hidden]
+napi_value Engine_setEmbedding(napi_env env, napi_callback_info info) {
+  napi_value a[1], self;
+  if (!get_args(env, info, 1, a, &self)) return nullptr;
+  Engine *e = unwrap_engine(env, self);
+  void *p;
+  if (!e || !dev(env, a[0], "embedding", &p)) return nullptr;
+  G4_CALL(env, g4_gemma_set_embedding(e->h, p));
+  return undefined(env);
+}
+
+// e.setPle(pleTable)
+napi_value Engine_setPle(napi_env env, napi_callback_info info) {
+  napi_value a[1], self;
+  if (!get_args(env, info, 1, a, &self)) return nullptr;
+  Engine *e = unwrap_engine(env, self);
+  if (!e) return nullptr;
+  Ple *t = unwrap_ple(env, a[0]);
+  if (!t) return nullptr;
+  G4_CALL(env, g4_gemma_set_ple(e->h, t->h));
+  return undefined(env);
+}
+
+// e.setPleDense(deviceBuffer)   BF16 [vocab, layers * pleDim]
+napi_value Engine_setPleDense(napi_env env, napi_callback_info info) {
+  napi_value a[1], self;
+  if (!get_args(env, info, 1, a, &self)) return nullptr;
+  Engine *e = unwrap_engine(env, self);
+  void *p;
+  if (!e || !dev(env, a[0], "per-layer embeddings", &p)) return nullptr;
+  G4_CALL(env, g4_gemma_set_ple_dense(e->h, p));
+  return undefined(env);
+}
+
+napi_value Engine_reset(napi_env env, napi_callback_info info) {
+  napi_value self;
+  if (!get_args(env, info, 0, nullptr, &self)) return nullptr;
+  Engine *e = unwrap_engine(env, self);
+  if (!e) return nullptr;
+  G4_CALL(env, g4_gemma_reset(e->h));
+  return undefined(env);
+}
+
+napi_value Engine_cacheLength(napi_env env, napi_callback_info info) {
+  napi_value self, v;
+  if (!get_args(env, info, 0, nullptr, &self)) return nullptr;
+  Engine *e = unwrap_engine(env, self);
+  if (!e) return nullptr;
+  int len = 0;
+  G4_CALL(env, g4_gemma_cache_length(e->h, &len));
+  NAPI_CALL(env, napi_create_int32(env, len, &v));
+  return v;
+}
+
+// e.forward(ids, startPos, lastHidden?)   lastHidden: DeviceBuffer of hidden floats
+napi_value Engine_forward(napi_env env, napi_callback_info info) {
+  napi_value a[3], self;
+  if (!get_args(env, info, 3, a, &self)) return nullptr;
+  Engine *e = unwrap_engine(env, self);
+  std::vector<int32_t> ids;
+  int64_t start;
+  void *out;
+  if (!e || !id_list(env, a[0], &ids) || !to_i64(env, a[1], &start, "startPos") ||
+      !dev_or_null(env, a[2], "lastHidden", &out))
+    return nullptr;
+  if (ids.empty()) {
+    napi_throw_range_error(env, nullptr, "forward needs at least one token id");
+    return nullptr;
+  }
+  G4_CALL(env, g4_gemma_forward(e->h, ids.data(), (int)ids.size(), (int)start,
+                                static_cast<float *>(out)));
+  return undefined(env);
+}
+
+// e.logits(lastHidden, logits)   both DeviceBuffers
+napi_value Engine_logits(napi_env env, napi_callback_info info) {
+  napi_value a[2], self;
+  if (!get_args(env, info, 2, a, &self)) return nullptr;
+  Engine *e = unwrap_engine(env, self);
+  void *h, *l;
+  if (!e || !dev(env, a[0], "lastHidden", &h) || !dev(env, a[1], "logits", &l)) return nullptr;
+  G4_CALL(env, g4_gemma_logits(e->h, static_cast<const float *>(h), static_cast<float *>(l)));
+  return undefined(env);
+}
+
+// e.greedy(ids, startPos, logits?) -> next token id
+napi_value Engine_greedy(napi_env env, napi_callback_info info) {
+  napi_value a[3], self, v;
+  if (!get_args(env, info, 3, a, &self)) return nullptr;
+  Engine *e = unwrap_engine(env, self);
+  std::vector<int32_t> ids;
+  int64_t start;
+  void *lg;
+  if (!e || !id_list(env, a[0], &ids) || !to_i64(env, a[1], &start, "startPos") ||
+      !dev_or_null(env, a[2], "logits", &lg))
+    return nullptr;
+  if (ids.empty()) {
+    napi_throw_range_error(env, nullptr, "greedy needs at least one token id");
+    return nullptr;
+  }
+  int32_t tok = -1;
+  G4_CALL(env, g4_gemma_greedy(e->h, ids.data(), (int)ids.size(), (int)start, &tok,
+                               static_cast<float *>(lg)));
+  NAPI_CALL(env, napi_create_int32(env, tok, &v));
+  return v;
+}
+
+// e.decode(steps) -> Int32Array of the next `steps` greedy tokens
+napi_value Engine_decode(napi_env env, napi_callback_info info) {
+  napi_value a[1], self;
+  if (!get_args(env, info, 1, a, &self)) return nullptr;
+  Engine *e = unwrap_engine(env, self);
+  int64_t steps;
+  if (!e || !to_i64(env, a[0], &steps, "steps")) return nullptr;
+  if (steps < 0 || steps > INT32_MAX / 4) {
+    napi_throw_range_error(env, nullptr, "steps must be a non-negative count");
+    return nullptr;
+  }
+  napi_value ab, arr;
+  void *data = nullptr;
+  NAPI_CALL(env, napi_create_arraybuffer(env, (size_t)steps * 4, &data, &ab));
+  G4_CALL(env, g4_gemma_decode(e->h, (int)steps, static_cast<int32_t *>(data)));
+  NAPI_CALL(env, napi_create_typedarray(env, napi_int32_array, (size_t)steps, ab, 0, &arr));
+  return arr;
+}
+
+napi_value Engine_dispose(napi_env env, napi_callback_info info) {
+  napi_value self;
+  if (!get_args(env, info, 0, nullptr, &self)) return nullptr;
+  void *p = nullptr;
+  if (!is_instance(env, self, g_engine_ctor) || napi_unwrap(env, self, &p) != napi_ok || !p) {
+    napi_throw_type_error(env, nullptr, "not a GemmaEngine");
+    return nullptr;
+  }
+  Engine *e = static_cast<Engine *>(p);
+  if (e->h) {
+    g4_gemma *h = e->h;
+    e->h = nullptr;
+    G4_CALL(env, g4_gemma_free(h));
+  }
+  return undefined(env);
+}
+
 napi_value define_class(napi_env env, napi_value exports, const char *name, napi_callback ctor,
                         const napi_property_descriptor *props, size_t nprops, napi_ref *ref) {
   napi_value cls;
@@ -900,15 +1304,25 @@ napi_value Init(napi_env env, napi_value exports) {
       METHOD("linear", W4_linear), METHOD("dequant", W4_dequant), METHOD("dispose", W4_dispose),
       METHOD("info", W4_info)};
   if (!define_class(env, exports, "W4Weight", W4_new, w4_props, 4, &g_w4_ctor)) return nullptr;
-  napi_ref ple_ref;
   const napi_property_descriptor ple_props[] = {
       METHOD("shardBytes", Ple_shardBytes), METHOD("uploadShard", Ple_uploadShard),
       METHOD("gather", Ple_gather), METHOD("gatherDev", Ple_gatherDev),
       METHOD("dispose", Ple_dispose)};
-  if (!define_class(env, exports, "PleTable", Ple_new, ple_props, 5, &ple_ref)) return nullptr;
+  if (!define_class(env, exports, "PleTable", Ple_new, ple_props, 5, &g_ple_ctor)) return nullptr;
   const napi_property_descriptor cmd_props[] = {METHOD("submit", Cmd_submit),
                                                 METHOD("destroy", Cmd_destroy)};
   if (!define_class(env, exports, "CommandBuffer", Cmd_new, cmd_props, 2, &g_cmd_ctor))
+    return nullptr;
+  const napi_property_descriptor engine_props[] = {
+      METHOD("setLinear", Engine_setLinear), METHOD("setNorm", Engine_setNorm),
+      METHOD("setLayerScalar", Engine_setLayerScalar), METHOD("setEmbedding", Engine_setEmbedding),
+      METHOD("setPle", Engine_setPle), METHOD("setPleDense", Engine_setPleDense),
+      METHOD("reset", Engine_reset), METHOD("cacheLength", Engine_cacheLength),
+      METHOD("forward", Engine_forward), METHOD("logits", Engine_logits),
+      METHOD("greedy", Engine_greedy), METHOD("decode", Engine_decode),
+      METHOD("dispose", Engine_dispose)};
+  if (!define_class(env, exports, "GemmaEngine", Engine_new, engine_props,
+                    sizeof engine_props / sizeof engine_props[0], &g_engine_ctor))
     return nullptr;
   const napi_property_descriptor fns[] = {
       METHOD("init", F_init), METHOD("deviceInfo", F_deviceInfo), METHOD("sync", F_sync),
@@ -917,7 +1331,7 @@ napi_value Init(napi_env env, napi_value exports) {
       METHOD("timeMs", F_timeMs), METHOD("rms", F_rms), METHOD("addScale", F_addScale),
       METHOD("scale", F_scale), METHOD("geluMul", F_geluMul), METHOD("geluPle", F_geluPle),
       METHOD("normRope", F_normRope), METHOD("attention", F_attention),
-      METHOD("pleMix", F_pleMix), METHOD("argmax", F_argmax)};
+      METHOD("pleMix", F_pleMix), METHOD("argmax", F_argmax), METHOD("e2bConfig", F_e2bConfig)};
   NAPI_CALL(env, napi_define_properties(env, exports, sizeof fns / sizeof fns[0], fns));
   napi_value v;
   napi_create_int32(env, G4_F32, &v);

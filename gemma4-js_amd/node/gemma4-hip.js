@@ -272,12 +272,199 @@ class Gemma4Hip {
   }
 }
 
+// Engine indices of the projections and norms (include/g4hip.h G4_PROJ_* /
+// G4_NORM_*).
+const PROJ = { q: 0, k: 1, v: 2, o: 3, gate: 4, up: 5, down: 6, pleGate: 7, pleProj: 8, top: 9 };
+const NORM = {
+  input: 0, postAttn: 1, preFfw: 2, postFfw: 3, postPle: 4, q: 5, k: 6, pleProjection: 7, final: 8,
+};
+
+// Gemma4WebGPU's surface (gemma4-webgpu.js:139-481) on the native decoder
+// engine (g4_gemma_*): load / resetCache / forward / logits / greedy keep the
+// reference's meaning and return values, and each runs as one C-ABI call
+// instead of one GPUOps dispatch per op.  decode(steps) continues a greedy
+// generation on the engine's recorded decode step (one HIP graph replay per
+// token, no host round trip), returning the chosen token ids.
+class Gemma4HipEngine {
+  constructor(device, reader, opts = {}) {
+    this.device = device;
+    this.reader = reader;
+    this.maxSeq = opts.maxSeq || 512;
+    this.lmChunkRows = opts.lmChunkRows || 4096;
+    this.log = opts.log || (() => {});
+    this.hidden = opts.hidden || 1536;
+    this.pleDim = opts.pleDim || 256;
+    this.numLayers = opts.layers || 35;
+    this.heads = opts.heads || 8;
+    this.window = opts.window || 512;
+    this.spec = opts.spec || e2bSpec;
+    this.engine = null;
+    this.owned = [];   // W4 weights and device buffers the engine borrows
+    this.vocab = 0;
+    this.loaded = false;
+  }
+
+  // Layer specs as the engine takes them: a shared-KV layer reads the cache of
+  // the last earlier layer that stores its attention type (encodeLayer's
+  // this.shared[attentionType], gemma4-webgpu.js:228-240).
+  engineLayers() {
+    const out = [], store = {};
+    for (let i = 0; i < this.numLayers; i++) {
+      const s = this.spec(i);
+      let kvSource = -1;
+      if (s.shared) {
+        if (store[s.attentionType] === undefined) {
+          throw new Error(`Missing shared ${s.attentionType} KV cache at layer ${i}`);
+        }
+        kvSource = store[s.attentionType];
+      } else if (s.storeShared) {
+        store[s.attentionType] = i;
+      }
+      out.push({
+        headDim: s.headDim, intermediate: s.intermediate, full: s.full ? 1 : 0, kvSource,
+        ropeBase: s.ropeBase, ropeProp: s.ropeProp,
+      });
+    }
+    return out;
+  }
+
+  async uploadTensor(name, label) {
+    const info = this.reader.info(name);
+    const [s, e] = info.data_offsets;
+    const bytes = e - s;
+    const buf = rt.createBuffer(this.device, bytes, U.STORAGE | U.COPY_DST, label);
+    this.owned.push(buf);
+    const chunk = 64 << 20;
+    for (let off = 0; off < bytes; off += chunk) {
+      const n = Math.min(chunk, bytes - off);
+      this.device.queue.writeBuffer(buf, off, await this.reader.rangeInTensor(name, off, n));
+    }
+    return { buf, info };
+  }
+
+  async linear(layer, which, base) {
+    const w = await rt.GPUW4Linear.load(this.device, this.reader, base);
+    this.owned.push(w);
+    this.engine.setLinear(layer, PROJ[which], w.weight);
+  }
+
+  // load() (gemma4-webgpu.js:150-189)
+  async load() {
+    const embedName = 'model.language_model.embed_tokens.weight';
+    const info = this.reader.info(embedName);
+    this.vocab = info.shape[0];
+    if (info.shape[1] !== this.hidden) throw new Error(`embedding width ${info.shape[1]} != hidden ${this.hidden}`);
+    this.engine = new rt.native.GemmaEngine({
+      hidden: this.hidden, heads: this.heads, pleDim: this.pleDim, vocab: this.vocab,
+      maxSeq: this.maxSeq, window: this.window, eps: 1e-6, softcap: 30,
+      layers: this.engineLayers(),
+    });
+    const E = this.engine, r = this.reader;
+    this.log('Loading top-level W4A16 projection...');
+    await this.linear(-1, 'top', 'model.language_model.per_layer_model_projection');
+    E.setNorm(-1, NORM.pleProjection, await r.bf16('model.language_model.per_layer_projection_norm.weight'));
+    E.setNorm(-1, NORM.final, await r.bf16('model.language_model.norm.weight'));
+    this.log(`Loading ${this.numLayers} quantized transformer layers...`);
+    for (let i = 0; i < this.numLayers; i++) {
+      const root = `model.language_model.layers.${i}`, s = this.spec(i);
+      const names = layerNames(i, s);
+      for (const key of Object.keys(names)) await this.linear(i, key, names[key]);
+      E.setNorm(i, NORM.input, await r.bf16(`${root}.input_layernorm.weight`));
+      E.setNorm(i, NORM.postAttn, await r.bf16(`${root}.post_attention_layernorm.weight`));
+      E.setNorm(i, NORM.preFfw, await r.bf16(`${root}.pre_feedforward_layernorm.weight`));
+      E.setNorm(i, NORM.postFfw, await r.bf16(`${root}.post_feedforward_layernorm.weight`));
+      E.setNorm(i, NORM.postPle, await r.bf16(`${root}.post_per_layer_input_norm.weight`));
+      E.setNorm(i, NORM.q, await r.bf16(`${root}.self_attn.q_norm.weight`));
+      if (!s.shared) E.setNorm(i, NORM.k, await r.bf16(`${root}.self_attn.k_norm.weight`));
+      E.setLayerScalar(i, await r.scalarBF16(`${root}.layer_scalar`));
+    }
+    this.log('Loading tied BF16 embedding / LM head...');
+    E.setEmbedding((await this.uploadTensor(embedName, 'embed-tokens')).buf);
+    if (r.pleBundle) {
+      await r.pleBundle.loadToDevice(this.device);
+      E.setPle(r.pleBundle.table);
+    } else {
+      const { buf } = await this.uploadTensor('model.language_model.embed_tokens_per_layer.weight', 'embed-tokens-per-layer');
+      E.setPleDense(buf);
+    }
+    this.loaded = true;
+    this.log('Device model preload complete.');
+  }
+
+  resetCache() { this.engine.reset(); }
+
+  check() { if (!this.loaded) throw new Error('Model not loaded.'); }
+
+  // forward (gemma4-webgpu.js:303-402): the final-norm last row [hidden] in a
+  // new device buffer the caller destroys.
+  async forward(tokenIds, startPos) {
+    this.check();
+    const last = rt.createBuffer(this.device, this.hidden * 4, U.STORAGE | U.COPY_SRC, 'last-hidden');
+    try {
+      this.engine.forward(Int32Array.from(tokenIds), startPos, last);
+    } catch (e) { last.destroy(); throw e; }
+    return last;
+  }
+
+  // logits (gemma4-webgpu.js:404-431)
+  async logits(lastHidden) {
+    this.check();
+    const buf = rt.createBuffer(this.device, this.vocab * 4, U.STORAGE | U.COPY_SRC, 'logits');
+    try {
+      this.engine.logits(lastHidden, buf);
+      return await rt.readF32(this.device, buf, this.vocab);
+    } finally { buf.destroy(); }
+  }
+
+  // greedy (gemma4-webgpu.js:441-481)
+  async greedy(tokenIds, startPos) {
+    this.check();
+    const buf = rt.createBuffer(this.device, this.vocab * 4, U.STORAGE | U.COPY_SRC, 'logits');
+    let l;
+    try {
+      this.engine.greedy(Int32Array.from(tokenIds), startPos, buf);
+      l = await rt.readF32(this.device, buf, this.vocab);
+    } finally { buf.destroy(); }
+    let finite = 0;
+    for (let i = 0; i < l.length; i++) if (Number.isFinite(l[i])) finite++;
+    if (finite !== l.length) throw new Error(`Non-finite logits: ${l.length - finite}/${l.length}`);
+    const top10 = rt.topK(l, 10);
+    return { logits: l, top10, nextTokenId: top10[0].tokenId };
+  }
+
+  // The next `steps` greedy tokens after the last greedy()/decode() call, on
+  // the recorded decode step; an Int32Array.
+  decode(steps) {
+    this.check();
+    return this.engine.decode(steps);
+  }
+
+  cacheLength() { return this.engine.cacheLength(); }
+
+  cacheSummary() {
+    const len = this.engine.cacheLength();
+    let bytes = 0, caches = 0;
+    for (const L of this.engineLayers()) {
+      if (L.kvSource < 0) { caches++; bytes += len * L.headDim * 4 * 2; }
+    }
+    return { caches, bytes };
+  }
+
+  dispose() {
+    if (this.engine) { this.engine.dispose(); this.engine = null; }
+    for (const x of this.owned) (x.dispose ? x.dispose() : x.destroy());
+    this.owned = [];
+    this.loaded = false;
+  }
+}
+
 // The distribution reader: the CORE safetensors reader plus pleRowsToGpu from
 // a device-resident W4 PLE bundle (gpu-runtime.js:905-907, 993-995).
 function withPleBundle(reader, bundle) {
   const r = Object.create(reader);
   r.pleRowsToGpu = (device, ids) => bundle.rowsToGpu(device, ids);
+  r.pleBundle = bundle;
   return r;
 }
 
-module.exports = { Gemma4Hip, KVCache, e2bSpec, withPleBundle };
+module.exports = { Gemma4Hip, Gemma4HipEngine, KVCache, e2bSpec, withPleBundle };

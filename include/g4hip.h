@@ -369,6 +369,10 @@ int g4_gemma_set_layer_scalar(g4_gemma *m, int layer, float s);
 int g4_gemma_set_embedding(g4_gemma *m, const void *E_dev);
 /* The W4 PLE table of pleRowsToGpu (width layers * ple_dim). */
 int g4_gemma_set_ple(g4_gemma *m, const g4_ple *t);
+/* Or a dense BF16 embed_tokens_per_layer [vocab, layers * ple_dim] in device
+ * memory, whose rows are widened to FP32 per token (inputBuffers without
+ * pleRowsToGpu, gemma4-webgpu.js:198-215).  The last of the two calls wins. */
+int g4_gemma_set_ple_dense(g4_gemma *m, const void *rows_dev);
 
 /* resetCache (gemma4-webgpu.js:190-194) and the current KV length. */
 int g4_gemma_reset(g4_gemma *m);

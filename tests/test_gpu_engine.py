@@ -90,14 +90,23 @@ def tiny(g4):
     ref = lo.Model(H, heads, P, V, layers, E, ple_rows, top, ple_norm, final_norm,
                    window=TINY["window"])
 
-    def make_engine(max_seq=40):
+    # the same rows as a dense BF16 embed_tokens_per_layer (values rounded to bf16)
+    dense_bits = syn.bf16_rne(ple_rows(np.arange(V)).reshape(V, NL * P))
+    dense_f32 = syn.bf16_to_f32(dense_bits).reshape(V, NL * P)
+    ref_dense = lo.Model(H, heads, P, V, layers, E, lambda ids: dense_f32[np.asarray(ids)], top,
+                         ple_norm, final_norm, window=TINY["window"])
+
+    def make_engine(max_seq=40, dense=False):
         m = g4.Gemma(tiny_config(g4, max_seq))
         Eb = g4.Buffer.from_array(E)
         m.set_embedding(Eb)
-        t = g4.PleTable(V, NL * P, 32, RPS)
-        for s, data in enumerate(shards):
-            t.upload_shard(s, data)
-        m.set_ple(t)
+        if dense:
+            m.set_ple_dense(g4.Buffer.from_array(dense_bits))
+        else:
+            t = g4.PleTable(V, NL * P, 32, RPS)
+            for s, data in enumerate(shards):
+                t.upload_shard(s, data)
+            m.set_ple(t)
         m.set_linear(-1, "top", g4.W4Linear(*top))
         m.set_norm(-1, "ple_projection", ple_norm)
         m.set_norm(-1, "final", final_norm)
@@ -109,6 +118,7 @@ def tiny(g4):
             m.set_layer_scalar(i, L["skip"])
         return m
 
+    make_engine.ref_dense = ref_dense
     return ref, make_engine
 
 
@@ -128,6 +138,26 @@ def test_tiny_prefill_greedy_matches_oracle(g4, tiny):
     assert rel(got_lg, want_lg) < 1e-3
     assert tok == want_tok or near_tie(want_lg, tok)
     assert m.cache_length() == 12
+
+
+def test_tiny_dense_ple_rows_match_oracle(g4, tiny):
+    # embed_tokens_per_layer as dense BF16 rows instead of the W4 table
+    _, make = tiny
+    ref = make.ref_dense
+    m = make(dense=True)
+    ids = syn.token_ids(13, 7, TINY["vocab"])
+    lg = g4.Buffer(TINY["vocab"] * 4)
+    tok = m.greedy(ids, 0, lg)
+    ref.reset()
+    want_tok, want_lg = ref.greedy(ids, 0)
+    assert rel(lg.download(np.float32), want_lg) < 1e-3
+    assert tok == want_tok or near_tie(want_lg, tok)
+    toks = m.decode(3)
+    prev, pos = tok, len(ids)
+    for t in toks:
+        want, lg2 = ref.greedy([prev], pos)
+        assert t == want or near_tie(lg2, int(t))
+        prev, pos = int(t), pos + 1
 
 
 def test_tiny_decode_matches_oracle_step_by_step(g4, tiny):

@@ -124,13 +124,16 @@ def _bf16_bytes(a):
 
 
 @pytest.mark.gpu
-def test_js_model_driver_matches_oracle(tmp_path, oracle):
-    """Gemma4Hip (gemma4-hip.js: Gemma4WebGPU's load/forward/logits/greedy on the
-    HIP GPUOps) on a 5-layer checkpoint in the reference's tensor layout - W4
-    projections, BF16 norms and layer scalars, tied BF16 embedding, dense BF16
-    per-layer embeddings - against the oracle model.  Logits of the prompt
-    within relative L2 1e-3; greedy tokens equal unless the oracle's top two
-    are within 1e-3."""
+@pytest.mark.parametrize("driver", ["ops", "engine"])
+def test_js_model_driver_matches_oracle(tmp_path, oracle, driver):
+    """Gemma4WebGPU's load/forward/logits/greedy from Node on a 5-layer
+    checkpoint in the reference's tensor layout - W4 projections, BF16 norms
+    and layer scalars, tied BF16 embedding, dense BF16 per-layer embeddings -
+    against the oracle model.  Two drivers: Gemma4Hip (one GPUOps call per op,
+    as gemma4-webgpu.js) and Gemma4HipEngine (the native engine).  Logits of
+    the prompt within relative L2 1e-3; greedy tokens equal unless the
+    oracle's top two are within 1e-3.  The engine's recorded decode step must
+    choose exactly the tokens of its one-token greedy calls."""
     import layer_oracle as lo
     H, heads, P, V, window = 128, 2, 32, 512, 8
     specs = [  # sliding/global, own or shared KV, as spec(i) describes E2B layers
@@ -202,7 +205,7 @@ def test_js_model_driver_matches_oracle(tmp_path, oracle):
     cfg = dict(hidden=H, heads=heads, pleDim=P, window=window, maxSeq=32, lmChunkRows=200,
                specs=specs, prompt=prompt, steps=steps)
     (tmp_path / "cfg.json").write_text(json.dumps(cfg))
-    res = run_node("model_parity.js", str(ckpt), str(tmp_path / "cfg.json"), timeout=300)
+    res = run_node("model_parity.js", str(ckpt), str(tmp_path / "cfg.json"), driver, timeout=300)
 
     ple_f32 = syn.bf16_to_f32(ple_dense).reshape(V, NL * P)
     ref = lo.Model(H, heads, P, V, layers, E, lambda ids: ple_f32[np.asarray(ids)], top, ple_norm,
@@ -223,3 +226,5 @@ def test_js_model_driver_matches_oracle(tmp_path, oracle):
         pos += 1
     assert res["cache"]["caches"] == 2 and res["cache"]["bytes"] == pos * (64 + 128) * 4 * 2
     assert res["appendError"] == "KV append position %d != cache length %d" % (pos + 5, pos)
+    if driver == "engine":
+        assert res["decoded"] == toks[1:]
