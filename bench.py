@@ -277,6 +277,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--skip-decode", action="store_true",
                     help="leave out the E2B decode extra")
+    ap.add_argument("--decode-only", action="store_true",
+                    help="run only the E2B decode leg and print its figures")
     ap.add_argument("--decode-eager", type=int, default=0, metavar="STEPS",
                     help="only run the E2B prompt and STEPS one-token greedy calls without "
                          "graph replay (for kernel profiles), then exit")
@@ -289,6 +291,9 @@ def main():
     g4hip.init(0)
     info = g4hip.device_info()
     log("device:", info)
+    if args.decode_only:
+        print(json.dumps({"decode_e2b": bench_decode()}), flush=True)
+        return
     if args.decode_eager:
         print(json.dumps({"decode_eager": bench_decode_eager(args.decode_eager)}), flush=True)
         return

@@ -58,6 +58,18 @@ __device__ __forceinline__ float fblock_sum(float v, float *red, int nwaves) {
   return s;
 }
 
+// Sum over the prologue waves 0..pw-1 (v of the other waves is ignored); all
+// threads get it.  Every wave of the block must call it.  red: pw floats,
+// not reused by the next call before a barrier.
+__device__ __forceinline__ float pro_sum(float v, float *red, int pw, bool pro) {
+  v = wave_sum(v);
+  if (pro && (threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  float s = 0.f;
+  for (int i = 0; i < pw; ++i) s += red[i];
+  return s;
+}
+
 __device__ __forceinline__ void load8(const float *p, size_t c, float (&v)[8]) {
   const float4 a = reinterpret_cast<const float4 *>(p)[2 * c];
   const float4 b = reinterpret_cast<const float4 *>(p)[2 * c + 1];
@@ -95,10 +107,25 @@ __device__ __forceinline__ void load_rows(const FusedArgs &A, int rg, int G, int
   }
 }
 
-// Grid: at most ~2 blocks per CU; block b handles row groups b, b + grid, ...
-// (ngroups in total), staging x once and prefetching the next group's
-// weights while the current group is reduced.
-template <int GC, int TC, int IPL, int PRO, int EPI>
+// The output segment that row group rg belongs to, and its first row.
+template <int EPI>
+__device__ __forceinline__ const FusedSeg &seg_for(const FusedArgs &A, int rg, int rows_here,
+                                                   int *o0) {
+  const int nseg = EPI == kEpiGeluUp ? 1 : A.nseg;
+  int si = 0;
+  if (nseg > 1 && rg >= A.seg[1].block0) si = 1;
+  if (nseg > 2 && rg >= A.seg[2].block0) si = 2;
+  const FusedSeg &S = si == 0 ? A.seg[0] : si == 1 ? A.seg[1] : A.seg[2];
+  *o0 = (rg - S.block0) * rows_here;
+  return S;
+}
+
+// Block b owns row groups b, b + grid, ..., IT of them (ngroups in total).
+// Every weight load of those groups is issued at the start, before the
+// prologue: the prologue's chain of dependent steps (activation loads, two
+// block reductions, staging) then overlaps one HBM round trip instead of
+// delaying the later groups' loads.
+template <int GC, int TC, int IPL, int IT, int PRO, int EPI>
 __global__ __launch_bounds__(TC ? TC : 1024) void fused_gemv_kernel(FusedArgs A, int RB_,
                                                                     int ngroups) {
   extern __shared__ uint4 lds[];
@@ -109,81 +136,107 @@ __global__ __launch_bounds__(TC ? TC : 1024) void fused_gemv_kernel(FusedArgs A,
   const int t = threadIdx.x;
   const int nwaves = (T + 63) >> 6;
 
+  // The prologue runs on the first pw waves only (the 4G chunks of 8 inputs,
+  // XI per lane): the other waves skip it and meet them at the barriers, so
+  // the SIMDs are not busy with copies of the same element-wise work.
+  const int wave = t >> 6, lane = t & 63;
+  const int pw = ((nch + 63) >> 6) < nwaves ? ((nch + 63) >> 6) : nwaves;
+  const bool pro = wave < pw;  // uniform per wave
+  const int cstride = 64 * pw;
+  constexpr int XI = (GC && TC) ? (4 * GC + 63) / 64 <= TC / 64 ? 1 : (4 * GC + TC - 1) / TC : IPL;
 
-  // 1. activation chunks, issued before the weight stream (XI per thread)
-  constexpr int XI = (GC && TC) ? (4 * GC + TC - 1) / TC : IPL;
+  // 1. activation chunks, issued before the weight stream
   float av[XI][8], hv[XI][8], w1v[XI][8], w2v[XI][8];
+  if (pro) {
 #pragma unroll
-  for (int i = 0; i < XI; ++i) {
-    const int ct = t + i * T;
-    const int cc = ct < nch ? ct : nch - 1;
-    load8(A.a, cc, av[i]);
-    if (PRO != kProNone) load8(A.w1, cc, w1v[i]);
-    if (PRO == kProRes || PRO == kProResNorm) load8(A.h, cc, hv[i]);
-    if (PRO == kProResNorm) load8(A.w2, cc, w2v[i]);
+    for (int i = 0; i < XI; ++i) {
+      const int ct = t + i * cstride;
+      const int cc = ct < nch ? ct : nch - 1;
+      load8(A.a, cc, av[i]);
+      if (PRO != kProNone) load8(A.w1, cc, w1v[i]);
+      if (PRO == kProRes || PRO == kProResNorm) load8(A.h, cc, hv[i]);
+      if (PRO == kProResNorm) load8(A.w2, cc, w2v[i]);
+    }
   }
 
-  // 2. weights of the first row group (rows past N re-read the last group)
-  int rg = blockIdx.x;
-  uint4 q[IPL];
-  uint32_t s[IPL];
-  load_rows<IPL, EPI>(A, rg, G, RB, T, t, q, s);
+  // 2. weights of all the block's row groups (groups past the last re-read it
+  // and store nothing; rows past N re-read the last group)
+  uint4 q[IT][IPL];
+  uint32_t s[IT][IPL];
+#pragma unroll
+  for (int k = 0; k < IT; ++k) {
+    const int rg = blockIdx.x + k * (int)gridDim.x;
+    load_rows<IPL, EPI>(A, rg < ngroups ? rg : ngroups - 1, G, RB, T, t, q[k], s[k]);
+  }
 
   // 3. prologue
   constexpr int CH = 2;  // FP32 activations: hi and lo
   uint4 *hi = lds;
   uint4 *lo = lds + 4 * G;
   float *sx = reinterpret_cast<float *>(lds + 4 * G * CH);
-  float *part = sx + G;
-  float *rs = part + RB * G;  // row sums (kEpiGeluUp)
-  float *red = rs + RB;
+  float *part = sx + G;              // [IT * RB][G]
+  float *rs = part + IT * RB * G;    // row sums [IT * RB] (kEpiGeluUp)
+  float *red = rs + IT * RB;         // 2 x 16 wave sums
+  // Everything element-wise stays inside `if (pro)`; the reductions are
+  // called by every wave.
   float xv[XI][8];
   if (PRO == kProNone) {
+    if (pro) {
 #pragma unroll
-    for (int i = 0; i < XI; ++i)
+      for (int i = 0; i < XI; ++i)
 #pragma unroll
-      for (int e = 0; e < 8; ++e) xv[i][e] = av[i][e];
+        for (int e = 0; e < 8; ++e) xv[i][e] = av[i][e];
+    }
   } else {
     float ss = 0.f;
-#pragma unroll
-    for (int i = 0; i < XI; ++i)
-      if (t + i * T < nch)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) ss += av[i][e] * av[i][e];
-    const float inv1 = 1.f / sqrtf(fblock_sum(ss, red, nwaves) / (float)A.K + A.eps);
-    if (PRO == kProNorm) {
+    if (pro) {
 #pragma unroll
       for (int i = 0; i < XI; ++i)
+        if (t + i * cstride < nch)
 #pragma unroll
-        for (int e = 0; e < 8; ++e) xv[i][e] = av[i][e] * inv1 * w1v[i][e];
-    } else {
-      float r[XI][8];
-      float ss2 = 0.f;
-#pragma unroll
-      for (int i = 0; i < XI; ++i)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          r[i][e] = (hv[i][e] + av[i][e] * inv1 * w1v[i][e]) * A.c;
-          if (t + i * T < nch) ss2 += r[i][e] * r[i][e];
-        }
-      if (blockIdx.x == 0) {
-#pragma unroll
-        for (int i = 0; i < XI; ++i) {
-          const int ct = t + i * T;
-          if (ct < nch) {
-            float4 *ro = reinterpret_cast<float4 *>(A.r_out) + 2 * ct;
-            ro[0] = make_float4(r[i][0], r[i][1], r[i][2], r[i][3]);
-            ro[1] = make_float4(r[i][4], r[i][5], r[i][6], r[i][7]);
-          }
-        }
-      }
-      if (PRO == kProRes) {
+          for (int e = 0; e < 8; ++e) ss += av[i][e] * av[i][e];
+    }
+    const float tot1 = pro_sum(ss, red, pw, pro);
+    float r[XI][8];
+    float ss2 = 0.f;
+    if (pro) {
+      const float inv1 = 1.f / sqrtf(tot1 / (float)A.K + A.eps);
+      if (PRO == kProNorm) {
 #pragma unroll
         for (int i = 0; i < XI; ++i)
 #pragma unroll
-          for (int e = 0; e < 8; ++e) xv[i][e] = r[i][e];
+          for (int e = 0; e < 8; ++e) xv[i][e] = av[i][e] * inv1 * w1v[i][e];
       } else {
-        const float inv2 = 1.f / sqrtf(fblock_sum(ss2, red, nwaves) / (float)A.K + A.eps);
+#pragma unroll
+        for (int i = 0; i < XI; ++i)
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            r[i][e] = (hv[i][e] + av[i][e] * inv1 * w1v[i][e]) * A.c;
+            if (t + i * cstride < nch) ss2 += r[i][e] * r[i][e];
+          }
+        if (blockIdx.x == 0) {
+#pragma unroll
+          for (int i = 0; i < XI; ++i) {
+            const int ct = t + i * cstride;
+            if (ct < nch) {
+              float4 *ro = reinterpret_cast<float4 *>(A.r_out) + 2 * ct;
+              ro[0] = make_float4(r[i][0], r[i][1], r[i][2], r[i][3]);
+              ro[1] = make_float4(r[i][4], r[i][5], r[i][6], r[i][7]);
+            }
+          }
+        }
+        if (PRO == kProRes) {
+#pragma unroll
+          for (int i = 0; i < XI; ++i)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) xv[i][e] = r[i][e];
+        }
+      }
+    }
+    if (PRO == kProResNorm) {
+      const float tot2 = pro_sum(ss2, red + 16, pw, pro);
+      if (pro) {
+        const float inv2 = 1.f / sqrtf(tot2 / (float)A.K + A.eps);
 #pragma unroll
         for (int i = 0; i < XI; ++i)
 #pragma unroll
@@ -193,46 +246,42 @@ __global__ __launch_bounds__(TC ? TC : 1024) void fused_gemv_kernel(FusedArgs A,
   }
 
   // 4. stage x: hi/lo bf16 pairs per chunk, 136 * group sum
+  if (pro) {
 #pragma unroll
-  for (int i = 0; i < XI; ++i) {
-    const int ct = t + i * T;
-    uint32_t hb[8], lb[8];
-    float sum = 0.f;
+    for (int i = 0; i < XI; ++i) {
+      const int ct = t + i * cstride;
+      uint32_t hb[8], lb[8];
+      float sum = 0.f;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      hb[e] = f32_to_bf16_rne(xv[i][e]);
-      lb[e] = f32_to_bf16_rne(xv[i][e] - bf16_to_f32(hb[e]));
-      sum += bf16_to_f32(hb[e]) + bf16_to_f32(lb[e]);
-    }
-    sum += dpp_f32<0xB1>(sum);  // chunks 4g..4g+3 of a group sit in one lane quad
-    sum += dpp_f32<0x4E>(sum);
-    if (ct < nch) {
-      const int g = ct >> 2, c = ct & 3;
-      hi[c * G + g] = make_uint4(bf16_pair(hb[0], hb[4]), bf16_pair(hb[1], hb[5]),
-                                 bf16_pair(hb[2], hb[6]), bf16_pair(hb[3], hb[7]));
-      lo[c * G + g] = make_uint4(bf16_pair(lb[0], lb[4]), bf16_pair(lb[1], lb[5]),
-                                 bf16_pair(lb[2], lb[6]), bf16_pair(lb[3], lb[7]));
-      if (c == 0) sx[g] = kPairBias * sum;
+      for (int e = 0; e < 8; ++e) {
+        hb[e] = f32_to_bf16_rne(xv[i][e]);
+        lb[e] = f32_to_bf16_rne(xv[i][e] - bf16_to_f32(hb[e]));
+        sum += bf16_to_f32(hb[e]) + bf16_to_f32(lb[e]);
+      }
+      sum += dpp_f32<0xB1>(sum);  // chunks 4g..4g+3 of a group sit in one lane quad
+      sum += dpp_f32<0x4E>(sum);
+      if (ct < nch) {
+        const int g = ct >> 2, c = ct & 3;
+        hi[c * G + g] = make_uint4(bf16_pair(hb[0], hb[4]), bf16_pair(hb[1], hb[5]),
+                                   bf16_pair(hb[2], hb[6]), bf16_pair(hb[3], hb[7]));
+        lo[c * G + g] = make_uint4(bf16_pair(lb[0], lb[4]), bf16_pair(lb[1], lb[5]),
+                                   bf16_pair(lb[2], lb[6]), bf16_pair(lb[3], lb[7]));
+        if (c == 0) sx[g] = kPairBias * sum;
+      }
     }
   }
   __syncthreads();
 
-  const int rows_here = EPI == kEpiGeluUp ? RB / 2 : RB;
+  // 5. one partial per group, for every row group of the block
   uint32_t mask = 0x000F000Fu;
   asm volatile("" : "+v"(mask));  // keep the mask in a VGPR: lets v_and_or_b32 take the magic
-  for (; rg < ngroups; rg += gridDim.x) {
-    // prefetch the next row group of this block
-    const int nrg = rg + (int)gridDim.x;
-    uint4 qn[IPL];
-    uint32_t sn[IPL];
-    if (nrg < ngroups) load_rows<IPL, EPI>(A, nrg, G, RB, T, t, qn, sn);
-
-    // 5. one partial per group
+#pragma unroll
+  for (int k = 0; k < IT; ++k)
 #pragma unroll
     for (int i = 0; i < IPL; ++i) {
       const int li = t + i * T;
       const int g = li % G;
-      const uint32_t wd[4] = {q[i].x, q[i].y, q[i].z, q[i].w};
+      const uint32_t wd[4] = {q[k][i].x, q[k][i].y, q[k][i].z, q[k][i].w};
       float d0 = 0.f, d1 = 0.f;
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
@@ -251,88 +300,101 @@ __global__ __launch_bounds__(TC ? TC : 1024) void fused_gemv_kernel(FusedArgs A,
         d0 = dot2_bf16(xl.z, p2, d0);
         d1 = dot2_bf16(xl.w, p3, d1);
       }
-      part[li] = bf16_to_f32(s[i]) * ((d0 + d1) - sx[g]);
+      part[k * RB * G + li] = bf16_to_f32(s[k][i]) * ((d0 + d1) - sx[g]);
     }
-    __syncthreads();
+  __syncthreads();
 
-    // 6. 16 lanes per row sum the row's G partials, then the epilogue
-    int si = 0;
-    const int nseg = EPI == kEpiGeluUp ? 1 : A.nseg;
-    if (nseg > 1 && rg >= A.seg[1].block0) si = 1;
-    if (nseg > 2 && rg >= A.seg[2].block0) si = 2;
-    const FusedSeg &S = si == 0 ? A.seg[0] : si == 1 ? A.seg[1] : A.seg[2];
-    const int o0 = (rg - S.block0) * rows_here;
-    for (int b = 0; b < RB * 16; b += T) {
-      const int idx = b + t;
-      const int r = idx >> 4, j = idx & 15;
-      float v = 0.f;
-      if (r < RB) {
-        if (GC) {
+  // 6. 16 lanes per row sum the row's G partials, then the epilogue
+  const int rows_here = EPI == kEpiGeluUp ? RB / 2 : RB;
+  for (int b = 0; b < IT * RB * 16; b += T) {
+    const int idx = b + t;
+    const int rr = idx >> 4, j = idx & 15;  // rr = k * RB + r
+    float v = 0.f;
+    if (rr < IT * RB) {
+      if (GC) {
 #pragma unroll
-          for (int g = j; g < GC; g += 16) v += part[r * GC + g];
-        } else {
-          for (int g = j; g < G; g += 16) v += part[r * G + g];
-        }
-      }
-      v = team_sum<16>(v);
-      if (j == 0 && r < RB) {
-        if (EPI == kEpiGeluUp) {
-          rs[r] = v;
-        } else {
-          const int row = o0 + r;
-          if (row < S.N) S.y[row] = EPI == kEpiGeluMul ? gelu_tanh(v) * A.mul[row] : v;
-        }
+        for (int g = j; g < GC; g += 16) v += part[rr * GC + g];
+      } else {
+        for (int g = j; g < G; g += 16) v += part[rr * G + g];
       }
     }
-    __syncthreads();  // part (and rs) are rewritten by the next group
-    if (EPI == kEpiGeluUp) {
-      if (t < rows_here) {
-        const int row = o0 + t;
-        if (row < S.N) S.y[row] = gelu_tanh(rs[t]) * rs[t + rows_here];
+    v = team_sum<16>(v);
+    if (j == 0 && rr < IT * RB) {
+      if (EPI == kEpiGeluUp) {
+        rs[rr] = v;
+      } else {
+        const int k = rr / RB, r = rr - k * RB;
+        const int rg = blockIdx.x + k * (int)gridDim.x;
+        int o0;
+        const FusedSeg &S = seg_for<EPI>(A, rg, rows_here, &o0);
+        const int row = o0 + r;
+        if (rg < ngroups && row < S.N)
+          S.y[row] = EPI == kEpiGeluMul ? gelu_tanh(v) * A.mul[row] : v;
       }
-      __syncthreads();
     }
-#pragma unroll
-    for (int i = 0; i < IPL; ++i) {
-      q[i] = qn[i];
-      s[i] = sn[i];
+  }
+  if (EPI == kEpiGeluUp) {
+    __syncthreads();
+    for (int e = t; e < IT * rows_here; e += T) {
+      const int k = e / rows_here, r = e - k * rows_here;
+      const int rg = blockIdx.x + k * (int)gridDim.x;
+      const int row = rg * rows_here + r;
+      if (rg < ngroups && row < A.seg[0].N)
+        A.seg[0].y[row] = gelu_tanh(rs[k * RB + r]) * rs[k * RB + rows_here + r];
     }
   }
 }
 
-template <int GC, int TC, int IPL, int PRO, int EPI>
-int launch_fused_i(const FusedArgs &a, const Gemv1Plan &p, int ngroups, size_t lds) {
-  const int cap = cu_count() > 0 ? cu_count() : 256;
-  const int blocks = ngroups < cap ? ngroups : cap;
-  hipLaunchKernelGGL((fused_gemv_kernel<GC, TC, IPL, PRO, EPI>), dim3(blocks), dim3(p.T), lds,
+// LDS of a fused launch: x hi/lo pairs, group sums, IT * RB rows of partials
+// and row sums, the reduction scratch.
+size_t fused_lds(int G, int RB, int IT) {
+  return (size_t)G * 4 * 16 * 2 + (size_t)G * 4 + (size_t)IT * RB * G * 4 + (size_t)IT * RB * 4 +
+         32 * 4;
+}
+
+template <int GC, int TC, int IPL, int IT, int PRO, int EPI>
+int launch_fused_it(const FusedArgs &a, const Gemv1Plan &p, int ngroups) {
+  const int blocks = (ngroups + IT - 1) / IT;
+  const size_t lds = fused_lds(GC ? GC : a.K / 32, p.RB, IT);
+  if (lds > 64 * 1024) return fail(G4_E_ARG, "fused GEMV: %zu bytes of LDS", lds);
+  hipLaunchKernelGGL((fused_gemv_kernel<GC, TC, IPL, IT, PRO, EPI>), dim3(blocks), dim3(p.T), lds,
                      stream(), a, p.RB, ngroups);
   G4_LAUNCH_CHECK("fused_gemv_kernel");
   return G4_OK;
 }
 
-// Rows per block: the largest power of two (at least 8) not above
-// rows / (2 CUs), every weight load of a row group issued at once (up to 4
-// groups per thread); launched with one block per CU looping over the groups
-// (measured best for the E2B gate/up shapes: 16 and 32 rows).
+// Row groups per block: one per block while they fit one wave of blocks on
+// the CUs, else more per block, up to 3 (measured: more loads per block
+// delay the blocks' activation loads behind their weight stream).
+template <int GC, int TC, int IPL, int PRO, int EPI>
+int launch_fused_i(const FusedArgs &a, const Gemv1Plan &p, int ngroups) {
+  constexpr int kMaxIt = IPL <= 2 ? 3 : 2;
+  const int cap = cu_count() > 0 ? cu_count() : 256;
+  int it = (ngroups + cap - 1) / cap;
+  it = it < 1 ? 1 : it > kMaxIt ? kMaxIt : it;
+  switch (it) {
+    case 1: return launch_fused_it<GC, TC, IPL, 1, PRO, EPI>(a, p, ngroups);
+    case 2: return launch_fused_it<GC, TC, IPL, 2, PRO, EPI>(a, p, ngroups);
+    default: return launch_fused_it<GC, TC, IPL, kMaxIt, PRO, EPI>(a, p, ngroups);
+  }
+}
+
+// Rows per block: 16 (8 when there are fewer than 2048 rows), one 16-byte
+// group per thread (measured best for the Gemma-4-E2B shapes with cold
+// weights: gate/up 6144 and 12288, q/k/v, the PLE gate).
 bool plan_fused(int G, int total_rows, Gemv1Plan *p) {
-  const int cus = cu_count() > 0 ? cu_count() : 256;
-  const int target = (total_rows + 2 * cus - 1) / (2 * cus);
-  bool found = false;
-  for (int RB = 8; RB <= 256; RB *= 2) {
-    if (found && RB > target) break;
+  const int want = total_rows >= 2048 ? 16 : 8;
+  for (int RB = want; RB <= 256; RB *= 2)
     for (int ipl = 1; ipl <= 4; ++ipl) {
       const long items = (long)RB * G;
       if (items % ipl || (items / ipl) % 64 || items / ipl > 1024) continue;
-      found = true;
       p->T = (int)(items / ipl);
       p->IPL = ipl;
       p->RB = RB;
-      break;
+      p->lds = fused_lds(G, RB, 3);
+      return p->lds <= 64 * 1024;
     }
-  }
-  if (!found) return plan_gemv1(G, true, p, 4);
-  p->lds = (size_t)G * 4 * 16 * 2 + (size_t)G * 4 + (size_t)p->RB * G * 4;
-  return p->lds <= 64 * 1024;
+  return false;
 }
 
 template <int PRO, int EPI>
@@ -356,19 +418,15 @@ int launch_fused(FusedArgs a) {
       groups += (a.seg[i].N + rows_per_group - 1) / rows_per_group;
     }
   }
-  const size_t lds = p.lds + (size_t)p.RB * 4 + 16 * 4;
   if (G == 48) {  // the E2B hidden size 1536
-    if (p.T == 384 && p.IPL == 1) return launch_fused_i<48, 384, 1, PRO, EPI>(a, p, groups, lds);
-    if (p.T == 768 && p.IPL == 1) return launch_fused_i<48, 768, 1, PRO, EPI>(a, p, groups, lds);
-    if (p.T == 768 && p.IPL == 2) return launch_fused_i<48, 768, 2, PRO, EPI>(a, p, groups, lds);
-    if (p.T == 768 && p.IPL == 4) return launch_fused_i<48, 768, 4, PRO, EPI>(a, p, groups, lds);
-    if (p.T == 1024 && p.IPL == 3) return launch_fused_i<48, 1024, 3, PRO, EPI>(a, p, groups, lds);
+    if (p.T == 384 && p.IPL == 1) return launch_fused_i<48, 384, 1, PRO, EPI>(a, p, groups);
+    if (p.T == 768 && p.IPL == 1) return launch_fused_i<48, 768, 1, PRO, EPI>(a, p, groups);
   }
   switch (p.IPL) {
-    case 1: return launch_fused_i<0, 0, 1, PRO, EPI>(a, p, groups, lds);
-    case 2: return launch_fused_i<0, 0, 2, PRO, EPI>(a, p, groups, lds);
-    case 3: return launch_fused_i<0, 0, 3, PRO, EPI>(a, p, groups, lds);
-    default: return launch_fused_i<0, 0, 4, PRO, EPI>(a, p, groups, lds);
+    case 1: return launch_fused_i<0, 0, 1, PRO, EPI>(a, p, groups);
+    case 2: return launch_fused_i<0, 0, 2, PRO, EPI>(a, p, groups);
+    case 3: return launch_fused_i<0, 0, 3, PRO, EPI>(a, p, groups);
+    default: return launch_fused_i<0, 0, 4, PRO, EPI>(a, p, groups);
   }
 }
 

@@ -33,6 +33,17 @@ __device__ __forceinline__ float team_sum(float v) {
   return v;
 }
 
+// Sum over the 64 lanes of a wave; every lane gets it (DPP within rows of 16
+// lanes, then the four row sums read from lanes 0, 16, 32 and 48).
+__device__ __forceinline__ float wave_sum(float v) {
+  v = team_sum<16>(v);
+  const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+  const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+  const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+  const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+  return (r0 + r1) + (r2 + r3);
+}
+
 __device__ __forceinline__ uint32_t bf16_pair(uint32_t lo16, uint32_t hi16) {
   return (lo16 & 0xffffu) | (hi16 << 16);
 }
