@@ -27,6 +27,7 @@ constexpr int kProjs = 9;  // q, k, v, o, gate, up, down, ple_gate, ple_proj
 
 struct Layer {
   int hd = 0, inter = 0, full = 0, kv_src = -1, rope_angles = 0;
+  int rope_slot = -1;  // RoPE table of the one-launch decode attention, -1: the op-by-op path
   float rope_base = 0.f;
   const g4_w4 *w[kProjs] = {};
   float *norm[kNorms] = {};
@@ -107,6 +108,9 @@ struct g4_gemma {
         *perlayer = nullptr, *last = nullptr, *logits = nullptr, *part = nullptr;
   float2 *hpart = nullptr;
   size_t part_floats = 0;
+  RopeSlots rope_slots = {};
+  float2 *rope_tab = nullptr;  // [kRopeSlots][kRopeTable] at the current position
+  int *attn_count = nullptr;   // [heads] split counters of the decode attention
   std::vector<void *> allocs;
   g4_cmdbuf *step = nullptr;  // recorded one-token decode step
 };
@@ -173,7 +177,8 @@ int run_token(g4_gemma *m, bool graph) {
   const int H = c.hidden, P = c.ple_dim, NL = c.layers;
   const float eps = c.eps;
   int rc;
-  if ((rc = launch_embed(m->E, c.vocab, H, m->ids, 1, (float)sqrt((double)H), m->h[0])))
+  if ((rc = launch_token_start(m->E, c.vocab, H, m->ids, (float)sqrt((double)H), m->h[0], m->pos,
+                               m->rope_slots, m->rope_tab)))
     return rc;
   if ((rc = token_ple(m, 1))) return rc;
   if ((rc = g4_w4_linear(m->top, m->h[0], G4_F32, 1, m->proj, G4_F32))) return rc;
@@ -203,13 +208,23 @@ int run_token(g4_gemma *m, bool graph) {
     }
     if (rc) return rc;
     const Layer &src = own ? l : m->L[l.kv_src];
-    if ((rc = launch_rope_qkv(m->qraw, m->kraw, m->vraw, c.heads, l.hd, m->pos,
-                              l.norm[G4_NORM_Q], l.norm[G4_NORM_K], l.rope_angles, l.rope_base,
-                              eps, m->q, l.kc, l.vc, own)))
-      return rc;
-    if ((rc = launch_attention(m->q, src.kc, src.vc, 1, c.heads, l.hd, keylen_host, 0, m->pos,
-                               max_keylen, !l.full, c.window, kpw_for(1), m->part, m->ctx)))
-      return rc;
+    if (l.rope_slot >= 0) {
+      // norm + RoPE, cache append, attention and split merge in one launch
+      rc = launch_attn_rope_dec(m->qraw, m->kraw, m->vraw, c.heads, l.hd, m->pos,
+                                l.norm[G4_NORM_Q], l.norm[G4_NORM_K],
+                                m->rope_tab + (size_t)l.rope_slot * kRopeTable, l.rope_angles,
+                                eps, src.kc, src.vc, own, !l.full, c.window, max_keylen,
+                                m->part, m->part_floats, m->attn_count, m->ctx);
+      if (rc) return rc;
+    } else {
+      if ((rc = launch_rope_qkv(m->qraw, m->kraw, m->vraw, c.heads, l.hd, m->pos,
+                                l.norm[G4_NORM_Q], l.norm[G4_NORM_K], l.rope_angles,
+                                l.rope_base, eps, m->q, l.kc, l.vc, own)))
+        return rc;
+      if ((rc = launch_attention(m->q, src.kc, src.vc, 1, c.heads, l.hd, keylen_host, 0, m->pos,
+                                 max_keylen, !l.full, c.window, kpw_for(1), m->part, m->ctx)))
+        return rc;
+    }
     if ((rc = g4_w4_linear(l.w[G4_PROJ_O], m->ctx, G4_F32, 1, m->attn, G4_F32))) return rc;
     if ((rc = fused_res_norm_gate_up(m->attn, hid, l.norm[G4_NORM_POST_ATTN], 1.f,
                                      l.norm[G4_NORM_PRE_FFW], eps, m->ares, l.w[G4_PROJ_GATE],
@@ -424,6 +439,20 @@ G4_API int g4_gemma_create(const g4_gemma_config *cfg, g4_gemma **out) {
     l.rope_angles = (int)floorf(c.rope_prop[i] * (float)l.hd / 2.f);
     if (l.hd > m->hd_max) m->hd_max = l.hd;
     if (l.inter > m->inter_max) m->inter_max = l.inter;
+    // one RoPE table per distinct (base, head_dim, angles) of the layers the
+    // one-launch decode attention serves
+    if (attn_rope_supported(l.hd) && l.rope_angles <= kRopeTable) {
+      RopeSlots &rs = m->rope_slots;
+      for (int j = 0; j < rs.n; ++j)
+        if (rs.base[j] == l.rope_base && rs.hd[j] == l.hd && rs.angles[j] == l.rope_angles)
+          l.rope_slot = j;
+      if (l.rope_slot < 0 && rs.n < kRopeSlots) {
+        rs.base[rs.n] = l.rope_base;
+        rs.hd[rs.n] = l.hd;
+        rs.angles[rs.n] = l.rope_angles;
+        l.rope_slot = rs.n++;
+      }
+    }
   }
   const size_t R = (size_t)m->max_rows, H = c.hidden;
   const size_t QD = (size_t)c.heads * m->hd_max;
@@ -467,10 +496,17 @@ G4_API int g4_gemma_create(const g4_gemma_config *cfg, g4_gemma **out) {
     const size_t a = attention_part_floats(small, c.heads, m->hd_max, c.max_seq, kpw_for(1));
     const size_t b = attention_part_floats(m->max_rows, c.heads, m->hd_max, c.max_seq,
                                            kpw_for(m->max_rows));
+    // and the one-launch decode attention's partials: heads x splits x (hd + 4)
+    const size_t d = (size_t)c.heads * attn_rope_splits(c.max_seq, false, c.window) *
+                     ((size_t)m->hd_max + 4);
     m->part_floats = a > b ? a : b;
+    if (d > m->part_floats) m->part_floats = d;
     A(&m->part, m->part_floats);
   }
   if (!rc) rc = galloc_n(m, head_argmax_blocks(c.vocab), &m->hpart);
+  if (!rc) rc = galloc_n(m, (size_t)kRopeSlots * kRopeTable, &m->rope_tab);
+  if (!rc) rc = galloc_n(m, (size_t)c.heads, &m->attn_count);  // zero-filled
+
   for (int i = 0; i < c.layers && !rc; ++i) {
     Layer &l = m->L[i];
     if (l.kv_src < 0) {

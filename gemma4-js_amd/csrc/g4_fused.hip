@@ -487,6 +487,362 @@ __global__ __launch_bounds__(256) void rope_qkv_kernel(
   yo[t + half] = cn * cs + an * sn;
 }
 
+// ---- token start: the scaled embedding row and the RoPE tables -------------
+// Block 0 writes y = bf16 row(ids[0]) * scale (NaN for an id out of range);
+// block 1 + j fills table j with (cos, sin) of theta = pos / base^(2t/hd) for
+// t < angles at the current position, the angles of NORM_ROPE_SHADER
+// (gpu-runtime.js:1175-1202), so the attention kernels do no pow/sin/cos.
+__global__ __launch_bounds__(256) void token_start_kernel(const uint16_t *__restrict__ E,
+                                                          int vocab, int width,
+                                                          const int *__restrict__ ids,
+                                                          float scale, float *__restrict__ y,
+                                                          const int *__restrict__ pos_dev,
+                                                          RopeSlots slots,
+                                                          float2 *__restrict__ tab) {
+  const int b = blockIdx.x;
+  if (b == 0) {
+    const int id = ids[0];
+    const bool ok = id >= 0 && id < vocab;
+    for (int i = threadIdx.x; i < width; i += 256)
+      y[i] = ok ? bf16_to_f32(E[(size_t)id * width + i]) * scale : __int_as_float(0x7fc00000);
+    return;
+  }
+  const int j = b - 1;
+  const int pos = *pos_dev;
+  const int hd = slots.hd[j];
+  for (int t = threadIdx.x; t < slots.angles[j]; t += 256) {
+    const float ex = 2.f * (float)t / (float)hd;
+    const float theta = (float)pos / powf(slots.base[j], ex);
+    tab[j * kRopeTable + t] = make_float2(cosf(theta), sinf(theta));
+  }
+}
+
+// ---- decode attention in one launch ------------------------------------------
+// The q/k RMS norm and RoPE and the v norm (NORM_ROPE_SHADER), the append of
+// k and v at position pos of the cache (KVCache.append), attention of the one
+// query over the visible keys (QK, SOFTMAX and ATTN_OUT shaders,
+// gpu-runtime.js:1204-1248) and the merge of the key splits.
+//
+// Grid: H * S blocks, block h * S + s = head h, split s of the visible keys
+// [lo, pos] (S a multiple of 8: the blocks of one split share an XCD and
+// its L2 copy of the k/v rows).  Block = 4 waves; wave w takes keys
+// k0 + w, k0 + w + 4, ...  A wave holds a whole head: lane l keeps dims
+// [l*DH, l*DH + DH) and their RoPE partners [hd/2 + l*DH, ...), so the norms
+// are wave reductions and the rotation stays in the lane.  Every wave
+// normalises and rotates q itself; the wave whose keys include pos also
+// builds the new k and v (block h = 0 writes them to the cache).
+// Each block writes (max, sum, unnormalised output) of its keys; the last
+// block of a head to finish (a device-scope counter, reset by that block)
+// merges the S partials into ctx.
+struct AttnRopeArgs {
+  const float *qraw, *kraw, *vraw;  // [H, hd], [hd], [hd]
+  const float *qnorm, *knorm;       // [hd]
+  const float2 *rope;               // (cos, sin) at the current position, [angles]
+  float *kc, *vc;                   // caches [max_seq, hd]
+  float *part;                      // [H][S][hd + 2]
+  int *count;                       // [H], zero between launches
+  float *ctx;                       // [H, hd]
+  const int *pos_dev;
+  int H, S, angles, own, sliding, window;
+  float eps;
+};
+
+template <int DH>
+__device__ __forceinline__ void load_halves(const float *p, int lane, float (&a)[DH],
+                                            float (&b)[DH]) {
+  constexpr int HALF = 64 * DH;
+  if constexpr (DH == 4) {
+    const float4 x = *reinterpret_cast<const float4 *>(p + lane * 4);
+    const float4 z = *reinterpret_cast<const float4 *>(p + HALF + lane * 4);
+    a[0] = x.x; a[1] = x.y; a[2] = x.z; a[3] = x.w;
+    b[0] = z.x; b[1] = z.y; b[2] = z.z; b[3] = z.w;
+  } else if constexpr (DH == 2) {
+    const float2 x = *reinterpret_cast<const float2 *>(p + lane * 2);
+    const float2 z = *reinterpret_cast<const float2 *>(p + HALF + lane * 2);
+    a[0] = x.x; a[1] = x.y;
+    b[0] = z.x; b[1] = z.y;
+  } else {
+    a[0] = p[lane];
+    b[0] = p[HALF + lane];
+  }
+}
+
+// Device-coherent buffer accesses (cache policy SC1): they bypass the L2
+// state that is private to one XCD, so data handed between blocks on
+// different XCDs needs no L2 writeback or invalidate.
+constexpr int kSc1 = 16;
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t coherent_rsrc(float *p, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(p, 0, bytes, 0x00020000);
+}
+
+template <int N>
+__device__ __forceinline__ void ld_coherent(__amdgpu_buffer_rsrc_t r, int off, float *v) {
+  if constexpr (N == 4) {
+    const u32x4v x = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kSc1);
+    v[0] = __uint_as_float(x.x); v[1] = __uint_as_float(x.y);
+    v[2] = __uint_as_float(x.z); v[3] = __uint_as_float(x.w);
+  } else if constexpr (N == 2) {
+    const u32x2 x = __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, kSc1);
+    v[0] = __uint_as_float(x.x); v[1] = __uint_as_float(x.y);
+  } else {
+    v[0] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, off, 0, kSc1));
+  }
+}
+
+__device__ __forceinline__ void st_coherent4(__amdgpu_buffer_rsrc_t r, int off, float a, float b,
+                                             float c, float d) {
+  const u32x4v x = {__float_as_uint(a), __float_as_uint(b), __float_as_uint(c), __float_as_uint(d)};
+  __builtin_amdgcn_raw_buffer_store_b128(x, r, off, 0, kSc1);
+}
+
+template <int DH>
+__device__ __forceinline__ void store_halves(float *p, int lane, const float (&a)[DH],
+                                             const float (&b)[DH]) {
+  constexpr int HALF = 64 * DH;
+#pragma unroll
+  for (int j = 0; j < DH; ++j) {
+    p[lane * DH + j] = a[j];
+    p[HALF + lane * DH + j] = b[j];
+  }
+}
+
+// x = rms(x) * scale (SCALE), then (ROPE) the rotation of the pairs
+// (t, t + hd/2) for t < angles: the arithmetic of rope_qkv_kernel.  Every
+// load is unconditional (clamped index) so that none waits inside a branch.
+template <int DH, bool SCALE, bool ROPE>
+__device__ __forceinline__ void norm_rope_wave(float (&a)[DH], float (&b)[DH],
+                                               const float *scale, const float2 *rope,
+                                               int angles, float eps, int lane) {
+  constexpr int HALF = 64 * DH;
+  float sa[DH], sb[DH];
+  float2 r[DH];
+#pragma unroll
+  for (int j = 0; j < DH; ++j) {
+    const int t = lane * DH + j;
+    if (SCALE) {
+      sa[j] = scale[t];
+      sb[j] = scale[HALF + t];
+    }
+    if (ROPE) {
+      r[j] = rope[t < angles ? t : (angles > 0 ? angles - 1 : 0)];
+      asm volatile("" ::"v"(r[j].x), "v"(r[j].y));  // load here, not in a branch below
+    }
+  }
+  float ss = 0.f;
+#pragma unroll
+  for (int j = 0; j < DH; ++j) ss += a[j] * a[j] + b[j] * b[j];
+  const float inv = 1.f / sqrtf(wave_sum(ss) / (float)(2 * HALF) + eps);
+#pragma unroll
+  for (int j = 0; j < DH; ++j) {
+    const int t = lane * DH + j;
+    const float an = SCALE ? a[j] * inv * sa[j] : a[j] * inv;
+    const float bn = SCALE ? b[j] * inv * sb[j] : b[j] * inv;
+    if (ROPE) {
+      const bool rot = t < angles;
+      a[j] = rot ? an * r[j].x - bn * r[j].y : an;
+      b[j] = rot ? bn * r[j].x + an * r[j].y : bn;
+    } else {
+      a[j] = an;
+      b[j] = bn;
+    }
+  }
+}
+
+template <int DH>
+__global__ __launch_bounds__(256) void attn_rope_dec_kernel(AttnRopeArgs A) {
+  constexpr int HALF = 64 * DH, HD = 2 * HALF;
+  constexpr int KC = DH == 4 ? 4 : 8;  // keys per wave whose loads are in flight together
+  __shared__ float wm[4], wl[4];
+  __shared__ float wo[4][HD];
+  __shared__ int last_sh;
+  const int h = blockIdx.x / A.S, s = blockIdx.x - h * A.S;
+  const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
+  const int pos = *A.pos_dev;
+  int lo = A.sliding ? pos - A.window + 1 : 0;
+  lo = lo > 0 ? lo : 0;
+  const int kps = (pos - lo + A.S) / A.S;  // ceil((pos - lo + 1) / S)
+  const int k0 = lo + s * kps;
+  const int k1 = k0 + kps < pos + 1 ? k0 + kps : pos + 1;  // [k0, k1), maybe empty
+
+  // k/v rows of the wave's first KC keys, issued before everything else
+  // (clamped to valid rows; keys past k1 are not used)
+  float ka[KC][DH], kb[KC][DH], xa[KC][DH], xb[KC][DH];
+  int base = k0 + wave;
+  auto load_chunk = [&](int b0) {
+#pragma unroll
+    for (int c = 0; c < KC; ++c) {
+      int key = b0 + 4 * c;
+      key = key < k1 ? key : k1 - 1;
+      load_halves<DH>(A.kc + (size_t)key * HD, lane, ka[c], kb[c]);
+      load_halves<DH>(A.vc + (size_t)key * HD, lane, xa[c], xb[c]);
+    }
+  };
+  load_chunk(base);
+
+  float qa[DH], qb[DH];
+  load_halves<DH>(A.qraw + (size_t)h * HD, lane, qa, qb);
+  norm_rope_wave<DH, true, true>(qa, qb, A.qnorm, A.rope, A.angles, A.eps, lane);
+
+  // the new key at pos (own-KV layers): built by the wave that owns it
+  const bool has_new = A.own && k0 <= pos && pos < k1 && ((pos - k0) & 3) == wave;
+  float na[DH], nb[DH], va[DH], vb[DH];
+  if (has_new) {
+    load_halves<DH>(A.kraw, lane, na, nb);
+    load_halves<DH>(A.vraw, lane, va, vb);
+    norm_rope_wave<DH, true, true>(na, nb, A.knorm, A.rope, A.angles, A.eps, lane);
+    norm_rope_wave<DH, false, false>(va, vb, nullptr, nullptr, 0, A.eps, lane);
+    if (h == 0) {
+      store_halves<DH>(A.kc + (size_t)pos * HD, lane, na, nb);
+      store_halves<DH>(A.vc + (size_t)pos * HD, lane, va, vb);
+    }
+  }
+
+  float m = -1e30f, l = 0.f, oa[DH], ob[DH];
+#pragma unroll
+  for (int j = 0; j < DH; ++j) oa[j] = ob[j] = 0.f;
+  for (;;) {  // one chunk of up to KC keys per pass (an empty chunk changes nothing)
+    float d[KC];
+    float mc = m;
+#pragma unroll
+    for (int c = 0; c < KC; ++c) {
+      const int key = base + 4 * c;
+      if (has_new && key == pos) {
+#pragma unroll
+        for (int j = 0; j < DH; ++j) {
+          ka[c][j] = na[j]; kb[c][j] = nb[j];
+          xa[c][j] = va[j]; xb[c][j] = vb[j];
+        }
+      }
+      float acc = 0.f;
+#pragma unroll
+      for (int j = 0; j < DH; ++j) acc = fmaf(qb[j], kb[c][j], fmaf(qa[j], ka[c][j], acc));
+      d[c] = wave_sum(acc);
+      if (key < k1) mc = fmaxf(mc, d[c]);
+    }
+    const float corr = expf(m - mc);
+    l *= corr;
+#pragma unroll
+    for (int j = 0; j < DH; ++j) {
+      oa[j] *= corr;
+      ob[j] *= corr;
+    }
+#pragma unroll
+    for (int c = 0; c < KC; ++c) {
+      if (base + 4 * c >= k1) break;  // wave-uniform; the clamped rows are not used
+      const float p = expf(d[c] - mc);
+      l += p;
+#pragma unroll
+      for (int j = 0; j < DH; ++j) {
+        oa[j] = fmaf(p, xa[c][j], oa[j]);
+        ob[j] = fmaf(p, xb[c][j], ob[j]);
+      }
+    }
+    m = mc;
+    base += 4 * KC;
+    if (base >= k1) break;
+    load_chunk(base);
+  }
+
+  // merge the 4 waves, write the block's partial
+  if (lane == 0) {
+    wm[wave] = m;
+    wl[wave] = l;
+  }
+#pragma unroll
+  for (int j = 0; j < DH; ++j) {
+    wo[wave][lane * DH + j] = oa[j];
+    wo[wave][HALF + lane * DH + j] = ob[j];
+  }
+  __syncthreads();
+  const float M = fmaxf(fmaxf(wm[0], wm[1]), fmaxf(wm[2], wm[3]));
+  const float e0 = expf(wm[0] - M), e1 = expf(wm[1] - M), e2 = expf(wm[2] - M),
+              e3 = expf(wm[3] - M);
+  // The partials cross XCDs (whose L2s are not coherent with each other):
+  // they are written and read with device-coherent accesses, so that no L2
+  // writeback or invalidate (a fence) is needed around the counter.
+  // Partial of split s: [max, sum, 0, 0, output[HD]] (stride HD + 4 floats).
+  constexpr int stride = HD + 4;
+  const __amdgpu_buffer_rsrc_t pr =
+      coherent_rsrc(A.part + (size_t)h * A.S * stride, (uint32_t)(A.S * stride * 4));
+  const int pbase = s * stride * 4;
+  if (t < HD / 4) {
+    float v[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int dd = 4 * t + j;
+      v[j] = wo[0][dd] * e0 + wo[1][dd] * e1 + wo[2][dd] * e2 + wo[3][dd] * e3;
+    }
+    st_coherent4(pr, pbase + 16 + 16 * t, v[0], v[1], v[2], v[3]);
+  } else if (t == HD / 4) {
+    st_coherent4(pr, pbase, M, wl[0] * e0 + wl[1] * e1 + wl[2] * e2 + wl[3] * e3, 0.f, 0.f);
+  }
+
+  // the last block of head h merges the S partials
+  __builtin_amdgcn_s_waitcnt(0);  // this wave's coherent stores are performed
+  __syncthreads();
+  if (t == 0)
+    last_sh = __hip_atomic_fetch_add(&A.count[h], 1, __ATOMIC_RELAXED,
+                                     __HIP_MEMORY_SCOPE_AGENT) == A.S - 1;
+  __syncthreads();
+  if (!last_sh) return;
+  // wave w merges splits w, w + 4, ... (up to 16 each, all loads in flight
+  // together; lanes hold the dims as above), then the 4 waves merge in LDS
+  constexpr int SW = 16;
+  float pm[SW], pl[SW], pa[SW][DH], pb[SW][DH];
+#pragma unroll
+  for (int i = 0; i < SW; ++i) {
+    int j = wave + 4 * i;
+    j = j < A.S ? j : A.S - 1;
+    const int pj = j * stride * 4;
+    float ml[2];
+    ld_coherent<2>(pr, pj, ml);
+    pm[i] = ml[0];
+    pl[i] = ml[1];
+    ld_coherent<DH>(pr, pj + 16 + 4 * lane * DH, pa[i]);
+    ld_coherent<DH>(pr, pj + 16 + 4 * (HALF + lane * DH), pb[i]);
+  }
+  float mw = -1e30f;
+#pragma unroll
+  for (int i = 0; i < SW; ++i) mw = fmaxf(mw, wave + 4 * i < A.S ? pm[i] : -1e30f);
+  float lw = 0.f;
+#pragma unroll
+  for (int j = 0; j < DH; ++j) oa[j] = ob[j] = 0.f;
+#pragma unroll
+  for (int i = 0; i < SW; ++i) {
+    // splits past S re-read split S - 1 and weigh 0: no load waits in a branch
+    const float w = wave + 4 * i < A.S ? expf(pm[i] - mw) : 0.f;
+    lw = fmaf(w, pl[i], lw);
+#pragma unroll
+    for (int j = 0; j < DH; ++j) {
+      oa[j] = fmaf(w, pa[i][j], oa[j]);
+      ob[j] = fmaf(w, pb[i][j], ob[j]);
+    }
+  }
+  if (lane == 0) {  // wm/wl/wo were last read before the barriers above
+    wm[wave] = mw;
+    wl[wave] = lw;
+  }
+#pragma unroll
+  for (int j = 0; j < DH; ++j) {
+    wo[wave][lane * DH + j] = oa[j];
+    wo[wave][HALF + lane * DH + j] = ob[j];
+  }
+  __syncthreads();
+  {
+    const float Mx = fmaxf(fmaxf(wm[0], wm[1]), fmaxf(wm[2], wm[3]));
+    const float f0 = expf(wm[0] - Mx), f1 = expf(wm[1] - Mx), f2 = expf(wm[2] - Mx),
+                f3 = expf(wm[3] - Mx);
+    const float L = wl[0] * f0 + wl[1] * f1 + wl[2] * f2 + wl[3] * f3;
+    for (int dd = t; dd < HD; dd += 256)
+      A.ctx[(size_t)h * HD + dd] =
+          (wo[0][dd] * f0 + wo[1][dd] * f1 + wo[2][dd] * f2 + wo[3][dd] * f3) / L;
+  }
+  if (t == 0) A.count[h] = 0;
+}
+
 // ---- standalone chain r = (h + rms(a) * w1) * c; x = rms(r) * w2 ------------
 // One block per row; writes r (if r_out) and x.
 __global__ __launch_bounds__(256) void norm_chain_kernel(const float *__restrict__ a,
@@ -593,6 +949,65 @@ int launch_rope_qkv(const float *qraw, const float *kraw, const float *vraw, int
                      qraw, kraw, vraw, heads, hd, pos_dev, qnorm, knorm, rope_angles, base, eps,
                      q, kc, vc);
   G4_LAUNCH_CHECK("rope_qkv_kernel");
+  return G4_OK;
+}
+
+int launch_token_start(const uint16_t *E, int vocab, int width, const int *ids_dev, float scale,
+                       float *y, const int *pos_dev, const RopeSlots &slots, float2 *tab) {
+  if (slots.n < 0 || slots.n > kRopeSlots) return fail(G4_E_ARG, "token start: %d RoPE tables", slots.n);
+  for (int j = 0; j < slots.n; ++j)
+    if (slots.angles[j] > kRopeTable) return fail(G4_E_ARG, "token start: %d RoPE angles", slots.angles[j]);
+  hipLaunchKernelGGL(token_start_kernel, dim3(1 + slots.n), dim3(256), 0, stream(), E, vocab,
+                     width, ids_dev, scale, y, pos_dev, slots, tab);
+  G4_LAUNCH_CHECK("token_start_kernel");
+  return G4_OK;
+}
+
+int attn_rope_splits(int max_keylen, bool sliding, int window) {
+  const int span = sliding && window < max_keylen ? window : max_keylen;
+  int S = (span + 31) / 32;
+  S = (S + 7) / 8 * 8;
+  return S < 8 ? 8 : S > 64 ? 64 : S;
+}
+
+bool attn_rope_supported(int hd) { return hd == 128 || hd == 256 || hd == 512; }
+
+int launch_attn_rope_dec(const float *qraw, const float *kraw, const float *vraw, int heads,
+                         int hd, const int *pos_dev, const float *qnorm, const float *knorm,
+                         const float2 *rope, int angles, float eps, float *kc, float *vc,
+                         bool own_kv, bool sliding, int window, int max_keylen, float *part,
+                         size_t part_floats, int *count, float *ctx) {
+  AttnRopeArgs a;
+  a.qraw = qraw;
+  a.kraw = kraw;
+  a.vraw = vraw;
+  a.qnorm = qnorm;
+  a.knorm = knorm;
+  a.rope = rope;
+  a.kc = kc;
+  a.vc = vc;
+  a.part = part;
+  a.count = count;
+  a.ctx = ctx;
+  a.pos_dev = pos_dev;
+  a.H = heads;
+  a.S = attn_rope_splits(max_keylen, sliding, window);
+  a.angles = angles;
+  a.own = own_kv ? 1 : 0;
+  a.sliding = sliding ? 1 : 0;
+  a.window = window;
+  a.eps = eps;
+  if ((size_t)heads * a.S * ((size_t)hd + 4) > part_floats)
+    return fail(G4_E_ARG, "decode attention: split scratch too small");
+  if (angles > hd / 2 || angles > kRopeTable) return fail(G4_E_ARG, "decode attention: %d angles", angles);
+  const dim3 grid(heads * a.S);
+  switch (hd) {
+    case 128: hipLaunchKernelGGL(attn_rope_dec_kernel<1>, grid, dim3(256), 0, stream(), a); break;
+    case 256: hipLaunchKernelGGL(attn_rope_dec_kernel<2>, grid, dim3(256), 0, stream(), a); break;
+    case 512: hipLaunchKernelGGL(attn_rope_dec_kernel<4>, grid, dim3(256), 0, stream(), a); break;
+    default: return fail(G4_E_ARG, "decode attention: head_dim %d", hd);
+  }
+  G4_LAUNCH_CHECK("attn_rope_dec_kernel");
   return G4_OK;
 }
 

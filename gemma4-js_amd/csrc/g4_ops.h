@@ -47,6 +47,29 @@ int launch_rope_qkv(const float *qraw, const float *kraw, const float *vraw, int
 int launch_norm_chain(const float *a, const float *h, const float *w1, const float *w2, float c,
                       float eps, int rows, int width, float *r_out, float *x_out);
 
+// RoPE (cos, sin) tables of the current position for up to kRopeSlots
+// (base, head_dim, angles) variants, kRopeTable entries each.
+constexpr int kRopeSlots = 4, kRopeTable = 256;
+struct RopeSlots {
+  float base[kRopeSlots];
+  int hd[kRopeSlots], angles[kRopeSlots];
+  int n;
+};
+// The decode step's first kernel: y = embedding row of ids[0] * scale, and
+// the RoPE tables at *pos_dev.
+int launch_token_start(const uint16_t *E, int vocab, int width, const int *ids_dev, float scale,
+                       float *y, const int *pos_dev, const RopeSlots &slots, float2 *tab);
+// One-query attention with the q/k norm + RoPE, the k/v cache append at
+// *pos_dev and the split merge in one launch (head_dim 128, 256 or 512).
+// count: heads ints, zero before the first launch (each launch leaves them 0).
+bool attn_rope_supported(int hd);
+int attn_rope_splits(int max_keylen, bool sliding, int window);
+int launch_attn_rope_dec(const float *qraw, const float *kraw, const float *vraw, int heads,
+                         int hd, const int *pos_dev, const float *qnorm, const float *knorm,
+                         const float2 *rope, int angles, float eps, float *kc, float *vc,
+                         bool own_kv, bool sliding, int window, int max_keylen, float *part,
+                         size_t part_floats, int *count, float *ctx);
+
 // Head partials for the device argmax: per block (max value, first index).
 size_t head_argmax_blocks(int rows);
 int launch_bf16_head(const float *x, const uint16_t *E, int rows, int K, float *out, float scale,
