@@ -110,7 +110,7 @@ struct g4_gemma {
   size_t part_floats = 0;
   RopeSlots rope_slots = {};
   float2 *rope_tab = nullptr;  // [kRopeSlots][kRopeTable] at the current position
-  int *attn_count = nullptr;   // [heads] split counters of the decode attention
+  int *attn_count = nullptr;   // [heads * kCountStride] split counters of the decode attention
   std::vector<void *> allocs;
   g4_cmdbuf *step = nullptr;  // recorded one-token decode step
 };
@@ -505,7 +505,7 @@ G4_API int g4_gemma_create(const g4_gemma_config *cfg, g4_gemma **out) {
   }
   if (!rc) rc = galloc_n(m, head_argmax_blocks(c.vocab), &m->hpart);
   if (!rc) rc = galloc_n(m, (size_t)kRopeSlots * kRopeTable, &m->rope_tab);
-  if (!rc) rc = galloc_n(m, (size_t)c.heads, &m->attn_count);  // zero-filled
+  if (!rc) rc = galloc_n(m, (size_t)c.heads * kCountStride, &m->attn_count);  // zero-filled
 
   for (int i = 0; i < c.layers && !rc; ++i) {
     Layer &l = m->L[i];

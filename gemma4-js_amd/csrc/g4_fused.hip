@@ -540,7 +540,7 @@ struct AttnRopeArgs {
   const float2 *rope;               // (cos, sin) at the current position, [angles]
   float *kc, *vc;                   // caches [max_seq, hd]
   float *part;                      // [H][S][hd + 2]
-  int *count;                       // [H], zero between launches
+  int *count;                       // [H * kCountStride], zero between launches
   float *ctx;                       // [H, hd]
   const int *pos_dev;
   int H, S, angles, own, sliding, window;
@@ -651,7 +651,8 @@ __device__ __forceinline__ void norm_rope_wave(float (&a)[DH], float (&b)[DH],
   }
 }
 
-template <int DH>
+// SMAX: the largest split count S this instantiation merges (4 waves x SMAX/4).
+template <int DH, int SMAX>
 __global__ __launch_bounds__(256) void attn_rope_dec_kernel(AttnRopeArgs A) {
   constexpr int HALF = 64 * DH, HD = 2 * HALF;
   constexpr int KC = DH == 4 ? 4 : 8;  // keys per wave whose loads are in flight together
@@ -660,6 +661,10 @@ __global__ __launch_bounds__(256) void attn_rope_dec_kernel(AttnRopeArgs A) {
   __shared__ int last_sh;
   const int h = blockIdx.x / A.S, s = blockIdx.x - h * A.S;
   const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
+  // q, its norm weights and the RoPE table do not depend on the position:
+  // their loads go out first
+  float qa[DH], qb[DH];
+  load_halves<DH>(A.qraw + (size_t)h * HD, lane, qa, qb);
   const int pos = *A.pos_dev;
   int lo = A.sliding ? pos - A.window + 1 : 0;
   lo = lo > 0 ? lo : 0;
@@ -682,8 +687,6 @@ __global__ __launch_bounds__(256) void attn_rope_dec_kernel(AttnRopeArgs A) {
   };
   load_chunk(base);
 
-  float qa[DH], qb[DH];
-  load_halves<DH>(A.qraw + (size_t)h * HD, lane, qa, qb);
   norm_rope_wave<DH, true, true>(qa, qb, A.qnorm, A.rope, A.angles, A.eps, lane);
 
   // the new key at pos (own-KV layers): built by the wave that owns it
@@ -784,13 +787,13 @@ __global__ __launch_bounds__(256) void attn_rope_dec_kernel(AttnRopeArgs A) {
   __builtin_amdgcn_s_waitcnt(0);  // this wave's coherent stores are performed
   __syncthreads();
   if (t == 0)
-    last_sh = __hip_atomic_fetch_add(&A.count[h], 1, __ATOMIC_RELAXED,
+    last_sh = __hip_atomic_fetch_add(&A.count[h * kCountStride], 1, __ATOMIC_RELAXED,
                                      __HIP_MEMORY_SCOPE_AGENT) == A.S - 1;
   __syncthreads();
   if (!last_sh) return;
   // wave w merges splits w, w + 4, ... (up to 16 each, all loads in flight
   // together; lanes hold the dims as above), then the 4 waves merge in LDS
-  constexpr int SW = 16;
+  constexpr int SW = SMAX / 4;  // splits per wave
   float pm[SW], pl[SW], pa[SW][DH], pb[SW][DH];
 #pragma unroll
   for (int i = 0; i < SW; ++i) {
@@ -840,7 +843,7 @@ __global__ __launch_bounds__(256) void attn_rope_dec_kernel(AttnRopeArgs A) {
       A.ctx[(size_t)h * HD + dd] =
           (wo[0][dd] * f0 + wo[1][dd] * f1 + wo[2][dd] * f2 + wo[3][dd] * f3) / L;
   }
-  if (t == 0) A.count[h] = 0;
+  if (t == 0) A.count[h * kCountStride] = 0;
 }
 
 // ---- standalone chain r = (h + rms(a) * w1) * c; x = rms(r) * w2 ------------
@@ -1001,12 +1004,24 @@ int launch_attn_rope_dec(const float *qraw, const float *kraw, const float *vraw
     return fail(G4_E_ARG, "decode attention: split scratch too small");
   if (angles > hd / 2 || angles > kRopeTable) return fail(G4_E_ARG, "decode attention: %d angles", angles);
   const dim3 grid(heads * a.S);
+#define G4_ATTN(DH)                                                                       \
+  do {                                                                                    \
+    if (a.S <= 8)                                                                         \
+      hipLaunchKernelGGL((attn_rope_dec_kernel<DH, 8>), grid, dim3(256), 0, stream(), a);  \
+    else if (a.S <= 16)                                                                   \
+      hipLaunchKernelGGL((attn_rope_dec_kernel<DH, 16>), grid, dim3(256), 0, stream(), a); \
+    else if (a.S <= 32)                                                                   \
+      hipLaunchKernelGGL((attn_rope_dec_kernel<DH, 32>), grid, dim3(256), 0, stream(), a); \
+    else                                                                                  \
+      hipLaunchKernelGGL((attn_rope_dec_kernel<DH, 64>), grid, dim3(256), 0, stream(), a); \
+  } while (0)
   switch (hd) {
-    case 128: hipLaunchKernelGGL(attn_rope_dec_kernel<1>, grid, dim3(256), 0, stream(), a); break;
-    case 256: hipLaunchKernelGGL(attn_rope_dec_kernel<2>, grid, dim3(256), 0, stream(), a); break;
-    case 512: hipLaunchKernelGGL(attn_rope_dec_kernel<4>, grid, dim3(256), 0, stream(), a); break;
+    case 128: G4_ATTN(1); break;
+    case 256: G4_ATTN(2); break;
+    case 512: G4_ATTN(4); break;
     default: return fail(G4_E_ARG, "decode attention: head_dim %d", hd);
   }
+#undef G4_ATTN
   G4_LAUNCH_CHECK("attn_rope_dec_kernel");
   return G4_OK;
 }

@@ -61,7 +61,9 @@ int launch_token_start(const uint16_t *E, int vocab, int width, const int *ids_d
                        float *y, const int *pos_dev, const RopeSlots &slots, float2 *tab);
 // One-query attention with the q/k norm + RoPE, the k/v cache append at
 // *pos_dev and the split merge in one launch (head_dim 128, 256 or 512).
-// count: heads ints, zero before the first launch (each launch leaves them 0).
+// count: heads * kCountStride ints (one 128-byte line per head), zero before
+// the first launch (each launch leaves them 0).
+constexpr int kCountStride = 32;
 bool attn_rope_supported(int hd);
 int attn_rope_splits(int max_keylen, bool sliding, int window);
 int launch_attn_rope_dec(const float *qraw, const float *kraw, const float *vraw, int heads,
