@@ -41,21 +41,32 @@ int kpw_for(int rows) { return rows <= 4 ? 4 : 64; }
 
 // Final argmax reduction + advance: ids[0] = token, gen[pos + rows] = token,
 // pos += rows.  One block.
-__global__ __launch_bounds__(256) void advance_kernel(const float2 *__restrict__ partials,
-                                                      int nparts, int rows, int *__restrict__ ids,
-                                                      int *__restrict__ pos,
-                                                      int *__restrict__ gen, int gen_cap) {
-  __shared__ float sv[4];
-  __shared__ int si[4];
+__global__ __launch_bounds__(1024) void advance_kernel(const float2 *__restrict__ partials,
+                                                       int nparts, int rows, int *__restrict__ ids,
+                                                       int *__restrict__ pos,
+                                                       int *__restrict__ gen, int gen_cap) {
+  __shared__ float sv[16];
+  __shared__ int si[16];
   float bv = -INFINITY;
   int bi = 0x7fffffff;
-  for (int i = threadIdx.x; i < nparts; i += 256) {
-    const float2 p = partials[i];
-    const float v = p.x;
-    const int ix = __float_as_int(p.y);
-    if (v > bv || (v == bv && ix < bi)) {
-      bv = v;
-      bi = ix;
+  // U partials per thread per pass, all loads in flight together; indices
+  // past the end re-read the last partial, which cannot change the result
+  constexpr int U = 8;
+  for (int b0 = threadIdx.x; b0 < nparts; b0 += 1024 * U) {
+    float2 p[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int i = b0 + u * 1024;
+      p[u] = partials[i < nparts ? i : nparts - 1];
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const float v = p[u].x;
+      const int ix = __float_as_int(p[u].y);
+      if (v > bv || (v == bv && ix < bi)) {
+        bv = v;
+        bi = ix;
+      }
     }
   }
 #pragma unroll
@@ -73,7 +84,7 @@ __global__ __launch_bounds__(256) void advance_kernel(const float2 *__restrict__
   }
   __syncthreads();
   if (threadIdx.x == 0) {
-    for (int w = 1; w < 4; ++w)
+    for (int w = 1; w < 16; ++w)
       if (sv[w] > bv || (sv[w] == bv && si[w] < bi)) {
         bv = sv[w];
         bi = si[w];
@@ -328,7 +339,7 @@ int run_head(g4_gemma *m, int rows) {
                             m->hpart);
   if (rc) return rc;
   const int nparts = (int)head_argmax_blocks(c.vocab);
-  hipLaunchKernelGGL(advance_kernel, dim3(1), dim3(256), 0, stream(), m->hpart, nparts, rows,
+  hipLaunchKernelGGL(advance_kernel, dim3(1), dim3(1024), 0, stream(), m->hpart, nparts, rows,
                      m->ids, m->pos, m->gen, c.max_seq + 1);
   G4_LAUNCH_CHECK("advance_kernel");
   return G4_OK;

@@ -503,8 +503,21 @@ __global__ __launch_bounds__(256) void token_start_kernel(const uint16_t *__rest
   if (b == 0) {
     const int id = ids[0];
     const bool ok = id >= 0 && id < vocab;
-    for (int i = threadIdx.x; i < width; i += 256)
-      y[i] = ok ? bf16_to_f32(E[(size_t)id * width + i]) * scale : __int_as_float(0x7fc00000);
+    const uint16_t *row = E + (size_t)(ok ? id : 0) * width;
+    constexpr int U = 8;
+    for (int b0 = threadIdx.x; b0 < width; b0 += 256 * U) {
+      uint16_t v[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int i = b0 + 256 * u;
+        v[u] = row[i < width ? i : width - 1];
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int i = b0 + 256 * u;
+        if (i < width) y[i] = ok ? bf16_to_f32(v[u]) * scale : __int_as_float(0x7fc00000);
+      }
+    }
     return;
   }
   const int j = b - 1;
@@ -857,6 +870,42 @@ __global__ __launch_bounds__(256) void norm_chain_kernel(const float *__restrict
                                                          float *__restrict__ x_out) {
   __shared__ float red[16];
   const size_t off = (size_t)blockIdx.x * width;
+  constexpr int U = 8;
+  if (width <= 256 * U) {
+    // every load first (indices past width re-read the last element and are
+    // left out of the sums and stores)
+    float av[U], hv[U], w1v[U], w2v[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      int i = threadIdx.x + 256 * u;
+      i = i < width ? i : width - 1;
+      av[u] = a[off + i];
+      hv[u] = h[off + i];
+      w1v[u] = w1[i];
+      w2v[u] = w2[i];
+    }
+    float ss = 0.f;
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      if (threadIdx.x + 256 * u < width) ss += av[u] * av[u];
+    const float inv1 = 1.f / sqrtf(fblock_sum(ss, red, 4) / (float)width + eps);
+    float r[U], ss2 = 0.f;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      r[u] = (hv[u] + av[u] * inv1 * w1v[u]) * c;
+      if (threadIdx.x + 256 * u < width) ss2 += r[u] * r[u];
+    }
+    const float inv2 = 1.f / sqrtf(fblock_sum(ss2, red + 4, 4) / (float)width + eps);
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int i = threadIdx.x + 256 * u;
+      if (i < width) {
+        if (r_out) r_out[off + i] = r[u];
+        x_out[off + i] = r[u] * inv2 * w2v[u];
+      }
+    }
+    return;
+  }
   float ss = 0.f;
   for (int i = threadIdx.x; i < width; i += 256) ss += a[off + i] * a[off + i];
   const float inv1 = 1.f / sqrtf(fblock_sum(ss, red, 4) / (float)width + eps);
