@@ -230,6 +230,22 @@ def bench_decode(prompt=512, steps=256, max_seq=1024, seed=4):
             "first_token": int(first)}
 
 
+def bench_decode_node(prompt=512, steps=256, max_seq=1024, seed=4, timeout=240):
+    """The same E2B decode driven from Node through the N-API bridge
+    (gemma4-js_amd/node/e2b-bench.js); None when node is not installed."""
+    import shutil
+    import subprocess
+    node = shutil.which("node")
+    if node is None:
+        return None
+    script = os.path.join(ROOT, "gemma4-js_amd", "node", "e2b-bench.js")
+    p = subprocess.run([node, script, str(prompt), str(steps), str(max_seq), str(seed)],
+                       stdout=subprocess.PIPE, stderr=subprocess.PIPE, text=True, timeout=timeout)
+    if p.returncode != 0:
+        raise RuntimeError("node decode bench failed: " + p.stderr[-2000:])
+    return json.loads(p.stdout.strip().splitlines()[-1])
+
+
 def bench_decode_eager(steps, prompt=512, max_seq=1024, seed=4):
     """The E2B prompt, then `steps` one-token greedy calls launched one by one
     (each a host round trip): the decode step's kernels without graph replay."""
@@ -292,7 +308,8 @@ def main():
     info = g4hip.device_info()
     log("device:", info)
     if args.decode_only:
-        print(json.dumps({"decode_e2b": bench_decode()}), flush=True)
+        print(json.dumps({"decode_e2b": bench_decode(), "decode_e2b_node": bench_decode_node()}),
+              flush=True)
         return
     if args.decode_eager:
         print(json.dumps({"decode_eager": bench_decode_eager(args.decode_eager)}), flush=True)
@@ -330,6 +347,9 @@ def main():
             log("E2B decode (config 4): prompt 512, 256 greedy steps ...")
             extra["decode_e2b"] = bench_decode()
             log("  ", extra["decode_e2b"])
+            log("E2B decode from Node (N-API bridge) ...")
+            extra["decode_e2b_node"] = bench_decode_node()
+            log("  ", extra["decode_e2b_node"])
 
     cpu = None
     if not args.no_cpu:

@@ -139,7 +139,7 @@ __global__ __launch_bounds__(TC ? TC : 1024) void fused_gemv_kernel(FusedArgs A,
   // The prologue runs on the first pw waves only (the 4G chunks of 8 inputs,
   // XI per lane): the other waves skip it and meet them at the barriers, so
   // the SIMDs are not busy with copies of the same element-wise work.
-  const int wave = t >> 6, lane = t & 63;
+  const int wave = t >> 6;
   const int pw = ((nch + 63) >> 6) < nwaves ? ((nch + 63) >> 6) : nwaves;
   const bool pro = wave < pw;  // uniform per wave
   const int cstride = 64 * pw;

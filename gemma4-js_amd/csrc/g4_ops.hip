@@ -239,7 +239,6 @@ __global__ __launch_bounds__(64) void attn_split_kernel(AttnArgs a) {
 constexpr int kDecMaxKeys = 16;
 constexpr int kMaxSplits = 1024;
 
-__device__ __forceinline__ float xor_shfl(float v, int m) { return __shfl_xor(v, m, 64); }
 
 template <int DPL>
 __global__ __launch_bounds__(kBlock) void attn_dec_kernel(const float *__restrict__ q,

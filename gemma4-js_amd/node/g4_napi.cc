@@ -201,6 +201,23 @@ bool buf_at(napi_env env, napi_value v, napi_value off_v, const char *what, void
   return true;
 }
 
+// A DeviceBuffer argument as a device pointer (whole buffer), or null.
+bool dev(napi_env env, napi_value v, const char *what, void **out) {
+  napi_value no_offset;
+  napi_get_undefined(env, &no_offset);
+  return buf_at(env, v, no_offset, what, out);
+}
+
+bool dev_or_null(napi_env env, napi_value v, const char *what, void **out) {
+  napi_valuetype t;
+  napi_typeof(env, v, &t);
+  if (t == napi_null || t == napi_undefined) {
+    *out = nullptr;
+    return true;
+  }
+  return dev(env, v, what, out);
+}
+
 // new DeviceBuffer(size)  - createBuffer (gpu-runtime.js:8-12)
 napi_value DevBuf_new(napi_env env, napi_callback_info info) {
   napi_value argv[1], self;
@@ -307,18 +324,34 @@ W4 *unwrap_w4(napi_env env, napi_value self) {
   return w;
 }
 
-// new W4Weight(packedBytes, scaleBytes, outDim, inDim, groupSize)
+// new W4Weight(packedBytes, scaleBytes, outDim, inDim, groupSize): host bytes
+// (ArrayBuffer / typed arrays), or two DeviceBuffers already holding the same
+// layouts on the device.
 napi_value W4_new(napi_env env, napi_callback_info info) {
   napi_value argv[5], self;
   if (!get_args(env, info, 5, argv, &self)) return nullptr;
-  void *pk, *sc;
-  size_t npk, nsc;
-  if (!host_bytes(env, argv[0], &pk, &npk, "packed")) return nullptr;
-  if (!host_bytes(env, argv[1], &sc, &nsc, "scales")) return nullptr;
   int64_t out_dim, in_dim, group;
   if (!to_i64(env, argv[2], &out_dim, "outDim") || !to_i64(env, argv[3], &in_dim, "inDim") ||
       !to_i64(env, argv[4], &group, "groupSize"))
     return nullptr;
+  if (is_instance(env, argv[0], g_devbuf_ctor)) {
+    void *pk, *sc;
+    if (!dev(env, argv[0], "packed", &pk) || !dev(env, argv[1], "scales", &sc)) return nullptr;
+    g4_w4 *h = nullptr;
+    G4_CALL(env, g4_w4_load_dev(pk, sc, (int)out_dim, (int)in_dim, (int)group, &h));
+    W4 *w = new W4{h, (int)out_dim, (int)in_dim, (int)group};
+    if (napi_wrap(env, self, w, w4_finalize, nullptr, nullptr) != napi_ok) {
+      g4_w4_free(h);
+      delete w;
+      napi_throw_error(env, nullptr, "napi_wrap failed");
+      return nullptr;
+    }
+    return self;
+  }
+  void *pk, *sc;
+  size_t npk, nsc;
+  if (!host_bytes(env, argv[0], &pk, &npk, "packed")) return nullptr;
+  if (!host_bytes(env, argv[1], &sc, &nsc, "scales")) return nullptr;
   if (out_dim <= 0 || in_dim <= 0 || group <= 0 || in_dim % 8 || in_dim % group) {
     // the C ABI reports the precise message
   } else if (npk != (size_t)(out_dim * (in_dim / 8) * 4)) {
@@ -480,6 +513,19 @@ napi_value Ple_uploadShard(napi_env env, napi_callback_info info) {
   if (!to_i64(env, argv[0], &i, "shard")) return nullptr;
   void *p;
   size_t n;
+  if (is_instance(env, argv[1], g_devbuf_ctor)) {  // the shard's bytes on the device
+    DevBuf *b = unwrap_buf(env, argv[1], "shard bytes");
+    if (!b) return nullptr;
+    size_t want = 0;
+    int nshards = 0;
+    G4_CALL(env, g4_ple_shard_bytes(t->h, (int)i, &nshards, &want));
+    if (want > b->size) {
+      napi_throw_range_error(env, nullptr, "shard bytes: the DeviceBuffer is smaller than the shard");
+      return nullptr;
+    }
+    G4_CALL(env, g4_ple_upload_shard_dev(t->h, (int)i, b->ptr, want));
+    return undefined(env);
+  }
   if (!host_bytes(env, argv[1], &p, &n, "shard bytes")) return nullptr;
   G4_CALL(env, g4_ple_upload_shard(t->h, (int)i, p, n));
   return undefined(env);
@@ -727,22 +773,6 @@ napi_value F_timeMs(napi_env env, napi_callback_info info) {
 // Each takes DeviceBuffers (whole-buffer pointers) and plain numbers and
 // enqueues one C-ABI op; the JS GPUOps allocates the outputs.
 
-bool dev(napi_env env, napi_value v, const char *what, void **out) {
-  napi_value no_offset;
-  napi_get_undefined(env, &no_offset);
-  return buf_at(env, v, no_offset, what, out);
-}
-
-bool dev_or_null(napi_env env, napi_value v, const char *what, void **out) {
-  napi_valuetype t;
-  napi_typeof(env, v, &t);
-  if (t == napi_null || t == napi_undefined) {
-    *out = nullptr;
-    return true;
-  }
-  return dev(env, v, what, out);
-}
-
 bool ints(napi_env env, napi_value *argv, const int *idx, int64_t *out, int n,
           const char *const *names) {
   for (int i = 0; i < n; ++i)
@@ -874,6 +904,28 @@ napi_value F_pleMix(napi_env env, napi_callback_info info) {
     return nullptr;
   G4_CALL(env, g4_ple_mix((const float *)p, (const float *)ns, (const float *)tp, (int)v[0],
                           (int)v[1], (int)v[2], (float *)y));
+  return undefined(env);
+}
+
+// fillRandom(buffer, count, kind, seed, sigma = 1, byteOffset = 0): device-side
+// synthetic data (g4_fill_random kinds)
+napi_value F_fillRandom(napi_env env, napi_callback_info info) {
+  napi_value a[6], self;
+  if (!get_args(env, info, 6, a, &self)) return nullptr;
+  void *p;
+  int64_t count, kind, seed;
+  double sigma = 1.0;
+  napi_valuetype t;
+  if (!buf_at(env, a[0], a[5], "buffer", &p) || !to_i64(env, a[1], &count, "count") ||
+      !to_i64(env, a[2], &kind, "kind") || !to_i64(env, a[3], &seed, "seed"))
+    return nullptr;
+  napi_typeof(env, a[4], &t);
+  if (t != napi_undefined && !to_f64(env, a[4], &sigma, "sigma")) return nullptr;
+  if (count < 0 || seed < 0) {
+    napi_throw_range_error(env, nullptr, "fillRandom: count and seed must be non-negative");
+    return nullptr;
+  }
+  G4_CALL(env, g4_fill_random(p, (size_t)count, (int)kind, (uint64_t)seed, (float)sigma));
   return undefined(env);
 }
 
@@ -1331,13 +1383,21 @@ napi_value Init(napi_env env, napi_value exports) {
       METHOD("timeMs", F_timeMs), METHOD("rms", F_rms), METHOD("addScale", F_addScale),
       METHOD("scale", F_scale), METHOD("geluMul", F_geluMul), METHOD("geluPle", F_geluPle),
       METHOD("normRope", F_normRope), METHOD("attention", F_attention),
-      METHOD("pleMix", F_pleMix), METHOD("argmax", F_argmax), METHOD("e2bConfig", F_e2bConfig)};
+      METHOD("pleMix", F_pleMix), METHOD("argmax", F_argmax), METHOD("e2bConfig", F_e2bConfig), METHOD("fillRandom", F_fillRandom)};
   NAPI_CALL(env, napi_define_properties(env, exports, sizeof fns / sizeof fns[0], fns));
   napi_value v;
   napi_create_int32(env, G4_F32, &v);
   napi_set_named_property(env, exports, "F32", v);
   napi_create_int32(env, G4_BF16, &v);
   napi_set_named_property(env, exports, "BF16", v);
+  const struct { const char *name; int value; } kinds[] = {
+      {"RAND_W4_PACKED", G4_RAND_W4_PACKED}, {"RAND_PLE_PACKED", G4_RAND_PLE_PACKED},
+      {"RAND_BF16_ABS_NORMAL", G4_RAND_BF16_ABS_NORMAL},
+      {"RAND_BF16_NORMAL", G4_RAND_BF16_NORMAL}, {"RAND_F32_NORMAL", G4_RAND_F32_NORMAL}};
+  for (const auto &k : kinds) {
+    napi_create_int32(env, k.value, &v);
+    napi_set_named_property(env, exports, k.name, v);
+  }
   return exports;
 }
 

@@ -55,6 +55,15 @@ def write_safetensors(path, tensors):
 
 
 @pytest.mark.gpu
+def test_js_device_side_loaders_match_host_loaders():
+    """W4Weight built from DeviceBuffers and PleTable shards uploaded from a
+    DeviceBuffer (both filled by fillRandom) give bit-identical linear
+    outputs and gathered rows to the same bytes loaded from the host."""
+    res = run_node("device_loaders.js")
+    assert res == {"w4": True, "scalesNonzero": True, "ple": True, "pleNonzero": True}
+
+
+@pytest.mark.gpu
 def test_js_surface_on_gpu_matches_oracle(tmp_path, oracle):
     d = tmp_path
     rows, n, k = 3, 2048, 1536
