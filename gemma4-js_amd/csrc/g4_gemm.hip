@@ -82,11 +82,20 @@ __global__ __launch_bounds__(kThreads) void gemm_xexp_kernel(const void *__restr
   if (m >= M) return;
   const int nch = K >> 3;
   float mx = 0.f;
-  for (int c = lane; c < nch; c += 64) {
-    float v[8];
-    load8<F32X>(x, (size_t)m * nch + c, v);
+  // U chunks per lane per pass with every load issued first (chunks past the
+  // row's end re-read its last chunk, which does not change the max)
+  constexpr int U = 8;
+  for (int c0 = lane; c0 < nch; c0 += 64 * U) {
+    float v[U][8];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) mx = fmaxf(mx, fabsf(v[e]));
+    for (int u = 0; u < U; ++u) {
+      const int c = c0 + 64 * u;
+      load8<F32X>(x, (size_t)m * nch + (c < nch ? c : nch - 1), v[u]);
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) mx = fmaxf(mx, fabsf(v[u][e]));
   }
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
