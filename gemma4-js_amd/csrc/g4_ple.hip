@@ -74,14 +74,17 @@ __global__ __launch_bounds__(256) void ple_gather_kernel(
     for (int i = 0; i < EPT; ++i) v[i] = (float)((int)((w >> (4 * i)) & 15u) - 8) * s;
   }
   const size_t o = (size_t)j * width + e0;
+  // streaming stores: the output is written once and not read back here
   if (BF16OUT) {
-    uint32_t p[4];
+    u32x4 p;
 #pragma unroll
     for (int k = 0; k < 4; ++k)
       p[k] = f32_to_bf16_rne(v[2 * k]) | (f32_to_bf16_rne(v[2 * k + 1]) << 16);
-    *reinterpret_cast<uint4 *>(static_cast<uint16_t *>(out) + o) = make_uint4(p[0], p[1], p[2], p[3]);
+    __builtin_nontemporal_store(p, reinterpret_cast<u32x4 *>(static_cast<uint16_t *>(out) + o));
   } else {
-    *reinterpret_cast<float4 *>(static_cast<float *>(out) + o) = make_float4(v[0], v[1], v[2], v[3]);
+    const u32x4 p = {__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]),
+                     __float_as_uint(v[3])};
+    __builtin_nontemporal_store(p, reinterpret_cast<u32x4 *>(static_cast<float *>(out) + o));
   }
 }
 
