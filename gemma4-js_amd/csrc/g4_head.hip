@@ -4,6 +4,7 @@
 // The reference runs one thread per vocabulary row with a serial K loop and
 // 64 dispatches of 4096 rows; here a wave owns a few rows at a time and the
 // whole [rows, K] slab streams through with 16-byte loads.
+#include "g4_gemv.h"
 #include "g4_internal.h"
 #include "g4_ops.h"
 
@@ -49,7 +50,13 @@ __device__ __forceinline__ void block_argmax_store(float bv, int bi, float2 *par
 }
 
 // Lane l holds x for the 8-element chunks l, l+64, ... (CPL chunks) and
-// reads the same chunks of every row it visits.
+// reads the same chunks of each of the wave's 8 rows. Every load is issued
+// before any arithmetic: rows past the end are clamped to the last row and
+// chunks past K are read in range and zeroed, so no load sits in a branch.
+// The 8 row sums are reduced transposed: each exchange step halves the rows
+// a lane carries (8 -> 4 -> 2 -> 1 over lane distances 32, 16, 8), and the
+// last 8-lane sum runs on DPP, so lane 8*r' + j ends with row
+// r' = 4*bit5 + 2*bit4 + bit3 of its lane index.
 template <int CPL>
 __global__ __launch_bounds__(256) void bf16_head_kernel(
     const float *__restrict__ x, const uint16_t *__restrict__ E, int rows, int K,
@@ -61,26 +68,27 @@ __global__ __launch_bounds__(256) void bf16_head_kernel(
   if (row0 >= rows && !partials) return;
   const int chunks = K >> 3;
 
+  uint4 w[kRowsPerWave][CPL];
+#pragma unroll
+  for (int r = 0; r < kRowsPerWave; ++r) {
+    const int row = min(row0 + r, rows - 1);
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) {
+      const int c = min(lane + 64 * i, chunks - 1);
+      w[r][i] = ld_nt(reinterpret_cast<const uint4 *>(E + (size_t)row * K) + c);
+    }
+  }
   float xv[CPL][8];
 #pragma unroll
   for (int i = 0; i < CPL; ++i) {
     const int c = lane + 64 * i;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) xv[i][e] = c < chunks ? x[c * 8 + e] : 0.f;
-  }
-
-  uint4 w[kRowsPerWave][CPL];
+    for (int e = 0; e < 8; ++e) xv[i][e] = x[min(c, chunks - 1) * 8 + e];
+    if (c >= chunks) {
 #pragma unroll
-  for (int r = 0; r < kRowsPerWave; ++r)
-#pragma unroll
-    for (int i = 0; i < CPL; ++i) {
-      const int c = lane + 64 * i;
-      const int row = row0 + r;
-      if (row < rows && c < chunks)
-        w[r][i] = ld_nt(reinterpret_cast<const uint4 *>(E + (size_t)row * K) + c);
-      else
-        w[r][i] = make_uint4(0, 0, 0, 0);
+      for (int r = 0; r < kRowsPerWave; ++r) w[r][i] = make_uint4(0, 0, 0, 0);
     }
+  }
 
   float acc[kRowsPerWave];
 #pragma unroll
@@ -95,22 +103,25 @@ __global__ __launch_bounds__(256) void bf16_head_kernel(
         a1 = fmaf(xv[i][2 * k + 1], __uint_as_float(u[k] & 0xffff0000u), a1);
       }
     }
-    float v = a0 + a1;
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-    acc[r] = v;
+    acc[r] = a0 + a1;
   }
 
-  // Lane r finishes row r: every lane holds every sum after the butterfly.
-  float mine = 0.f;
+  const bool b5 = lane & 32, b4 = lane & 16, b3 = lane & 8;
+  float a4[4], a2[2];
 #pragma unroll
-  for (int r = 0; r < kRowsPerWave; ++r)
-    if (lane == r) mine = acc[r];
-  const int row = row0 + lane;
+  for (int r = 0; r < 4; ++r)
+    a4[r] = (b5 ? acc[r + 4] : acc[r]) + __shfl_xor(b5 ? acc[r] : acc[r + 4], 32, 64);
+#pragma unroll
+  for (int r = 0; r < 2; ++r)
+    a2[r] = (b4 ? a4[r + 2] : a4[r]) + __shfl_xor(b4 ? a4[r] : a4[r + 2], 16, 64);
+  float sum = (b3 ? a2[1] : a2[0]) + __shfl_xor(b3 ? a2[0] : a2[1], 8, 64);
+  sum = team_sum<8>(sum);
+
+  const int row = row0 + (b5 ? 4 : 0) + (b4 ? 2 : 0) + (b3 ? 1 : 0);
   float bv = -INFINITY;
   int bi = kNoIndex;
-  if (lane < kRowsPerWave && row < rows) {
-    const float raw = mine * scale;
+  if ((lane & 7) == 0 && row < rows) {
+    const float raw = sum * scale;
     const float v = softcap > 0.f ? tanhf(raw / softcap) * softcap : raw;
     out[row] = v;
     if (isfinite(v)) {
