@@ -132,17 +132,11 @@ def _bf16_bytes(a):
     return syn.bf16_rne(np.asarray(a, np.float32)).astype(np.uint16).tobytes()
 
 
-@pytest.mark.gpu
-@pytest.mark.parametrize("driver", ["ops", "engine"])
-def test_js_model_driver_matches_oracle(tmp_path, oracle, driver):
-    """Gemma4WebGPU's load/forward/logits/greedy from Node on a 5-layer
-    checkpoint in the reference's tensor layout - W4 projections, BF16 norms
-    and layer scalars, tied BF16 embedding, dense BF16 per-layer embeddings -
-    against the oracle model.  Two drivers: Gemma4Hip (one GPUOps call per op,
-    as gemma4-webgpu.js) and Gemma4HipEngine (the native engine).  Logits of
-    the prompt within relative L2 1e-3; greedy tokens equal unless the
-    oracle's top two are within 1e-3.  The engine's recorded decode step must
-    choose exactly the tokens of its one-token greedy calls."""
+def small_checkpoint(tmp_path, max_seq=32):
+    """A 5-layer model in the reference's tensor layout - W4 projections, BF16
+    norms and layer scalars, tied BF16 embedding, dense BF16 per-layer
+    embeddings - written to tmp_path/core.safetensors, with the driver config
+    in tmp_path/cfg.json.  Returns (cfg, oracle Model)."""
     import layer_oracle as lo
     H, heads, P, V, window = 128, 2, 32, 512, 8
     specs = [  # sliding/global, own or shared KV, as spec(i) describes E2B layers
@@ -211,22 +205,36 @@ def test_js_model_driver_matches_oracle(tmp_path, oracle, driver):
     write_safetensors(str(ckpt), T)
     prompt = [int(t) for t in syn.token_ids(21, 11, V)]
     steps = 4
-    cfg = dict(hidden=H, heads=heads, pleDim=P, window=window, maxSeq=32, lmChunkRows=200,
+    cfg = dict(hidden=H, heads=heads, pleDim=P, window=window, maxSeq=max_seq, lmChunkRows=200,
                specs=specs, prompt=prompt, steps=steps)
     (tmp_path / "cfg.json").write_text(json.dumps(cfg))
-    res = run_node("model_parity.js", str(ckpt), str(tmp_path / "cfg.json"), driver, timeout=300)
-
     ple_f32 = syn.bf16_to_f32(ple_dense).reshape(V, NL * P)
     ref = lo.Model(H, heads, P, V, layers, E, lambda ids: ple_f32[np.asarray(ids)], top, ple_norm,
                    final_norm, window=window)
+    return cfg, ref
+
+
+def near_tie(lg, tok):
+    return float(np.max(lg) - lg[tok]) <= 1e-3
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("driver", ["ops", "engine"])
+def test_js_model_driver_matches_oracle(tmp_path, oracle, driver):
+    """Gemma4WebGPU's load/forward/logits/greedy from Node on the small
+    checkpoint against the oracle model.  Two drivers: Gemma4Hip (one GPUOps
+    call per op, as gemma4-webgpu.js) and Gemma4HipEngine (the native
+    engine).  Logits of the prompt within relative L2 1e-3; greedy tokens
+    equal unless the oracle's top two are within 1e-3.  The engine's recorded
+    decode step must choose exactly the tokens of its one-token greedy calls."""
+    cfg, ref = small_checkpoint(tmp_path)
+    prompt = cfg["prompt"]
+    res = run_node("model_parity.js", str(tmp_path / "core.safetensors"), str(tmp_path / "cfg.json"),
+                   driver, timeout=300)
     want_tok, want_lg = ref.greedy(prompt, 0)
     got_lg = np.asarray(res["logits0"], np.float64)
     assert np.linalg.norm(got_lg - want_lg) / np.linalg.norm(want_lg) < 1e-3
     toks = res["tokens"]
-
-    def near_tie(lg, tok):
-        return float(np.max(lg) - lg[tok]) <= 1e-3
-
     assert toks[0] == want_tok or near_tie(want_lg, toks[0])
     pos = len(prompt)
     for t_prev, t in zip(toks[:-1], toks[1:]):
@@ -237,3 +245,82 @@ def test_js_model_driver_matches_oracle(tmp_path, oracle, driver):
     assert res["appendError"] == "KV append position %d != cache length %d" % (pos + 5, pos)
     if driver == "engine":
         assert res["decoded"] == toks[1:]
+
+
+def reference_decode(tj, ids, skip_special):
+    """standalone-tokenizer.js decode on a Gemma-layout tokenizer.json: ids to
+    token texts (special added tokens dropped when skip_special), "▁" to
+    space, runs of <0xHH> tokens as UTF-8 with U+FFFD per maximal invalid
+    subpart, joined."""
+    import re
+    inv = {v: k for k, v in tj["model"]["vocab"].items()}
+    special = {a["id"] for a in tj["added_tokens"] if a["special"]}
+    out, buf = [], bytearray()
+    for i in ids:
+        if skip_special and i in special:
+            continue
+        t = inv[i].replace("▁", " ")
+        m = re.fullmatch(r"<0x([0-9A-Fa-f]{2})>", t)
+        if m:
+            buf.append(int(m.group(1), 16))
+            continue
+        if buf:
+            out.append(bytes(buf).decode("utf-8", "replace"))
+            buf = bytearray()
+        out.append(t)
+    if buf:
+        out.append(bytes(buf).decode("utf-8", "replace"))
+    return "".join(out)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("driver", ["ops", "engine"])
+def test_js_generate_matches_oracle(tmp_path, oracle, driver):
+    """The generation loop of main.js:342-556 (gemma4-js_amd/node/generate.js)
+    on the small checkpoint with a 512-token toy tokenizer: the chat prompt
+    encodes as Hugging Face `tokenizers` encodes it; every generated token is
+    the oracle model's greedy choice (or within 1e-3 of its top logit), fed
+    back at position prompt + g - 1; the text is the reference's decoding; a
+    stop token ends the loop before it is appended, and the KV capacity ends
+    it after prompt + 4 positions.  The engine's chunked device decode gives
+    the same tokens."""
+    import toy_tokenizer as tt
+    tokenizers = pytest.importorskip("tokenizers")
+    cfg, ref = small_checkpoint(tmp_path, max_seq=64)
+    cfg.update(genPrompt="hi there", genMax=12)
+    (tmp_path / "cfg.json").write_text(json.dumps(cfg))
+    tj = tt.write_toy_dir(str(tmp_path / "tok"), 512, 5)
+    hf = tokenizers.Tokenizer.from_str(json.dumps(tj))
+    res = run_node("generate_parity.js", str(tmp_path / "core.safetensors"), str(tmp_path / "cfg.json"),
+                   str(tmp_path / "tok"), driver, timeout=300)
+    runs = res["runs"]
+    step = runs["step"]
+    rendered = "<bos><|turn>user\nhi there<turn|>\n<|turn>model\n"
+    assert step["rendered"] == rendered and step["inputIds"] == hf.encode(rendered).ids
+    stops = {1, 5, tj["model"]["vocab"]["<turn|>"]}
+    gen = step["generated"]
+    assert not stops & set(gen)
+    assert step["stopReason"] in ("max_new_tokens", "stop_token")
+    seq = gen + ([step["stopTokenId"]] if step["stopReason"] == "stop_token" else [])
+    if step["stopReason"] == "max_new_tokens":
+        assert len(gen) == cfg["genMax"]
+    ids = step["inputIds"]
+    w, lg = ref.greedy(ids, 0)
+    for g, t in enumerate(seq):
+        assert t == w or near_tie(lg, t), (g, t, w)
+        if g + 1 < len(seq):
+            w, lg = ref.greedy([t], len(ids) + g)
+    assert step["text"] == reference_decode(tj, gen, True)
+    assert step["rawText"] == reference_decode(tj, gen, False)
+    if driver == "engine":
+        assert runs["chunk"]["generated"] == gen and runs["chunk"]["stopReason"] == step["stopReason"]
+    k = res["k"]
+    if k >= 0:
+        for name in ["stop"] + (["stopChunk"] if driver == "engine" else []):
+            assert runs[name]["generated"] == gen[:k], name
+            assert runs[name]["stopReason"] == "stop_token" and runs[name]["stopTokenId"] == gen[k], name
+    cap = runs["cap"]
+    if len(gen) >= 5:
+        assert cap["generated"] == gen[:5] and cap["stopReason"] == "kv_capacity"
+    else:
+        assert cap["generated"] == gen and cap["stopReason"] == step["stopReason"]
