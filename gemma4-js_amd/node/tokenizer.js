@@ -1,6 +1,6 @@
 'use strict';
 // Gemma 4 text tokenizer for Node: the host-side counterpart of the reference's
-// Gemma4Tokenizer (custom-webgpu/standalone-tokenizer.js:275-827), written for
+// Gemma4Tokenizer (custom-webgpu/standalone-tokenizer.js:294-827), written for
 // Node 12 (no `?.`, `??` or String#replaceAll).
 //
 // It reads a Hugging Face tokenizer.json whose model is BPE. The Gemma 4 file
@@ -9,9 +9,9 @@
 // byte_fallback over 262144 tokens and 514906 merges, and decoder
 // Replace("▁" -> " "), ByteFallback, Fuse.
 //
-// Encoding (standalone-tokenizer.js:392-571):
+// Encoding (standalone-tokenizer.js:405-598):
 //   normalize -> split out special added tokens -> pre-tokenize -> BPE each piece.
-// BPE (484-551): the piece starts as its code points; a code point missing
+// BPE (484-572): the piece starts as its code points; a code point missing
 // from the vocabulary becomes its UTF-8 byte tokens <0xHH>. Then, while any
 // adjacent pair has a merge rule, the pair with the lowest rank is merged, the
 // leftmost one among equal ranks. Here the candidate pairs sit in a binary
@@ -79,7 +79,7 @@ function normalize(text, n) {
 
 // A part is {text, special}; special parts pass through every pre-tokenizer.
 
-// Split (standalone-tokenizer.js:72-169): matched and unmatched stretches
+// Split (standalone-tokenizer.js:75-170): matched and unmatched stretches
 // become parts; `behavior` decides what happens to the matched ones.
 function splitParts(parts, cfg) {
   const re = new RegExp(regexSource(cfg.pattern), 'gu');
@@ -117,7 +117,7 @@ function splitParts(parts, cfg) {
   return merged;
 }
 
-// Metaspace (standalone-tokenizer.js:171-233). As in the reference, the
+// Metaspace (standalone-tokenizer.js:172-229). As in the reference, the
 // prepend scheme is "always" whenever prepend_scheme (or, without it,
 // add_prefix_space) is truthy, and "never" otherwise.
 function metaspaceParts(parts, cfg) {
@@ -246,7 +246,7 @@ class Gemma4Tokenizer {
 
   // Reads tokenizer.json, tokenizer_config.json and, when present,
   // generation_config.json from a local directory (the reference fetches the
-  // same three files from a base URL: standalone-tokenizer.js:346-378).
+  // same three files from a base URL: standalone-tokenizer.js:372-403).
   static fromDirectorySync(dir) {
     const read = (name, required) => {
       const p = path.join(dir, name);
@@ -263,7 +263,7 @@ class Gemma4Tokenizer {
   static async fromDirectory(dir) { return Gemma4Tokenizer.fromDirectorySync(dir); }
 
   // Special added tokens are cut out of the text first: the earliest match,
-  // the longest at one position (standalone-tokenizer.js:380-428).
+  // the longest at one position (standalone-tokenizer.js:405-448).
   splitAddedTokens(text) {
     if (!this.specialRe) return text.length ? [{ text, special: false }] : [];
     const out = [];
@@ -300,7 +300,7 @@ class Gemma4Tokenizer {
       for (const b of UTF8_ENCODER.encode(ch)) sym.push(byteToken(b));
     }
     const n = sym.length;
-    // a lone symbol is looked up as it is, with no byte fallback (standalone-tokenizer.js:511-513)
+    // a lone symbol is looked up as it is, with no byte fallback (standalone-tokenizer.js:517-519)
     if (n < 2) return sym.map((s) => def(this.vocab.get(s), this.unkId));
     {
       const next = new Int32Array(n), prev = new Int32Array(n);
@@ -353,7 +353,7 @@ class Gemma4Tokenizer {
     return ids;
   }
 
-  // The decoder chain over token strings (standalone-tokenizer.js:574-683).
+  // The decoder chain over token strings (standalone-tokenizer.js:600-704).
   // ByteFallback turns each run of <0xHH> tokens into text with a
   // non-fatal UTF-8 decode, so an invalid sequence becomes U+FFFD.
   decodeTokens(tokens) {
@@ -398,7 +398,7 @@ class Gemma4Tokenizer {
   }
 
   // Unknown ids decode as the unknown-token text; special added tokens are
-  // dropped unless skipSpecialTokens is false (standalone-tokenizer.js:685-716).
+  // dropped unless skipSpecialTokens is false (standalone-tokenizer.js:706-734).
   decode(ids, opts) {
     const skip = opts && opts.skipSpecialTokens !== undefined ? opts.skipSpecialTokens : true;
     const tokens = [];
@@ -414,7 +414,7 @@ class Gemma4Tokenizer {
   }
 
   // The user/assistant text-chat rendering of Gemma 4's template
-  // (standalone-tokenizer.js:718-754): <bos>, an optional system turn that
+  // (standalone-tokenizer.js:736-768): <bos>, an optional system turn that
   // enables thinking, one turn per message, then the open model turn.
   renderChat(messages, opts) {
     opts = opts || {};
@@ -439,7 +439,7 @@ class Gemma4Tokenizer {
   }
 
   // generation_config's eos_token_id (a number or a list) plus the ids of the
-  // eos and end-of-turn tokens (standalone-tokenizer.js:768-806).
+  // eos and end-of-turn tokens (standalone-tokenizer.js:782-814).
   stopTokenIds() {
     const out = new Set();
     const add = (v) => {

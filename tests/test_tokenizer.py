@@ -96,8 +96,8 @@ def test_byte_fallback_decode_follows_textdecoder(tmp_path):
 
 
 def test_chat_template_stop_ids_and_errors(tmp_path):
-    """renderChat/encodeChat (standalone-tokenizer.js:718-766), stopTokenIds
-    (768-806) and the reasoning split of main.js:127-161, by their closed
+    """renderChat/encodeChat (standalone-tokenizer.js:736-780), stopTokenIds
+    (782-814) and the reasoning split of main.js:127-161, by their closed
     forms."""
     d = tmp_path / "tok"
     tj = tt.write_toy_dir(str(d), 512, 0, eos_ids=(1, 7))
