@@ -171,8 +171,8 @@ __device__ __forceinline__ uint32_t deq_pair(uint32_t w, int t, f16x2 s2) {
 }
 
 // Requires Mp a multiple of BM and (K / 32) a multiple of KS (the launcher
-// checks both).
-template <int TM, int TN, int NX, int KS, int P>
+// checks both); FLAT requires the stage count a multiple of an even P.
+template <int TM, int TN, int NX, int KS, int P, bool FLAT>
 __global__ __launch_bounds__(kThreads, 2) void w4_gemm_kernel(
     const u32x4 *__restrict__ xt, const int *__restrict__ xe, const u32x4 *__restrict__ wq,
     const uint16_t *__restrict__ ws, int shift, void *__restrict__ y, int y_bf16, int M, int Mp,
@@ -183,8 +183,10 @@ __global__ __launch_bounds__(kThreads, 2) void w4_gemm_kernel(
   constexpr int BG = BN * KS;             // weight groups per stage
   constexpr int BE = (BG + kThreads - 1) / kThreads;
   static_assert(BM * KC % kThreads == 0, "A tile must split evenly over the block");
+  // idle B entries (BG not a multiple of the block) store into a pad row
+  constexpr int BNP = BG % kThreads ? BN + 1 : BN;
   __shared__ u32x4 As[2][NX][KC][BM];
-  __shared__ u32x4 Bs[2][KC][BN];
+  __shared__ u32x4 Bs[2][KC][BNP];
 
   const int G = K >> 5;
   const int S = G / KS;
@@ -221,7 +223,6 @@ __global__ __launch_bounds__(kThreads, 2) void w4_gemm_kernel(
   }
   // B: entry i is group b_kk[i] of the stage for tile row b_row[i]
   int b_row[BE], b_kk[BE];
-  bool b_live[BE];
   // Scales: with an even KS, one aligned 32-bit load brings the scales of
   // groups kk & ~1 and kk | 1 (G is even then); the half is picked at store.
   constexpr int SW = KS % 2 == 0 ? 2 : 1;  // scales per scale load
@@ -230,11 +231,10 @@ __global__ __launch_bounds__(kThreads, 2) void w4_gemm_kernel(
 #pragma unroll
   for (int i = 0; i < BE; ++i) {
     const int idx = t + i * kThreads;
-    b_live[i] = idx < BG;  // idle entries load group 0 of row 0 and store nothing
-    const int id = b_live[i] ? idx : 0;
-    b_row[i] = id / KS;
-    b_kk[i] = id % KS;
-    const int gn = n0 + b_row[i] < N ? n0 + b_row[i] : N - 1;
+    const bool live = idx < BG;  // idle entries load group 0 of row n0 into the pad row
+    b_row[i] = live ? idx / KS : BN;
+    b_kk[i] = live ? idx % KS : 0;
+    const int gn = !live ? n0 : n0 + b_row[i] < N ? n0 + b_row[i] : N - 1;
     b_src[i] = wq + (size_t)gn * G + b_kk[i];
     s_src[i] = ws + (size_t)gn * G + (b_kk[i] & ~(SW - 1));
   }
@@ -267,18 +267,17 @@ __global__ __launch_bounds__(kThreads, 2) void w4_gemm_kernel(
 #pragma unroll
       for (int i = 0; i < AE; ++i) As[buf][x][a_c[i]][a_row[i]] = ra[slot][x][i];
 #pragma unroll
-    for (int i = 0; i < BE; ++i)
-      if (b_live[i]) {
-        const uint32_t sbits = SW == 2 && (b_kk[i] & 1) ? rs[slot][i] >> 16 : rs[slot][i] & 0xffffu;
-        const _Float16 sh = (_Float16)ldexpf(bf16_to_f32(sbits), shift);
-        const f16x2 s2 = {sh, sh};
-        const u32x4 w = rb[slot][i];
+    for (int i = 0; i < BE; ++i) {
+      const uint32_t sbits = SW == 2 && (b_kk[i] & 1) ? rs[slot][i] >> 16 : rs[slot][i] & 0xffffu;
+      const _Float16 sh = (_Float16)ldexpf(bf16_to_f32(sbits), shift);
+      const f16x2 s2 = {sh, sh};
+      const u32x4 w = rb[slot][i];
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
-          Bs[buf][4 * b_kk[i] + j][b_row[i]] =
-              (u32x4){deq_pair(w[j], 0, s2), deq_pair(w[j], 1, s2), deq_pair(w[j], 2, s2),
-                      deq_pair(w[j], 3, s2)};
-      }
+      for (int j = 0; j < 4; ++j)
+        Bs[buf][4 * b_kk[i] + j][b_row[i]] =
+            (u32x4){deq_pair(w[j], 0, s2), deq_pair(w[j], 1, s2), deq_pair(w[j], 2, s2),
+                    deq_pair(w[j], 3, s2)};
+    }
   };
 
   f32x4 acc[TM][TN];
@@ -311,6 +310,34 @@ __global__ __launch_bounds__(kThreads, 2) void w4_gemm_kernel(
   for (int s = 0; s < P - 1; ++s) fetch(s, s);
   store(0, 0);
   __syncthreads();
+  if constexpr (FLAT) {
+    // Each step is one branch-free scheduling region: unrolled by an even P,
+    // the ring slot and the LDS buffer of every step are constants, and the
+    // step after the last stores a re-read stage into the idle buffer.  The
+    // group barriers interleave the MFMAs with the next operands' LDS reads,
+    // the global loads, the dequant VALU and the LDS writes of the next stage.
+    constexpr int NM = TM * TN * NX * KS;   // MFMAs per step
+    constexpr int NR = (TM * NX + TN) * KS; // LDS operand reads
+    constexpr int NW = AE * NX + 4 * BE;    // LDS writes
+    for (int st0 = 0; st0 < S; st0 += P) {
+#pragma unroll
+      for (int s = 0; s < P; ++s) {
+        fetch(st0 + s + P - 1, (s + P - 1) % P);
+        compute(s & 1);
+        store((s + 1) % P, (s + 1) & 1);
+        __builtin_amdgcn_sched_group_barrier(0x020, AE * NX + 2 * BE, 0);  // global loads
+        __builtin_amdgcn_sched_group_barrier(0x100, TM * NX + TN, 0);      // LDS reads, first k
+#pragma unroll
+        for (int k = 0; k < NM; ++k) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+          if (k < NR - (TM * NX + TN)) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);  // VALU
+          if (k >= NM - NW) __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);  // LDS write
+        }
+        __syncthreads();
+      }
+    }
+  } else {
   // unrolled by P, so the ring slot of every step is a constant
   for (int st0 = 0; st0 < S; st0 += P) {
 #pragma unroll
@@ -323,28 +350,35 @@ __global__ __launch_bounds__(kThreads, 2) void w4_gemm_kernel(
       __syncthreads();
     }
   }
+  }
 
-  // epilogue: lane holds rows 4*lc + r (r = 0..3) of column lr of each tile
+  // epilogue: lane holds rows 4*lc + r (r = 0..3) of column lr of each tile;
+  // one branch-free copy per output type
+  auto epilogue = [&](auto *out) {
 #pragma unroll
-  for (int i = 0; i < TM; ++i) {
+    for (int i = 0; i < TM; ++i) {
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int m = m0 + wm * 16 * TM + i * 16 + 4 * lc + r;
-      if (m >= M) continue;
-      const int sc = xe[m] - shift;
+      for (int r = 0; r < 4; ++r) {
+        const int m = m0 + wm * 16 * TM + i * 16 + 4 * lc + r;
+        if (m >= M) continue;
+        const int sc = xe[m] - shift;
 #pragma unroll
-      for (int j = 0; j < TN; ++j) {
-        const int n = n0 + wn * 16 * TN + j * 16 + lr;
-        if (n >= N) continue;
-        const float v = ldexpf(acc[i][j][r], sc);
-        const size_t o = (size_t)m * N + n;
-        if (y_bf16)
-          static_cast<uint16_t *>(y)[o] = (uint16_t)f32_to_bf16_rne(v);
-        else
-          static_cast<float *>(y)[o] = v;
+        for (int j = 0; j < TN; ++j) {
+          const int n = n0 + wn * 16 * TN + j * 16 + lr;
+          if (n >= N) continue;
+          const float v = ldexpf(acc[i][j][r], sc);
+          if constexpr (sizeof(*out) == 2)
+            out[(size_t)m * N + n] = (uint16_t)f32_to_bf16_rne(v);
+          else
+            out[(size_t)m * N + n] = v;
+        }
       }
     }
-  }
+  };
+  if (y_bf16)
+    epilogue(static_cast<uint16_t *>(y));
+  else
+    epilogue(static_cast<float *>(y));
 }
 
 template <int TM, int TN, int NX, int KS, int P>
@@ -356,8 +390,10 @@ int launch_gemm(const g4_w4 *w, const uint4 *xt, const int *xe, int rows, int Mp
                 rows, w->K);
   const int nm = (rows + BM - 1) / BM, nn = (w->N + BN - 1) / BN;
   const int xcd_map = nm % 8 == 0;
-  hipLaunchKernelGGL((w4_gemm_kernel<TM, TN, NX, KS, P>), dim3(nm * nn), dim3(kThreads), 0,
-                     stream(), reinterpret_cast<const u32x4 *>(xt), xe,
+  const bool flat = P % 2 == 0 && (w->G / KS) % P == 0;
+  auto kernel = flat ? w4_gemm_kernel<TM, TN, NX, KS, P, true> : w4_gemm_kernel<TM, TN, NX, KS, P, false>;
+  hipLaunchKernelGGL(kernel, dim3(nm * nn), dim3(kThreads), 0, stream(),
+                     reinterpret_cast<const u32x4 *>(xt), xe,
                      reinterpret_cast<const u32x4 *>(w->packed), w->scales, w->shift, y,
                      (int)y_bf16, rows, Mp, w->N, w->K, xcd_map);
   G4_LAUNCH_CHECK("w4_gemm_kernel");
@@ -379,6 +415,11 @@ int launch_gemm_auto(const g4_w4 *w, const uint4 *xt, const int *xe, int rows, i
   };
   if (blocks(128, 128) >= 2L * cus)
     return launch_gemm<4, 4, NX, 2, P>(w, xt, xe, rows, Mp, y, y_bf16);
+  // one 128 x 96 tile per CU (e.g. M 2048, N 1536): 72 vs 80 us for 64 x 96 at K 6144
+  if constexpr (NX == 1) {
+    if (w->N % 96 == 0 && blocks(128, 96) % cus == 0)
+      return launch_gemm<4, 3, NX, 2, P>(w, xt, xe, rows, Mp, y, y_bf16);
+  }
   if (w->N % 96 == 0 && blocks(64, 96) % cus == 0)
     return launch_gemm<2, 3, NX, 2, P>(w, xt, xe, rows, Mp, y, y_bf16);
   if (blocks(64, 128) >= cus) return launch_gemm<2, 4, NX, 2, P>(w, xt, xe, rows, Mp, y, y_bf16);

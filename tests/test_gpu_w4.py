@@ -143,11 +143,14 @@ def test_prefill_gemm_config3(g4, oracle):
 
 
 @pytest.mark.parametrize("x_dtype_name", ["f32", "bf16"])
-def test_gemm_ragged_shapes_and_activation_ranges(g4, x_dtype_name):
+@pytest.mark.parametrize("k", [256, 320, 96])
+def test_gemm_ragged_shapes_and_activation_ranges(g4, x_dtype_name, k):
     # Rows and columns that are not tile multiples, and activation rows far
     # outside FP16's range (1e5..1e-7 scale factors): the per-row power-of-two
-    # rescale must keep every row inside the tolerance.
-    n, k, m = 200, 256, 130
+    # rescale must keep every row inside the tolerance.  K 256 runs the
+    # unrolled branch-free stage loop (8 groups: 4 stages of 2), K 320 (5
+    # stages) and K 96 (3 groups, one per stage) the general one.
+    n, m = 200, 130
     packed, scales, q = syn.w4_weights(9, n, k)
     rng = np.random.default_rng(9)
     x = rng.standard_normal((m, k)).astype(np.float32)
