@@ -15,7 +15,7 @@
 // only values 2^28 below the row maximum lose bits).  FP32 activations are
 // split as x' = hi + lo (two FP16 values, ~22 bits) and take two MFMAs.
 //
-// Pre-pass.  One block per 16 rows finds e[m] and writes x' as FP16 chunks
+// Pre-pass.  Per row it finds e[m] and writes x' as FP16 chunks
 // of 8 values in "pair order": chunk (x0..x7) is stored as (x0,x4)(x1,x5)
 // (x2,x6)(x3,x7), the order in which ((w >> 4t) & 0x000F000F) | 0x64006400
 // unpacks a packed word into FP16 pairs (1024 + n_t, 1024 + n_t+4).  The
@@ -156,6 +156,108 @@ __global__ __launch_bounds__(kThreads) void gemm_xprep_kernel(const void *__rest
     xt[o] = hs[cc][r];
     if (F32X) xt[lo_plane + o] = ls[cc][r];
   }
+}
+
+// Both pre-pass steps in one launch, for rows that fit a block's registers:
+// a block owns kRowsFused = 8 whole rows, 32 threads per row, and thread
+// (r, j) holds chunks j, j + 32, ... (up to CPT) of row r.  Each row is read
+// once: its maximum comes from a 32-lane reduction, then the chunks are
+// converted as in gemm_xprep_kernel and leave through an LDS tile [chunk][8
+// rows], so every wave store writes 128 contiguous bytes per chunk.  Rows
+// M <= m < Mp are written as zeros.  Grid: Mp / 8.
+constexpr int kRowsFused = 8;
+template <bool F32X, int CPT>
+__global__ __launch_bounds__(kThreads) void gemm_xprep_fused_kernel(const void *__restrict__ x,
+                                                                    int M, int Mp, int K,
+                                                                    int *__restrict__ xe,
+                                                                    uint4 *__restrict__ xt) {
+  constexpr int NCH = 32 * CPT;  // chunk capacity of a row
+  __shared__ uint4 hs[NCH][kRowsFused];
+  __shared__ uint4 ls[F32X ? NCH : 1][kRowsFused];
+  const int nch = K >> 3;
+  const int t = threadIdx.x, r = t >> 5, j = t & 31;
+  const int m = blockIdx.x * kRowsFused + r;
+  const bool row_live = m < M;
+  // raw chunks: 16 bytes (BF16) or 32 bytes (FP32) each
+  constexpr int W = F32X ? 2 : 1;
+  uint4 raw[CPT][W];
+  const uint4 *src = static_cast<const uint4 *>(x);
+#pragma unroll
+  for (int i = 0; i < CPT; ++i) {
+    const int c = j + 32 * i;
+    // every load issued first; chunks past the row re-read its first chunk
+    // and rows past M re-read row 0 (both are left out below)
+    const size_t cc = (size_t)(row_live ? m : 0) * nch + (c < nch ? c : 0);
+#pragma unroll
+    for (int w = 0; w < W; ++w) raw[i][w] = src[W * cc + w];
+  }
+  auto unpack = [&](int i, float (&v)[8]) {
+    if (F32X) {
+      const uint32_t u[8] = {raw[i][0].x, raw[i][0].y, raw[i][0].z, raw[i][0].w,
+                             raw[i][W - 1].x, raw[i][W - 1].y, raw[i][W - 1].z, raw[i][W - 1].w};
+#pragma unroll
+      for (int q = 0; q < 8; ++q) v[q] = __uint_as_float(u[q]);
+    } else {
+      const uint32_t u[4] = {raw[i][0].x, raw[i][0].y, raw[i][0].z, raw[i][0].w};
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        v[2 * q] = bf16_to_f32(u[q] & 0xffffu);
+        v[2 * q + 1] = bf16_to_f32(u[q] >> 16);
+      }
+    }
+  };
+  float mx = 0.f;
+#pragma unroll
+  for (int i = 0; i < CPT; ++i) {
+    float v[8];
+    unpack(i, v);
+    if (j + 32 * i < nch)
+#pragma unroll
+      for (int q = 0; q < 8; ++q) mx = fmaxf(mx, fabsf(v[q]));
+  }
+#pragma unroll
+  for (int o = 16; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 32));
+  int e = 0;
+  if (row_live && mx > 0.f && mx <= 3.4e38f) e = ilogbf(mx) - 13;
+  if (j == 0 && row_live) xe[m] = e;
+#pragma unroll
+  for (int i = 0; i < CPT; ++i) {
+    const int c = j + 32 * i;
+    if (c >= nch) continue;
+    float v[8];
+    unpack(i, v);
+    _Float16 h[8], l[8];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const float sv = row_live ? ldexpf(v[q], -e) : 0.f;
+      h[q] = (_Float16)sv;
+      if (F32X) l[q] = (_Float16)(sv - (float)h[q]);
+    }
+    hs[c][r] = make_uint4(h2bits(h[0], h[4]), h2bits(h[1], h[5]), h2bits(h[2], h[6]),
+                          h2bits(h[3], h[7]));
+    if (F32X)
+      ls[c][r] = make_uint4(h2bits(l[0], l[4]), h2bits(l[1], l[5]), h2bits(l[2], l[6]),
+                            h2bits(l[3], l[7]));
+  }
+  __syncthreads();
+  const size_t lo_plane = (size_t)nch * Mp;
+  const int m0 = blockIdx.x * kRowsFused;
+  for (int idx = t; idx < nch * kRowsFused; idx += kThreads) {
+    const int c = idx / kRowsFused, rr = idx % kRowsFused;
+    const size_t o = (size_t)c * Mp + m0 + rr;
+    xt[o] = hs[c][rr];
+    if (F32X) xt[lo_plane + o] = ls[c][rr];
+  }
+}
+
+// Chunks per thread of the fused pre-pass for K, or 0 when the rows do not
+// fit (then the two-kernel pre-pass runs).
+int fused_prep_cpt(int K, bool f32x) {
+  const int need = (K / 8 + 31) / 32;
+  const int caps[] = {2, 4, 8, 16, 24, 32};
+  for (int c : caps)
+    if (need <= c && (!f32x || c <= 16)) return c;
+  return 0;
 }
 
 // ---- main kernel -------------------------------------------------------------
@@ -442,6 +544,34 @@ int w4_gemm(const g4_w4 *w, const void *x, bool f32x, int rows, void *y, bool y_
   if (rc) return rc;
   uint4 *xt = static_cast<uint4 *>(ws);
   int *xe = reinterpret_cast<int *>(static_cast<char *>(ws) + eoff);
+  const int cpt = fused_prep_cpt(w->K, f32x);
+  if (cpt) {
+    const dim3 fgrid(Mp / kRowsFused);
+#define G4_PREP_FUSED(F, C)                                                                   \
+  hipLaunchKernelGGL((gemm_xprep_fused_kernel<F, C>), fgrid, dim3(kThreads), 0, stream(), x, \
+                     rows, Mp, w->K, xe, xt)
+    if (f32x) {
+      switch (cpt) {
+        case 2: G4_PREP_FUSED(true, 2); break;
+        case 4: G4_PREP_FUSED(true, 4); break;
+        case 8: G4_PREP_FUSED(true, 8); break;
+        default: G4_PREP_FUSED(true, 16); break;
+      }
+    } else {
+      switch (cpt) {
+        case 2: G4_PREP_FUSED(false, 2); break;
+        case 4: G4_PREP_FUSED(false, 4); break;
+        case 8: G4_PREP_FUSED(false, 8); break;
+        case 16: G4_PREP_FUSED(false, 16); break;
+        case 24: G4_PREP_FUSED(false, 24); break;
+        default: G4_PREP_FUSED(false, 32); break;
+      }
+    }
+#undef G4_PREP_FUSED
+    G4_LAUNCH_CHECK("gemm_xprep_fused_kernel");
+    return f32x ? launch_gemm_auto<2>(w, xt, xe, rows, Mp, y, y_bf16)
+                : launch_gemm_auto<1>(w, xt, xe, rows, Mp, y, y_bf16);
+  }
   const dim3 egrid((rows + kThreads / 64 - 1) / (kThreads / 64));
   const dim3 pgrid(Mp / kPrepTileM, (w->K / 8 + kPrepTileC - 1) / kPrepTileC);
   if (f32x) {
