@@ -24,6 +24,9 @@ using namespace g4;
 
 constexpr int kNorms = 7;  // input, post_attn, pre_ffw, post_ffw, post_ple, q, k
 constexpr int kProjs = 9;  // q, k, v, o, gate, up, down, ple_gate, ple_proj
+// The one-token down projection is split over input slices of this width,
+// at most this many (the PLE gate prologue adds the partial sums).
+constexpr int kDownSlice = 1536, kDownMaxSlices = 8;
 
 struct Layer {
   int hd = 0, inter = 0, full = 0, kv_src = -1, rope_angles = 0;
@@ -114,6 +117,7 @@ struct g4_gemma {
   float *h[2] = {}, *pre = nullptr, *qraw = nullptr, *q = nullptr, *kraw = nullptr,
         *vraw = nullptr, *ctx = nullptr, *attn = nullptr, *an = nullptr, *ares = nullptr,
         *pf = nullptr, *gate = nullptr, *up = nullptr, *act = nullptr, *down = nullptr,
+        *downp = nullptr,
         *fn = nullptr, *fres = nullptr, *pg = nullptr, *pm = nullptr, *pp = nullptr,
         *pn = nullptr, *tokple = nullptr, *proj = nullptr, *projs = nullptr,
         *perlayer = nullptr, *last = nullptr, *logits = nullptr, *part = nullptr;
@@ -241,8 +245,20 @@ int run_token(g4_gemma *m, bool graph) {
                                      l.norm[G4_NORM_PRE_FFW], eps, m->ares, l.w[G4_PROJ_GATE],
                                      l.w[G4_PROJ_UP], m->act)))
       return rc;
-    if ((rc = g4_w4_linear(l.w[G4_PROJ_DOWN], m->act, G4_F32, 1, m->down, G4_F32))) return rc;
-    if ((rc = fused_res_linear_gelu_mul(m->down, m->ares, l.norm[G4_NORM_POST_FFW], eps, m->fres,
+    // down: split over 1536-wide input slices (per-slice partial sums that the
+    // PLE gate's prologue adds) when the input is 2..8 slices long
+    const g4_w4 *wd = l.w[G4_PROJ_DOWN];
+    int parts = 0;
+    if (wd->K % kDownSlice == 0 && wd->K / kDownSlice <= kDownMaxSlices) {
+      parts = launch_gemv1_split(wd, m->act, m->downp);
+      if (parts < 0) return -parts;
+    }
+    if (parts == 0) {
+      if ((rc = g4_w4_linear(wd, m->act, G4_F32, 1, m->down, G4_F32))) return rc;
+      parts = 1;
+    }
+    if ((rc = fused_res_linear_gelu_mul(parts > 1 ? m->downp : m->down, parts, m->ares,
+                                        l.norm[G4_NORM_POST_FFW], eps, m->fres,
                                         l.w[G4_PROJ_PLE_GATE], m->perlayer + (size_t)i * P,
                                         m->pm)))
       return rc;
@@ -490,6 +506,7 @@ G4_API int g4_gemma_create(const g4_gemma_config *cfg, g4_gemma **out) {
   A(&m->up, R * m->inter_max);
   A(&m->act, R * m->inter_max);
   A(&m->down, R * H);
+  A(&m->downp, (size_t)kDownMaxSlices * H);
   A(&m->fn, R * H);
   A(&m->fres, R * H);
   A(&m->pg, R * c.ple_dim);

@@ -27,6 +27,7 @@ namespace {
 
 enum { kProNone = 0, kProNorm = 1, kProResNorm = 2, kProRes = 3 };
 enum { kEpiNone = 0, kEpiGeluUp = 1, kEpiGeluMul = 2 };
+constexpr int kMaxParts = 8;  // partial input vectors a kProRes prologue adds
 
 struct FusedSeg {
   const uint4 *wq;
@@ -40,6 +41,7 @@ struct FusedArgs {
   FusedSeg seg[3];
   int nseg;
   const float *a, *h, *w1, *w2;  // prologue inputs
+  int a_parts;                    // kProRes: a is the sum of a_parts vectors of K floats
   float c, eps;
   float *r_out;       // residual written by block 0 (kProRes, kProResNorm)
   const float *mul;   // kEpiGeluMul multiplier per output row
@@ -145,14 +147,23 @@ __global__ __launch_bounds__(TC ? TC : 1024) void fused_gemv_kernel(FusedArgs A,
   const int cstride = 64 * pw;
   constexpr int XI = (GC && TC) ? (4 * GC + 63) / 64 <= TC / 64 ? 1 : (4 * GC + TC - 1) / TC : IPL;
 
-  // 1. activation chunks, issued before the weight stream
-  float av[XI][8], hv[XI][8], w1v[XI][8], w2v[XI][8];
+  // 1. activation chunks, issued before the weight stream.  With kProRes, a
+  // may come as up to kMaxParts partial vectors (split-K sums of the previous
+  // GEMV): all are loaded here (past a_parts the last is re-read) and added
+  // in order in the prologue.
+  constexpr int NPART = PRO == kProRes ? kMaxParts : 1;
+  float av[XI][8], hv[XI][8], w1v[XI][8], w2v[XI][8], apv[NPART > 1 ? NPART - 1 : 1][XI][8];
   if (pro) {
 #pragma unroll
     for (int i = 0; i < XI; ++i) {
       const int ct = t + i * cstride;
       const int cc = ct < nch ? ct : nch - 1;
       load8(A.a, cc, av[i]);
+#pragma unroll
+      for (int pp = 1; pp < NPART; ++pp) {
+        const int pc = pp < A.a_parts ? pp : A.a_parts - 1;
+        load8(A.a + (size_t)pc * A.K, cc, apv[pp - 1][i]);
+      }
       if (PRO != kProNone) load8(A.w1, cc, w1v[i]);
       if (PRO == kProRes || PRO == kProResNorm) load8(A.h, cc, hv[i]);
       if (PRO == kProResNorm) load8(A.w2, cc, w2v[i]);
@@ -188,6 +199,15 @@ __global__ __launch_bounds__(TC ? TC : 1024) void fused_gemv_kernel(FusedArgs A,
         for (int e = 0; e < 8; ++e) xv[i][e] = av[i][e];
     }
   } else {
+    if (NPART > 1 && pro) {
+#pragma unroll
+      for (int pp = 1; pp < NPART; ++pp)
+        if (pp < A.a_parts)
+#pragma unroll
+          for (int i = 0; i < XI; ++i)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) av[i][e] += apv[pp - 1][i][e];
+    }
     float ss = 0.f;
     if (pro) {
 #pragma unroll
@@ -976,13 +996,18 @@ int fused_res_norm_gate_up(const float *a, const float *h, const float *w1, floa
   return launch_fused<kProResNorm, kEpiGeluUp>(f);
 }
 
-// r = h + rms(a) * w1 (written to r_out); y = gelu(W . r) * mul.
-int fused_res_linear_gelu_mul(const float *a, const float *h, const float *w1, float eps,
-                              float *r_out, const g4_w4 *w, const float *mul, float *y) {
+// r = h + rms(a) * w1 (written to r_out); y = gelu(W . r) * mul.  a is the
+// sum of a_parts vectors of W's input width, added in order.
+int fused_res_linear_gelu_mul(const float *a, int a_parts, const float *h, const float *w1,
+                              float eps, float *r_out, const g4_w4 *w, const float *mul,
+                              float *y) {
+  if (a_parts < 1 || a_parts > kMaxParts)
+    return fail(G4_E_ARG, "fused PLE gate: %d partial inputs (1..%d)", a_parts, kMaxParts);
   FusedArgs f = {};
   f.nseg = 1;
   f.seg[0] = seg_of(w, y);
   f.a = a;
+  f.a_parts = a_parts;
   f.h = h;
   f.w1 = w1;
   f.c = 1.f;

@@ -126,6 +126,10 @@ struct g4_w4 {
 namespace g4 {
 // Prefill GEMM (rows >= 2): y[rows, N] = x[rows, K] . W^T, MFMA (g4_gemm.hip).
 int w4_gemm(const g4_w4 *w, const void *x, bool f32x, int rows, void *y, bool y_bf16);
+// Split-K decode GEMV of one FP32 row into per-slice partial sums
+// parts[K / 1536][N] (g4_w4.hip); returns the slice count, 0 if K does not
+// split (nothing launched), or minus a status.
+int launch_gemv1_split(const g4_w4 *w, const float *x, float *parts);
 }  // namespace g4
 
 struct g4_ple;

@@ -39,8 +39,9 @@ int fused_res_norm_linear(const float *a, const float *h, const float *w1, float
 int fused_res_norm_gate_up(const float *a, const float *h, const float *w1, float c,
                            const float *w2, float eps, float *r_out, const g4_w4 *gate,
                            const g4_w4 *up, float *act);
-int fused_res_linear_gelu_mul(const float *a, const float *h, const float *w1, float eps,
-                              float *r_out, const g4_w4 *w, const float *mul, float *y);
+int fused_res_linear_gelu_mul(const float *a, int a_parts, const float *h, const float *w1,
+                              float eps, float *r_out, const g4_w4 *w, const float *mul,
+                              float *y);
 int launch_rope_qkv(const float *qraw, const float *kraw, const float *vraw, int heads, int hd,
                     const int *pos_dev, const float *qnorm, const float *knorm, int rope_angles,
                     float base, float eps, float *q, float *kc, float *vc, bool own_kv);

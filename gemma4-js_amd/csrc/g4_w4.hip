@@ -264,16 +264,27 @@ int gemv_rows_per_launch(int K, bool f32x) {
 // ---------------------------------------------------------------------------
 // GC, TC: the group count and block size when known at compile time (0 =
 // taken from K and blockDim at run time); the E2B shapes use fixed ones.
-template <int GC, int TC, int IPL, bool F32X>
+//
+// SPLIT: slice blockIdx.y of the input dimension.  The kernel then reads
+// groups [slice * G, slice * G + G) of rows whose length in memory is gstride
+// groups, x from slice * K, and writes FP32 partial sums to y + slice * N.
+template <int GC, int TC, int IPL, bool F32X, bool SPLIT = false>
 __global__ __launch_bounds__(TC ? TC : 1024) void w4_gemv1_kernel(
     const void *__restrict__ x, const uint4 *__restrict__ wq, const uint16_t *__restrict__ ws,
-    void *__restrict__ y, int y_bf16, int K, int N, int RB_) {
+    void *__restrict__ y, int y_bf16, int K, int N, int RB_, int gstride) {
   extern __shared__ uint4 lds[];
   const int T = TC ? TC : (int)blockDim.x;
   const int G = GC ? GC : K >> 5;
   const int RB = GC ? TC * IPL / GC : RB_;
   const int nch = 4 * G;
   const int t = threadIdx.x;
+  if (SPLIT) {
+    const int slice = blockIdx.y;
+    x = static_cast<const char *>(x) + (size_t)slice * K * (F32X ? 4 : 2);
+    wq += (size_t)slice * G;
+    ws += (size_t)slice * G;
+    y = static_cast<float *>(y) + (size_t)slice * N;
+  }
 
   // 1. x chunks (L2-resident), issued first
   uint4 xa[IPL], xb[IPL];
@@ -296,8 +307,15 @@ __global__ __launch_bounds__(TC ? TC : 1024) void w4_gemv1_kernel(
   uint32_t s[IPL];
 #pragma unroll
   for (int i = 0; i < IPL; ++i) {
-    size_t it = base + t + (size_t)i * T;
-    it = it < last ? it : last;
+    size_t it;
+    if (SPLIT) {
+      const int li = t + i * T, r = li / G;
+      const int row = (int)blockIdx.x * RB + r < N ? (int)blockIdx.x * RB + r : N - 1;
+      it = (size_t)row * gstride + (li - r * G);
+    } else {
+      it = base + t + (size_t)i * T;
+      it = it < last ? it : last;
+    }
     q[i] = ld_nt(&wq[it]);
     s[i] = ws[it];
   }
@@ -408,7 +426,7 @@ template <int GC, int TC, int IPL, bool F32X>
 int launch_gemv1_i(const g4_w4 *w, const Gemv1Plan &p, const void *x, void *y, int y_bf16) {
   const int blocks = (w->N + p.RB - 1) / p.RB;
   hipLaunchKernelGGL((w4_gemv1_kernel<GC, TC, IPL, F32X>), dim3(blocks), dim3(p.T), p.lds,
-                     stream(), x, w->packed, w->scales, y, y_bf16, w->K, w->N, p.RB);
+                     stream(), x, w->packed, w->scales, y, y_bf16, w->K, w->N, p.RB, w->G);
   G4_LAUNCH_CHECK("w4_gemv1_kernel");
   return G4_OK;
 }
@@ -492,6 +510,29 @@ __global__ __launch_bounds__(256) void w4_dequant_kernel(
 bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 }  // namespace
+
+namespace g4 {
+
+// Split-K decode GEMV for one FP32 row: parts[s][n] = sum over inputs
+// [1536 s, 1536 s + 1536) of x[k] * W[n, k], each slice on the K = 1536 plan
+// (8 rows per 192-thread block).  A long input row then needs neither the
+// whole row staged per block nor fewer blocks than CUs; the consumer adds the
+// slices in order.  Returns the slice count, 0 when K is not a multiple of
+// 1536 of at least two slices (nothing launched), or a negative status.
+int launch_gemv1_split(const g4_w4 *w, const float *x, float *parts) {
+  constexpr int kSliceK = 1536, G = kSliceK / 32, T = 192, IPL = 2, RB = 8;
+  if (w->K % kSliceK || w->K / kSliceK < 2) return 0;
+  const int slices = w->K / kSliceK;
+  const size_t lds = (size_t)G * 4 * 16 * 2 + G * 4 + (size_t)RB * G * 4;
+  hipLaunchKernelGGL((w4_gemv1_kernel<G, T, IPL, true, true>),
+                     dim3((w->N + RB - 1) / RB, slices), dim3(T), lds, stream(), x, w->packed,
+                     w->scales, parts, 0, kSliceK, w->N, RB, w->G);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return -fail(G4_E_HIP, "w4_gemv1_kernel (split): %s", hipGetErrorString(e));
+  return slices;
+}
+
+}  // namespace g4
 
 G4_API int g4_w4_load(const void *packed, const void *scales, int out_dim,
                       int in_dim, int group, g4_w4 **out) {

@@ -25,9 +25,11 @@ pytestmark = pytest.mark.gpu
 TINY = dict(hidden=128, heads=2, ple_dim=32, vocab=512, window=8, layers=[
     dict(head_dim=64, full=0, kv_source=-1, intermediate=256, rope_base=1e4, rope_prop=1.0),
     dict(head_dim=128, full=1, kv_source=-1, intermediate=256, rope_base=1e6, rope_prop=0.25),
-    dict(head_dim=64, full=0, kv_source=0, intermediate=512, rope_base=1e4, rope_prop=1.0),
+    # widths 3072 and 4608: the one-token down projection runs split over 2 and
+    # 3 input slices of 1536, summed by the PLE gate's prologue
+    dict(head_dim=64, full=0, kv_source=0, intermediate=3072, rope_base=1e4, rope_prop=1.0),
     dict(head_dim=128, full=1, kv_source=1, intermediate=512, rope_base=1e6, rope_prop=0.25),
-    dict(head_dim=64, full=0, kv_source=0, intermediate=512, rope_base=1e4, rope_prop=1.0),
+    dict(head_dim=64, full=0, kv_source=0, intermediate=4608, rope_base=1e4, rope_prop=1.0),
 ])
 RPS = 64  # PLE rows per shard
 
