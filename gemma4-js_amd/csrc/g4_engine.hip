@@ -119,7 +119,7 @@ struct g4_gemma {
         *pf = nullptr, *gate = nullptr, *up = nullptr, *act = nullptr, *down = nullptr,
         *downp = nullptr,
         *fn = nullptr, *fres = nullptr, *pg = nullptr, *pm = nullptr, *pp = nullptr,
-        *pn = nullptr, *tokple = nullptr, *proj = nullptr, *projs = nullptr,
+        *pn = nullptr, *tokple = nullptr, *proj = nullptr,
         *perlayer = nullptr, *last = nullptr, *logits = nullptr, *part = nullptr;
   float2 *hpart = nullptr;
   size_t part_floats = 0;
@@ -197,10 +197,9 @@ int run_token(g4_gemma *m, bool graph) {
     return rc;
   if ((rc = token_ple(m, 1))) return rc;
   if ((rc = g4_w4_linear(m->top, m->h[0], G4_F32, 1, m->proj, G4_F32))) return rc;
-  if ((rc = launch_scale(m->proj, (size_t)NL * P, (float)(1.0 / sqrt((double)H)), m->projs)))
-    return rc;
-  if ((rc = launch_ple_mix(m->projs, m->ple_norm, m->tokple, 1, P, NL, 1e-6f, 16.f,
-                           0.7071067811865476f, m->perlayer)))
+  // ops.scale(proj, 1/sqrt(hidden)) happens inside the PLE mix
+  if ((rc = launch_ple_mix(m->proj, (float)(1.0 / sqrt((double)H)), m->ple_norm, m->tokple, 1,
+                           P, NL, 1e-6f, 16.f, 0.7071067811865476f, m->perlayer)))
     return rc;
   const int keylen_host = m->cache_len + 1;
   const int max_keylen = graph ? c.max_seq : keylen_host;
@@ -284,11 +283,8 @@ int run_layers(g4_gemma *m, int rows, bool graph) {
     return rc;
   if ((rc = token_ple(m, rows))) return rc;
   if ((rc = g4_w4_linear(m->top, m->h[0], G4_F32, rows, m->proj, G4_F32))) return rc;
-  if ((rc = launch_scale(m->proj, (size_t)rows * NL * P, (float)(1.0 / sqrt((double)H)),
-                         m->projs)))
-    return rc;
-  if ((rc = launch_ple_mix(m->projs, m->ple_norm, m->tokple, rows, P, NL, 1e-6f, 16.f,
-                           0.7071067811865476f, m->perlayer)))
+  if ((rc = launch_ple_mix(m->proj, (float)(1.0 / sqrt((double)H)), m->ple_norm, m->tokple,
+                           rows, P, NL, 1e-6f, 16.f, 0.7071067811865476f, m->perlayer)))
     return rc;
 
   const int keylen_host = m->cache_len + rows;  // prefill calls know it; graphs read *pos
@@ -515,7 +511,6 @@ G4_API int g4_gemma_create(const g4_gemma_config *cfg, g4_gemma **out) {
   A(&m->pn, R * H);
   A(&m->tokple, R * m->ple_total);
   A(&m->proj, R * m->ple_total);
-  A(&m->projs, R * m->ple_total);
   A(&m->perlayer, R * m->ple_total);
   A(&m->last, H);
   A(&m->logits, (size_t)c.vocab);

@@ -25,8 +25,9 @@ size_t attention_part_floats(int qrows, int heads, int hd, int max_keylen, int k
 int launch_attention(const float *q, const float *k, const float *v, int qrows, int heads,
                      int hd, int keylen, int qpos0, const int *pos_dev, int max_keylen,
                      bool sliding, int window, int kpw, float *part, float *out);
-int launch_ple_mix(const float *proj, const float *norm_scale, const float *token_ple, int rows,
-                   int width, int layers, float eps, float ple_scale, float out_scale, float *y);
+int launch_ple_mix(const float *proj, float pre_scale, const float *norm_scale,
+                   const float *token_ple, int rows, int width, int layers, float eps,
+                   float ple_scale, float out_scale, float *y);
 int launch_embed(const uint16_t *E, int vocab, int width, const int *ids_dev, int n, float scale,
                  float *y);
 

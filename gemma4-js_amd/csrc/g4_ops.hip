@@ -441,8 +441,12 @@ __global__ __launch_bounds__(kBlock) void attn_combine_kernel(const float *__res
 }
 
 // ---- PLE_MIX_SHADER (gpu-runtime.js:1250-1263) ------------------------------
-// One block per (row, layer) chunk of `width` values.
+// One block per (row, layer) chunk of `width` values.  p = proj * pre_scale
+// is the input of the norm: the model's ops.scale of the projection
+// (gemma4-webgpu.js, 1/sqrt(hidden)) travels here as the same FP32 product,
+// and GPUOps.pleMix passes 1.
 __global__ __launch_bounds__(kBlock) void ple_mix_kernel(const float *__restrict__ proj,
+                                                         float pre_scale,
                                                          const float *__restrict__ norm_scale,
                                                          const float *__restrict__ token_ple,
                                                          int width, float eps, float ple_scale,
@@ -451,10 +455,13 @@ __global__ __launch_bounds__(kBlock) void ple_mix_kernel(const float *__restrict
   __shared__ float red[4];
   const size_t base = (size_t)blockIdx.x * width;
   float ss = 0.f;
-  for (int d = threadIdx.x; d < width; d += kBlock) ss += proj[base + d] * proj[base + d];
+  for (int d = threadIdx.x; d < width; d += kBlock) {
+    const float p = proj[base + d] * pre_scale;
+    ss += p * p;
+  }
   const float inv = inv_rms(block_sum(ss, red), width, eps);
   for (int d = threadIdx.x; d < width; d += kBlock) {
-    const float n = proj[base + d] * inv * norm_scale[d];
+    const float n = proj[base + d] * pre_scale * inv * norm_scale[d];
     y[base + d] = (n + token_ple[base + d] * ple_scale) * out_scale;
   }
 }
@@ -617,12 +624,12 @@ int launch_attention(const float *q, const float *k, const float *v, int qrows, 
   return G4_OK;
 }
 
-int launch_ple_mix(const float *proj, const float *norm_scale, const float *token_ple, int rows,
-                   int width, int layers, float eps, float ple_scale, float out_scale,
-                   float *y) {
+int launch_ple_mix(const float *proj, float pre_scale, const float *norm_scale,
+                   const float *token_ple, int rows, int width, int layers, float eps,
+                   float ple_scale, float out_scale, float *y) {
   if (rows == 0) return G4_OK;
   hipLaunchKernelGGL(ple_mix_kernel, dim3(rows * layers), dim3(kBlock), 0, stream(), proj,
-                     norm_scale, token_ple, width, eps, ple_scale, out_scale, y);
+                     pre_scale, norm_scale, token_ple, width, eps, ple_scale, out_scale, y);
   G4_LAUNCH_CHECK("ple_mix_kernel");
   return G4_OK;
 }
@@ -772,7 +779,7 @@ G4_API int g4_ple_mix(const float *proj, const float *norm_scale, const float *t
   if (!rc) rc = check_f32(y, n, "g4_ple_mix y");
   // PLE_MIX_SHADER constants: eps 1e-6, token rows * 16 (= sqrt(256)), * 1/sqrt(2)
   if (!rc)
-    rc = launch_ple_mix(proj, norm_scale, token_ple, rows, width, layers, 1e-6f, 16.f,
+    rc = launch_ple_mix(proj, 1.f, norm_scale, token_ple, rows, width, layers, 1e-6f, 16.f,
                         0.7071067811865476f, y);
   return rc ? rc : ok();
 }
