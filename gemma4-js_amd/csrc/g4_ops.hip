@@ -158,6 +158,7 @@ struct AttnArgs {
   int H, hd, keylen, qpos0, sliding, window, kpw, nsplit;
   const int *pos_dev;   // if set: qpos0 = *pos_dev and keylen = *pos_dev + qrows
   int qrows;
+  float *out;           // [qrows, H, hd] (attn_rows_mfma_kernel)
 };
 
 template <int DPL>
@@ -223,6 +224,182 @@ __global__ __launch_bounds__(64) void attn_split_kernel(AttnArgs a) {
       ph[0] = m[h];
       ph[1] = l[h];
     }
+  }
+}
+
+// ---- multi-row attention on the FP32 matrix cores ------------------------------
+// q [qrows, H, hd] is read as nrows = qrows * H rows; row R sits at position
+// qpos0 + R / H and sees the keys (pos - window, pos] (sliding) or [0, pos],
+// all from the one k/v head.  A block (4 waves) owns 16 consecutive rows,
+// staged in LDS; its waves take turns over the 16-key tiles of the rows' key
+// range.  Per tile, with v_mfma_f32_16x16x4f32 (FP32 products, FP32 sums):
+//   S = Q . K^T (16 x 16)        hd/4 MFMAs; lane (c, g) feeds Q row c / key
+//                                c, dims 16j + 4g + i at step (j, i)
+//   online softmax per row       rows 4g + v live in the 16 lanes of group g
+//                                (one DPP row): max and sum by DPP
+//   O += P . V (16 x hd)         P goes through LDS into the A layout; output
+//                                tile n, column c holds dim 64(n/4) + 4c + n%4,
+//                                so V and O move as 16-byte vectors
+// Masked keys (the shader's -1e30 logits) get weight exactly 0, and key rows
+// are clamped into the visible range, so rows past keylen are never read.
+// The 4 waves' (max, sum, O) merge in LDS in wave order; the block writes the
+// normalised rows.  The arithmetic is the reference's softmax(q.k) . v; only
+// the summation order differs (MFMA dot chunks, online rescaling).
+template <typename F>
+__device__ __forceinline__ float row16_reduce(float v, F op) {
+  v = op(v, dpp_f32<0xB1>(v));   // quad_perm [1,0,3,2]
+  v = op(v, dpp_f32<0x4E>(v));   // quad_perm [2,3,0,1]
+  v = op(v, dpp_f32<0x141>(v));  // row_half_mirror
+  v = op(v, dpp_f32<0x140>(v));  // row_mirror
+  return v;
+}
+
+constexpr int kFaRows = 16, kFaWaves = 4, kFaPStride = 20;
+
+template <int HD>
+__global__ __launch_bounds__(256) void attn_rows_mfma_kernel(AttnArgs a) {
+  constexpr int QS = HD + 4;  // padded LDS row (floats): conflict-free 16-byte reads
+  constexpr int NT = HD / 16;
+  __shared__ float qs[kFaRows * QS];                 // the Q tile, later the merged O
+  __shared__ float ps[kFaWaves][kFaRows * kFaPStride];  // per wave: P[row][g * 4 + s]
+  __shared__ float wm[kFaWaves][kFaRows], wl[kFaWaves][kFaRows];
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+  const int c = lane & 15, g = lane >> 4;
+  const int H = a.H;
+  const int qpos0 = a.pos_dev ? *a.pos_dev : a.qpos0;
+  const int keylen = a.pos_dev ? *a.pos_dev + a.qrows : a.keylen;
+  const int nrows = a.qrows * H;
+  const int R0 = blockIdx.x * kFaRows;
+  const int Rl = (R0 + kFaRows < nrows ? R0 + kFaRows : nrows) - 1;  // last live row
+
+  for (int i = t; i < kFaRows * HD / 4; i += 256) {
+    const int r = i / (HD / 4), d4 = i - r * (HD / 4);
+    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (R0 + r < nrows) v = reinterpret_cast<const float4 *>(a.q + (size_t)(R0 + r) * HD)[d4];
+    *reinterpret_cast<float4 *>(&qs[r * QS + 4 * d4]) = v;
+  }
+  // keys of the block's rows: [kmin, kmax]
+  const int pos_first = qpos0 + R0 / H, pos_last = qpos0 + Rl / H;
+  int kmin = a.sliding ? pos_first - a.window + 1 : 0;
+  kmin = kmin > 0 ? kmin : 0;
+  const int kmax = pos_last < keylen - 1 ? pos_last : keylen - 1;
+  int rpos[4];
+  bool rlive[4];
+#pragma unroll
+  for (int v = 0; v < 4; ++v) {
+    const int R = R0 + 4 * g + v;
+    rlive[v] = R < nrows;
+    rpos[v] = qpos0 + (rlive[v] ? R : Rl) / H;
+  }
+  float m[4] = {-1e30f, -1e30f, -1e30f, -1e30f}, l[4] = {0.f, 0.f, 0.f, 0.f};
+  f32x4 o[NT];
+#pragma unroll
+  for (int n = 0; n < NT; ++n) o[n] = (f32x4){0.f, 0.f, 0.f, 0.f};
+  __syncthreads();
+
+  float *pw = ps[w];
+  for (int kt = kmin / 16 + w; kt <= kmax / 16; kt += kFaWaves) {
+    const int key0 = kt * 16;
+    // S = Q . K^T
+    const int kc = key0 + c < kmax ? key0 + c : kmax;
+    const float *kp = a.k + (size_t)kc * HD + 4 * g;
+    const float *qp = &qs[c * QS + 4 * g];
+    // four independent accumulators (dims 16j + 4g + i, i = 0..3), added
+    // pairwise: shorter rounding chains, and the MFMAs do not wait on each other
+    f32x4 sa[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) sa[i] = (f32x4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll 8
+    for (int j = 0; j < NT; ++j) {
+      const float4 kv = *reinterpret_cast<const float4 *>(kp + 16 * j);
+      const float4 qv = *reinterpret_cast<const float4 *>(qp + 16 * j);
+      sa[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(qv.x, kv.x, sa[0], 0, 0, 0);
+      sa[1] = __builtin_amdgcn_mfma_f32_16x16x4f32(qv.y, kv.y, sa[1], 0, 0, 0);
+      sa[2] = __builtin_amdgcn_mfma_f32_16x16x4f32(qv.z, kv.z, sa[2], 0, 0, 0);
+      sa[3] = __builtin_amdgcn_mfma_f32_16x16x4f32(qv.w, kv.w, sa[3], 0, 0, 0);
+    }
+    const f32x4 s = (sa[0] + sa[1]) + (sa[2] + sa[3]);
+    // online softmax: lane (c, g) holds S[row 4g + v][key key0 + c]
+    const int key = key0 + c;
+    float corr[4];
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const bool ok = rlive[v] && key <= rpos[v] && key < keylen &&
+                      (!a.sliding || key > rpos[v] - a.window);
+      const float tm = row16_reduce(ok ? s[v] : -1e30f, [](float x, float y) { return fmaxf(x, y); });
+      const float mn = fmaxf(m[v], tm);
+      corr[v] = expf(m[v] - mn);
+      const float p = ok ? expf(s[v] - mn) : 0.f;
+      l[v] = l[v] * corr[v] + row16_reduce(p, [](float x, float y) { return x + y; });
+      m[v] = mn;
+      pw[(4 * g + v) * kFaPStride + (c & 3) * 4 + (c >> 2)] = p;
+    }
+#pragma unroll
+    for (int n = 0; n < NT; ++n)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) o[n][v] *= corr[v];
+    // P in the A layout: lane (c, g) holds P[row c][key 4 s + g], s = 0..3
+    const float4 pa = *reinterpret_cast<const float4 *>(&pw[c * kFaPStride + 4 * g]);
+    const float pv[4] = {pa.x, pa.y, pa.z, pa.w};
+    // O += P . V
+#pragma unroll
+    for (int sp = 0; sp < 4; ++sp) {
+      const int kr = key0 + 4 * sp + g < kmax ? key0 + 4 * sp + g : kmax;
+      const float *vp = a.v + (size_t)kr * HD + 4 * c;
+#pragma unroll
+      for (int q = 0; q < HD / 64; ++q) {
+        const float4 vv = *reinterpret_cast<const float4 *>(vp + 64 * q);
+        o[4 * q + 0] = __builtin_amdgcn_mfma_f32_16x16x4f32(pv[sp], vv.x, o[4 * q + 0], 0, 0, 0);
+        o[4 * q + 1] = __builtin_amdgcn_mfma_f32_16x16x4f32(pv[sp], vv.y, o[4 * q + 1], 0, 0, 0);
+        o[4 * q + 2] = __builtin_amdgcn_mfma_f32_16x16x4f32(pv[sp], vv.z, o[4 * q + 2], 0, 0, 0);
+        o[4 * q + 3] = __builtin_amdgcn_mfma_f32_16x16x4f32(pv[sp], vv.w, o[4 * q + 3], 0, 0, 0);
+      }
+    }
+  }
+
+  // merge the waves: weights e^(m_w - M), O summed into qs in wave order
+  if (c == 0)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      wm[w][4 * g + v] = m[v];
+      wl[w][4 * g + v] = l[v];
+    }
+  __syncthreads();
+  float f[4];
+#pragma unroll
+  for (int v = 0; v < 4; ++v) {
+    const int r = 4 * g + v;
+    const float M = fmaxf(fmaxf(wm[0][r], wm[1][r]), fmaxf(wm[2][r], wm[3][r]));
+    f[v] = expf(m[v] - M);
+  }
+  for (int ww = 0; ww < kFaWaves; ++ww) {
+    if (w == ww) {
+#pragma unroll
+      for (int q = 0; q < HD / 64; ++q)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          float4 *dst = reinterpret_cast<float4 *>(&qs[(4 * g + v) * QS + 64 * q + 4 * c]);
+          const float4 add = make_float4(o[4 * q][v] * f[v], o[4 * q + 1][v] * f[v],
+                                         o[4 * q + 2][v] * f[v], o[4 * q + 3][v] * f[v]);
+          if (ww == 0) {
+            *dst = add;
+          } else {
+            const float4 cur = *dst;
+            *dst = make_float4(cur.x + add.x, cur.y + add.y, cur.z + add.z, cur.w + add.w);
+          }
+        }
+    }
+    __syncthreads();
+  }
+  for (int i = t; i < kFaRows * HD / 4; i += 256) {
+    const int r = i / (HD / 4), d4 = i - r * (HD / 4);
+    if (R0 + r >= nrows) continue;
+    const float M = fmaxf(fmaxf(wm[0][r], wm[1][r]), fmaxf(wm[2][r], wm[3][r]));
+    const float L = wl[0][r] * expf(wm[0][r] - M) + wl[1][r] * expf(wm[1][r] - M) +
+                    wl[2][r] * expf(wm[2][r] - M) + wl[3][r] * expf(wm[3][r] - M);
+    const float4 x = *reinterpret_cast<const float4 *>(&qs[r * QS + 4 * d4]);
+    reinterpret_cast<float4 *>(a.out + (size_t)(R0 + r) * HD)[d4] =
+        make_float4(x.x / L, x.y / L, x.z / L, x.w / L);
   }
 }
 
@@ -595,6 +772,7 @@ int launch_attention(const float *q, const float *k, const float *v, int qrows, 
   }
   kpw = split_kpw(kpw, max_keylen);
   AttnArgs a;
+  a.out = out;
   a.q = q;
   a.k = k;
   a.v = v;
@@ -609,6 +787,20 @@ int launch_attention(const float *q, const float *k, const float *v, int qrows, 
   a.nsplit = (max_keylen + kpw - 1) / kpw;
   a.pos_dev = pos_dev;
   a.qrows = qrows;
+  // Many rows, or few keys: the matrix-core kernel (16 rows per block, no
+  // merge pass).  A handful of rows over a long cache keeps the key split.
+  if ((size_t)qrows * heads >= 64 || max_keylen <= 512) {
+    const dim3 fgrid((qrows * heads + kFaRows - 1) / kFaRows);
+    switch (hd) {
+      case 64: hipLaunchKernelGGL(attn_rows_mfma_kernel<64>, fgrid, dim3(256), 0, stream(), a); break;
+      case 128: hipLaunchKernelGGL(attn_rows_mfma_kernel<128>, fgrid, dim3(256), 0, stream(), a); break;
+      case 256: hipLaunchKernelGGL(attn_rows_mfma_kernel<256>, fgrid, dim3(256), 0, stream(), a); break;
+      case 512: hipLaunchKernelGGL(attn_rows_mfma_kernel<512>, fgrid, dim3(256), 0, stream(), a); break;
+      default: return fail(G4_E_ARG, "attention: head_dim %d must be 64, 128, 256 or 512", hd);
+    }
+    G4_LAUNCH_CHECK("attn_rows_mfma_kernel");
+    return G4_OK;
+  }
   const dim3 grid(a.nsplit, qrows);
   switch (hd / 64) {
     case 1: hipLaunchKernelGGL(attn_split_kernel<1>, grid, dim3(64), 0, stream(), a); break;

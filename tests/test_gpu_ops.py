@@ -101,7 +101,11 @@ def test_norm_rope(g4, rows, heads, hd, pos0, prop, base):
 @pytest.mark.parametrize("qrows,heads,hd,keylen,sliding,window", [
     (1, 8, 256, 1, True, 512), (1, 8, 256, 37, True, 512), (1, 8, 512, 600, False, 512),
     (1, 8, 256, 700, True, 512), (1, 8, 256, 700, True, 100), (5, 8, 256, 40, True, 16),
-    (64, 8, 512, 64, False, 512), (33, 2, 128, 80, True, 20), (3, 1, 64, 9, False, 512)])
+    (64, 8, 512, 64, False, 512), (33, 2, 128, 80, True, 20), (3, 1, 64, 9, False, 512),
+    # a prompt: 512 rows over 512 keys (the matrix-core kernel, 256 row tiles)
+    (512, 8, 256, 512, True, 512), (96, 8, 512, 300, False, 512), (40, 3, 64, 57, True, 11),
+    # a few rows over a long cache: the key-split kernel
+    (2, 8, 256, 700, True, 512), (3, 8, 512, 900, False, 512)])
 def test_attention(g4, qrows, heads, hd, keylen, sliding, window):
     rng = np.random.default_rng([qrows, heads, hd, keylen, window])
     q = rng.standard_normal((qrows, heads * hd)).astype(np.float32) * 0.2
@@ -113,7 +117,39 @@ def test_attention(g4, qrows, heads, hd, keylen, sliding, window):
                  window, y)
     got = y.download(np.float32).reshape(qrows, heads * hd)
     want = lo.attention(q, k, v, qrows, heads, hd, keylen, qpos0, sliding, window)
-    np.testing.assert_allclose(got, want, rtol=2e-5, atol=2e-6)
+    check_attention(got, want, fp32_attention(q, k, v, qrows, heads, hd, keylen, qpos0, sliding,
+                                              window))
+
+
+def fp32_attention(q, k, v, qrows, heads, hd, keylen, qpos0, sliding, window):
+    """The same attention evaluated plainly in float32 (numpy): the yardstick
+    for FP32 rounding against the float64 oracle."""
+    q = np.asarray(q, np.float32).reshape(qrows, heads, hd)
+    k = np.asarray(k, np.float32)[:keylen]
+    v = np.asarray(v, np.float32)[:keylen]
+    lg = np.einsum("rhd,kd->rhk", q, k, dtype=np.float32)
+    key = np.arange(keylen)[None, :]
+    qp = (qpos0 + np.arange(qrows))[:, None]
+    valid = key <= qp
+    if sliding:
+        valid &= key + window > qp
+    lg = np.where(valid[:, None, :], lg, np.float32(-1e30))
+    e = np.exp(lg - lg.max(axis=2, keepdims=True)).astype(np.float32)
+    p = (e / e.sum(axis=2, keepdims=True)).astype(np.float32)
+    return np.einsum("rhk,kd->rhd", p, v, dtype=np.float32).reshape(qrows, heads * hd)
+
+
+def check_attention(got, want, plain):
+    # An output is a convex combination of N(0,1) value rows computed in FP32;
+    # against the float64 oracle its error is rounding of order keys * 2^-24 *
+    # sum p|v|, whatever the summation order.  Bounds: every element within
+    # 1e-5 absolute (or 2e-5 relative), and the mean error within 3x that of a
+    # plain float32 evaluation of the same inputs; a mistake in the masks or
+    # the indexing moves whole rows far beyond both.
+    np.testing.assert_allclose(got, want, rtol=2e-5, atol=1e-5)
+    err = float(np.abs(got.astype(np.float64) - want).mean())
+    ref = float(np.abs(plain.astype(np.float64) - want).mean())
+    assert err <= 3 * ref + 1e-8, (err, ref)
 
 
 def test_attention_cache_longer_than_keylen(g4):
@@ -131,6 +167,26 @@ def test_attention_cache_longer_than_keylen(g4):
     assert np.all(np.isfinite(got))
     np.testing.assert_allclose(got, lo.attention(q, k, v, 1, heads, hd, keylen, keylen - 1, True,
                                                  512)[0], rtol=2e-5, atol=2e-6)
+
+
+@pytest.mark.parametrize("qrows", [7, 40])
+def test_attention_rows_cache_longer_than_keylen(g4, qrows):
+    # many query rows (the matrix-core kernel): cache rows past keylen are NaN
+    # and must never be read, whatever the tile overhang
+    hd, heads, keylen, cap = 128, 8, 45, 96
+    rng = np.random.default_rng(qrows)
+    q = rng.standard_normal((qrows, heads * hd)).astype(np.float32) * 0.3
+    k = np.full((cap, hd), np.nan, np.float32)
+    v = np.full((cap, hd), np.nan, np.float32)
+    k[:keylen] = rng.standard_normal((keylen, hd))
+    v[:keylen] = rng.standard_normal((keylen, hd))
+    qpos0 = keylen - qrows
+    y = out(g4, qrows * heads * hd)
+    g4.attention(dev(g4, q), dev(g4, k), dev(g4, v), qrows, heads, hd, keylen, qpos0, True, 16, y)
+    got = y.download(np.float32).reshape(qrows, heads * hd)
+    assert np.all(np.isfinite(got))
+    want = lo.attention(q, k[:keylen], v[:keylen], qrows, heads, hd, keylen, qpos0, True, 16)
+    check_attention(got, want, fp32_attention(q, k, v, qrows, heads, hd, keylen, qpos0, True, 16))
 
 
 def test_ple_mix(g4):
