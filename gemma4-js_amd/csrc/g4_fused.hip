@@ -824,7 +824,7 @@ __global__ __launch_bounds__(256) void attn_rope_dec_kernel(AttnRopeArgs A) {
                                      __HIP_MEMORY_SCOPE_AGENT) == A.S - 1;
   __syncthreads();
   if (!last_sh) return;
-  // wave w merges splits w, w + 4, ... (up to 16 each, all loads in flight
+  // wave w merges splits w, w + 4, ... (up to 8 each, all loads in flight
   // together; lanes hold the dims as above), then the 4 waves merge in LDS
   constexpr int SW = SMAX / 4;  // splits per wave
   float pm[SW], pl[SW], pa[SW][DH], pb[SW][DH];
@@ -1040,11 +1040,14 @@ int launch_token_start(const uint16_t *E, int vocab, int width, const int *ids_d
   return G4_OK;
 }
 
+// About 32 keys per block, in multiples of 8 splits, 8 to 32: past 32 splits
+// the last block's merge (more than 8 partials per wave) costs more than the
+// longer key loops save (hd 512 at 1000 keys: 7.7 us at 32 splits, 10.4 at 64).
 int attn_rope_splits(int max_keylen, bool sliding, int window) {
   const int span = sliding && window < max_keylen ? window : max_keylen;
   int S = (span + 31) / 32;
   S = (S + 7) / 8 * 8;
-  return S < 8 ? 8 : S > 64 ? 64 : S;
+  return S < 8 ? 8 : S > 32 ? 32 : S;
 }
 
 bool attn_rope_supported(int hd) { return hd == 128 || hd == 256 || hd == 512; }
@@ -1084,10 +1087,8 @@ int launch_attn_rope_dec(const float *qraw, const float *kraw, const float *vraw
       hipLaunchKernelGGL((attn_rope_dec_kernel<DH, 8>), grid, dim3(256), 0, stream(), a);  \
     else if (a.S <= 16)                                                                   \
       hipLaunchKernelGGL((attn_rope_dec_kernel<DH, 16>), grid, dim3(256), 0, stream(), a); \
-    else if (a.S <= 32)                                                                   \
-      hipLaunchKernelGGL((attn_rope_dec_kernel<DH, 32>), grid, dim3(256), 0, stream(), a); \
     else                                                                                  \
-      hipLaunchKernelGGL((attn_rope_dec_kernel<DH, 64>), grid, dim3(256), 0, stream(), a); \
+      hipLaunchKernelGGL((attn_rope_dec_kernel<DH, 32>), grid, dim3(256), 0, stream(), a); \
   } while (0)
   switch (hd) {
     case 128: G4_ATTN(1); break;
