@@ -103,27 +103,37 @@ E2B_SLIDING_LAYER = [("q", 2048, 1536), ("k", 256, 1536), ("v", 256, 1536), ("o"
                      ("gate", 6144, 1536), ("up", 6144, 1536), ("down", 1536, 6144)]
 
 
+# The layer's GEMVs by shared input: q/k/v and gate/up each run as one launch.
+E2B_SLIDING_LAUNCHES = [("q", "k", "v"), ("o",), ("gate", "up"), ("down",)]
+
+
 def bench_layer(reps=50, seed=1):
     """Config 2: the 7 GEMVs of one E2B sliding layer, M=1, chained through
-    their real input sizes; rotated over enough layer copies to stay cold."""
-    mats = [(name, syn.w4_weights(seed + i, n, k)[:2], n, k)
-            for i, (name, n, k) in enumerate(E2B_SLIDING_LAYER)]
-    layer_bytes = sum(w4_bytes(n, k) for _, _, n, k in mats)
+    their real input sizes, the ones that share an input in one launch
+    (g4_w4_linear_multi: 4 launches per layer); rotated over enough layer
+    copies to stay cold."""
+    mats = {name: (syn.w4_weights(seed + i, n, k)[:2], n, k)
+            for i, (name, n, k) in enumerate(E2B_SLIDING_LAYER)}
+    layer_bytes = sum(w4_bytes(n, k) for _, n, k in mats.values())
     copies = int(math.ceil(COLD_BYTES / layer_bytes))
-    layers = [[g4hip.W4Linear(p, s) for _, (p, s), _, _ in mats] for _ in range(copies)]
+    layers = [{name: g4hip.W4Linear(*ps) for name, (ps, _, _) in mats.items()}
+              for _ in range(copies)]
     xs = {k: g4hip.Buffer.from_array(syn.activations(seed, 1, k)[0]) for k in (1536, 2048, 6144)}
-    ys = {n: g4hip.Buffer(n * 4) for n in (2048, 256, 1536, 6144)}
+    ys = {name: g4hip.Buffer(n * 4) for name, (_, n, _) in mats.items()}
 
     def f():
         for layer in layers:
-            for lin, (_, _, n, k) in zip(layer, mats):
-                lin.linear(xs[k].ptr, g4hip.BF16, 1, ys[n].ptr, g4hip.F32)
+            for names in E2B_SLIDING_LAUNCHES:
+                k = mats[names[0]][2]
+                g4hip.W4Linear.linear_multi([layer[nm] for nm in names], xs[k].ptr, g4hip.BF16,
+                                            1, [ys[nm].ptr for nm in names], g4hip.F32)
 
     cb = record(f)
     time_cmdbufs([cb], 2)
     ms = time_cmdbufs([cb], reps)
     n_layers = reps * copies
-    return {"gemvs_per_layer": 7, "bytes_per_layer": layer_bytes, "copies": copies,
+    return {"gemvs_per_layer": 7, "launches_per_layer": len(E2B_SLIDING_LAUNCHES),
+            "bytes_per_layer": layer_bytes, "copies": copies,
             "us_per_layer": ms * 1e3 / n_layers,
             "gbs": layer_bytes * n_layers / (ms * 1e-3) / 1e9}
 

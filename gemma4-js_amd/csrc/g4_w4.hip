@@ -268,10 +268,15 @@ int gemv_rows_per_launch(int K, bool f32x) {
 // SPLIT: slice blockIdx.y of the input dimension.  The kernel then reads
 // groups [slice * G, slice * G + G) of rows whose length in memory is gstride
 // groups, x from slice * K, and writes FP32 partial sums to y + slice * N.
-template <int GC, int TC, int IPL, bool F32X, bool SPLIT = false>
-__global__ __launch_bounds__(TC ? TC : 1024) void w4_gemv1_kernel(
-    const void *__restrict__ x, const uint4 *__restrict__ wq, const uint16_t *__restrict__ ws,
-    void *__restrict__ y, int y_bf16, int K, int N, int RB_, int gstride) {
+//
+// bx: the block's index among the blocks of this weight (blockIdx.x, or the
+// index within its weight's blocks when one launch covers several weights).
+template <int GC, int TC, int IPL, bool F32X, bool SPLIT>
+__device__ __forceinline__ void gemv1_body(const void *__restrict__ x,
+                                           const uint4 *__restrict__ wq,
+                                           const uint16_t *__restrict__ ws, void *__restrict__ y,
+                                           int y_bf16, int K, int N, int RB_, int gstride,
+                                           unsigned bx) {
   extern __shared__ uint4 lds[];
   const int T = TC ? TC : (int)blockDim.x;
   const int G = GC ? GC : K >> 5;
@@ -301,7 +306,7 @@ __global__ __launch_bounds__(TC ? TC : 1024) void w4_gemv1_kernel(
   }
 
   // 2. weight groups (HBM); rows past N re-read the last group and are not stored
-  const size_t base = (size_t)blockIdx.x * RB * G;
+  const size_t base = (size_t)bx * RB * G;
   const size_t last = (size_t)N * G - 1;
   uint4 q[IPL];
   uint32_t s[IPL];
@@ -310,7 +315,7 @@ __global__ __launch_bounds__(TC ? TC : 1024) void w4_gemv1_kernel(
     size_t it;
     if (SPLIT) {
       const int li = t + i * T, r = li / G;
-      const int row = (int)blockIdx.x * RB + r < N ? (int)blockIdx.x * RB + r : N - 1;
+      const int row = (int)bx * RB + r < N ? (int)bx * RB + r : N - 1;
       it = (size_t)row * gstride + (li - r * G);
     } else {
       it = base + t + (size_t)i * T;
@@ -412,7 +417,7 @@ __global__ __launch_bounds__(TC ? TC : 1024) void w4_gemv1_kernel(
       }
     }
     v = team_sum<16>(v);
-    const size_t row = (size_t)blockIdx.x * RB + r;
+    const size_t row = (size_t)bx * RB + r;
     if (j == 0 && r < RB && row < (size_t)N) {
       if (y_bf16)
         static_cast<uint16_t *>(y)[row] = (uint16_t)f32_to_bf16_rne(v);
@@ -420,6 +425,35 @@ __global__ __launch_bounds__(TC ? TC : 1024) void w4_gemv1_kernel(
         static_cast<float *>(y)[row] = v;
     }
   }
+}
+
+template <int GC, int TC, int IPL, bool F32X, bool SPLIT = false>
+__global__ __launch_bounds__(TC ? TC : 1024) void w4_gemv1_kernel(
+    const void *__restrict__ x, const uint4 *__restrict__ wq, const uint16_t *__restrict__ ws,
+    void *__restrict__ y, int y_bf16, int K, int N, int RB_, int gstride) {
+  gemv1_body<GC, TC, IPL, F32X, SPLIT>(x, wq, ws, y, y_bf16, K, N, RB_, gstride, blockIdx.x);
+}
+
+// Up to kMaxLinearSegs weights of one input dimension over the same x in one
+// launch: the blocks of weight i are block0[i] .. block0[i + 1] - 1, each
+// running the single-weight body on its own rows.
+constexpr int kMaxLinearSegs = 3;
+struct Gemv1Segs {
+  const uint4 *wq[kMaxLinearSegs];
+  const uint16_t *ws[kMaxLinearSegs];
+  void *y[kMaxLinearSegs];
+  int N[kMaxLinearSegs];
+  int block0[kMaxLinearSegs];
+  int n;
+};
+
+template <int GC, int TC, int IPL, bool F32X>
+__global__ __launch_bounds__(TC ? TC : 1024) void w4_gemv1_multi_kernel(
+    const void *__restrict__ x, Gemv1Segs S, int y_bf16, int K, int RB_) {
+  const int b = blockIdx.x;
+  const int i = S.n > 2 && b >= S.block0[2] ? 2 : S.n > 1 && b >= S.block0[1] ? 1 : 0;
+  gemv1_body<GC, TC, IPL, F32X, false>(x, S.wq[i], S.ws[i], S.y[i], y_bf16, K, S.N[i], RB_,
+                                       K >> 5, (unsigned)(b - S.block0[i]));
 }
 
 template <int GC, int TC, int IPL, bool F32X>
@@ -431,22 +465,29 @@ int launch_gemv1_i(const g4_w4 *w, const Gemv1Plan &p, const void *x, void *y, i
   return G4_OK;
 }
 
+// The M = 1 launch shape for w's input dimension.
 template <bool F32X>
-int launch_gemv1(const g4_w4 *w, const void *x, void *y, int y_bf16) {
+int gemv1_plan(const g4_w4 *w, Gemv1Plan *p) {
   // FP32 x of a long row is 4 K bytes per block against 4 rows * K / 2 bytes of
   // weights: from K = 4096 on, 8 rows per block halve that re-read.
-  Gemv1Plan p;
   const int min_rb = F32X && w->K >= 4096 ? 8 : 4;
-  if (!plan_gemv1(w->G, F32X, &p, min_rb) && !plan_gemv1(w->G, F32X, &p))
+  if (!plan_gemv1(w->G, F32X, p, min_rb) && !plan_gemv1(w->G, F32X, p))
     return fail(G4_E_ARG, "g4_w4_linear: no decode GEMV plan for in_dim %d", w->K);
   if (w->G == 48) {
     // K = 1536: 8 rows per 192-thread block, two groups per thread (measured
     // 3.21 vs 3.26 us at N 6144 and 4.02 vs 4.57 us at N 12288, cold weights)
-    p.T = 192;
-    p.IPL = 2;
-    p.RB = 8;
-    p.lds = (size_t)48 * 4 * 16 * (F32X ? 2 : 1) + 48 * 4 + (size_t)8 * 48 * 4;
+    p->T = 192;
+    p->IPL = 2;
+    p->RB = 8;
+    p->lds = (size_t)48 * 4 * 16 * (F32X ? 2 : 1) + 48 * 4 + (size_t)8 * 48 * 4;
   }
+  return G4_OK;
+}
+
+template <bool F32X>
+int launch_gemv1(const g4_w4 *w, const void *x, void *y, int y_bf16) {
+  Gemv1Plan p;
+  if (int rc = gemv1_plan<F32X>(w, &p)) return rc;
   // compile-time variants for the plans of the Gemma-4-E2B projections
 #define G4_GEMV1_FIXED(GG, TT, II)                                      \
   if (w->G == GG && p.T == TT && p.IPL == II)                           \
@@ -466,6 +507,42 @@ int launch_gemv1(const g4_w4 *w, const void *x, void *y, int y_bf16) {
     case 2: return launch_gemv1_i<0, 0, 2, F32X>(w, p, x, y, y_bf16);
     case 3: return launch_gemv1_i<0, 0, 3, F32X>(w, p, x, y, y_bf16);
     default: return launch_gemv1_i<0, 0, 4, F32X>(w, p, x, y, y_bf16);
+  }
+}
+
+template <int GC, int TC, int IPL, bool F32X>
+int launch_gemv1_multi_i(const g4_w4 *const *w, int n, const Gemv1Plan &p, const void *x,
+                         void *const *y, int y_bf16) {
+  Gemv1Segs S{};
+  int blocks = 0;
+  for (int i = 0; i < n; ++i) {
+    S.wq[i] = w[i]->packed;
+    S.ws[i] = w[i]->scales;
+    S.y[i] = y[i];
+    S.N[i] = w[i]->N;
+    S.block0[i] = blocks;
+    blocks += (w[i]->N + p.RB - 1) / p.RB;
+  }
+  S.n = n;
+  hipLaunchKernelGGL((w4_gemv1_multi_kernel<GC, TC, IPL, F32X>), dim3(blocks), dim3(p.T), p.lds,
+                     stream(), x, S, y_bf16, w[0]->K, p.RB);
+  G4_LAUNCH_CHECK("w4_gemv1_multi_kernel");
+  return G4_OK;
+}
+
+// n (2..kMaxLinearSegs) weights of one input dimension over one x row.
+template <bool F32X>
+int launch_gemv1_multi(const g4_w4 *const *w, int n, const void *x, void *const *y,
+                       int y_bf16) {
+  Gemv1Plan p;
+  if (int rc = gemv1_plan<F32X>(w[0], &p)) return rc;
+  if (w[0]->G == 48 && p.T == 192 && p.IPL == 2)  // K = 1536: q/k/v, gate/up
+    return launch_gemv1_multi_i<48, 192, 2, F32X>(w, n, p, x, y, y_bf16);
+  switch (p.IPL) {
+    case 1: return launch_gemv1_multi_i<0, 0, 1, F32X>(w, n, p, x, y, y_bf16);
+    case 2: return launch_gemv1_multi_i<0, 0, 2, F32X>(w, n, p, x, y, y_bf16);
+    case 3: return launch_gemv1_multi_i<0, 0, 3, F32X>(w, n, p, x, y, y_bf16);
+    default: return launch_gemv1_multi_i<0, 0, 4, F32X>(w, n, p, x, y, y_bf16);
   }
 }
 
@@ -746,6 +823,42 @@ G4_API int g4_w4_linear(const g4_w4 *w, const void *x, int x_dtype, int rows,
     if (rc) return rc;
   }
   return ok();
+}
+
+G4_API int g4_w4_linear_multi(const g4_w4 *const *w, int n, const void *x, int x_dtype,
+                              int rows, void *const *y, int y_dtype) {
+  G4_CHECK_INIT();
+  if (!w || !y) return fail(G4_E_ARG, "g4_w4_linear_multi: null weight or output array");
+  if (n < 1 || n > kMaxLinearSegs)
+    return fail(G4_E_ARG, "g4_w4_linear_multi: takes 1..%d weights, got %d", kMaxLinearSegs, n);
+  for (int i = 0; i < n; ++i) {
+    if (!w[i]) return fail(G4_E_ARG, "g4_w4_linear_multi: null weight handle %d", i);
+    if (w[i]->K != w[0]->K)
+      return fail(G4_E_ARG, "g4_w4_linear_multi: weight %d has in_dim %d, weight 0 has %d", i,
+                  w[i]->K, w[0]->K);
+  }
+  if (rows != 1 || n == 1) {
+    for (int i = 0; i < n; ++i)
+      if (int rc = g4_w4_linear(w[i], x, x_dtype, rows, y[i], y_dtype)) return rc;
+    return ok();
+  }
+  if (x_dtype != G4_F32 && x_dtype != G4_BF16)
+    return fail(G4_E_ARG, "g4_w4_linear_multi: bad x dtype %d", x_dtype);
+  if (y_dtype != G4_F32 && y_dtype != G4_BF16)
+    return fail(G4_E_ARG, "g4_w4_linear_multi: bad y dtype %d", y_dtype);
+  if (!aligned16(x)) return fail(G4_E_ARG, "g4_w4_linear_multi: x must be 16-byte aligned");
+  const bool f32x = x_dtype == G4_F32;
+  const size_t xe = f32x ? 4 : 2, ye = y_dtype == G4_F32 ? 4 : 2;
+  int rc = check_device_range(x, (size_t)w[0]->K * xe, "g4_w4_linear_multi x");
+  if (rc) return rc;
+  for (int i = 0; i < n; ++i)
+    if ((rc = check_device_range(y[i], (size_t)w[i]->N * ye, "g4_w4_linear_multi y"))) return rc;
+  if (gemv_lds_per_row(w[0]->K, f32x) > kGemvLdsBudget)
+    return fail(G4_E_ARG, "g4_w4_linear_multi: in_dim %d exceeds the GEMV staging limit (%s x)",
+                w[0]->K, f32x ? "FP32" : "BF16");
+  rc = f32x ? launch_gemv1_multi<true>(w, n, x, y, y_dtype == G4_BF16)
+            : launch_gemv1_multi<false>(w, n, x, y, y_dtype == G4_BF16);
+  return rc ? rc : ok();
 }
 
 G4_API int g4_w4_dequant(const g4_w4 *w, int row_start, int row_count, void *out,

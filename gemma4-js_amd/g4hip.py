@@ -51,6 +51,7 @@ SIGNATURES = {
     "g4_w4_free": (_int, [_vp]),
     "g4_w4_info": (_int, [_vp, _c.POINTER(_int), _c.POINTER(_int), _c.POINTER(_int), _c.POINTER(_sz)]),
     "g4_w4_linear": (_int, [_vp, _vp, _int, _int, _vp, _int]),
+    "g4_w4_linear_multi": (_int, [_c.POINTER(_vp), _int, _vp, _int, _int, _c.POINTER(_vp), _int]),
     "g4_w4_dequant": (_int, [_vp, _int, _int, _vp, _int]),
     "g4_ple_create": (_int, [_int, _int, _int, _int, _c.POINTER(_vp)]),
     "g4_ple_upload_shard": (_int, [_vp, _int, _vp, _sz]),
@@ -291,6 +292,17 @@ class W4Linear:
 
     def linear(self, x_ptr, x_dtype, rows, y_ptr, y_dtype=F32):
         check(lib().g4_w4_linear(self.h, x_ptr, x_dtype, rows, y_ptr, y_dtype))
+
+    @staticmethod
+    def linear_multi(linears, x_ptr, x_dtype, rows, y_ptrs, y_dtype=F32):
+        """g4_w4_linear_multi: every linear of `linears` (same in_dim) over
+        one x; y_ptrs[i] receives linears[i]'s output."""
+        n = len(linears)
+        if len(y_ptrs) != n:
+            raise ValueError("one output per linear")
+        ws = (_vp * n)(*[w.h for w in linears])
+        ys = (_vp * n)(*y_ptrs)
+        check(lib().g4_w4_linear_multi(ws, n, x_ptr, x_dtype, rows, ys, y_dtype))
 
     def dequant(self, row_start, row_count, out_ptr, out_dtype=F32):
         check(lib().g4_w4_dequant(self.h, row_start, row_count, out_ptr, out_dtype))

@@ -390,6 +390,47 @@ napi_value W4_linear(napi_env env, napi_callback_info info) {
   return undefined(env);
 }
 
+// linearMulti([w...], x, xDtype, rows, [y...], yDtype): g4_w4_linear_multi,
+// every weight over the same x, y[i] receiving weight i's output.
+napi_value F_linearMulti(napi_env env, napi_callback_info info) {
+  napi_value argv[6];
+  if (!get_args(env, info, 6, argv, nullptr)) return nullptr;
+  bool wa = false, ya = false;
+  napi_is_array(env, argv[0], &wa);
+  napi_is_array(env, argv[4], &ya);
+  if (!wa || !ya) {
+    napi_throw_type_error(env, nullptr, "linearMulti: weights and outputs must be arrays");
+    return nullptr;
+  }
+  uint32_t n = 0, ny = 0;
+  napi_get_array_length(env, argv[0], &n);
+  napi_get_array_length(env, argv[4], &ny);
+  if (n != ny || n == 0 || n > 3) {
+    napi_throw_range_error(env, nullptr,
+                           "linearMulti: 1..3 weights and one output buffer per weight");
+    return nullptr;
+  }
+  const g4_w4 *ws[3];
+  void *ys[3];
+  for (uint32_t i = 0; i < n; ++i) {
+    napi_value e;
+    napi_get_element(env, argv[0], i, &e);
+    W4 *w = unwrap_w4(env, e);
+    if (!w) return nullptr;
+    ws[i] = w->h;
+    napi_get_element(env, argv[4], i, &e);
+    if (!dev(env, e, "y", &ys[i])) return nullptr;
+  }
+  void *x;
+  if (!dev(env, argv[1], "x", &x)) return nullptr;
+  int64_t xd, rows, yd;
+  if (!to_i64(env, argv[2], &xd, "xDtype") || !to_i64(env, argv[3], &rows, "rows") ||
+      !to_i64(env, argv[5], &yd, "yDtype"))
+    return nullptr;
+  G4_CALL(env, g4_w4_linear_multi(ws, (int)n, x, (int)xd, (int)rows, ys, (int)yd));
+  return undefined(env);
+}
+
 // w.dequant(rowStart, rowCount, out, dtype, outByteOffset = 0)
 napi_value W4_dequant(napi_env env, napi_callback_info info) {
   napi_value argv[5], self;
@@ -1378,7 +1419,7 @@ napi_value Init(napi_env env, napi_value exports) {
     return nullptr;
   const napi_property_descriptor fns[] = {
       METHOD("init", F_init), METHOD("deviceInfo", F_deviceInfo), METHOD("sync", F_sync),
-      METHOD("copy", F_copy), METHOD("bf16Head", F_bf16Head),
+      METHOD("copy", F_copy), METHOD("bf16Head", F_bf16Head), METHOD("linearMulti", F_linearMulti),
       METHOD("encoderBegin", F_encoderBegin), METHOD("encoderFinish", F_encoderFinish),
       METHOD("timeMs", F_timeMs), METHOD("rms", F_rms), METHOD("addScale", F_addScale),
       METHOD("scale", F_scale), METHOD("geluMul", F_geluMul), METHOD("geluPle", F_geluPle),

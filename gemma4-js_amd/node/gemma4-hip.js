@@ -164,14 +164,15 @@ class Gemma4Hip {
     const nHidden = rows * H;
     const trash = (x) => { if (x) garbage.push(x); return x; };
     const pre = ops.rms(encoder, hidden, rows, H, N.input, garbage);
-    const q = ops.normRope(encoder, trash(ops.w4(encoder, L.q, pre, rows, garbage)), rows, this.heads, s.headDim, startPos, N.q, s.ropeProp, s.ropeBase, garbage);
+    const [qRaw, kRaw, vRaw] = ops.w4Multi(encoder, s.shared ? [L.q] : [L.q, L.k, L.v], pre, rows, garbage);
+    const q = ops.normRope(encoder, trash(qRaw), rows, this.heads, s.headDim, startPos, N.q, s.ropeProp, s.ropeBase, garbage);
     let cache;
     if (s.shared) {
       cache = this.shared[s.attentionType];
       if (!cache) throw new Error(`Missing shared ${s.attentionType} KV cache at layer ${layer.i}`);
     } else {
-      const k = ops.normRope(encoder, trash(ops.w4(encoder, L.k, pre, rows, garbage)), rows, 1, s.headDim, startPos, N.k, s.ropeProp, s.ropeBase, garbage);
-      const v = ops.rms(encoder, trash(ops.w4(encoder, L.v, pre, rows, garbage)), rows, s.headDim, null, garbage);
+      const k = ops.normRope(encoder, trash(kRaw), rows, 1, s.headDim, startPos, N.k, s.ropeProp, s.ropeBase, garbage);
+      const v = ops.rms(encoder, trash(vRaw), rows, s.headDim, null, garbage);
       cache = this.caches[layer.i];
       cache.append(encoder, k, v, rows, startPos);
       trash(k);
@@ -185,8 +186,7 @@ class Gemma4Hip {
     const attnResidual = ops.addScale(encoder, hidden, attnNorm, nHidden, 1, garbage);
     trash(hidden);
     const preFfw = trash(ops.rms(encoder, attnResidual, rows, H, N.preFfw, garbage));
-    const gate = trash(ops.w4(encoder, L.gate, preFfw, rows, garbage));
-    const up = trash(ops.w4(encoder, L.up, preFfw, rows, garbage));
+    const [gate, up] = ops.w4Multi(encoder, [L.gate, L.up], preFfw, rows, garbage).map(trash);
     const act = trash(ops.geluMul(encoder, gate, up, rows * s.intermediate, garbage));
     const ffwNorm = trash(ops.rms(encoder, trash(ops.w4(encoder, L.down, act, rows, garbage)), rows, H, N.postFfw, garbage));
     const ffwResidual = trash(ops.addScale(encoder, attnResidual, ffwNorm, nHidden, 1, garbage));

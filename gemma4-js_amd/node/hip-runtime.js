@@ -242,6 +242,14 @@ class GPUOps {
     linear.weight.linear(x, F32, rows, y, F32);
     return y;
   }
+  // Consecutive w4 dispatches over one input (q/k/v at gemma4-webgpu.js:225,
+  // 237-238; gate/up at 280-281) as one call, one launch for a single row;
+  // returns one output buffer per linear.
+  w4Multi(encoder, linears, x, rows, garbage = null) {
+    const ys = linears.map((l) => this.emptyF32(rows * l.outDim, `${l.name}:out`));
+    native.linearMulti(linears.map((l) => l.weight), x, F32, rows, ys, F32);
+    return ys;
+  }
   // RMS_SHADER (gpu-runtime.js:1325-1332): y = x / rms(x) * (scale or 1), eps 1e-6
   rms(encoder, x, rows, width, scale = null, garbage = null) {
     const y = this.emptyF32(rows * width, 'rms-out');

@@ -90,9 +90,9 @@ void *g4_stream(void);
 /* ---- command encoders ------------------------------------------------------
  * device.createCommandEncoder() / encoder.finish() / device.queue.submit()
  * (gemma4-webgpu.js:316-323, 339-358): between g4_encoder_begin and
- * g4_encoder_finish, kernel-launching calls (g4_w4_linear, g4_w4_dequant,
- * g4_ple_gather_dev, g4_bf16_head, g4_copy) are recorded instead of run;
- * g4_submit replays the recording on the queue (a HIP graph).  Calls that
+ * g4_encoder_finish, kernel-launching calls (g4_w4_linear, g4_w4_linear_multi,
+ * g4_w4_dequant, g4_ple_gather_dev, g4_bf16_head, g4_copy) are recorded instead
+ * of run; g4_submit replays the recording on the queue (a HIP graph).  Calls that
  * must wait for the device or move host memory (g4_alloc, g4_free,
  * g4_upload, g4_download, g4_sync, g4_ple_gather with host ids, loads) fail
  * with G4_E_STATE while an encoder is open.  Unlike a WebGPU command buffer,
@@ -146,6 +146,14 @@ int g4_w4_info(const g4_w4 *w, int *out_dim, int *in_dim, int *group,
  * GEMV kernel, large ones the MFMA GEMM kernel. */
 int g4_w4_linear(const g4_w4 *w, const void *x, int x_dtype, int rows,
                  void *y, int y_dtype);
+
+/* Consecutive GPUOps.w4 dispatches over one input (gemma4-webgpu.js:225,
+ * 237-238 for q/k/v and 280-281 for gate/up): y[i] = x * W[i]^T for i < n,
+ * 1 <= n <= 3, every W[i] of the same in_dim, outputs as g4_w4_linear's.
+ * For one activation row the n GEMVs run as one launch; otherwise each weight
+ * takes g4_w4_linear.  The outputs must not overlap x or each other. */
+int g4_w4_linear_multi(const g4_w4 *const *w, int n, const void *x, int x_dtype,
+                       int rows, void *const *y, int y_dtype);
 
 /* dequantizeOfficialW4A16Rows (official-w4a16.js:50-101) on the device:
  * out[r, k] = (nibble - 8) * scale for rows row_start..row_start+row_count-1,

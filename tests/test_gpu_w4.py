@@ -203,3 +203,74 @@ def test_errors_are_reported_not_faulted(g4):
     with pytest.raises(g4.G4Error) as e:
         lin.dequant(200, 100, g4.Buffer(100 * 512 * 4).ptr)
     assert e.value.code == g4.G4_E_RANGE
+
+
+# Weights sharing one input, as q/k/v and gate/up do (and ragged and generic-plan shapes).
+MULTI_SHAPES = {
+    "qkv_sliding": ((2048, 1536), (256, 1536), (256, 1536)),
+    "gate_up": ((6144, 1536), (6144, 1536)),
+    "ragged_k2048": ((100, 2048), (36, 2048), (1536, 2048)),
+    "ragged_k256": ((260, 256), (12, 256)),
+}
+
+
+@pytest.mark.parametrize("x_dtype_name", ["bf16", "f32"])
+@pytest.mark.parametrize("name", sorted(MULTI_SHAPES))
+def test_linear_multi_matches_single_launches(g4, oracle, name, x_dtype_name):
+    shapes = MULTI_SHAPES[name]
+    k = shapes[0][1]
+    x_dtype = g4.BF16 if x_dtype_name == "bf16" else g4.F32
+    x_bits, x = syn.activations(7, 1, k)
+    lins, refs = [], []
+    for i, (n, _) in enumerate(shapes):
+        packed, scales, _ = syn.w4_weights(300 + i, n, k)
+        lins.append(g4.W4Linear(packed, scales))
+        refs.append(np.asarray(oracle.w4_linear(x, packed, scales), np.float64).reshape(1, n))
+    xb = g4.Buffer.from_array(x_bits if x_dtype == g4.BF16 else x.astype(np.float32))
+    for y_dtype in (g4.F32, g4.BF16):
+        ye, dt = (4, np.float32) if y_dtype == g4.F32 else (2, np.uint16)
+        ys = [g4.Buffer(lin.out_dim * ye) for lin in lins]
+        g4.W4Linear.linear_multi(lins, xb.ptr, x_dtype, 1, [y.ptr for y in ys], y_dtype)
+        for lin, y, ref in zip(lins, ys, refs):
+            got = y.download(dt)
+            single = g4.Buffer(lin.out_dim * ye)
+            lin.linear(xb.ptr, x_dtype, 1, single.ptr, y_dtype)
+            # every row runs the single-weight kernel body: identical bits
+            assert np.array_equal(got, single.download(dt))
+            if y_dtype == g4.F32:
+                assert rel_l2_rows(got.reshape(1, -1), ref) <= TOL
+
+
+@pytest.mark.parametrize("rows", [3, 64])
+def test_linear_multi_several_rows(g4, oracle, rows):
+    k = 1536
+    x_bits, x = syn.activations(8, rows, k)
+    xb = g4.Buffer.from_array(x_bits)
+    lins, refs = [], []
+    for i, n in enumerate((512, 96)):
+        packed, scales, _ = syn.w4_weights(310 + i, n, k)
+        lins.append(g4.W4Linear(packed, scales))
+        refs.append(np.asarray(oracle.w4_linear(x, packed, scales), np.float64).reshape(rows, n))
+    ys = [g4.Buffer(rows * lin.out_dim * 4) for lin in lins]
+    g4.W4Linear.linear_multi(lins, xb.ptr, g4.BF16, rows, [y.ptr for y in ys], g4.F32)
+    for lin, y, ref in zip(lins, ys, refs):
+        got = y.download(np.float32).reshape(rows, lin.out_dim)
+        assert np.array_equal(got, run_linear(g4, lin, x_bits, x, rows, g4.BF16))
+        assert rel_l2_rows(got, ref) <= TOL
+
+
+def test_linear_multi_errors(g4):
+    a = g4.W4Linear(*syn.w4_weights(320, 64, 512)[:2])
+    b = g4.W4Linear(*syn.w4_weights(321, 64, 256)[:2])
+    x = g4.Buffer(512 * 4)
+    ys = [g4.Buffer(64 * 4) for _ in range(4)]
+    with pytest.raises(g4.G4Error) as e:  # different input dims
+        g4.W4Linear.linear_multi([a, b], x.ptr, g4.F32, 1, [y.ptr for y in ys[:2]])
+    assert e.value.code == g4.G4_E_ARG
+    with pytest.raises(g4.G4Error) as e:  # more than three weights
+        g4.W4Linear.linear_multi([a] * 4, x.ptr, g4.F32, 1, [y.ptr for y in ys])
+    assert e.value.code == g4.G4_E_ARG
+    short = g4.Buffer(63 * 4)
+    with pytest.raises(g4.G4Error) as e:  # second output too short
+        g4.W4Linear.linear_multi([a, a], x.ptr, g4.F32, 1, [ys[0].ptr, short.ptr])
+    assert e.value.code == g4.G4_E_RANGE
