@@ -272,13 +272,19 @@ __device__ __forceinline__ uint32_t deq_pair(uint32_t w, int t, f16x2 s2) {
   return __builtin_bit_cast(uint32_t, h);
 }
 
-// Requires Mp a multiple of BM and (K / 32) a multiple of KS (the launcher
-// checks both); FLAT requires the stage count a multiple of an even P.
+// Requires Mp a multiple of BM and (K / 32) a multiple of KS * gridDim.y (the
+// launcher checks both); FLAT requires the stage count of a slice a multiple
+// of an even P.
+//
+// Split K: with gridDim.y > 1, block row blockIdx.y covers stages
+// [y * S, y * S + S) of the input dimension and writes its FP32 partial
+// products (already rescaled) to part + y * pstride, rows < M only; the
+// slices are then added in order by gemm_splitk_sum_kernel.
 template <int TM, int TN, int NX, int KS, int P, bool FLAT>
 __global__ __launch_bounds__(kThreads, 2) void w4_gemm_kernel(
     const u32x4 *__restrict__ xt, const int *__restrict__ xe, const u32x4 *__restrict__ wq,
     const uint16_t *__restrict__ ws, int shift, void *__restrict__ y, int y_bf16, int M, int Mp,
-    int N, int K, int xcd_map) {
+    int N, int K, int xcd_map, float *__restrict__ part, size_t pstride) {
   constexpr int BM = 32 * TM, BN = 32 * TN;
   constexpr int KC = 4 * KS;              // 16-byte chunks per row per stage
   constexpr int AE = BM * KC / kThreads;  // x' chunks per thread per stage (per plane)
@@ -291,7 +297,8 @@ __global__ __launch_bounds__(kThreads, 2) void w4_gemm_kernel(
   __shared__ u32x4 Bs[2][KC][BNP];
 
   const int G = K >> 5;
-  const int S = G / KS;
+  const int S = G / KS / (int)gridDim.y;  // stages of this block's slice of K
+  const int st0_slice = (int)blockIdx.y * S;
   const int t = threadIdx.x;
   const int lane = t & 63, wave = t >> 6;
   const int wm = wave >> 1, wn = wave & 1;
@@ -321,7 +328,7 @@ __global__ __launch_bounds__(kThreads, 2) void w4_gemm_kernel(
     const int idx = t + i * kThreads;
     a_c[i] = idx / BM;
     a_row[i] = idx % BM;
-    a_src[i] = xt + (size_t)a_c[i] * Mp + m0 + a_row[i];
+    a_src[i] = xt + (size_t)(st0_slice * KC + a_c[i]) * Mp + m0 + a_row[i];
   }
   // B: entry i is group b_kk[i] of the stage for tile row b_row[i]
   int b_row[BE], b_kk[BE];
@@ -337,8 +344,8 @@ __global__ __launch_bounds__(kThreads, 2) void w4_gemm_kernel(
     b_row[i] = live ? idx / KS : BN;
     b_kk[i] = live ? idx % KS : 0;
     const int gn = !live ? n0 : n0 + b_row[i] < N ? n0 + b_row[i] : N - 1;
-    b_src[i] = wq + (size_t)gn * G + b_kk[i];
-    s_src[i] = ws + (size_t)gn * G + (b_kk[i] & ~(SW - 1));
+    b_src[i] = wq + (size_t)gn * G + st0_slice * KS + b_kk[i];
+    s_src[i] = ws + (size_t)gn * G + st0_slice * KS + (b_kk[i] & ~(SW - 1));
   }
 
   // Ring of P register slots: stage j is loaded into slot j % P, P - 1
@@ -477,55 +484,137 @@ __global__ __launch_bounds__(kThreads, 2) void w4_gemm_kernel(
       }
     }
   };
-  if (y_bf16)
+  if (gridDim.y > 1)
+    epilogue(part + blockIdx.y * pstride);
+  else if (y_bf16)
     epilogue(static_cast<uint16_t *>(y));
   else
     epilogue(static_cast<float *>(y));
 }
 
+// y[i] = sum of part[s * pstride + i] over the slices s in order, as FP32 or
+// BF16.  VEC: four outputs per thread (n a multiple of 4, y 16-byte aligned).
+template <bool VEC>
+__global__ __launch_bounds__(kThreads) void gemm_splitk_sum_kernel(const float *__restrict__ part,
+                                                                   int slices, size_t pstride,
+                                                                   size_t n, void *__restrict__ y,
+                                                                   int y_bf16) {
+  const size_t i = ((size_t)blockIdx.x * kThreads + threadIdx.x) * (VEC ? 4 : 1);
+  if (i >= n) return;
+  if (VEC) {
+    f32x4 v = *reinterpret_cast<const f32x4 *>(part + i);
+    for (int s = 1; s < slices; ++s) v += *reinterpret_cast<const f32x4 *>(part + s * pstride + i);
+    if (y_bf16) {
+      const uint32_t lo = f32_to_bf16_rne(v[0]) | (f32_to_bf16_rne(v[1]) << 16);
+      const uint32_t hi = f32_to_bf16_rne(v[2]) | (f32_to_bf16_rne(v[3]) << 16);
+      *reinterpret_cast<uint2 *>(static_cast<uint16_t *>(y) + i) = make_uint2(lo, hi);
+    } else {
+      *reinterpret_cast<f32x4 *>(static_cast<float *>(y) + i) = v;
+    }
+  } else {
+    float v = part[i];
+    for (int s = 1; s < slices; ++s) v += part[s * pstride + i];
+    if (y_bf16)
+      static_cast<uint16_t *>(y)[i] = (uint16_t)f32_to_bf16_rne(v);
+    else
+      static_cast<float *>(y)[i] = v;
+  }
+}
+
+// Floats between consecutive split-K partial planes of rows x N outputs.
+size_t splitk_pstride(int rows, int N) { return ((size_t)rows * N + 63) & ~size_t(63); }
+
 template <int TM, int TN, int NX, int KS, int P>
 int launch_gemm(const g4_w4 *w, const uint4 *xt, const int *xe, int rows, int Mp, void *y,
-                bool y_bf16) {
+                bool y_bf16, float *part, int slices) {
   constexpr int BM = 32 * TM, BN = 32 * TN;
-  if (Mp % BM != 0 || w->G % KS != 0)
-    return fail(G4_E_ARG, "w4_gemm: tile %dx%d (KS %d) does not fit rows %d, K %d", BM, BN, KS,
-                rows, w->K);
+  if (Mp % BM != 0 || w->G % (KS * slices) != 0)
+    return fail(G4_E_ARG, "w4_gemm: tile %dx%d (KS %d, %d slices) does not fit rows %d, K %d",
+                BM, BN, KS, slices, rows, w->K);
   const int nm = (rows + BM - 1) / BM, nn = (w->N + BN - 1) / BN;
   const int xcd_map = nm % 8 == 0;
-  const bool flat = P % 2 == 0 && (w->G / KS) % P == 0;
+  const bool flat = P % 2 == 0 && (w->G / KS / slices) % P == 0;
+  const size_t pstride = splitk_pstride(rows, w->N);
   auto kernel = flat ? w4_gemm_kernel<TM, TN, NX, KS, P, true> : w4_gemm_kernel<TM, TN, NX, KS, P, false>;
-  hipLaunchKernelGGL(kernel, dim3(nm * nn), dim3(kThreads), 0, stream(),
+  hipLaunchKernelGGL(kernel, dim3(nm * nn, slices), dim3(kThreads), 0, stream(),
                      reinterpret_cast<const u32x4 *>(xt), xe,
                      reinterpret_cast<const u32x4 *>(w->packed), w->scales, w->shift, y,
-                     (int)y_bf16, rows, Mp, w->N, w->K, xcd_map);
+                     (int)y_bf16, rows, Mp, w->N, w->K, xcd_map, part, pstride);
   G4_LAUNCH_CHECK("w4_gemm_kernel");
+  if (slices > 1) {
+    const size_t n = (size_t)rows * w->N;
+    const bool vec = n % 4 == 0 && (reinterpret_cast<uintptr_t>(y) & 15u) == 0;
+    const size_t threads = vec ? n / 4 : n;
+    const dim3 grid((unsigned)((threads + kThreads - 1) / kThreads));
+    if (vec)
+      hipLaunchKernelGGL(gemm_splitk_sum_kernel<true>, grid, dim3(kThreads), 0, stream(), part,
+                         slices, pstride, n, y, (int)y_bf16);
+    else
+      hipLaunchKernelGGL(gemm_splitk_sum_kernel<false>, grid, dim3(kThreads), 0, stream(), part,
+                         slices, pstride, n, y, (int)y_bf16);
+    G4_LAUNCH_CHECK("gemm_splitk_sum_kernel");
+  }
   return G4_OK;
 }
 
-// Tile choice: the largest tile (128 x 128) unless that leaves CUs idle or a
-// ragged last wave; then 64-row tiles, and 96-column tiles when those divide
-// N into a multiple of the CU count (e.g. M 2048, N 1536 -> 32 x 16 = 512).
-// Two groups per stage unless the group count is odd.
-template <int NX>
-int launch_gemm_auto(const g4_w4 *w, const uint4 *xt, const int *xe, int rows, int Mp, void *y,
-                     bool y_bf16) {
-  constexpr int P = 4;
-  if (w->G % 2 != 0) return launch_gemm<2, 2, NX, 1, P>(w, xt, xe, rows, Mp, y, y_bf16);
+// Tile and K split of one prefill GEMM.  Tile: the largest (128 x 128)
+// unless that leaves CUs idle or a ragged last wave; then 128 x 96 or 64 x 96
+// tiles when those fill whole rounds of the CUs (e.g. M 2048, N 1536 -> 256
+// tiles of 128 x 96), then 64 x 128 and 64 x 64.  Two groups per stage unless
+// the group count is odd.
+//
+// K split (partial planes added by gemm_splitk_sum_kernel): a grid of fewer
+// 64 x 64 tiles than CUs (the E2B prefill's 1536-wide outputs at 512 rows:
+// 192 tiles) takes 64 x 96 (or 64 x 64) tiles and splits K into slices of at
+// least 16 stages, up to two blocks per CU; a grid below a quarter of the
+// CUs takes slices of 6 or more stages, up to one block per CU.  One round of
+// 128 x 96 tiles over a long K (M 2048, N 1536, K 6144) splits in two.
+// Measured at M 512 with FP32 x: N 1536 at K 6144 / 12288 / 2048 37 / 61 /
+// 21 us instead of 70 / 127 / 25; N 256 at K 1536 10.6 instead of 18.
+struct GemmPlan {
+  int tm, tn, ks, slices;
+};
+constexpr int kMaxSplitK = 8;
+
+GemmPlan plan_gemm(const g4_w4 *w, int rows, bool f32x) {
   const int cus = cu_count() > 0 ? cu_count() : 256;
+  if (w->G % 2 != 0) return {2, 2, 1, 1};
+  const int S = w->G / 2;
   auto blocks = [&](int bm, int bn) {
     return (long)((rows + bm - 1) / bm) * ((w->N + bn - 1) / bn);
   };
-  if (blocks(128, 128) >= 2L * cus)
-    return launch_gemm<4, 4, NX, 2, P>(w, xt, xe, rows, Mp, y, y_bf16);
-  // one 128 x 96 tile per CU (e.g. M 2048, N 1536): 72 vs 80 us for 64 x 96 at K 6144
+  if (blocks(128, 128) >= 2L * cus) return {4, 4, 2, 1};
+  if (!f32x && w->N % 96 == 0 && blocks(128, 96) % cus == 0)
+    return {4, 3, 2, blocks(128, 96) == cus && S % 2 == 0 && S / 2 >= 16 ? 2 : 1};
+  if (w->N % 96 == 0 && blocks(64, 96) % cus == 0) return {2, 3, 2, 1};
+  if (blocks(64, 128) >= cus) return {2, 4, 2, 1};
+  if (blocks(64, 64) >= cus) return {2, 2, 2, 1};
+  const bool n96 = w->N % 96 == 0;
+  const long b = n96 ? blocks(64, 96) : blocks(64, 64);
+  int slices = 1;
+  for (int k = 2; k <= kMaxSplitK; ++k)
+    if (S % k == 0 && S / k >= 16 && b * k <= 2L * cus) slices = k;
+  if (slices == 1 && b * 4 < cus)
+    for (int k = 2; k <= kMaxSplitK; ++k)
+      if (S % k == 0 && S / k >= 6 && b * k <= cus) slices = k;
+  return {2, n96 ? 3 : 2, 2, slices};
+}
+
+template <int NX>
+int launch_planned(const GemmPlan &pl, const g4_w4 *w, const uint4 *xt, const int *xe, int rows,
+                   int Mp, void *y, bool y_bf16, float *part) {
+  constexpr int P = 4;
+  const int sl = pl.slices;
+  if (pl.ks == 1) return launch_gemm<2, 2, NX, 1, P>(w, xt, xe, rows, Mp, y, y_bf16, part, sl);
+  if (pl.tm == 4 && pl.tn == 4)
+    return launch_gemm<4, 4, NX, 2, P>(w, xt, xe, rows, Mp, y, y_bf16, part, sl);
   if constexpr (NX == 1) {
-    if (w->N % 96 == 0 && blocks(128, 96) % cus == 0)
-      return launch_gemm<4, 3, NX, 2, P>(w, xt, xe, rows, Mp, y, y_bf16);
+    if (pl.tm == 4 && pl.tn == 3)
+      return launch_gemm<4, 3, NX, 2, P>(w, xt, xe, rows, Mp, y, y_bf16, part, sl);
   }
-  if (w->N % 96 == 0 && blocks(64, 96) % cus == 0)
-    return launch_gemm<2, 3, NX, 2, P>(w, xt, xe, rows, Mp, y, y_bf16);
-  if (blocks(64, 128) >= cus) return launch_gemm<2, 4, NX, 2, P>(w, xt, xe, rows, Mp, y, y_bf16);
-  return launch_gemm<2, 2, NX, 2, P>(w, xt, xe, rows, Mp, y, y_bf16);
+  if (pl.tn == 3) return launch_gemm<2, 3, NX, 2, P>(w, xt, xe, rows, Mp, y, y_bf16, part, sl);
+  if (pl.tn == 4) return launch_gemm<2, 4, NX, 2, P>(w, xt, xe, rows, Mp, y, y_bf16, part, sl);
+  return launch_gemm<2, 2, NX, 2, P>(w, xt, xe, rows, Mp, y, y_bf16, part, sl);
 }
 
 // x' (and its low half) and the row exponents, reused by every later call.
@@ -539,11 +628,15 @@ int w4_gemm(const g4_w4 *w, const void *x, bool f32x, int rows, void *y, bool y_
   const int Mp = (rows + kRowPad - 1) / kRowPad * kRowPad;
   const size_t xt_bytes = (size_t)Mp * w->K * 2 * (f32x ? 2 : 1);  // FP16 x' (hi [+ lo])
   const size_t eoff = (xt_bytes + 255) & ~size_t(255);
+  const size_t poff = (eoff + (size_t)rows * 4 + 255) & ~size_t(255);
+  const GemmPlan plan = plan_gemm(w, rows, f32x);
+  const size_t part_bytes = plan.slices > 1 ? plan.slices * splitk_pstride(rows, w->N) * 4 : 0;
   void *ws = nullptr;
-  int rc = g_ws.get(eoff + (size_t)rows * 4, &ws, "g4_w4_linear (prefill)");
+  int rc = g_ws.get(poff + part_bytes, &ws, "g4_w4_linear (prefill)");
   if (rc) return rc;
   uint4 *xt = static_cast<uint4 *>(ws);
   int *xe = reinterpret_cast<int *>(static_cast<char *>(ws) + eoff);
+  float *part = reinterpret_cast<float *>(static_cast<char *>(ws) + poff);
   const int cpt = fused_prep_cpt(w->K, f32x);
   if (cpt) {
     const dim3 fgrid(Mp / kRowsFused);
@@ -569,8 +662,8 @@ int w4_gemm(const g4_w4 *w, const void *x, bool f32x, int rows, void *y, bool y_
     }
 #undef G4_PREP_FUSED
     G4_LAUNCH_CHECK("gemm_xprep_fused_kernel");
-    return f32x ? launch_gemm_auto<2>(w, xt, xe, rows, Mp, y, y_bf16)
-                : launch_gemm_auto<1>(w, xt, xe, rows, Mp, y, y_bf16);
+    return f32x ? launch_planned<2>(plan, w, xt, xe, rows, Mp, y, y_bf16, part)
+                : launch_planned<1>(plan, w, xt, xe, rows, Mp, y, y_bf16, part);
   }
   const dim3 egrid((rows + kThreads / 64 - 1) / (kThreads / 64));
   const dim3 pgrid(Mp / kPrepTileM, (w->K / 8 + kPrepTileC - 1) / kPrepTileC);
@@ -586,8 +679,8 @@ int w4_gemm(const g4_w4 *w, const void *x, bool f32x, int rows, void *y, bool y_
                        Mp, w->K, xt);
   }
   G4_LAUNCH_CHECK("gemm_xprep_kernel");
-  return f32x ? launch_gemm_auto<2>(w, xt, xe, rows, Mp, y, y_bf16)
-              : launch_gemm_auto<1>(w, xt, xe, rows, Mp, y, y_bf16);
+  return f32x ? launch_planned<2>(plan, w, xt, xe, rows, Mp, y, y_bf16, part)
+              : launch_planned<1>(plan, w, xt, xe, rows, Mp, y, y_bf16, part);
 }
 
 }  // namespace g4

@@ -169,6 +169,24 @@ def test_gemm_ragged_shapes_and_activation_ranges(g4, x_dtype_name, k):
     assert np.all(y[5] == 0.0)
 
 
+@pytest.mark.parametrize("rows,n,k", [(512, 1536, 6144), (512, 1536, 12288), (512, 1536, 2048),
+                                        (512, 256, 1536), (300, 1536, 6144)])
+def test_gemm_split_k_prefill_shapes(g4, rows, n, k):
+    # The E2B prefill's 1536- and 256-wide outputs at 512 rows leave most CUs
+    # idle as whole tiles, so K is split into partial planes that are added in
+    # slice order (slices of 16+ stages; of 6 for N 256, the general loop).
+    # FP32 activations, as the model feeds them, against the binary64 product:
+    # hi + lo halves keep the error near FP32 rounding.
+    packed, scales, q = syn.w4_weights(21, n, k)
+    x = np.random.default_rng(21).standard_normal((rows, k)).astype(np.float32)
+    lin = g4.W4Linear(packed, scales)
+    y = run_linear(g4, lin, None, x, rows, g4.F32)
+    ref = x.astype(np.float64) @ dense(q, scales).T
+    assert rel_l2_rows(y, ref) <= 1e-5
+    yb = run_linear(g4, lin, None, x, rows, g4.F32, g4.BF16)
+    assert np.array_equal(yb, syn.bf16_rne(y).reshape(rows, n))
+
+
 def test_gemm_matches_gemv_path(g4):
     # Rows 1..4 take the streaming GEMV, more rows the MFMA GEMM: the row a
     # caller computes must not depend on how many rows come with it.
