@@ -115,12 +115,11 @@ struct g4_gemma {
   // device state
   int *ids = nullptr, *pos = nullptr, *gen = nullptr;
   float *h[2] = {}, *pre = nullptr, *qraw = nullptr, *q = nullptr, *kraw = nullptr,
-        *vraw = nullptr, *ctx = nullptr, *attn = nullptr, *an = nullptr, *ares = nullptr,
-        *pf = nullptr, *gate = nullptr, *up = nullptr, *act = nullptr, *down = nullptr,
-        *downp = nullptr,
-        *fn = nullptr, *fres = nullptr, *pg = nullptr, *pm = nullptr, *pp = nullptr,
-        *pn = nullptr, *tokple = nullptr, *proj = nullptr,
-        *perlayer = nullptr, *last = nullptr, *logits = nullptr, *part = nullptr;
+        *vraw = nullptr, *ctx = nullptr, *attn = nullptr, *ares = nullptr, *pf = nullptr,
+        *gate = nullptr, *up = nullptr, *act = nullptr, *down = nullptr, *downp = nullptr,
+        *fres = nullptr, *pg = nullptr, *pm = nullptr, *pp = nullptr, *tokple = nullptr,
+        *proj = nullptr, *perlayer = nullptr, *last = nullptr, *logits = nullptr,
+        *part = nullptr;
   float2 *hpart = nullptr;
   size_t part_floats = 0;
   RopeSlots rope_slots = {};
@@ -291,20 +290,27 @@ int run_layers(g4_gemma *m, int rows, bool graph) {
   const int max_keylen = graph ? c.max_seq : keylen_host;
   const int kpw = kpw_for(rows);
   int cur = 0;
+  // Each norm -> residual add -> norm run of encodeLayer is one norm_chain
+  // launch: post-attention norm + residual + pre-FFN norm; post-FFN norm +
+  // residual; post-PLE norm + residual + layer scalar + the next layer's
+  // input norm (so only layer 0 runs its input norm alone).
+  if ((rc = launch_rms(m->h[0], rows, H, m->L[0].norm[G4_NORM_INPUT], eps, m->pre, nullptr)))
+    return rc;
   for (int i = 0; i < NL; ++i) {
     const Layer &l = m->L[i];
     float *hid = m->h[cur], *out = m->h[cur ^ 1];
-    const int HD = c.heads * l.hd;
-    // encodeLayer (gemma4-webgpu.js:215-301)
-    if ((rc = launch_rms(hid, rows, H, l.norm[G4_NORM_INPUT], eps, m->pre, nullptr))) return rc;
-    if ((rc = g4_w4_linear(l.w[G4_PROJ_Q], m->pre, G4_F32, rows, m->qraw, G4_F32))) return rc;
+    // encodeLayer (gemma4-webgpu.js:215-301); m->pre holds rms(hid) * input norm
+    // q, and k/v for a layer with its own cache, from one pre-pass and launch
+    const g4_w4 *qkv[3] = {l.w[G4_PROJ_Q], l.w[G4_PROJ_K], l.w[G4_PROJ_V]};
+    void *qkv_out[3] = {m->qraw, m->kraw, m->vraw};
+    if ((rc = g4_w4_linear_multi(qkv, l.kv_src < 0 ? 3 : 1, m->pre, G4_F32, rows, qkv_out,
+                                 G4_F32)))
+      return rc;
     if ((rc = launch_norm_rope(m->qraw, rows, c.heads, l.hd, 0, m->pos, l.norm[G4_NORM_Q],
                                l.rope_angles, l.rope_base, eps, m->q, false)))
       return rc;
     const Layer &src = l.kv_src >= 0 ? m->L[l.kv_src] : l;
     if (l.kv_src < 0) {
-      if ((rc = g4_w4_linear(l.w[G4_PROJ_K], m->pre, G4_F32, rows, m->kraw, G4_F32))) return rc;
-      if ((rc = g4_w4_linear(l.w[G4_PROJ_V], m->pre, G4_F32, rows, m->vraw, G4_F32))) return rc;
       // KVCache.append: rows go straight to positions pos .. pos + rows - 1
       if ((rc = launch_norm_rope(m->kraw, rows, 1, l.hd, 0, m->pos, l.norm[G4_NORM_K],
                                  l.rope_angles, l.rope_base, eps, l.kc, true)))
@@ -315,27 +321,27 @@ int run_layers(g4_gemma *m, int rows, bool graph) {
                                max_keylen, !l.full, c.window, kpw, m->part, m->ctx)))
       return rc;
     if ((rc = g4_w4_linear(l.w[G4_PROJ_O], m->ctx, G4_F32, rows, m->attn, G4_F32))) return rc;
-    if ((rc = launch_rms(m->attn, rows, H, l.norm[G4_NORM_POST_ATTN], eps, m->an, nullptr)))
+    if ((rc = launch_norm_chain(m->attn, hid, l.norm[G4_NORM_POST_ATTN], l.norm[G4_NORM_PRE_FFW],
+                                1.f, eps, rows, H, m->ares, m->pf)))
       return rc;
-    if ((rc = launch_add_scale(hid, m->an, (size_t)rows * H, 1.f, m->ares))) return rc;
-    if ((rc = launch_rms(m->ares, rows, H, l.norm[G4_NORM_PRE_FFW], eps, m->pf, nullptr)))
-      return rc;
-    if ((rc = g4_w4_linear(l.w[G4_PROJ_GATE], m->pf, G4_F32, rows, m->gate, G4_F32))) return rc;
-    if ((rc = g4_w4_linear(l.w[G4_PROJ_UP], m->pf, G4_F32, rows, m->up, G4_F32))) return rc;
+    const g4_w4 *gu[2] = {l.w[G4_PROJ_GATE], l.w[G4_PROJ_UP]};
+    void *gu_out[2] = {m->gate, m->up};
+    if ((rc = g4_w4_linear_multi(gu, 2, m->pf, G4_F32, rows, gu_out, G4_F32))) return rc;
     if ((rc = launch_gelu_mul(m->gate, m->up, (size_t)rows * l.inter, m->act))) return rc;
     if ((rc = g4_w4_linear(l.w[G4_PROJ_DOWN], m->act, G4_F32, rows, m->down, G4_F32))) return rc;
-    if ((rc = launch_rms(m->down, rows, H, l.norm[G4_NORM_POST_FFW], eps, m->fn, nullptr)))
+    if ((rc = launch_norm_chain(m->down, m->ares, l.norm[G4_NORM_POST_FFW], nullptr, 1.f, eps,
+                                rows, H, m->fres, nullptr)))
       return rc;
-    if ((rc = launch_add_scale(m->ares, m->fn, (size_t)rows * H, 1.f, m->fres))) return rc;
     if ((rc = g4_w4_linear(l.w[G4_PROJ_PLE_GATE], m->fres, G4_F32, rows, m->pg, G4_F32)))
       return rc;
     if ((rc = launch_gelu_ple(m->pg, m->perlayer, rows, i, P, NL, m->pm))) return rc;
     if ((rc = g4_w4_linear(l.w[G4_PROJ_PLE_PROJ], m->pm, G4_F32, rows, m->pp, G4_F32)))
       return rc;
-    if ((rc = launch_rms(m->pp, rows, H, l.norm[G4_NORM_POST_PLE], eps, m->pn, nullptr)))
+    const bool last = i + 1 == NL;
+    if ((rc = launch_norm_chain(m->pp, m->fres, l.norm[G4_NORM_POST_PLE],
+                                last ? nullptr : m->L[i + 1].norm[G4_NORM_INPUT], l.skip, eps,
+                                rows, H, out, last ? nullptr : m->pre)))
       return rc;
-    if ((rc = launch_add_scale(m->fres, m->pn, (size_t)rows * H, l.skip, out))) return rc;
-    (void)HD;
     cur ^= 1;
   }
   // final norm of the last row (gemma4-webgpu.js:394-400)
@@ -495,7 +501,6 @@ G4_API int g4_gemma_create(const g4_gemma_config *cfg, g4_gemma **out) {
   A(&m->vraw, R * m->hd_max);
   A(&m->ctx, R * QD);
   A(&m->attn, R * H);
-  A(&m->an, R * H);
   A(&m->ares, R * H);
   A(&m->pf, R * H);
   A(&m->gate, R * m->inter_max);
@@ -503,12 +508,10 @@ G4_API int g4_gemma_create(const g4_gemma_config *cfg, g4_gemma **out) {
   A(&m->act, R * m->inter_max);
   A(&m->down, R * H);
   A(&m->downp, (size_t)kDownMaxSlices * H);
-  A(&m->fn, R * H);
   A(&m->fres, R * H);
   A(&m->pg, R * c.ple_dim);
   A(&m->pm, R * c.ple_dim);
   A(&m->pp, R * H);
-  A(&m->pn, R * H);
   A(&m->tokple, R * m->ple_total);
   A(&m->proj, R * m->ple_total);
   A(&m->perlayer, R * m->ple_total);

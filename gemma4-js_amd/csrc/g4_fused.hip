@@ -880,7 +880,8 @@ __global__ __launch_bounds__(256) void attn_rope_dec_kernel(AttnRopeArgs A) {
 }
 
 // ---- standalone chain r = (h + rms(a) * w1) * c; x = rms(r) * w2 ------------
-// One block per row; writes r (if r_out) and x.
+// One block per row; writes r (if r_out) and x (if x_out; without x_out, r_out
+// is required and w2 is not read).
 __global__ __launch_bounds__(256) void norm_chain_kernel(const float *__restrict__ a,
                                                          const float *__restrict__ h,
                                                          const float *__restrict__ w1,
@@ -902,7 +903,7 @@ __global__ __launch_bounds__(256) void norm_chain_kernel(const float *__restrict
       av[u] = a[off + i];
       hv[u] = h[off + i];
       w1v[u] = w1[i];
-      w2v[u] = w2[i];
+      w2v[u] = x_out ? w2[i] : 0.f;
     }
     float ss = 0.f;
 #pragma unroll
@@ -914,6 +915,12 @@ __global__ __launch_bounds__(256) void norm_chain_kernel(const float *__restrict
     for (int u = 0; u < U; ++u) {
       r[u] = (hv[u] + av[u] * inv1 * w1v[u]) * c;
       if (threadIdx.x + 256 * u < width) ss2 += r[u] * r[u];
+    }
+    if (!x_out) {  // the residual alone
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+        if (threadIdx.x + 256 * u < width) r_out[off + threadIdx.x + 256 * u] = r[u];
+      return;
     }
     const float inv2 = 1.f / sqrtf(fblock_sum(ss2, red + 4, 4) / (float)width + eps);
 #pragma unroll
@@ -935,6 +942,7 @@ __global__ __launch_bounds__(256) void norm_chain_kernel(const float *__restrict
     if (r_out) r_out[off + i] = r;
     ss2 += r * r;
   }
+  if (!x_out) return;
   const float inv2 = 1.f / sqrtf(fblock_sum(ss2, red, 4) / (float)width + eps);
   for (int i = threadIdx.x; i < width; i += 256) {
     const float r = (h[off + i] + a[off + i] * inv1 * w1[i]) * c;

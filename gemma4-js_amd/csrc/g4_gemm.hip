@@ -280,11 +280,22 @@ __device__ __forceinline__ uint32_t deq_pair(uint32_t w, int t, f16x2 s2) {
 // [y * S, y * S + S) of the input dimension and writes its FP32 partial
 // products (already rescaled) to part + y * pstride, rows < M only; the
 // slices are then added in order by gemm_splitk_sum_kernel.
+// Weights of one input dimension over the same x' in one launch: the n tiles
+// of weight i are t0[i] .. t0[i + 1] - 1 of the grid's tile axis.
+constexpr int kMaxGemmSegs = 3;
+struct GemmSegs {
+  const u32x4 *wq[kMaxGemmSegs];
+  const uint16_t *ws[kMaxGemmSegs];
+  void *y[kMaxGemmSegs];
+  int N[kMaxGemmSegs], shift[kMaxGemmSegs];
+  int t0[kMaxGemmSegs + 1];
+  int n;
+};
+
 template <int TM, int TN, int NX, int KS, int P, bool FLAT>
 __global__ __launch_bounds__(kThreads, 2) void w4_gemm_kernel(
-    const u32x4 *__restrict__ xt, const int *__restrict__ xe, const u32x4 *__restrict__ wq,
-    const uint16_t *__restrict__ ws, int shift, void *__restrict__ y, int y_bf16, int M, int Mp,
-    int N, int K, int xcd_map, float *__restrict__ part, size_t pstride) {
+    const u32x4 *__restrict__ xt, const int *__restrict__ xe, GemmSegs SG, int y_bf16, int M,
+    int Mp, int K, int xcd_map, float *__restrict__ part, size_t pstride) {
   constexpr int BM = 32 * TM, BN = 32 * TN;
   constexpr int KC = 4 * KS;              // 16-byte chunks per row per stage
   constexpr int AE = BM * KC / kThreads;  // x' chunks per thread per stage (per plane)
@@ -306,7 +317,7 @@ __global__ __launch_bounds__(kThreads, 2) void w4_gemm_kernel(
   // block -> (m tile, n tile); with xcd_map, all n tiles of one m band run on
   // one XCD (blocks are dealt to the 8 XCDs round-robin), so its L2 holds
   // that band of x' for every one of them.
-  const int nn = (N + BN - 1) / BN;
+  const int nn = SG.t0[SG.n];
   int mt, ntile;
   if (xcd_map) {
     const int b = blockIdx.x, xcd = b & 7, j = b >> 3;
@@ -316,7 +327,12 @@ __global__ __launch_bounds__(kThreads, 2) void w4_gemm_kernel(
     mt = blockIdx.x / nn;
     ntile = blockIdx.x - mt * nn;
   }
-  const int m0 = mt * BM, n0 = ntile * BN;
+  const int si = SG.n > 2 && ntile >= SG.t0[2] ? 2 : SG.n > 1 && ntile >= SG.t0[1] ? 1 : 0;
+  const u32x4 *__restrict__ wq = SG.wq[si];
+  const uint16_t *__restrict__ ws = SG.ws[si];
+  void *__restrict__ y = SG.y[si];
+  const int N = SG.N[si], shift = SG.shift[si];
+  const int m0 = mt * BM, n0 = (ntile - SG.t0[si]) * BN;
 
   // A: entry i of this thread is chunk a_c[i] of tile row a_row[i]
   const size_t a_stage = (size_t)KC * Mp;  // xt entries per stage
@@ -524,25 +540,37 @@ __global__ __launch_bounds__(kThreads) void gemm_splitk_sum_kernel(const float *
 // Floats between consecutive split-K partial planes of rows x N outputs.
 size_t splitk_pstride(int rows, int N) { return ((size_t)rows * N + 63) & ~size_t(63); }
 
+// n weights (1..kMaxGemmSegs) of one input dimension, y[i] receiving weight
+// i's output; a K split (slices > 1) takes one weight.
 template <int TM, int TN, int NX, int KS, int P>
-int launch_gemm(const g4_w4 *w, const uint4 *xt, const int *xe, int rows, int Mp, void *y,
-                bool y_bf16, float *part, int slices) {
+int launch_gemm(const g4_w4 *const *w, int nw, const uint4 *xt, const int *xe, int rows, int Mp,
+                void *const *ys, bool y_bf16, float *part, int slices) {
   constexpr int BM = 32 * TM, BN = 32 * TN;
-  if (Mp % BM != 0 || w->G % (KS * slices) != 0)
+  if (Mp % BM != 0 || w[0]->G % (KS * slices) != 0 || (slices > 1 && nw != 1))
     return fail(G4_E_ARG, "w4_gemm: tile %dx%d (KS %d, %d slices) does not fit rows %d, K %d",
-                BM, BN, KS, slices, rows, w->K);
-  const int nm = (rows + BM - 1) / BM, nn = (w->N + BN - 1) / BN;
+                BM, BN, KS, slices, rows, w[0]->K);
+  GemmSegs sg{};
+  sg.n = nw;
+  for (int i = 0; i < nw; ++i) {
+    sg.wq[i] = reinterpret_cast<const u32x4 *>(w[i]->packed);
+    sg.ws[i] = w[i]->scales;
+    sg.y[i] = ys[i];
+    sg.N[i] = w[i]->N;
+    sg.shift[i] = w[i]->shift;
+    sg.t0[i + 1] = sg.t0[i] + (w[i]->N + BN - 1) / BN;
+  }
+  const int nm = (rows + BM - 1) / BM, nn = sg.t0[nw];
   const int xcd_map = nm % 8 == 0;
-  const bool flat = P % 2 == 0 && (w->G / KS / slices) % P == 0;
-  const size_t pstride = splitk_pstride(rows, w->N);
+  const bool flat = P % 2 == 0 && (w[0]->G / KS / slices) % P == 0;
+  const size_t pstride = splitk_pstride(rows, w[0]->N);
   auto kernel = flat ? w4_gemm_kernel<TM, TN, NX, KS, P, true> : w4_gemm_kernel<TM, TN, NX, KS, P, false>;
   hipLaunchKernelGGL(kernel, dim3(nm * nn, slices), dim3(kThreads), 0, stream(),
-                     reinterpret_cast<const u32x4 *>(xt), xe,
-                     reinterpret_cast<const u32x4 *>(w->packed), w->scales, w->shift, y,
-                     (int)y_bf16, rows, Mp, w->N, w->K, xcd_map, part, pstride);
+                     reinterpret_cast<const u32x4 *>(xt), xe, sg, (int)y_bf16, rows, Mp,
+                     w[0]->K, xcd_map, part, pstride);
   G4_LAUNCH_CHECK("w4_gemm_kernel");
   if (slices > 1) {
-    const size_t n = (size_t)rows * w->N;
+    void *y = ys[0];
+    const size_t n = (size_t)rows * w[0]->N;
     const bool vec = n % 4 == 0 && (reinterpret_cast<uintptr_t>(y) & 15u) == 0;
     const size_t threads = vec ? n / 4 : n;
     const dim3 grid((unsigned)((threads + kThreads - 1) / kThreads));
@@ -576,20 +604,24 @@ struct GemmPlan {
 };
 constexpr int kMaxSplitK = 8;
 
-GemmPlan plan_gemm(const g4_w4 *w, int rows, bool f32x) {
+GemmPlan plan_gemm(const g4_w4 *const *w, int nw, int rows, bool f32x) {
   const int cus = cu_count() > 0 ? cu_count() : 256;
-  if (w->G % 2 != 0) return {2, 2, 1, 1};
-  const int S = w->G / 2;
+  if (w[0]->G % 2 != 0) return {2, 2, 1, 1};
+  const int S = w[0]->G / 2;
   auto blocks = [&](int bm, int bn) {
-    return (long)((rows + bm - 1) / bm) * ((w->N + bn - 1) / bn);
+    long tiles = 0;
+    for (int i = 0; i < nw; ++i) tiles += (w[i]->N + bn - 1) / bn;
+    return (long)((rows + bm - 1) / bm) * tiles;
   };
+  bool n96 = true;
+  for (int i = 0; i < nw; ++i) n96 = n96 && w[i]->N % 96 == 0;
+  const int split_ok = nw == 1;  // a K split takes one weight
   if (blocks(128, 128) >= 2L * cus) return {4, 4, 2, 1};
-  if (!f32x && w->N % 96 == 0 && blocks(128, 96) % cus == 0)
-    return {4, 3, 2, blocks(128, 96) == cus && S % 2 == 0 && S / 2 >= 16 ? 2 : 1};
-  if (w->N % 96 == 0 && blocks(64, 96) % cus == 0) return {2, 3, 2, 1};
+  if (!f32x && n96 && blocks(128, 96) % cus == 0)
+    return {4, 3, 2, split_ok && blocks(128, 96) == cus && S % 2 == 0 && S / 2 >= 16 ? 2 : 1};
+  if (n96 && blocks(64, 96) % cus == 0) return {2, 3, 2, 1};
   if (blocks(64, 128) >= cus) return {2, 4, 2, 1};
-  if (blocks(64, 64) >= cus) return {2, 2, 2, 1};
-  const bool n96 = w->N % 96 == 0;
+  if (blocks(64, 64) >= cus || !split_ok) return {2, 2, 2, 1};
   const long b = n96 ? blocks(64, 96) : blocks(64, 64);
   int slices = 1;
   for (int k = 2; k <= kMaxSplitK; ++k)
@@ -601,20 +633,21 @@ GemmPlan plan_gemm(const g4_w4 *w, int rows, bool f32x) {
 }
 
 template <int NX>
-int launch_planned(const GemmPlan &pl, const g4_w4 *w, const uint4 *xt, const int *xe, int rows,
-                   int Mp, void *y, bool y_bf16, float *part) {
+int launch_planned(const GemmPlan &pl, const g4_w4 *const *w, int nw, const uint4 *xt,
+                   const int *xe, int rows, int Mp, void *const *y, bool y_bf16, float *part) {
   constexpr int P = 4;
   const int sl = pl.slices;
-  if (pl.ks == 1) return launch_gemm<2, 2, NX, 1, P>(w, xt, xe, rows, Mp, y, y_bf16, part, sl);
-  if (pl.tm == 4 && pl.tn == 4)
-    return launch_gemm<4, 4, NX, 2, P>(w, xt, xe, rows, Mp, y, y_bf16, part, sl);
+#define G4_GEMM_TILE(TM, TN, KS) \
+  return launch_gemm<TM, TN, NX, KS, P>(w, nw, xt, xe, rows, Mp, y, y_bf16, part, sl)
+  if (pl.ks == 1) G4_GEMM_TILE(2, 2, 1);
+  if (pl.tm == 4 && pl.tn == 4) G4_GEMM_TILE(4, 4, 2);
   if constexpr (NX == 1) {
-    if (pl.tm == 4 && pl.tn == 3)
-      return launch_gemm<4, 3, NX, 2, P>(w, xt, xe, rows, Mp, y, y_bf16, part, sl);
+    if (pl.tm == 4 && pl.tn == 3) G4_GEMM_TILE(4, 3, 2);
   }
-  if (pl.tn == 3) return launch_gemm<2, 3, NX, 2, P>(w, xt, xe, rows, Mp, y, y_bf16, part, sl);
-  if (pl.tn == 4) return launch_gemm<2, 4, NX, 2, P>(w, xt, xe, rows, Mp, y, y_bf16, part, sl);
-  return launch_gemm<2, 2, NX, 2, P>(w, xt, xe, rows, Mp, y, y_bf16, part, sl);
+  if (pl.tn == 3) G4_GEMM_TILE(2, 3, 2);
+  if (pl.tn == 4) G4_GEMM_TILE(2, 4, 2);
+  G4_GEMM_TILE(2, 2, 2);
+#undef G4_GEMM_TILE
 }
 
 // x' (and its low half) and the row exponents, reused by every later call.
@@ -624,25 +657,37 @@ Workspace g_ws;
 
 namespace g4 {
 
-int w4_gemm(const g4_w4 *w, const void *x, bool f32x, int rows, void *y, bool y_bf16) {
+int w4_gemm_multi(const g4_w4 *const *w, int nw, const void *x, bool f32x, int rows,
+                  void *const *y, bool y_bf16) {
+  // weights whose joint grid still leaves CUs idle run one by one (each may
+  // then split K)
+  const int cus = cu_count() > 0 ? cu_count() : 256;
+  long tiles64 = 0;
+  for (int i = 0; i < nw; ++i) tiles64 += (long)((rows + 63) / 64) * ((w[i]->N + 63) / 64);
+  if (nw > 1 && tiles64 < cus) {
+    for (int i = 0; i < nw; ++i)
+      if (int rc = w4_gemm_multi(w + i, 1, x, f32x, rows, y + i, y_bf16)) return rc;
+    return G4_OK;
+  }
+  const g4_w4 *w0 = w[0];
   const int Mp = (rows + kRowPad - 1) / kRowPad * kRowPad;
-  const size_t xt_bytes = (size_t)Mp * w->K * 2 * (f32x ? 2 : 1);  // FP16 x' (hi [+ lo])
+  const size_t xt_bytes = (size_t)Mp * w0->K * 2 * (f32x ? 2 : 1);  // FP16 x' (hi [+ lo])
   const size_t eoff = (xt_bytes + 255) & ~size_t(255);
   const size_t poff = (eoff + (size_t)rows * 4 + 255) & ~size_t(255);
-  const GemmPlan plan = plan_gemm(w, rows, f32x);
-  const size_t part_bytes = plan.slices > 1 ? plan.slices * splitk_pstride(rows, w->N) * 4 : 0;
+  const GemmPlan plan = plan_gemm(w, nw, rows, f32x);
+  const size_t part_bytes = plan.slices > 1 ? plan.slices * splitk_pstride(rows, w0->N) * 4 : 0;
   void *ws = nullptr;
   int rc = g_ws.get(poff + part_bytes, &ws, "g4_w4_linear (prefill)");
   if (rc) return rc;
   uint4 *xt = static_cast<uint4 *>(ws);
   int *xe = reinterpret_cast<int *>(static_cast<char *>(ws) + eoff);
   float *part = reinterpret_cast<float *>(static_cast<char *>(ws) + poff);
-  const int cpt = fused_prep_cpt(w->K, f32x);
+  const int cpt = fused_prep_cpt(w0->K, f32x);
   if (cpt) {
     const dim3 fgrid(Mp / kRowsFused);
 #define G4_PREP_FUSED(F, C)                                                                   \
   hipLaunchKernelGGL((gemm_xprep_fused_kernel<F, C>), fgrid, dim3(kThreads), 0, stream(), x, \
-                     rows, Mp, w->K, xe, xt)
+                     rows, Mp, w0->K, xe, xt)
     if (f32x) {
       switch (cpt) {
         case 2: G4_PREP_FUSED(true, 2); break;
@@ -662,25 +707,29 @@ int w4_gemm(const g4_w4 *w, const void *x, bool f32x, int rows, void *y, bool y_
     }
 #undef G4_PREP_FUSED
     G4_LAUNCH_CHECK("gemm_xprep_fused_kernel");
-    return f32x ? launch_planned<2>(plan, w, xt, xe, rows, Mp, y, y_bf16, part)
-                : launch_planned<1>(plan, w, xt, xe, rows, Mp, y, y_bf16, part);
+    return f32x ? launch_planned<2>(plan, w, nw, xt, xe, rows, Mp, y, y_bf16, part)
+                : launch_planned<1>(plan, w, nw, xt, xe, rows, Mp, y, y_bf16, part);
   }
   const dim3 egrid((rows + kThreads / 64 - 1) / (kThreads / 64));
-  const dim3 pgrid(Mp / kPrepTileM, (w->K / 8 + kPrepTileC - 1) / kPrepTileC);
+  const dim3 pgrid(Mp / kPrepTileM, (w0->K / 8 + kPrepTileC - 1) / kPrepTileC);
   if (f32x) {
-    hipLaunchKernelGGL(gemm_xexp_kernel<true>, egrid, dim3(kThreads), 0, stream(), x, rows, w->K,
+    hipLaunchKernelGGL(gemm_xexp_kernel<true>, egrid, dim3(kThreads), 0, stream(), x, rows, w0->K,
                        xe);
     hipLaunchKernelGGL(gemm_xprep_kernel<true>, pgrid, dim3(kThreads), 0, stream(), x, xe, rows,
-                       Mp, w->K, xt);
+                       Mp, w0->K, xt);
   } else {
     hipLaunchKernelGGL(gemm_xexp_kernel<false>, egrid, dim3(kThreads), 0, stream(), x, rows,
-                       w->K, xe);
+                       w0->K, xe);
     hipLaunchKernelGGL(gemm_xprep_kernel<false>, pgrid, dim3(kThreads), 0, stream(), x, xe, rows,
-                       Mp, w->K, xt);
+                       Mp, w0->K, xt);
   }
   G4_LAUNCH_CHECK("gemm_xprep_kernel");
-  return f32x ? launch_planned<2>(plan, w, xt, xe, rows, Mp, y, y_bf16, part)
-              : launch_planned<1>(plan, w, xt, xe, rows, Mp, y, y_bf16, part);
+  return f32x ? launch_planned<2>(plan, w, nw, xt, xe, rows, Mp, y, y_bf16, part)
+              : launch_planned<1>(plan, w, nw, xt, xe, rows, Mp, y, y_bf16, part);
+}
+
+int w4_gemm(const g4_w4 *w, const void *x, bool f32x, int rows, void *y, bool y_bf16) {
+  return w4_gemm_multi(&w, 1, x, f32x, rows, &y, y_bf16);
 }
 
 }  // namespace g4

@@ -126,6 +126,11 @@ struct g4_w4 {
 namespace g4 {
 // Prefill GEMM (rows >= 2): y[rows, N] = x[rows, K] . W^T, MFMA (g4_gemm.hip).
 int w4_gemm(const g4_w4 *w, const void *x, bool f32x, int rows, void *y, bool y_bf16);
+// nw (1..3) weights of one input dimension over the same x, y[i] receiving
+// weight i's output: one x pre-pass and, when their joint grid fills the CUs,
+// one GEMM launch.
+int w4_gemm_multi(const g4_w4 *const *w, int nw, const void *x, bool f32x, int rows,
+                  void *const *y, bool y_bf16);
 // Split-K decode GEMV of one FP32 row into per-slice partial sums
 // parts[K / 1536][N] (g4_w4.hip); returns the slice count, 0 if K does not
 // split (nothing launched), or minus a status.

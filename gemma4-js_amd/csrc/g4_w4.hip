@@ -837,7 +837,7 @@ G4_API int g4_w4_linear_multi(const g4_w4 *const *w, int n, const void *x, int x
       return fail(G4_E_ARG, "g4_w4_linear_multi: weight %d has in_dim %d, weight 0 has %d", i,
                   w[i]->K, w[0]->K);
   }
-  if (rows != 1 || n == 1) {
+  if (n == 1 || (rows > 1 && rows <= kMaxGemvRows)) {
     for (int i = 0; i < n; ++i)
       if (int rc = g4_w4_linear(w[i], x, x_dtype, rows, y[i], y_dtype)) return rc;
     return ok();
@@ -846,16 +846,23 @@ G4_API int g4_w4_linear_multi(const g4_w4 *const *w, int n, const void *x, int x
     return fail(G4_E_ARG, "g4_w4_linear_multi: bad x dtype %d", x_dtype);
   if (y_dtype != G4_F32 && y_dtype != G4_BF16)
     return fail(G4_E_ARG, "g4_w4_linear_multi: bad y dtype %d", y_dtype);
+  if (rows <= 0)
+    return fail(G4_E_ARG, "g4_w4_linear_multi: rows must be positive, got %d", rows);
   if (!aligned16(x)) return fail(G4_E_ARG, "g4_w4_linear_multi: x must be 16-byte aligned");
   const bool f32x = x_dtype == G4_F32;
   const size_t xe = f32x ? 4 : 2, ye = y_dtype == G4_F32 ? 4 : 2;
-  int rc = check_device_range(x, (size_t)w[0]->K * xe, "g4_w4_linear_multi x");
+  int rc = check_device_range(x, (size_t)rows * w[0]->K * xe, "g4_w4_linear_multi x");
   if (rc) return rc;
   for (int i = 0; i < n; ++i)
-    if ((rc = check_device_range(y[i], (size_t)w[i]->N * ye, "g4_w4_linear_multi y"))) return rc;
+    if ((rc = check_device_range(y[i], (size_t)rows * w[i]->N * ye, "g4_w4_linear_multi y")))
+      return rc;
   if (gemv_lds_per_row(w[0]->K, f32x) > kGemvLdsBudget)
     return fail(G4_E_ARG, "g4_w4_linear_multi: in_dim %d exceeds the GEMV staging limit (%s x)",
                 w[0]->K, f32x ? "FP32" : "BF16");
+  if (rows > 1) {  // more than kMaxGemvRows: one x pre-pass, one GEMM launch when it fills
+    rc = w4_gemm_multi(w, n, x, f32x, rows, y, y_dtype == G4_BF16);
+    return rc ? rc : ok();
+  }
   rc = f32x ? launch_gemv1_multi<true>(w, n, x, y, y_dtype == G4_BF16)
             : launch_gemv1_multi<false>(w, n, x, y, y_dtype == G4_BF16);
   return rc ? rc : ok();

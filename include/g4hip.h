@@ -150,8 +150,10 @@ int g4_w4_linear(const g4_w4 *w, const void *x, int x_dtype, int rows,
 /* Consecutive GPUOps.w4 dispatches over one input (gemma4-webgpu.js:225,
  * 237-238 for q/k/v and 280-281 for gate/up): y[i] = x * W[i]^T for i < n,
  * 1 <= n <= 3, every W[i] of the same in_dim, outputs as g4_w4_linear's.
- * For one activation row the n GEMVs run as one launch; otherwise each weight
- * takes g4_w4_linear.  The outputs must not overlap x or each other. */
+ * One activation row runs the n GEMVs as one launch; more than 4 rows share
+ * one activation pre-pass and, when the weights' tiles fill the GPU, one GEMM
+ * launch; 2-4 rows take g4_w4_linear per weight.  The outputs must not
+ * overlap x or each other. */
 int g4_w4_linear_multi(const g4_w4 *const *w, int n, const void *x, int x_dtype,
                        int rows, void *const *y, int y_dtype);
 

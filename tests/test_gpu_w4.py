@@ -277,6 +277,31 @@ def test_linear_multi_several_rows(g4, oracle, rows):
         assert rel_l2_rows(got, ref) <= TOL
 
 
+@pytest.mark.parametrize("shapes", [((2048, 1536), (256, 1536), (256, 1536)),
+                                    ((6144, 1536), (6144, 1536)),
+                                    ((1000, 2048), (70, 2048))])
+def test_linear_multi_prefill_gemm(g4, shapes):
+    # 512 FP32 rows, as the model's prefill: one x pre-pass and one GEMM launch
+    # over the weights' tiles; each output against the binary64 product, and
+    # a weight that plans the same tile alone gives identical bits.
+    rows, k = 512, shapes[0][1]
+    x = np.random.default_rng(31).standard_normal((rows, k)).astype(np.float32)
+    xb = g4.Buffer.from_array(x)
+    lins, refs = [], []
+    for i, (n, _) in enumerate(shapes):
+        packed, scales, q = syn.w4_weights(330 + i, n, k)
+        lins.append(g4.W4Linear(packed, scales))
+        refs.append(x.astype(np.float64) @ dense(q, scales).T)
+    ys = [g4.Buffer(rows * lin.out_dim * 4) for lin in lins]
+    g4.W4Linear.linear_multi(lins, xb.ptr, g4.F32, rows, [y.ptr for y in ys], g4.F32)
+    for lin, y, ref in zip(lins, ys, refs):
+        got = y.download(np.float32).reshape(rows, lin.out_dim)
+        assert rel_l2_rows(got, ref) <= 1e-5
+    if shapes[0][0] == 2048:  # q plans 64 x 64 tiles alone and with k, v
+        alone = run_linear(g4, lins[0], None, x, rows, g4.F32)
+        assert np.array_equal(ys[0].download(np.float32).reshape(rows, 2048), alone)
+
+
 def test_linear_multi_errors(g4):
     a = g4.W4Linear(*syn.w4_weights(320, 64, 512)[:2])
     b = g4.W4Linear(*syn.w4_weights(321, 64, 256)[:2])
