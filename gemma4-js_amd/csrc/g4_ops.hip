@@ -298,61 +298,139 @@ __global__ __launch_bounds__(256) void attn_rows_mfma_kernel(AttnArgs a) {
   __syncthreads();
 
   float *pw = ps[w];
-  for (int kt = kmin / 16 + w; kt <= kmax / 16; kt += kFaWaves) {
-    const int key0 = kt * 16;
-    // S = Q . K^T
-    const int kc = key0 + c < kmax ? key0 + c : kmax;
-    const float *kp = a.k + (size_t)kc * HD + 4 * g;
-    const float *qp = &qs[c * QS + 4 * g];
-    // four independent accumulators (dims 16j + 4g + i, i = 0..3), added
-    // pairwise: shorter rounding chains, and the MFMAs do not wait on each other
-    f32x4 sa[4];
+  if constexpr (HD <= 256) {
+    // The next key tile's K is loaded once this tile's scores are formed, its V
+    // once this tile's P.V is done: each load has a phase of work to land in
+    // (tile indices past the last re-read the last tile).
+    constexpr int NV = HD / 64;
+    const int kt_last = kmax / 16;
+    float4 kr[NT], vr[4][NV];
+    auto load_k = [&](int kt) {
+      kt = kt < kt_last ? kt : kt_last;
+      const int kc = kt * 16 + c < kmax ? kt * 16 + c : kmax;
+      const float *kp = a.k + (size_t)kc * HD + 4 * g;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) sa[i] = (f32x4){0.f, 0.f, 0.f, 0.f};
+      for (int j = 0; j < NT; ++j) kr[j] = *reinterpret_cast<const float4 *>(kp + 16 * j);
+    };
+    auto load_v = [&](int kt) {
+      kt = kt < kt_last ? kt : kt_last;
+#pragma unroll
+      for (int sp = 0; sp < 4; ++sp) {
+        const int kr2 = kt * 16 + 4 * sp + g < kmax ? kt * 16 + 4 * sp + g : kmax;
+        const float *vp = a.v + (size_t)kr2 * HD + 4 * c;
+#pragma unroll
+        for (int q = 0; q < NV; ++q) vr[sp][q] = *reinterpret_cast<const float4 *>(vp + 64 * q);
+      }
+    };
+    int kt = kmin / 16 + w;
+    load_k(kt);
+    load_v(kt);
+    for (; kt <= kt_last; kt += kFaWaves) {
+      const int key0 = kt * 16;
+      const float *qp = &qs[c * QS + 4 * g];
+      f32x4 sa[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) sa[i] = (f32x4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int j = 0; j < NT; ++j) {
+        const float4 kv = kr[j];
+        const float4 qv = *reinterpret_cast<const float4 *>(qp + 16 * j);
+        sa[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(qv.x, kv.x, sa[0], 0, 0, 0);
+        sa[1] = __builtin_amdgcn_mfma_f32_16x16x4f32(qv.y, kv.y, sa[1], 0, 0, 0);
+        sa[2] = __builtin_amdgcn_mfma_f32_16x16x4f32(qv.z, kv.z, sa[2], 0, 0, 0);
+        sa[3] = __builtin_amdgcn_mfma_f32_16x16x4f32(qv.w, kv.w, sa[3], 0, 0, 0);
+      }
+      load_k(kt + kFaWaves);
+      const f32x4 s = (sa[0] + sa[1]) + (sa[2] + sa[3]);
+      const int key = key0 + c;
+      float corr[4];
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const bool ok = rlive[v] && key <= rpos[v] && key < keylen &&
+                        (!a.sliding || key > rpos[v] - a.window);
+        const float tm = row16_reduce(ok ? s[v] : -1e30f, [](float x, float y) { return fmaxf(x, y); });
+        const float mn = fmaxf(m[v], tm);
+        corr[v] = expf(m[v] - mn);
+        const float p = ok ? expf(s[v] - mn) : 0.f;
+        l[v] = l[v] * corr[v] + row16_reduce(p, [](float x, float y) { return x + y; });
+        m[v] = mn;
+        pw[(4 * g + v) * kFaPStride + (c & 3) * 4 + (c >> 2)] = p;
+      }
+#pragma unroll
+      for (int n = 0; n < NT; ++n)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) o[n][v] *= corr[v];
+      const float4 pa = *reinterpret_cast<const float4 *>(&pw[c * kFaPStride + 4 * g]);
+      const float pv[4] = {pa.x, pa.y, pa.z, pa.w};
+#pragma unroll
+      for (int sp = 0; sp < 4; ++sp)
+#pragma unroll
+        for (int q = 0; q < NV; ++q) {
+          const float4 vv = vr[sp][q];
+          o[4 * q + 0] = __builtin_amdgcn_mfma_f32_16x16x4f32(pv[sp], vv.x, o[4 * q + 0], 0, 0, 0);
+          o[4 * q + 1] = __builtin_amdgcn_mfma_f32_16x16x4f32(pv[sp], vv.y, o[4 * q + 1], 0, 0, 0);
+          o[4 * q + 2] = __builtin_amdgcn_mfma_f32_16x16x4f32(pv[sp], vv.z, o[4 * q + 2], 0, 0, 0);
+          o[4 * q + 3] = __builtin_amdgcn_mfma_f32_16x16x4f32(pv[sp], vv.w, o[4 * q + 3], 0, 0, 0);
+        }
+      load_v(kt + kFaWaves);
+    }
+  } else {  // head dim 512: the prefetch registers would spill
+    for (int kt = kmin / 16 + w; kt <= kmax / 16; kt += kFaWaves) {
+      const int key0 = kt * 16;
+      // S = Q . K^T
+      const int kc = key0 + c < kmax ? key0 + c : kmax;
+      const float *kp = a.k + (size_t)kc * HD + 4 * g;
+      const float *qp = &qs[c * QS + 4 * g];
+      // four independent accumulators (dims 16j + 4g + i, i = 0..3), added
+      // pairwise: shorter rounding chains, and the MFMAs do not wait on each other
+      f32x4 sa[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) sa[i] = (f32x4){0.f, 0.f, 0.f, 0.f};
 #pragma unroll 8
-    for (int j = 0; j < NT; ++j) {
-      const float4 kv = *reinterpret_cast<const float4 *>(kp + 16 * j);
-      const float4 qv = *reinterpret_cast<const float4 *>(qp + 16 * j);
-      sa[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(qv.x, kv.x, sa[0], 0, 0, 0);
-      sa[1] = __builtin_amdgcn_mfma_f32_16x16x4f32(qv.y, kv.y, sa[1], 0, 0, 0);
-      sa[2] = __builtin_amdgcn_mfma_f32_16x16x4f32(qv.z, kv.z, sa[2], 0, 0, 0);
-      sa[3] = __builtin_amdgcn_mfma_f32_16x16x4f32(qv.w, kv.w, sa[3], 0, 0, 0);
-    }
-    const f32x4 s = (sa[0] + sa[1]) + (sa[2] + sa[3]);
-    // online softmax: lane (c, g) holds S[row 4g + v][key key0 + c]
-    const int key = key0 + c;
-    float corr[4];
+      for (int j = 0; j < NT; ++j) {
+        const float4 kv = *reinterpret_cast<const float4 *>(kp + 16 * j);
+        const float4 qv = *reinterpret_cast<const float4 *>(qp + 16 * j);
+        sa[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(qv.x, kv.x, sa[0], 0, 0, 0);
+        sa[1] = __builtin_amdgcn_mfma_f32_16x16x4f32(qv.y, kv.y, sa[1], 0, 0, 0);
+        sa[2] = __builtin_amdgcn_mfma_f32_16x16x4f32(qv.z, kv.z, sa[2], 0, 0, 0);
+        sa[3] = __builtin_amdgcn_mfma_f32_16x16x4f32(qv.w, kv.w, sa[3], 0, 0, 0);
+      }
+      const f32x4 s = (sa[0] + sa[1]) + (sa[2] + sa[3]);
+      // online softmax: lane (c, g) holds S[row 4g + v][key key0 + c]
+      const int key = key0 + c;
+      float corr[4];
 #pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      const bool ok = rlive[v] && key <= rpos[v] && key < keylen &&
-                      (!a.sliding || key > rpos[v] - a.window);
-      const float tm = row16_reduce(ok ? s[v] : -1e30f, [](float x, float y) { return fmaxf(x, y); });
-      const float mn = fmaxf(m[v], tm);
-      corr[v] = expf(m[v] - mn);
-      const float p = ok ? expf(s[v] - mn) : 0.f;
-      l[v] = l[v] * corr[v] + row16_reduce(p, [](float x, float y) { return x + y; });
-      m[v] = mn;
-      pw[(4 * g + v) * kFaPStride + (c & 3) * 4 + (c >> 2)] = p;
-    }
+      for (int v = 0; v < 4; ++v) {
+        const bool ok = rlive[v] && key <= rpos[v] && key < keylen &&
+                        (!a.sliding || key > rpos[v] - a.window);
+        const float tm = row16_reduce(ok ? s[v] : -1e30f, [](float x, float y) { return fmaxf(x, y); });
+        const float mn = fmaxf(m[v], tm);
+        corr[v] = expf(m[v] - mn);
+        const float p = ok ? expf(s[v] - mn) : 0.f;
+        l[v] = l[v] * corr[v] + row16_reduce(p, [](float x, float y) { return x + y; });
+        m[v] = mn;
+        pw[(4 * g + v) * kFaPStride + (c & 3) * 4 + (c >> 2)] = p;
+      }
 #pragma unroll
-    for (int n = 0; n < NT; ++n)
+      for (int n = 0; n < NT; ++n)
 #pragma unroll
-      for (int v = 0; v < 4; ++v) o[n][v] *= corr[v];
-    // P in the A layout: lane (c, g) holds P[row c][key 4 s + g], s = 0..3
-    const float4 pa = *reinterpret_cast<const float4 *>(&pw[c * kFaPStride + 4 * g]);
-    const float pv[4] = {pa.x, pa.y, pa.z, pa.w};
-    // O += P . V
+        for (int v = 0; v < 4; ++v) o[n][v] *= corr[v];
+      // P in the A layout: lane (c, g) holds P[row c][key 4 s + g], s = 0..3
+      const float4 pa = *reinterpret_cast<const float4 *>(&pw[c * kFaPStride + 4 * g]);
+      const float pv[4] = {pa.x, pa.y, pa.z, pa.w};
+      // O += P . V
 #pragma unroll
-    for (int sp = 0; sp < 4; ++sp) {
-      const int kr = key0 + 4 * sp + g < kmax ? key0 + 4 * sp + g : kmax;
-      const float *vp = a.v + (size_t)kr * HD + 4 * c;
+      for (int sp = 0; sp < 4; ++sp) {
+        const int kr = key0 + 4 * sp + g < kmax ? key0 + 4 * sp + g : kmax;
+        const float *vp = a.v + (size_t)kr * HD + 4 * c;
 #pragma unroll
-      for (int q = 0; q < HD / 64; ++q) {
-        const float4 vv = *reinterpret_cast<const float4 *>(vp + 64 * q);
-        o[4 * q + 0] = __builtin_amdgcn_mfma_f32_16x16x4f32(pv[sp], vv.x, o[4 * q + 0], 0, 0, 0);
-        o[4 * q + 1] = __builtin_amdgcn_mfma_f32_16x16x4f32(pv[sp], vv.y, o[4 * q + 1], 0, 0, 0);
-        o[4 * q + 2] = __builtin_amdgcn_mfma_f32_16x16x4f32(pv[sp], vv.z, o[4 * q + 2], 0, 0, 0);
-        o[4 * q + 3] = __builtin_amdgcn_mfma_f32_16x16x4f32(pv[sp], vv.w, o[4 * q + 3], 0, 0, 0);
+        for (int q = 0; q < HD / 64; ++q) {
+          const float4 vv = *reinterpret_cast<const float4 *>(vp + 64 * q);
+          o[4 * q + 0] = __builtin_amdgcn_mfma_f32_16x16x4f32(pv[sp], vv.x, o[4 * q + 0], 0, 0, 0);
+          o[4 * q + 1] = __builtin_amdgcn_mfma_f32_16x16x4f32(pv[sp], vv.y, o[4 * q + 1], 0, 0, 0);
+          o[4 * q + 2] = __builtin_amdgcn_mfma_f32_16x16x4f32(pv[sp], vv.z, o[4 * q + 2], 0, 0, 0);
+          o[4 * q + 3] = __builtin_amdgcn_mfma_f32_16x16x4f32(pv[sp], vv.w, o[4 * q + 3], 0, 0, 0);
+        }
       }
     }
   }
