@@ -268,6 +268,14 @@ int run_token(g4_gemma *m, bool graph) {
                            eps, 1, H, nullptr, m->last);
 }
 
+// y = x . W^T for prefill rows (FP32), a GEMM's K slices left unsummed for a
+// consumer that adds them; the GEMV path (up to kMaxGemvRows rows) writes y.
+int linear_parts(const g4_w4 *w, const float *x, int rows, float *y, GemmParts *p) {
+  if (rows > kMaxGemvRows) return w4_gemm_parts(w, x, rows, y, p);
+  *p = {y, 1, 0};
+  return g4_w4_linear(w, x, G4_F32, rows, y, G4_F32);
+}
+
 // Enqueue the forward of `rows` tokens whose ids are in m->ids and whose first
 // position is *m->pos; leaves the final-norm last row in m->last.
 int run_layers(g4_gemma *m, int rows, bool graph) {
@@ -320,17 +328,19 @@ int run_layers(g4_gemma *m, int rows, bool graph) {
     if ((rc = launch_attention(m->q, src.kc, src.vc, rows, c.heads, l.hd, keylen_host, 0, m->pos,
                                max_keylen, !l.full, c.window, kpw, m->part, m->ctx)))
       return rc;
-    if ((rc = g4_w4_linear(l.w[G4_PROJ_O], m->ctx, G4_F32, rows, m->attn, G4_F32))) return rc;
-    if ((rc = launch_norm_chain(m->attn, hid, l.norm[G4_NORM_POST_ATTN], l.norm[G4_NORM_PRE_FFW],
-                                1.f, eps, rows, H, m->ares, m->pf)))
+    GemmParts op;
+    if ((rc = linear_parts(l.w[G4_PROJ_O], m->ctx, rows, m->attn, &op))) return rc;
+    if ((rc = launch_norm_chain(op.parts, hid, l.norm[G4_NORM_POST_ATTN], l.norm[G4_NORM_PRE_FFW],
+                                1.f, eps, rows, H, m->ares, m->pf, op.n, op.stride)))
       return rc;
     const g4_w4 *gu[2] = {l.w[G4_PROJ_GATE], l.w[G4_PROJ_UP]};
     void *gu_out[2] = {m->gate, m->up};
     if ((rc = g4_w4_linear_multi(gu, 2, m->pf, G4_F32, rows, gu_out, G4_F32))) return rc;
     if ((rc = launch_gelu_mul(m->gate, m->up, (size_t)rows * l.inter, m->act))) return rc;
-    if ((rc = g4_w4_linear(l.w[G4_PROJ_DOWN], m->act, G4_F32, rows, m->down, G4_F32))) return rc;
-    if ((rc = launch_norm_chain(m->down, m->ares, l.norm[G4_NORM_POST_FFW], nullptr, 1.f, eps,
-                                rows, H, m->fres, nullptr)))
+    GemmParts dp;
+    if ((rc = linear_parts(l.w[G4_PROJ_DOWN], m->act, rows, m->down, &dp))) return rc;
+    if ((rc = launch_norm_chain(dp.parts, m->ares, l.norm[G4_NORM_POST_FFW], nullptr, 1.f, eps,
+                                rows, H, m->fres, nullptr, dp.n, dp.stride)))
       return rc;
     if ((rc = g4_w4_linear(l.w[G4_PROJ_PLE_GATE], m->fres, G4_F32, rows, m->pg, G4_F32)))
       return rc;

@@ -881,8 +881,10 @@ __global__ __launch_bounds__(256) void attn_rope_dec_kernel(AttnRopeArgs A) {
 
 // ---- standalone chain r = (h + rms(a) * w1) * c; x = rms(r) * w2 ------------
 // One block per row; writes r (if r_out) and x (if x_out; without x_out, r_out
-// is required and w2 is not read).
+// is required and w2 is not read).  a is the sum of a_parts planes a_stride
+// floats apart, added in order (a GEMM's K slices).
 __global__ __launch_bounds__(256) void norm_chain_kernel(const float *__restrict__ a,
+                                                         int a_parts, size_t a_stride,
                                                          const float *__restrict__ h,
                                                          const float *__restrict__ w1,
                                                          const float *__restrict__ w2, float c,
@@ -901,6 +903,7 @@ __global__ __launch_bounds__(256) void norm_chain_kernel(const float *__restrict
       int i = threadIdx.x + 256 * u;
       i = i < width ? i : width - 1;
       av[u] = a[off + i];
+      for (int s = 1; s < a_parts; ++s) av[u] += a[s * a_stride + off + i];
       hv[u] = h[off + i];
       w1v[u] = w1[i];
       w2v[u] = x_out ? w2[i] : 0.f;
@@ -933,19 +936,24 @@ __global__ __launch_bounds__(256) void norm_chain_kernel(const float *__restrict
     }
     return;
   }
+  auto a_at = [&](int i) {
+    float v = a[off + i];
+    for (int s = 1; s < a_parts; ++s) v += a[s * a_stride + off + i];
+    return v;
+  };
   float ss = 0.f;
-  for (int i = threadIdx.x; i < width; i += 256) ss += a[off + i] * a[off + i];
+  for (int i = threadIdx.x; i < width; i += 256) ss += a_at(i) * a_at(i);
   const float inv1 = 1.f / sqrtf(fblock_sum(ss, red, 4) / (float)width + eps);
   float ss2 = 0.f;
   for (int i = threadIdx.x; i < width; i += 256) {
-    const float r = (h[off + i] + a[off + i] * inv1 * w1[i]) * c;
+    const float r = (h[off + i] + a_at(i) * inv1 * w1[i]) * c;
     if (r_out) r_out[off + i] = r;
     ss2 += r * r;
   }
   if (!x_out) return;
   const float inv2 = 1.f / sqrtf(fblock_sum(ss2, red, 4) / (float)width + eps);
   for (int i = threadIdx.x; i < width; i += 256) {
-    const float r = (h[off + i] + a[off + i] * inv1 * w1[i]) * c;
+    const float r = (h[off + i] + a_at(i) * inv1 * w1[i]) * c;
     x_out[off + i] = r * inv2 * w2[i];
   }
 }
@@ -1110,10 +1118,11 @@ int launch_attn_rope_dec(const float *qraw, const float *kraw, const float *vraw
 }
 
 int launch_norm_chain(const float *a, const float *h, const float *w1, const float *w2, float c,
-                      float eps, int rows, int width, float *r_out, float *x_out) {
+                      float eps, int rows, int width, float *r_out, float *x_out, int a_parts,
+                      size_t a_stride) {
   if (rows == 0) return G4_OK;
-  hipLaunchKernelGGL(norm_chain_kernel, dim3(rows), dim3(256), 0, stream(), a, h, w1, w2, c, eps,
-                     width, r_out, x_out);
+  hipLaunchKernelGGL(norm_chain_kernel, dim3(rows), dim3(256), 0, stream(), a, a_parts, a_stride,
+                     h, w1, w2, c, eps, width, r_out, x_out);
   G4_LAUNCH_CHECK("norm_chain_kernel");
   return G4_OK;
 }

@@ -544,7 +544,7 @@ size_t splitk_pstride(int rows, int N) { return ((size_t)rows * N + 63) & ~size_
 // i's output; a K split (slices > 1) takes one weight.
 template <int TM, int TN, int NX, int KS, int P>
 int launch_gemm(const g4_w4 *const *w, int nw, const uint4 *xt, const int *xe, int rows, int Mp,
-                void *const *ys, bool y_bf16, float *part, int slices) {
+                void *const *ys, bool y_bf16, float *part, int slices, bool sum) {
   constexpr int BM = 32 * TM, BN = 32 * TN;
   if (Mp % BM != 0 || w[0]->G % (KS * slices) != 0 || (slices > 1 && nw != 1))
     return fail(G4_E_ARG, "w4_gemm: tile %dx%d (KS %d, %d slices) does not fit rows %d, K %d",
@@ -568,7 +568,7 @@ int launch_gemm(const g4_w4 *const *w, int nw, const uint4 *xt, const int *xe, i
                      reinterpret_cast<const u32x4 *>(xt), xe, sg, (int)y_bf16, rows, Mp,
                      w[0]->K, xcd_map, part, pstride);
   G4_LAUNCH_CHECK("w4_gemm_kernel");
-  if (slices > 1) {
+  if (slices > 1 && sum) {
     void *y = ys[0];
     const size_t n = (size_t)rows * w[0]->N;
     const bool vec = n % 4 == 0 && (reinterpret_cast<uintptr_t>(y) & 15u) == 0;
@@ -636,11 +636,12 @@ GemmPlan plan_gemm(const g4_w4 *const *w, int nw, int rows, bool f32x) {
 
 template <int NX>
 int launch_planned(const GemmPlan &pl, const g4_w4 *const *w, int nw, const uint4 *xt,
-                   const int *xe, int rows, int Mp, void *const *y, bool y_bf16, float *part) {
+                   const int *xe, int rows, int Mp, void *const *y, bool y_bf16, float *part,
+                   bool sum) {
   constexpr int P = 4;
   const int sl = pl.slices;
 #define G4_GEMM_TILE(TM, TN, KS) \
-  return launch_gemm<TM, TN, NX, KS, P>(w, nw, xt, xe, rows, Mp, y, y_bf16, part, sl)
+  return launch_gemm<TM, TN, NX, KS, P>(w, nw, xt, xe, rows, Mp, y, y_bf16, part, sl, sum)
   if (pl.ks == 1) G4_GEMM_TILE(2, 2, 1);
   if (pl.tm == 4 && pl.tn == 4) G4_GEMM_TILE(4, 4, 2);
   if constexpr (NX == 1) {
@@ -659,8 +660,10 @@ Workspace g_ws;
 
 namespace g4 {
 
-int w4_gemm_multi(const g4_w4 *const *w, int nw, const void *x, bool f32x, int rows,
-                  void *const *y, bool y_bf16) {
+// keep: when set and the plan splits K, the partial planes are left for the
+// caller to add (keep->parts, ->n, ->stride) instead of summed into y.
+static int gemm_run(const g4_w4 *const *w, int nw, const void *x, bool f32x, int rows,
+                    void *const *y, bool y_bf16, GemmParts *keep) {
   // weights whose joint grid still leaves CUs idle run one by one (each may
   // then split K)
   const int cus = cu_count() > 0 ? cu_count() : 256;
@@ -668,7 +671,7 @@ int w4_gemm_multi(const g4_w4 *const *w, int nw, const void *x, bool f32x, int r
   for (int i = 0; i < nw; ++i) tiles64 += (long)((rows + 63) / 64) * ((w[i]->N + 63) / 64);
   if (nw > 1 && tiles64 < cus) {
     for (int i = 0; i < nw; ++i)
-      if (int rc = w4_gemm_multi(w + i, 1, x, f32x, rows, y + i, y_bf16)) return rc;
+      if (int rc = gemm_run(w + i, 1, x, f32x, rows, y + i, y_bf16, nullptr)) return rc;
     return G4_OK;
   }
   const g4_w4 *w0 = w[0];
@@ -684,6 +687,12 @@ int w4_gemm_multi(const g4_w4 *const *w, int nw, const void *x, bool f32x, int r
   uint4 *xt = static_cast<uint4 *>(ws);
   int *xe = reinterpret_cast<int *>(static_cast<char *>(ws) + eoff);
   float *part = reinterpret_cast<float *>(static_cast<char *>(ws) + poff);
+  const bool sum = !keep || plan.slices == 1;
+  if (keep) {
+    keep->parts = sum ? static_cast<const float *>(y[0]) : part;
+    keep->n = sum ? 1 : plan.slices;
+    keep->stride = splitk_pstride(rows, w0->N);
+  }
   const int cpt = fused_prep_cpt(w0->K, f32x);
   if (cpt) {
     const dim3 fgrid(Mp / kRowsFused);
@@ -709,8 +718,8 @@ int w4_gemm_multi(const g4_w4 *const *w, int nw, const void *x, bool f32x, int r
     }
 #undef G4_PREP_FUSED
     G4_LAUNCH_CHECK("gemm_xprep_fused_kernel");
-    return f32x ? launch_planned<2>(plan, w, nw, xt, xe, rows, Mp, y, y_bf16, part)
-                : launch_planned<1>(plan, w, nw, xt, xe, rows, Mp, y, y_bf16, part);
+    return f32x ? launch_planned<2>(plan, w, nw, xt, xe, rows, Mp, y, y_bf16, part, sum)
+                : launch_planned<1>(plan, w, nw, xt, xe, rows, Mp, y, y_bf16, part, sum);
   }
   const dim3 egrid((rows + kThreads / 64 - 1) / (kThreads / 64));
   const dim3 pgrid(Mp / kPrepTileM, (w0->K / 8 + kPrepTileC - 1) / kPrepTileC);
@@ -726,12 +735,22 @@ int w4_gemm_multi(const g4_w4 *const *w, int nw, const void *x, bool f32x, int r
                        Mp, w0->K, xt);
   }
   G4_LAUNCH_CHECK("gemm_xprep_kernel");
-  return f32x ? launch_planned<2>(plan, w, nw, xt, xe, rows, Mp, y, y_bf16, part)
-              : launch_planned<1>(plan, w, nw, xt, xe, rows, Mp, y, y_bf16, part);
+  return f32x ? launch_planned<2>(plan, w, nw, xt, xe, rows, Mp, y, y_bf16, part, sum)
+              : launch_planned<1>(plan, w, nw, xt, xe, rows, Mp, y, y_bf16, part, sum);
+}
+
+int w4_gemm_multi(const g4_w4 *const *w, int nw, const void *x, bool f32x, int rows,
+                  void *const *y, bool y_bf16) {
+  return gemm_run(w, nw, x, f32x, rows, y, y_bf16, nullptr);
 }
 
 int w4_gemm(const g4_w4 *w, const void *x, bool f32x, int rows, void *y, bool y_bf16) {
-  return w4_gemm_multi(&w, 1, x, f32x, rows, &y, y_bf16);
+  return gemm_run(&w, 1, x, f32x, rows, &y, y_bf16, nullptr);
+}
+
+int w4_gemm_parts(const g4_w4 *w, const float *x, int rows, float *y, GemmParts *out) {
+  void *yv = y;
+  return gemm_run(&w, 1, x, true, rows, &yv, false, out);
 }
 
 }  // namespace g4

@@ -124,13 +124,27 @@ struct g4_w4 {
 };
 
 namespace g4 {
-// Prefill GEMM (rows >= 2): y[rows, N] = x[rows, K] . W^T, MFMA (g4_gemm.hip).
+// Activation rows up to which g4_w4_linear streams the weights (GEMV); more
+// rows take the MFMA GEMM.
+constexpr int kMaxGemvRows = 4;
+// Prefill GEMM (more than kMaxGemvRows rows): y[rows, N] = x[rows, K] . W^T on
+// the matrix cores (g4_gemm.hip).
 int w4_gemm(const g4_w4 *w, const void *x, bool f32x, int rows, void *y, bool y_bf16);
 // nw (1..3) weights of one input dimension over the same x, y[i] receiving
 // weight i's output: one x pre-pass and, when their joint grid fills the CUs,
 // one GEMM launch.
 int w4_gemm_multi(const g4_w4 *const *w, int nw, const void *x, bool f32x, int rows,
                   void *const *y, bool y_bf16);
+// FP32 rows >= 2 (more than the GEMV's row count) whose consumer adds the K
+// slices itself: y = x . W^T as out->n partial planes out->parts + s *
+// out->stride (s < n, added in order), or in y itself (n = 1).  The planes
+// live in the GEMM scratch until the next GEMM call on the stream.
+struct GemmParts {
+  const float *parts;
+  int n;
+  size_t stride;
+};
+int w4_gemm_parts(const g4_w4 *w, const float *x, int rows, float *y, GemmParts *out);
 // Split-K decode GEMV of one FP32 row into per-slice partial sums
 // parts[K / 1536][N] (g4_w4.hip); returns the slice count, 0 if K does not
 // split (nothing launched), or minus a status.

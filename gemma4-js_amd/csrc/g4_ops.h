@@ -46,8 +46,11 @@ int fused_res_linear_gelu_mul(const float *a, int a_parts, const float *h, const
 int launch_rope_qkv(const float *qraw, const float *kraw, const float *vraw, int heads, int hd,
                     const int *pos_dev, const float *qnorm, const float *knorm, int rope_angles,
                     float base, float eps, float *q, float *kc, float *vc, bool own_kv);
+// r = (h + rms(a) * w1) * c; x = rms(r) * w2 (x_out optional), a the sum of
+// a_parts planes a_stride floats apart.
 int launch_norm_chain(const float *a, const float *h, const float *w1, const float *w2, float c,
-                      float eps, int rows, int width, float *r_out, float *x_out);
+                      float eps, int rows, int width, float *r_out, float *x_out,
+                      int a_parts = 1, size_t a_stride = 0);
 
 // RoPE (cos, sin) tables of the current position for up to kRopeSlots
 // (base, head_dim, angles) variants, kRopeTable entries each.

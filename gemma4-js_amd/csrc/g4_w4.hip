@@ -88,8 +88,6 @@ __device__ __forceinline__ void stage_group(const void *__restrict__ xrow, int g
   sx[g] = kPairBias * sum;
 }
 
-constexpr int kMaxGemvRows = 4;
-
 // B: groups per lane whose loads are issued together (divides G / L).
 // M: rows of x (1..4), uniform.
 template <int L, int B, bool F32X>
