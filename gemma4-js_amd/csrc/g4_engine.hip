@@ -333,10 +333,14 @@ int run_layers(g4_gemma *m, int rows, bool graph) {
     if ((rc = launch_norm_chain(op.parts, hid, l.norm[G4_NORM_POST_ATTN], l.norm[G4_NORM_PRE_FFW],
                                 1.f, eps, rows, H, m->ares, m->pf, op.n, op.stride)))
       return rc;
-    const g4_w4 *gu[2] = {l.w[G4_PROJ_GATE], l.w[G4_PROJ_UP]};
-    void *gu_out[2] = {m->gate, m->up};
-    if ((rc = g4_w4_linear_multi(gu, 2, m->pf, G4_F32, rows, gu_out, G4_F32))) return rc;
-    if ((rc = launch_gelu_mul(m->gate, m->up, (size_t)rows * l.inter, m->act))) return rc;
+    if (rows > kMaxGemvRows) {  // gate, up and gelu(gate) * up in one GEMM launch
+      if ((rc = w4_gemm_glu(l.w[G4_PROJ_GATE], l.w[G4_PROJ_UP], m->pf, rows, m->act))) return rc;
+    } else {
+      const g4_w4 *gu[2] = {l.w[G4_PROJ_GATE], l.w[G4_PROJ_UP]};
+      void *gu_out[2] = {m->gate, m->up};
+      if ((rc = g4_w4_linear_multi(gu, 2, m->pf, G4_F32, rows, gu_out, G4_F32))) return rc;
+      if ((rc = launch_gelu_mul(m->gate, m->up, (size_t)rows * l.inter, m->act))) return rc;
+    }
     GemmParts dp;
     if ((rc = linear_parts(l.w[G4_PROJ_DOWN], m->act, rows, m->down, &dp))) return rc;
     if ((rc = launch_norm_chain(dp.parts, m->ares, l.norm[G4_NORM_POST_FFW], nullptr, 1.f, eps,

@@ -36,6 +36,7 @@
 // operand touch consecutive addresses.
 #include <math.h>
 
+#include "g4_gemv.h"
 #include "g4_internal.h"
 
 namespace {
@@ -282,6 +283,10 @@ __device__ __forceinline__ uint32_t deq_pair(uint32_t w, int t, f16x2 s2) {
 // slices are then added in order by gemm_splitk_sum_kernel.
 // Weights of one input dimension over the same x' in one launch: the n tiles
 // of weight i are t0[i] .. t0[i + 1] - 1 of the grid's tile axis.
+//
+// glu: weights 0 and 1 are gate and up of one width N; n tile j covers
+// columns [j BN/2, (j + 1) BN/2) of both (gate in the first half of the tile,
+// up in the second), and the block writes y[0] = gelu(gate) * up (FP32).
 constexpr int kMaxGemmSegs = 3;
 struct GemmSegs {
   const u32x4 *wq[kMaxGemmSegs];
@@ -289,7 +294,7 @@ struct GemmSegs {
   void *y[kMaxGemmSegs];
   int N[kMaxGemmSegs], shift[kMaxGemmSegs];
   int t0[kMaxGemmSegs + 1];
-  int n;
+  int n, glu;
 };
 
 template <int TM, int TN, int NX, int KS, int P, bool FLAT>
@@ -317,7 +322,9 @@ __global__ __launch_bounds__(kThreads, 2) void w4_gemm_kernel(
   // block -> (m tile, n tile); with xcd_map, all n tiles of one m band run on
   // one XCD (blocks are dealt to the 8 XCDs round-robin), so its L2 holds
   // that band of x' for every one of them.
-  const int nn = SG.t0[SG.n];
+  const bool glu = SG.glu != 0;
+  constexpr int HALF = BN / 2;  // glu: gate and up columns per tile
+  const int nn = glu ? (SG.N[0] + HALF - 1) / HALF : SG.t0[SG.n];
   int mt, ntile;
   if (xcd_map) {
     const int b = blockIdx.x, xcd = b & 7, j = b >> 3;
@@ -327,12 +334,12 @@ __global__ __launch_bounds__(kThreads, 2) void w4_gemm_kernel(
     mt = blockIdx.x / nn;
     ntile = blockIdx.x - mt * nn;
   }
-  const int si = SG.n > 2 && ntile >= SG.t0[2] ? 2 : SG.n > 1 && ntile >= SG.t0[1] ? 1 : 0;
+  const int si = glu ? 0 : SG.n > 2 && ntile >= SG.t0[2] ? 2 : SG.n > 1 && ntile >= SG.t0[1] ? 1 : 0;
   const u32x4 *__restrict__ wq = SG.wq[si];
   const uint16_t *__restrict__ ws = SG.ws[si];
   void *__restrict__ y = SG.y[si];
   const int N = SG.N[si], shift = SG.shift[si];
-  const int m0 = mt * BM, n0 = (ntile - SG.t0[si]) * BN;
+  const int m0 = mt * BM, n0 = glu ? ntile * HALF : (ntile - SG.t0[si]) * BN;
 
   // A: entry i of this thread is chunk a_c[i] of tile row a_row[i]
   const size_t a_stage = (size_t)KC * Mp;  // xt entries per stage
@@ -353,15 +360,19 @@ __global__ __launch_bounds__(kThreads, 2) void w4_gemm_kernel(
   constexpr int SW = KS % 2 == 0 ? 2 : 1;  // scales per scale load
   const u32x4 *b_src[BE];
   const uint16_t *s_src[BE];
+  int b_shift[BE];
 #pragma unroll
   for (int i = 0; i < BE; ++i) {
     const int idx = t + i * kThreads;
     const bool live = idx < BG;  // idle entries load group 0 of row n0 into the pad row
     b_row[i] = live ? idx / KS : BN;
     b_kk[i] = live ? idx % KS : 0;
-    const int gn = !live ? n0 : n0 + b_row[i] < N ? n0 + b_row[i] : N - 1;
-    b_src[i] = wq + (size_t)gn * G + st0_slice * KS + b_kk[i];
-    s_src[i] = ws + (size_t)gn * G + st0_slice * KS + (b_kk[i] & ~(SW - 1));
+    const int up = glu && live && b_row[i] >= HALF;  // glu: the tile's up half
+    const int rn = live ? b_row[i] - up * HALF : 0;
+    const int gn = n0 + rn < N ? n0 + rn : N - 1;
+    b_src[i] = (up ? SG.wq[1] : wq) + (size_t)gn * G + st0_slice * KS + b_kk[i];
+    s_src[i] = (up ? SG.ws[1] : ws) + (size_t)gn * G + st0_slice * KS + (b_kk[i] & ~(SW - 1));
+    b_shift[i] = up ? SG.shift[1] : shift;
   }
 
   // Ring of P register slots: stage j is loaded into slot j % P, P - 1
@@ -394,7 +405,7 @@ __global__ __launch_bounds__(kThreads, 2) void w4_gemm_kernel(
 #pragma unroll
     for (int i = 0; i < BE; ++i) {
       const uint32_t sbits = SW == 2 && (b_kk[i] & 1) ? rs[slot][i] >> 16 : rs[slot][i] & 0xffffu;
-      const _Float16 sh = (_Float16)ldexpf(bf16_to_f32(sbits), shift);
+      const _Float16 sh = (_Float16)ldexpf(bf16_to_f32(sbits), b_shift[i]);
       const f16x2 s2 = {sh, sh};
       const u32x4 w = rb[slot][i];
 #pragma unroll
@@ -500,7 +511,46 @@ __global__ __launch_bounds__(kThreads, 2) void w4_gemm_kernel(
       }
     }
   };
-  if (gridDim.y > 1)
+  if (glu) {
+    // waves wn = 1 hold the up values of the positions waves wn = 0 hold the
+    // gate values of (same lane and register): they pass them through the
+    // A tile's LDS, free after the last stage's barrier
+    constexpr int NE = TM * TN * 4;  // accumulator floats per lane
+    static_assert(2 * NE * 64 * sizeof(float) <= sizeof(As), "up values must fit the A tile");
+    float *upv = reinterpret_cast<float *>(&As[0][0][0][0]);
+    if (wn == 1) {
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int m = m0 + wm * 16 * TM + i * 16 + 4 * lc + r;
+          const int sc = (m < M ? xe[m] : 0) - SG.shift[1];
+#pragma unroll
+          for (int j = 0; j < TN; ++j)
+            upv[(wm * NE + (i * TN + j) * 4 + r) * 64 + lane] = ldexpf(acc[i][j][r], sc);
+        }
+    }
+    __syncthreads();
+    if (wn == 0) {
+      float *out = static_cast<float *>(y);
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int m = m0 + wm * 16 * TM + i * 16 + 4 * lc + r;
+          if (m >= M) continue;
+          const int sc = xe[m] - shift;
+#pragma unroll
+          for (int j = 0; j < TN; ++j) {
+            const int n = n0 + j * 16 + lr;
+            if (n >= N) continue;
+            const float g = ldexpf(acc[i][j][r], sc);
+            out[(size_t)m * N + n] = gelu_tanh(g) * upv[(wm * NE + (i * TN + j) * 4 + r) * 64 + lane];
+          }
+        }
+      }
+    }
+  } else if (gridDim.y > 1)
     epilogue(part + blockIdx.y * pstride);
   else if (y_bf16)
     epilogue(static_cast<uint16_t *>(y));
@@ -544,7 +594,7 @@ size_t splitk_pstride(int rows, int N) { return ((size_t)rows * N + 63) & ~size_
 // i's output; a K split (slices > 1) takes one weight.
 template <int TM, int TN, int NX, int KS, int P>
 int launch_gemm(const g4_w4 *const *w, int nw, const uint4 *xt, const int *xe, int rows, int Mp,
-                void *const *ys, bool y_bf16, float *part, int slices, bool sum) {
+                void *const *ys, bool y_bf16, float *part, int slices, bool sum, bool glu) {
   constexpr int BM = 32 * TM, BN = 32 * TN;
   if (Mp % BM != 0 || w[0]->G % (KS * slices) != 0 || (slices > 1 && nw != 1))
     return fail(G4_E_ARG, "w4_gemm: tile %dx%d (KS %d, %d slices) does not fit rows %d, K %d",
@@ -559,7 +609,9 @@ int launch_gemm(const g4_w4 *const *w, int nw, const uint4 *xt, const int *xe, i
     sg.shift[i] = w[i]->shift;
     sg.t0[i + 1] = sg.t0[i] + (w[i]->N + BN - 1) / BN;
   }
-  const int nm = (rows + BM - 1) / BM, nn = sg.t0[nw];
+  sg.glu = glu;
+  const int nm = (rows + BM - 1) / BM;
+  const int nn = glu ? (w[0]->N + BN / 2 - 1) / (BN / 2) : sg.t0[nw];
   const int xcd_map = nm % 8 == 0;
   const bool flat = P % 2 == 0 && (w[0]->G / KS / slices) % P == 0;
   const size_t pstride = splitk_pstride(rows, w[0]->N);
@@ -637,11 +689,11 @@ GemmPlan plan_gemm(const g4_w4 *const *w, int nw, int rows, bool f32x) {
 template <int NX>
 int launch_planned(const GemmPlan &pl, const g4_w4 *const *w, int nw, const uint4 *xt,
                    const int *xe, int rows, int Mp, void *const *y, bool y_bf16, float *part,
-                   bool sum) {
+                   bool sum, bool glu) {
   constexpr int P = 4;
   const int sl = pl.slices;
 #define G4_GEMM_TILE(TM, TN, KS) \
-  return launch_gemm<TM, TN, NX, KS, P>(w, nw, xt, xe, rows, Mp, y, y_bf16, part, sl, sum)
+  return launch_gemm<TM, TN, NX, KS, P>(w, nw, xt, xe, rows, Mp, y, y_bf16, part, sl, sum, glu)
   if (pl.ks == 1) G4_GEMM_TILE(2, 2, 1);
   if (pl.tm == 4 && pl.tn == 4) G4_GEMM_TILE(4, 4, 2);
   if constexpr (NX == 1) {
@@ -663,13 +715,13 @@ namespace g4 {
 // keep: when set and the plan splits K, the partial planes are left for the
 // caller to add (keep->parts, ->n, ->stride) instead of summed into y.
 static int gemm_run(const g4_w4 *const *w, int nw, const void *x, bool f32x, int rows,
-                    void *const *y, bool y_bf16, GemmParts *keep) {
+                    void *const *y, bool y_bf16, GemmParts *keep, bool glu = false) {
   // weights whose joint grid still leaves CUs idle run one by one (each may
   // then split K)
   const int cus = cu_count() > 0 ? cu_count() : 256;
   long tiles64 = 0;
   for (int i = 0; i < nw; ++i) tiles64 += (long)((rows + 63) / 64) * ((w[i]->N + 63) / 64);
-  if (nw > 1 && tiles64 < cus) {
+  if (nw > 1 && tiles64 < cus && !glu) {
     for (int i = 0; i < nw; ++i)
       if (int rc = gemm_run(w + i, 1, x, f32x, rows, y + i, y_bf16, nullptr)) return rc;
     return G4_OK;
@@ -718,8 +770,8 @@ static int gemm_run(const g4_w4 *const *w, int nw, const void *x, bool f32x, int
     }
 #undef G4_PREP_FUSED
     G4_LAUNCH_CHECK("gemm_xprep_fused_kernel");
-    return f32x ? launch_planned<2>(plan, w, nw, xt, xe, rows, Mp, y, y_bf16, part, sum)
-                : launch_planned<1>(plan, w, nw, xt, xe, rows, Mp, y, y_bf16, part, sum);
+    return f32x ? launch_planned<2>(plan, w, nw, xt, xe, rows, Mp, y, y_bf16, part, sum, glu)
+                : launch_planned<1>(plan, w, nw, xt, xe, rows, Mp, y, y_bf16, part, sum, glu);
   }
   const dim3 egrid((rows + kThreads / 64 - 1) / (kThreads / 64));
   const dim3 pgrid(Mp / kPrepTileM, (w0->K / 8 + kPrepTileC - 1) / kPrepTileC);
@@ -735,8 +787,8 @@ static int gemm_run(const g4_w4 *const *w, int nw, const void *x, bool f32x, int
                        Mp, w0->K, xt);
   }
   G4_LAUNCH_CHECK("gemm_xprep_kernel");
-  return f32x ? launch_planned<2>(plan, w, nw, xt, xe, rows, Mp, y, y_bf16, part, sum)
-              : launch_planned<1>(plan, w, nw, xt, xe, rows, Mp, y, y_bf16, part, sum);
+  return f32x ? launch_planned<2>(plan, w, nw, xt, xe, rows, Mp, y, y_bf16, part, sum, glu)
+              : launch_planned<1>(plan, w, nw, xt, xe, rows, Mp, y, y_bf16, part, sum, glu);
 }
 
 int w4_gemm_multi(const g4_w4 *const *w, int nw, const void *x, bool f32x, int rows,
@@ -746,6 +798,15 @@ int w4_gemm_multi(const g4_w4 *const *w, int nw, const void *x, bool f32x, int r
 
 int w4_gemm(const g4_w4 *w, const void *x, bool f32x, int rows, void *y, bool y_bf16) {
   return gemm_run(&w, 1, x, f32x, rows, &y, y_bf16, nullptr);
+}
+
+int w4_gemm_glu(const g4_w4 *gate, const g4_w4 *up, const float *x, int rows, float *act) {
+  if (gate->N != up->N || gate->K != up->K)
+    return fail(G4_E_ARG, "w4_gemm_glu: gate [%d, %d] and up [%d, %d] differ", gate->N, gate->K,
+                up->N, up->K);
+  const g4_w4 *w[2] = {gate, up};
+  void *y[2] = {act, nullptr};
+  return gemm_run(w, 2, x, true, rows, y, false, nullptr, true);
 }
 
 int w4_gemm_parts(const g4_w4 *w, const float *x, int rows, float *y, GemmParts *out) {

@@ -145,6 +145,10 @@ struct GemmParts {
   size_t stride;
 };
 int w4_gemm_parts(const g4_w4 *w, const float *x, int rows, float *y, GemmParts *out);
+// FP32 rows (more than kMaxGemvRows): act = gelu(x . Wg^T) * (x . Wu^T) in one
+// launch, each tile holding the same columns of gate and up (the GEMM outputs
+// and the product as GELU_MUL computes them).
+int w4_gemm_glu(const g4_w4 *gate, const g4_w4 *up, const float *x, int rows, float *act);
 // Split-K decode GEMV of one FP32 row into per-slice partial sums
 // parts[K / 1536][N] (g4_w4.hip); returns the slice count, 0 if K does not
 // split (nothing launched), or minus a status.
