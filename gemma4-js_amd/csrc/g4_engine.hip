@@ -302,8 +302,15 @@ int run_layers(g4_gemma *m, int rows, bool graph) {
   // launch: post-attention norm + residual + pre-FFN norm; post-FFN norm +
   // residual; post-PLE norm + residual + layer scalar + the next layer's
   // input norm (so only layer 0 runs its input norm alone).
+  //
+  // With the GEMM path (more than kMaxGemvRows rows) the chains whose output
+  // feeds a GEMM (q/k/v, gate/up, PLE gate) also write it as the GEMM's x'
+  // (launch_norm_chain_xprep after w4_gemm_prepare), so those GEMMs skip
+  // their x pre-pass.
+  const bool gemm = rows > kMaxGemvRows;
   if ((rc = launch_rms(m->h[0], rows, H, m->L[0].norm[G4_NORM_INPUT], eps, m->pre, nullptr)))
     return rc;
+  bool pre_prepped = false;  // x' of m->pre already in the GEMM's prepared scratch
   for (int i = 0; i < NL; ++i) {
     const Layer &l = m->L[i];
     float *hid = m->h[cur], *out = m->h[cur ^ 1];
@@ -311,9 +318,12 @@ int run_layers(g4_gemma *m, int rows, bool graph) {
     // q, and k/v for a layer with its own cache, from one pre-pass and launch
     const g4_w4 *qkv[3] = {l.w[G4_PROJ_Q], l.w[G4_PROJ_K], l.w[G4_PROJ_V]};
     void *qkv_out[3] = {m->qraw, m->kraw, m->vraw};
-    if ((rc = g4_w4_linear_multi(qkv, l.kv_src < 0 ? 3 : 1, m->pre, G4_F32, rows, qkv_out,
-                                 G4_F32)))
-      return rc;
+    const int nqkv = l.kv_src < 0 ? 3 : 1;
+    if (pre_prepped)
+      rc = w4_gemm_multi(qkv, nqkv, nullptr, true, rows, qkv_out, false);
+    else
+      rc = g4_w4_linear_multi(qkv, nqkv, m->pre, G4_F32, rows, qkv_out, G4_F32);
+    if (rc) return rc;
     if ((rc = launch_norm_rope(m->qraw, rows, c.heads, l.hd, 0, m->pos, l.norm[G4_NORM_Q],
                                l.rope_angles, l.rope_base, eps, m->q, false)))
       return rc;
@@ -330,32 +340,60 @@ int run_layers(g4_gemma *m, int rows, bool graph) {
       return rc;
     GemmParts op;
     if ((rc = linear_parts(l.w[G4_PROJ_O], m->ctx, rows, m->attn, &op))) return rc;
-    if ((rc = launch_norm_chain(op.parts, hid, l.norm[G4_NORM_POST_ATTN], l.norm[G4_NORM_PRE_FFW],
-                                1.f, eps, rows, H, m->ares, m->pf, op.n, op.stride)))
-      return rc;
-    if (rows > kMaxGemvRows) {  // gate, up and gelu(gate) * up in one GEMM launch
-      if ((rc = w4_gemm_glu(l.w[G4_PROJ_GATE], l.w[G4_PROJ_UP], m->pf, rows, m->act))) return rc;
+    const g4_w4 *gu[2] = {l.w[G4_PROJ_GATE], l.w[G4_PROJ_UP]};
+    if (gemm) {  // gate, up and gelu(gate) * up in one GEMM launch on the chain's x'
+      GemmXPrep xp;
+      if ((rc = w4_gemm_prepare(gu, 2, rows, &xp))) return rc;
+      if ((rc = launch_norm_chain_xprep(op.parts, op.n, op.stride, hid,
+                                        l.norm[G4_NORM_POST_ATTN], l.norm[G4_NORM_PRE_FFW], 1.f,
+                                        eps, rows, H, m->ares, nullptr, xp.xt, xp.xe, xp.Mp)))
+        return rc;
+      if ((rc = w4_gemm_glu(gu[0], gu[1], nullptr, rows, m->act))) return rc;
     } else {
-      const g4_w4 *gu[2] = {l.w[G4_PROJ_GATE], l.w[G4_PROJ_UP]};
+      if ((rc = launch_norm_chain(op.parts, hid, l.norm[G4_NORM_POST_ATTN],
+                                  l.norm[G4_NORM_PRE_FFW], 1.f, eps, rows, H, m->ares, m->pf,
+                                  op.n, op.stride)))
+        return rc;
       void *gu_out[2] = {m->gate, m->up};
       if ((rc = g4_w4_linear_multi(gu, 2, m->pf, G4_F32, rows, gu_out, G4_F32))) return rc;
       if ((rc = launch_gelu_mul(m->gate, m->up, (size_t)rows * l.inter, m->act))) return rc;
     }
     GemmParts dp;
     if ((rc = linear_parts(l.w[G4_PROJ_DOWN], m->act, rows, m->down, &dp))) return rc;
-    if ((rc = launch_norm_chain(dp.parts, m->ares, l.norm[G4_NORM_POST_FFW], nullptr, 1.f, eps,
-                                rows, H, m->fres, nullptr, dp.n, dp.stride)))
-      return rc;
-    if ((rc = g4_w4_linear(l.w[G4_PROJ_PLE_GATE], m->fres, G4_F32, rows, m->pg, G4_F32)))
-      return rc;
+    const g4_w4 *pgw = l.w[G4_PROJ_PLE_GATE];
+    if (gemm) {  // the residual itself is the PLE gate's input
+      GemmXPrep xp;
+      if ((rc = w4_gemm_prepare(&pgw, 1, rows, &xp))) return rc;
+      if ((rc = launch_norm_chain_xprep(dp.parts, dp.n, dp.stride, m->ares,
+                                        l.norm[G4_NORM_POST_FFW], nullptr, 1.f, eps, rows, H,
+                                        m->fres, nullptr, xp.xt, xp.xe, xp.Mp)))
+        return rc;
+      if ((rc = w4_gemm(pgw, nullptr, true, rows, m->pg, false))) return rc;
+    } else {
+      if ((rc = launch_norm_chain(dp.parts, m->ares, l.norm[G4_NORM_POST_FFW], nullptr, 1.f, eps,
+                                  rows, H, m->fres, nullptr, dp.n, dp.stride)))
+        return rc;
+      if ((rc = g4_w4_linear(pgw, m->fres, G4_F32, rows, m->pg, G4_F32))) return rc;
+    }
     if ((rc = launch_gelu_ple(m->pg, m->perlayer, rows, i, P, NL, m->pm))) return rc;
     if ((rc = g4_w4_linear(l.w[G4_PROJ_PLE_PROJ], m->pm, G4_F32, rows, m->pp, G4_F32)))
       return rc;
     const bool last = i + 1 == NL;
-    if ((rc = launch_norm_chain(m->pp, m->fres, l.norm[G4_NORM_POST_PLE],
-                                last ? nullptr : m->L[i + 1].norm[G4_NORM_INPUT], l.skip, eps,
-                                rows, H, out, last ? nullptr : m->pre)))
+    pre_prepped = gemm && !last;
+    if (pre_prepped) {  // the next layer's q/k/v input, as that GEMM's x'
+      const Layer &nx = m->L[i + 1];
+      const g4_w4 *nq = nx.w[G4_PROJ_Q];
+      GemmXPrep xp;
+      if ((rc = w4_gemm_prepare(&nq, 1, rows, &xp))) return rc;
+      if ((rc = launch_norm_chain_xprep(m->pp, 1, 0, m->fres, l.norm[G4_NORM_POST_PLE],
+                                        nx.norm[G4_NORM_INPUT], l.skip, eps, rows, H, out,
+                                        nullptr, xp.xt, xp.xe, xp.Mp)))
+        return rc;
+    } else if ((rc = launch_norm_chain(m->pp, m->fres, l.norm[G4_NORM_POST_PLE],
+                                       last ? nullptr : m->L[i + 1].norm[G4_NORM_INPUT], l.skip,
+                                       eps, rows, H, out, last ? nullptr : m->pre))) {
       return rc;
+    }
     cur ^= 1;
   }
   // final norm of the last row (gemma4-webgpu.js:394-400)

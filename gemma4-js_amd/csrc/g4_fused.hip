@@ -958,6 +958,109 @@ __global__ __launch_bounds__(256) void norm_chain_kernel(const float *__restrict
   }
 }
 
+// Block maximum; all threads get it.  red: >= 4 floats, not reused by the
+// next call before a barrier.
+__device__ __forceinline__ float fblock_max(float v, float *red) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  return fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+}
+
+__device__ __forceinline__ uint32_t half2_bits(_Float16 a, _Float16 b) {
+  return (uint32_t)__builtin_bit_cast(uint16_t, a) |
+         ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
+}
+
+// norm_chain_kernel's chain for a row of up to 2048 values (a multiple of 8)
+// with the prefill GEMM's x pre-pass of its output fused in: the GEMM input
+// (x = rms(r) * w2, or r itself without w2) leaves as x' for the GEMM that
+// follows - per row the exponent xe (max |x * 2^-xe| in [2^13, 2^14), 0 for
+// an all-zero or non-finite row), per 8-value chunk c the FP16 pairs (0,4)
+// (1,5) (2,6) (3,7) of x * 2^-xe (hi) and of the rounding remainders (lo) at
+// xt[c * Mp + row] and xt[(width / 8 + c) * Mp + row].  r_out and x_out (FP32)
+// are optional.  Grid: Mp blocks; rows past `rows` write zero chunks.
+__global__ __launch_bounds__(256) void norm_chain_xprep_kernel(
+    const float *__restrict__ a, int a_parts, size_t a_stride, const float *__restrict__ h,
+    const float *__restrict__ w1, const float *__restrict__ w2, float c, float eps, int width,
+    int rows, float *__restrict__ r_out, float *__restrict__ x_out, uint4 *__restrict__ xt,
+    int *__restrict__ xe, int Mp) {
+  __shared__ float red[16];
+  __shared__ float xs[2048];
+  const int row = blockIdx.x;
+  const int nch = width >> 3;
+  const size_t lo_plane = (size_t)nch * Mp;
+  if (row >= rows) {
+    for (int ch = threadIdx.x; ch < nch; ch += 256) {
+      xt[(size_t)ch * Mp + row] = make_uint4(0u, 0u, 0u, 0u);
+      xt[lo_plane + (size_t)ch * Mp + row] = make_uint4(0u, 0u, 0u, 0u);
+    }
+    return;
+  }
+  const size_t off = (size_t)row * width;
+  constexpr int U = 8;
+  float av[U], hv[U], w1v[U], w2v[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    int i = threadIdx.x + 256 * u;
+    i = i < width ? i : width - 1;
+    av[u] = a[off + i];
+    for (int s = 1; s < a_parts; ++s) av[u] += a[s * a_stride + off + i];
+    hv[u] = h[off + i];
+    w1v[u] = w1[i];
+    w2v[u] = w2 ? w2[i] : 0.f;
+  }
+  float ss = 0.f;
+#pragma unroll
+  for (int u = 0; u < U; ++u)
+    if (threadIdx.x + 256 * u < width) ss += av[u] * av[u];
+  const float inv1 = 1.f / sqrtf(fblock_sum(ss, red, 4) / (float)width + eps);
+  float r[U], ss2 = 0.f;
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    r[u] = (hv[u] + av[u] * inv1 * w1v[u]) * c;
+    if (threadIdx.x + 256 * u < width) ss2 += r[u] * r[u];
+  }
+  float xv[U];
+  if (w2) {
+    const float inv2 = 1.f / sqrtf(fblock_sum(ss2, red + 4, 4) / (float)width + eps);
+#pragma unroll
+    for (int u = 0; u < U; ++u) xv[u] = r[u] * inv2 * w2v[u];
+  } else {
+#pragma unroll
+    for (int u = 0; u < U; ++u) xv[u] = r[u];
+  }
+  float mx = 0.f;
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int i = threadIdx.x + 256 * u;
+    if (i < width) {
+      if (r_out) r_out[off + i] = r[u];
+      if (x_out) x_out[off + i] = xv[u];
+      xs[i] = xv[u];
+      mx = fmaxf(mx, fabsf(xv[u]));
+    }
+  }
+  mx = fblock_max(mx, red + 8);  // its barrier also publishes xs
+  const int e = mx > 0.f && mx <= 3.4e38f ? ilogbf(mx) - 13 : 0;
+  if (threadIdx.x == 0) xe[row] = e;
+  for (int ch = threadIdx.x; ch < nch; ch += 256) {
+    _Float16 hh[8], ll[8];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const float sv = ldexpf(xs[8 * ch + q], -e);
+      hh[q] = (_Float16)sv;
+      ll[q] = (_Float16)(sv - (float)hh[q]);
+    }
+    xt[(size_t)ch * Mp + row] = make_uint4(half2_bits(hh[0], hh[4]), half2_bits(hh[1], hh[5]),
+                                           half2_bits(hh[2], hh[6]), half2_bits(hh[3], hh[7]));
+    xt[lo_plane + (size_t)ch * Mp + row] =
+        make_uint4(half2_bits(ll[0], ll[4]), half2_bits(ll[1], ll[5]), half2_bits(ll[2], ll[6]),
+                   half2_bits(ll[3], ll[7]));
+  }
+}
+
 }  // namespace
 
 // ---- launchers used by the engine --------------------------------------------
@@ -1124,6 +1227,19 @@ int launch_norm_chain(const float *a, const float *h, const float *w1, const flo
   hipLaunchKernelGGL(norm_chain_kernel, dim3(rows), dim3(256), 0, stream(), a, a_parts, a_stride,
                      h, w1, w2, c, eps, width, r_out, x_out);
   G4_LAUNCH_CHECK("norm_chain_kernel");
+  return G4_OK;
+}
+
+int launch_norm_chain_xprep(const float *a, int a_parts, size_t a_stride, const float *h,
+                            const float *w1, const float *w2, float c, float eps, int rows,
+                            int width, float *r_out, float *x_out, void *xt, int *xe, int Mp) {
+  if (width > 2048 || width % 8 || rows > Mp)
+    return fail(G4_E_ARG, "norm chain with x pre-pass: width %d (<= 2048, multiple of 8), "
+                "rows %d <= %d", width, rows, Mp);
+  hipLaunchKernelGGL(norm_chain_xprep_kernel, dim3(Mp), dim3(256), 0, stream(), a, a_parts,
+                     a_stride, h, w1, w2, c, eps, width, rows, r_out, x_out,
+                     static_cast<uint4 *>(xt), xe, Mp);
+  G4_LAUNCH_CHECK("norm_chain_xprep_kernel");
   return G4_OK;
 }
 

@@ -705,8 +705,9 @@ int launch_planned(const GemmPlan &pl, const g4_w4 *const *w, int nw, const uint
 #undef G4_GEMM_TILE
 }
 
-// x' (and its low half) and the row exponents, reused by every later call.
-Workspace g_ws;
+// x' (and its low half), the row exponents and the K-slice planes, reused by
+// every later call; g_ws_x: x' and exponents written by the producer of x.
+Workspace g_ws, g_ws_x;
 
 }  // namespace
 
@@ -714,37 +715,81 @@ namespace g4 {
 
 // keep: when set and the plan splits K, the partial planes are left for the
 // caller to add (keep->parts, ->n, ->stride) instead of summed into y.
+// The GEMM scratch for one call: x' planes, row exponents and K-slice planes.
+struct GemmScratch {
+  GemmPlan plan;
+  int Mp;
+  uint4 *xt;
+  int *xe;
+  float *part;
+};
+
+// prepped: x' and the exponents live in their own scratch (g_ws_x), written
+// by the producer of x while the GEMM scratch may still hold the producer's
+// inputs (its K-slice planes).
+// Rows padded to the tile height, and the byte offsets of the exponents and
+// of the end of x' + exponents in a scratch buffer.
+void xprep_layout(int K, int rows, bool f32x, int *Mp, size_t *eoff, size_t *xend) {
+  *Mp = (rows + kRowPad - 1) / kRowPad * kRowPad;
+  const size_t xt_bytes = (size_t)*Mp * K * 2 * (f32x ? 2 : 1);  // FP16 x' (hi [+ lo])
+  *eoff = (xt_bytes + 255) & ~size_t(255);
+  *xend = *eoff + (size_t)rows * 4;
+}
+
+int gemm_scratch(const g4_w4 *const *w, int nw, bool f32x, int rows, bool prepped,
+                 GemmScratch *sc) {
+  const g4_w4 *w0 = w[0];
+  size_t eoff, xend;
+  xprep_layout(w0->K, rows, f32x, &sc->Mp, &eoff, &xend);
+  const size_t poff = prepped ? 0 : (xend + 255) & ~size_t(255);
+  sc->plan = plan_gemm(w, nw, rows, f32x);
+  const size_t part_bytes =
+      sc->plan.slices > 1 ? sc->plan.slices * splitk_pstride(rows, w0->N) * 4 : 0;
+  void *ws = nullptr, *wx = nullptr;
+  if (poff + part_bytes > 0)
+    if (int rc = g_ws.get(poff + part_bytes, &ws, "g4_w4_linear (prefill)")) return rc;
+  if (prepped) {
+    if (int rc = g_ws_x.get(xend, &wx, "g4_w4_linear (prefill, prepared x)")) return rc;
+  } else {
+    wx = ws;
+  }
+  sc->xt = static_cast<uint4 *>(wx);
+  sc->xe = reinterpret_cast<int *>(static_cast<char *>(wx) + eoff);
+  sc->part = reinterpret_cast<float *>(static_cast<char *>(ws) + poff);
+  return G4_OK;
+}
+
+// x == nullptr: x' and the row exponents are already in the scratch
+// (written by the producer after w4_gemm_prepare).
 static int gemm_run(const g4_w4 *const *w, int nw, const void *x, bool f32x, int rows,
                     void *const *y, bool y_bf16, GemmParts *keep, bool glu = false) {
   // weights whose joint grid still leaves CUs idle run one by one (each may
-  // then split K)
+  // then split K); not with x' prepared, whose scratch is sized for the joint call
   const int cus = cu_count() > 0 ? cu_count() : 256;
   long tiles64 = 0;
   for (int i = 0; i < nw; ++i) tiles64 += (long)((rows + 63) / 64) * ((w[i]->N + 63) / 64);
-  if (nw > 1 && tiles64 < cus && !glu) {
+  if (nw > 1 && tiles64 < cus && !glu && x) {
     for (int i = 0; i < nw; ++i)
       if (int rc = gemm_run(w + i, 1, x, f32x, rows, y + i, y_bf16, nullptr)) return rc;
     return G4_OK;
   }
   const g4_w4 *w0 = w[0];
-  const int Mp = (rows + kRowPad - 1) / kRowPad * kRowPad;
-  const size_t xt_bytes = (size_t)Mp * w0->K * 2 * (f32x ? 2 : 1);  // FP16 x' (hi [+ lo])
-  const size_t eoff = (xt_bytes + 255) & ~size_t(255);
-  const size_t poff = (eoff + (size_t)rows * 4 + 255) & ~size_t(255);
-  const GemmPlan plan = plan_gemm(w, nw, rows, f32x);
-  const size_t part_bytes = plan.slices > 1 ? plan.slices * splitk_pstride(rows, w0->N) * 4 : 0;
-  void *ws = nullptr;
-  int rc = g_ws.get(poff + part_bytes, &ws, "g4_w4_linear (prefill)");
-  if (rc) return rc;
-  uint4 *xt = static_cast<uint4 *>(ws);
-  int *xe = reinterpret_cast<int *>(static_cast<char *>(ws) + eoff);
-  float *part = reinterpret_cast<float *>(static_cast<char *>(ws) + poff);
+  GemmScratch sc;
+  if (int rc = gemm_scratch(w, nw, f32x, rows, !x, &sc)) return rc;
+  const GemmPlan plan = sc.plan;
+  const int Mp = sc.Mp;
+  uint4 *xt = sc.xt;
+  int *xe = sc.xe;
+  float *part = sc.part;
   const bool sum = !keep || plan.slices == 1;
   if (keep) {
     keep->parts = sum ? static_cast<const float *>(y[0]) : part;
     keep->n = sum ? 1 : plan.slices;
     keep->stride = splitk_pstride(rows, w0->N);
   }
+  if (!x)
+    return f32x ? launch_planned<2>(plan, w, nw, xt, xe, rows, Mp, y, y_bf16, part, sum, glu)
+                : launch_planned<1>(plan, w, nw, xt, xe, rows, Mp, y, y_bf16, part, sum, glu);
   const int cpt = fused_prep_cpt(w0->K, f32x);
   if (cpt) {
     const dim3 fgrid(Mp / kRowsFused);
@@ -807,6 +852,19 @@ int w4_gemm_glu(const g4_w4 *gate, const g4_w4 *up, const float *x, int rows, fl
   const g4_w4 *w[2] = {gate, up};
   void *y[2] = {act, nullptr};
   return gemm_run(w, 2, x, true, rows, y, false, nullptr, true);
+}
+
+int w4_gemm_prepare(const g4_w4 *const *w, int nw, int rows, GemmXPrep *out) {
+  // only the x' scratch: the GEMM scratch may still hold the producer's
+  // inputs, and is sized by the GEMM call itself
+  (void)nw;
+  size_t eoff, xend;
+  xprep_layout(w[0]->K, rows, true, &out->Mp, &eoff, &xend);
+  void *wx = nullptr;
+  if (int rc = g_ws_x.get(xend, &wx, "g4_w4_linear (prefill, prepared x)")) return rc;
+  out->xt = static_cast<uint4 *>(wx);
+  out->xe = reinterpret_cast<int *>(static_cast<char *>(wx) + eoff);
+  return G4_OK;
 }
 
 int w4_gemm_parts(const g4_w4 *w, const float *x, int rows, float *y, GemmParts *out) {

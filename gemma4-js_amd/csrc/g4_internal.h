@@ -149,6 +149,19 @@ int w4_gemm_parts(const g4_w4 *w, const float *x, int rows, float *y, GemmParts 
 // launch, each tile holding the same columns of gate and up (the GEMM outputs
 // and the product as GELU_MUL computes them).
 int w4_gemm_glu(const g4_w4 *gate, const g4_w4 *up, const float *x, int rows, float *act);
+// The x pre-pass done by the producer of x instead: w4_gemm_prepare sizes the
+// GEMM scratch for the call that follows (the same weights, FP32 rows) and
+// returns where x' goes: hi plane xt[c * Mp + m] and lo plane
+// xt[(K / 8 + c) * Mp + m] for chunk c (8 values, FP16 pairs (0,4) (1,5)
+// (2,6) (3,7) of x * 2^-xe[m]), rows M..Mp-1 zero, xe[m] with max |x * 2^-xe|
+// in [2^13, 2^14) (0 for all-zero or non-finite rows).  The GEMM entry points
+// then take x = nullptr; no other GEMM call may come in between.
+struct GemmXPrep {
+  uint4 *xt;
+  int *xe;
+  int Mp;
+};
+int w4_gemm_prepare(const g4_w4 *const *w, int nw, int rows, GemmXPrep *out);
 // Split-K decode GEMV of one FP32 row into per-slice partial sums
 // parts[K / 1536][N] (g4_w4.hip); returns the slice count, 0 if K does not
 // split (nothing launched), or minus a status.

@@ -51,6 +51,11 @@ int launch_rope_qkv(const float *qraw, const float *kraw, const float *vraw, int
 int launch_norm_chain(const float *a, const float *h, const float *w1, const float *w2, float c,
                       float eps, int rows, int width, float *r_out, float *x_out,
                       int a_parts = 1, size_t a_stride = 0);
+// The same chain writing its GEMM input (x, or r without w2) as the prefill
+// GEMM's x' (xt, xe, Mp from w4_gemm_prepare); r_out / x_out optional.
+int launch_norm_chain_xprep(const float *a, int a_parts, size_t a_stride, const float *h,
+                            const float *w1, const float *w2, float c, float eps, int rows,
+                            int width, float *r_out, float *x_out, void *xt, int *xe, int Mp);
 
 // RoPE (cos, sin) tables of the current position for up to kRopeSlots
 // (base, head_dim, angles) variants, kRopeTable entries each.
