@@ -23,7 +23,7 @@ also reported as "decode_tok_s" on the line, and prefill tokens/s.
 
 cpu_baseline: the oracle's TF.js-semantics FP32 dequant + matMul
 restatement (single-threaded C, the reference's CPU path is single-threaded
-JS) timed on the host on a bounded number of config-0 GEMVs.
+JS) timed on the host on a bounded number of M1 K1536 N6144 GEMVs.
 """
 import argparse
 import json
@@ -108,7 +108,7 @@ E2B_SLIDING_LAUNCHES = [("q", "k", "v"), ("o",), ("gate", "up"), ("down",)]
 
 
 def bench_layer(reps=50, seed=1):
-    """Config 2: the 7 GEMVs of one E2B sliding layer, M=1, chained through
+    """One E2B sliding decoder layer: its 7 GEMVs at M=1, chained through
     their real input sizes, the ones that share an input in one launch
     (g4_w4_linear_multi: 4 launches per layer); rotated over enough layer
     copies to stay cold."""
@@ -207,7 +207,7 @@ def bench_gemm(reps=3, seed=3):
 
 
 def bench_decode(prompt=512, steps=256, max_seq=1024, seed=4):
-    """Config 4: random-init Gemma-4-E2B (35 layers, vocab 262144, W4 projections,
+    """E2B decode: random-init Gemma-4-E2B (35 layers, vocab 262144, W4 projections,
     W4 PLE table, BF16 tied head) - a prompt of random ids, then greedy decode
     steps, each a replay of the recorded one-token step."""
     import e2b
@@ -288,7 +288,7 @@ def cpu_baseline(n, k, budget_s=10.0, seed=0):
             break
     return {"value": w4_bytes(n, k) * calls / el / 1e9, "unit": "GB/s", "cores": 1,
             "kind": "port",
-            "sample": "%d config-0 GEMVs (M1 K%d N%d) through the oracle's TF.js-semantics "
+            "sample": "%d GEMVs (M1 K%d N%d) through the oracle's TF.js-semantics "
                       "restatement (FP32 dequant per 256-row chunk, then blocked FP32 matMul), "
                       "%.1f s, %.1f ms/GEMV" % (calls, k, n, el, el / calls * 1e3)}
 
@@ -341,20 +341,20 @@ def main():
 
     extra = {}
     if not args.no_extra:
-        log("layer (config 2) ...")
+        log("E2B sliding layer, 7 GEMVs at M=1 ...")
         extra["layer_e2b_sliding_7gemv"] = bench_layer()
         log("  ", extra["layer_e2b_sliding_7gemv"])
-        log("PLE gather (config 1) ...")
+        log("PLE gather-dequant, 1 and 2048 ids ...")
         extra["ple_gather"] = bench_ple()
         log("  ", extra["ple_gather"])
         log("BF16 LM head ...")
         extra["lm_head_262144x1536"] = bench_head()
         log("  ", extra["lm_head_262144x1536"])
-        log("prefill GEMM (config 3) ...")
+        log("prefill GEMM, M2048 ...")
         extra["gemm_prefill"] = bench_gemm()
         log("  ", extra["gemm_prefill"])
         if not args.skip_decode:
-            log("E2B decode (config 4): prompt 512, 256 greedy steps ...")
+            log("E2B decode: prompt 512, 256 greedy steps ...")
             extra["decode_e2b"] = bench_decode()
             log("  ", extra["decode_e2b"])
             log("E2B decode from Node (N-API bridge) ...")

@@ -417,8 +417,8 @@ def fill_random(buf, count, kind, seed, sigma=1.0):
 
 
 def w4_random(n, k, seed, scale_sigma=0.02):
-    """A W4Linear of random weights generated on the device (config-style
-    distributions: q uniform in [-7, 7], scales bf16 |N(0,1)| * sigma)."""
+    """A W4Linear of random weights generated on the device (q uniform in
+    [-7, 7], scales bf16 |N(0,1)| * sigma)."""
     packed = Buffer(n * k // 2)
     scales = Buffer(n * (k // 32) * 2)
     fill_random(packed, n * k // 8, RAND_W4_PACKED, seed)
