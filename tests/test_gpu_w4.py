@@ -302,6 +302,30 @@ def test_linear_multi_prefill_gemm(g4, shapes):
         assert np.array_equal(ys[0].download(np.float32).reshape(rows, 2048), alone)
 
 
+@pytest.mark.parametrize("rows", [5, 200, 512])
+def test_linear_multi_gemm_bf16_out_ragged(g4, rows):
+    # BF16 x and BF16 y through the several-weight GEMM: ragged widths (not
+    # tile multiples), a joint grid that fills the GPU (512 rows) or not (5,
+    # 200 rows: each weight alone); every output is the RNE of the FP32 one.
+    k = 1024
+    x_bits, x = syn.activations(41, rows, k)
+    xb = g4.Buffer.from_array(x_bits)
+    lins, refs = [], []
+    for i, n in enumerate((1000, 100, 36)):
+        packed, scales, q = syn.w4_weights(340 + i, n, k)
+        lins.append(g4.W4Linear(packed, scales))
+        refs.append(x.astype(np.float64) @ dense(q, scales).T)
+    y32 = [g4.Buffer(rows * lin.out_dim * 4) for lin in lins]
+    y16 = [g4.Buffer(rows * lin.out_dim * 2) for lin in lins]
+    g4.W4Linear.linear_multi(lins, xb.ptr, g4.BF16, rows, [y.ptr for y in y32], g4.F32)
+    g4.W4Linear.linear_multi(lins, xb.ptr, g4.BF16, rows, [y.ptr for y in y16], g4.BF16)
+    for lin, a, b, ref in zip(lins, y32, y16, refs):
+        got = a.download(np.float32).reshape(rows, lin.out_dim)
+        assert rel_l2_rows(got, ref) <= 1e-4
+        assert np.array_equal(b.download(np.uint16).reshape(rows, lin.out_dim),
+                              syn.bf16_rne(got).reshape(rows, lin.out_dim))
+
+
 def test_linear_multi_errors(g4):
     a = g4.W4Linear(*syn.w4_weights(320, 64, 512)[:2])
     b = g4.W4Linear(*syn.w4_weights(321, 64, 256)[:2])
