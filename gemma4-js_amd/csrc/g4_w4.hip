@@ -463,6 +463,14 @@ int launch_gemv1_i(const g4_w4 *w, const Gemv1Plan &p, const void *x, void *y, i
   return G4_OK;
 }
 
+// Whether the one-row GEMV has a launch shape for G groups per row (RB * G =
+// T * IPL needs a block size of whole waves); other widths take the general
+// GEMV with one row.
+bool has_gemv1_plan(int G, bool f32x) {
+  Gemv1Plan p;
+  return plan_gemv1(G, f32x, &p);
+}
+
 // The M = 1 launch shape for w's input dimension.
 template <bool F32X>
 int gemv1_plan(const g4_w4 *w, Gemv1Plan *p) {
@@ -802,7 +810,7 @@ G4_API int g4_w4_linear(const g4_w4 *w, const void *x, int x_dtype, int rows,
   if (gemv_lds_per_row(w->K, f32x) > kGemvLdsBudget)
     return fail(G4_E_ARG, "g4_w4_linear: in_dim %d exceeds the GEMV staging limit (%s x)",
                 w->K, f32x ? "FP32" : "BF16");
-  if (rows == 1) {
+  if (rows == 1 && has_gemv1_plan(w->G, f32x)) {
     rc = f32x ? launch_gemv1<true>(w, x, y, y_dtype == G4_BF16)
               : launch_gemv1<false>(w, x, y, y_dtype == G4_BF16);
     return rc ? rc : ok();
@@ -835,7 +843,8 @@ G4_API int g4_w4_linear_multi(const g4_w4 *const *w, int n, const void *x, int x
       return fail(G4_E_ARG, "g4_w4_linear_multi: weight %d has in_dim %d, weight 0 has %d", i,
                   w[i]->K, w[0]->K);
   }
-  if (n == 1 || (rows > 1 && rows <= kMaxGemvRows)) {
+  if (n == 1 || (rows > 1 && rows <= kMaxGemvRows) ||
+      (rows == 1 && !has_gemv1_plan(w[0]->G, x_dtype == G4_F32))) {
     for (int i = 0; i < n; ++i)
       if (int rc = g4_w4_linear(w[i], x, x_dtype, rows, y[i], y_dtype)) return rc;
     return ok();
