@@ -1,11 +1,12 @@
-"""Seeded random shapes through the W4 linear entry points.
+"""Seeded random shapes through the W4 linear, dequant and PLE entry points.
 
-Each case draws a row count (the GEMV sizes 1-4 and the GEMM sizes above),
-an output width that is rarely a tile multiple, an input width (a multiple
-of the 32-value group), an activation dtype and an output dtype, and checks
-the result against the binary64 product x . dequant(W)^T (max relative L2
-error per row).  BF16 outputs must be the round-to-nearest-even of the FP32
-outputs of the same call.
+A linear case draws a row count (the GEMV sizes 1-4 and the GEMM sizes
+above), an output width that is rarely a tile multiple, an input width (a
+multiple of the 32-value group), an activation dtype and an output dtype, and
+checks the result against the binary64 product x . dequant(W)^T (max
+relative L2 error per row); BF16 outputs must be the round-to-nearest-even of
+the FP32 outputs of the same call.  Dequant and PLE cases draw shapes, row
+ranges, table geometry and ids, and must match the oracle bit for bit.
 """
 import numpy as np
 import pytest
@@ -44,7 +45,7 @@ def activations(g4, rng, rows, k, f32x):
     return g4.Buffer.from_array(bits), syn.bf16_to_f32(bits).reshape(rows, k), g4.BF16
 
 
-@pytest.mark.parametrize("seed", range(24))
+@pytest.mark.parametrize("seed", range(48))
 def test_random_linear(g4, seed):
     rng, rows, n, k, f32x = draw(seed)
     packed, scales, q = syn.w4_weights(500 + seed, n, k)
@@ -61,7 +62,7 @@ def test_random_linear(g4, seed):
                           syn.bf16_rne(got).reshape(rows, n)), (rows, n, k, f32x)
 
 
-@pytest.mark.parametrize("seed", range(8))
+@pytest.mark.parametrize("seed", range(16))
 def test_random_linear_multi(g4, seed):
     rng, rows, _, k, f32x = draw(100 + seed)
     widths = [int(v) for v in rng.integers(1, 700, size=int(rng.integers(2, 4)))]
@@ -76,3 +77,47 @@ def test_random_linear_multi(g4, seed):
     for y, n, ref in zip(ys, widths, refs):
         got = y.download(np.float32).reshape(rows, n)
         assert rel_l2_rows(got, ref) <= 1e-4, (rows, widths, k, f32x)
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_random_ple_geometry(g4, oracle, seed):
+    # Random table geometry (vocab, width, rows per shard, a short last
+    # shard) and ids with the edges: rows bit-exact against the oracle's
+    # readRows restatement, BF16 the round-to-nearest-even of FP32.
+    rng = np.random.default_rng(2000 + seed)
+    width = 32 * int(rng.integers(1, 129))
+    rps = 8 * int(rng.integers(1, 65))
+    vocab = int(rng.integers(1, 5000))
+    shards = syn.ple_table(300 + seed, vocab, width, rps, threads=4)
+    t = g4.PleTable(vocab, width, 32, rps)
+    for i, s in enumerate(shards):
+        t.upload_shard(i, s)
+    host = np.concatenate(shards)
+    ids = rng.integers(0, vocab, size=int(rng.integers(1, 300))).astype(np.int32)
+    ids[: min(3, len(ids))] = [0, vocab - 1, min(rps, vocab - 1)][: min(3, len(ids))]
+    want = oracle.ple_gather(host, vocab, width, rps, ids)
+    out = g4.Buffer(len(ids) * width * 4)
+    t.gather(ids, out.ptr, g4.F32)
+    assert np.array_equal(out.download(np.uint32).reshape(-1), want.view(np.uint32).reshape(-1))
+    out16 = g4.Buffer(len(ids) * width * 2)
+    t.gather(ids, out16.ptr, g4.BF16)
+    assert np.array_equal(out16.download(np.uint16).reshape(-1), oracle.f32_to_bf16_array(want))
+    t.free()
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_random_dequant(g4, oracle, seed):
+    # dequantizeOfficialW4A16Rows over random shapes and row ranges, bit-exact.
+    rng = np.random.default_rng(3000 + seed)
+    n, k = int(rng.integers(1, 600)), 32 * int(rng.integers(1, 129))
+    packed, scales, _ = syn.w4_weights(700 + seed, n, k)
+    lin = g4.W4Linear(packed, scales)
+    r0 = int(rng.integers(0, n))
+    rc = int(rng.integers(0, n - r0 + 1))
+    want_rc, want = oracle.w4_dequant_rows(packed, syn.bf16_to_f32(scales), n, k, r0, rc)
+    assert want_rc == 0
+    if rc == 0:
+        return
+    out = g4.Buffer(rc * k * 4)
+    lin.dequant(r0, rc, out.ptr, g4.F32)
+    assert np.array_equal(out.download(np.uint32).reshape(-1), want.view(np.uint32).reshape(-1))
