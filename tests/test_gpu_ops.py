@@ -121,6 +121,31 @@ def test_attention(g4, qrows, heads, hd, keylen, sliding, window):
                                               window))
 
 
+@pytest.mark.parametrize("seed", range(24))
+def test_attention_random_shapes(g4, seed):
+    # Seeded random row counts, head counts and dims, cache lengths and
+    # sliding windows: whichever kernel the shape selects (one row, key
+    # split, matrix-core rows with or without the key-tile prefetch).
+    rng = np.random.default_rng(4000 + seed)
+    qrows = int(rng.choice([1, 2, 3, 5, 16, 17, 40, 64, 100, 200]))
+    heads = int(rng.choice([1, 2, 3, 4, 8]))
+    hd = int(rng.choice([64, 128, 256, 512]))
+    keylen = qrows + int(rng.integers(0, 700 - qrows))
+    sliding = bool(rng.integers(0, 2))
+    window = int(rng.integers(1, 600))
+    q = rng.standard_normal((qrows, heads * hd)).astype(np.float32) * 0.2
+    k = rng.standard_normal((keylen, hd)).astype(np.float32)
+    v = rng.standard_normal((keylen, hd)).astype(np.float32)
+    qpos0 = keylen - qrows
+    y = out(g4, qrows * heads * hd)
+    g4.attention(dev(g4, q), dev(g4, k), dev(g4, v), qrows, heads, hd, keylen, qpos0, sliding,
+                 window, y)
+    got = y.download(np.float32).reshape(qrows, heads * hd)
+    want = lo.attention(q, k, v, qrows, heads, hd, keylen, qpos0, sliding, window)
+    check_attention(got, want, fp32_attention(q, k, v, qrows, heads, hd, keylen, qpos0, sliding,
+                                              window))
+
+
 def fp32_attention(q, k, v, qrows, heads, hd, keylen, qpos0, sliding, window):
     """The same attention evaluated plainly in float32 (numpy): the yardstick
     for FP32 rounding against the float64 oracle."""
