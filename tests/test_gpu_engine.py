@@ -142,6 +142,22 @@ def test_tiny_prefill_greedy_matches_oracle(g4, tiny):
     assert m.cache_length() == 12
 
 
+@pytest.mark.parametrize("n", [2, 4, 5, 9, 31, 40, 64])
+def test_tiny_prefill_lengths_match_oracle(g4, tiny, n):
+    # Prompt lengths on both sides of the GEMV/GEMM switch (4 rows) and past
+    # the 8-key window: the GEMM path's fused chains (x' written by the norm
+    # chain, K slices added by it, the GELU epilogue) at several row paddings.
+    ref, make = tiny
+    m = make(max_seq=64)
+    ids = syn.token_ids(50 + n, n, TINY["vocab"])
+    lg = g4.Buffer(TINY["vocab"] * 4)
+    tok = m.greedy(ids, 0, lg)
+    ref.reset()
+    want_tok, want_lg = ref.greedy(ids, 0)
+    assert rel(lg.download(np.float32), want_lg) < 1e-3
+    assert tok == want_tok or near_tie(want_lg, tok)
+
+
 def test_tiny_dense_ple_rows_match_oracle(g4, tiny):
     # embed_tokens_per_layer as dense BF16 rows instead of the W4 table
     _, make = tiny
