@@ -50,3 +50,21 @@ def test_head_no_softcap_and_scale(g4, oracle):
     g4.bf16_head(hb.ptr, Eb.ptr, rows, k, out.ptr, 0.5, 0.0)
     want = oracle.bf16_head(h, E, 0.5, 0.0)
     assert np.allclose(out.download(np.float32), want, rtol=1e-5, atol=1e-4)
+
+
+@pytest.mark.parametrize("seed", range(16))
+def test_head_random_shapes(g4, oracle, seed):
+    # Seeded random row counts (ragged against the kernel's 8-row groups and
+    # blocks) and input widths (multiples of 8 up to 4096), with and without
+    # the softcap.
+    rng = np.random.default_rng(5000 + seed)
+    rows = int(rng.integers(1, 3000))
+    k = 8 * int(rng.integers(1, 513))
+    scale, softcap = (1.0, 30.0) if seed % 2 == 0 else (0.5, 0.0)
+    E = syn.bf16_rne(rng.standard_normal((rows, k), dtype=np.float32) * np.float32(0.05))
+    h = rng.standard_normal(k).astype(np.float32)
+    Eb, hb, out = g4.Buffer.from_array(E), g4.Buffer.from_array(h), g4.Buffer(rows * 4)
+    g4.bf16_head(hb.ptr, Eb.ptr, rows, k, out.ptr, scale, softcap)
+    got = out.download(np.float32)
+    want = oracle.bf16_head(h, E, scale, softcap)
+    assert np.allclose(got, want, rtol=1e-4, atol=1e-4), (rows, k)
