@@ -16,6 +16,7 @@
 #include "g4_oracle.h"
 
 #include <math.h>
+#include <omp.h>
 #include <stdlib.h>
 #include <string.h>
 
@@ -152,6 +153,55 @@ int g4o_w4_linear(const float *x, int M, const int32_t *packed,
   free(wchunk);
   free(ychunk);
   return rc;
+}
+
+int g4o_w4_linear_mt(const float *x, int M, const int32_t *packed,
+                     const uint16_t *scales_bf16, int N, int K, int groupSize,
+                     int chunk, float *y, int threads) {
+  /* official-quantized-linear.js:82-128, chunks in parallel */
+  if (chunk <= 0) chunk = 256;
+  if (K % 8 != 0) return 1;
+  if (groupSize <= 0 || K % groupSize != 0) return 2;
+  const int groups = K / groupSize;
+  const size_t nscales = (size_t)N * groups;
+  float *scales = (float *)malloc(nscales * sizeof(float));
+  if (!scales) return -1;
+  for (size_t i = 0; i < nscales; ++i) scales[i] = g4o_bf16_to_f32(scales_bf16[i]);
+  const int nchunks = (N + chunk - 1) / chunk;
+  int rc = 0;
+  const int nt = g4o_omp_threads(threads);
+#pragma omp parallel num_threads(nt) reduction(| : rc)
+  {
+    float *wchunk = (float *)malloc((size_t)chunk * K * sizeof(float));
+    float *ychunk = (float *)malloc((size_t)M * chunk * sizeof(float));
+    if (!wchunk || !ychunk) {
+      rc |= 1 << 8;
+    } else {
+#pragma omp for schedule(dynamic, 1)
+      for (int c = 0; c < nchunks; ++c) {
+        const int rowStart = c * chunk;
+        const int rowCount = chunk < N - rowStart ? chunk : N - rowStart;
+        int r = g4o_w4_dequant_rows(packed, (size_t)N * (K / 8), scales, nscales, N, K,
+                                    rowStart, rowCount, groupSize, wchunk);
+        if (r) {
+          rc |= r;
+          continue;
+        }
+        tfjs_matmul_xwT(x, M, wchunk, rowCount, K, ychunk, rowCount);
+        for (int i = 0; i < M; ++i)
+          memcpy(&y[(size_t)i * N + rowStart], &ychunk[(size_t)i * rowCount],
+                 (size_t)rowCount * sizeof(float));
+      }
+    }
+    free(wchunk);
+    free(ychunk);
+  }
+  free(scales);
+  return rc ? (rc & 0xff ? rc & 0xff : -1) : 0;
+}
+
+int g4o_omp_threads(int threads) {
+  return threads > 0 ? threads : omp_get_max_threads();
 }
 
 int g4o_w4_linear_f64(const float *x, int M, const int32_t *packed,

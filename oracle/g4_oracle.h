@@ -8,8 +8,9 @@
  *
  * Every function restates one piece of the reference, cited by file:line
  * (paths relative to the gemma4-js repository root).  Plain C99, scalar,
- * single-threaded: the reference's own CPU path (TF.js on tfjs-backend-cpu)
- * is single-threaded JavaScript.
+ * single-threaded (the reference's own CPU path, TF.js on tfjs-backend-cpu,
+ * is single-threaded JavaScript), except g4o_w4_linear_mt, which shares the
+ * output chunks of the same computation out over OpenMP threads.
  */
 #ifndef G4_ORACLE_H
 #define G4_ORACLE_H
@@ -63,6 +64,18 @@ int g4o_w4_dequant_rows(const int32_t *packed, size_t packed_len,
 int g4o_w4_linear(const float *x, int M, const int32_t *packed,
                   const uint16_t *scales_bf16, int N, int K, int groupSize,
                   int chunk, float *y);
+
+/* g4o_w4_linear with the output chunks shared out over `threads` OpenMP
+ * threads (threads <= 0: the OpenMP default).  Each output element goes
+ * through exactly the same dequant and k-block sequence as in
+ * g4o_w4_linear, so the result is bit-identical; only the chunks run
+ * concurrently.  The benchmark's all-core CPU leg. */
+int g4o_w4_linear_mt(const float *x, int M, const int32_t *packed,
+                     const uint16_t *scales_bf16, int N, int K, int groupSize,
+                     int chunk, float *y, int threads);
+
+/* Threads an OpenMP parallel region of g4o_w4_linear_mt gets for `threads`. */
+int g4o_omp_threads(int threads);
 
 /* The same product in double precision (the error yardstick). */
 int g4o_w4_linear_f64(const float *x, int M, const int32_t *packed,

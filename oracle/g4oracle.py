@@ -5,7 +5,8 @@ __graft_entry__.smoke() and by bench.py's CPU-baseline leg, always as the
 checker; nothing in the product path calls it.
 
 Build recipe (also run by __graft_entry__.build()):
-    gcc -O2 -std=c99 -fPIC -shared oracle/g4_oracle.c -lm -o oracle/_build/libg4oracle.so
+    gcc -O2 -std=c99 -fPIC -shared -fopenmp -ffp-contract=off oracle/g4_oracle.c -lm \
+        -o oracle/_build/libg4oracle.so
 """
 import ctypes
 import os
@@ -32,6 +33,8 @@ _SIGS = {
     "g4o_w4_dequant_rows": (_i, [_p, _z, _p, _z, _i, _i, _i, _i, _i, _p]),
     "g4o_w4_linear": (_i, [_p, _i, _p, _p, _i, _i, _i, _i, _p]),
     "g4o_w4_linear_f64": (_i, [_p, _i, _p, _p, _i, _i, _i, _p]),
+    "g4o_w4_linear_mt": (_i, [_p, _i, _p, _p, _i, _i, _i, _i, _p, _i]),
+    "g4o_omp_threads": (_i, [_i]),
     "g4o_ple_dequant_row": (None, [_p, _p, _i, _p]),
     "g4o_ple_locate": (_i, [_c.c_longlong, _i, _i, _c.POINTER(_i), _c.POINTER(_i)]),
     "g4o_ple_row_offsets": (None, [_i, _i, _i, _i, _i, _c.POINTER(_z), _c.POINTER(_z)]),
@@ -46,7 +49,7 @@ def build(force=False):
     if force or not os.path.exists(LIB_PATH) or os.path.getmtime(LIB_PATH) < os.path.getmtime(SRC):
         os.makedirs(os.path.dirname(LIB_PATH), exist_ok=True)
         tmp = LIB_PATH + ".tmp"
-        subprocess.run(["gcc", "-O2", "-std=c99", "-Wall", "-fPIC", "-shared",
+        subprocess.run(["gcc", "-O2", "-std=c99", "-Wall", "-fPIC", "-shared", "-fopenmp",
                         "-ffp-contract=off", SRC, "-lm", "-o", tmp], check=True)
         os.replace(tmp, LIB_PATH)
     return LIB_PATH
@@ -124,6 +127,26 @@ def w4_linear(x, packed, scales_bf16, group=32, chunk=256):
     if rc:
         raise ValueError("g4o_w4_linear failed with %d" % rc)
     return y
+
+
+def w4_linear_mt(x, packed, scales_bf16, threads=0, group=32, chunk=256):
+    """w4_linear with the output chunks over `threads` OpenMP threads (0: all);
+    bit-identical to w4_linear."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    packed = np.ascontiguousarray(packed).view(np.int32)
+    scales_bf16 = np.ascontiguousarray(scales_bf16).view(np.uint16)
+    m, k = x.shape
+    n = packed.shape[0]
+    y = np.empty((m, n), dtype=np.float32)
+    rc = lib().g4o_w4_linear_mt(_ptr(x), m, _ptr(packed), _ptr(scales_bf16), n, k, group, chunk,
+                                _ptr(y), int(threads))
+    if rc:
+        raise ValueError("g4o_w4_linear_mt failed with %d" % rc)
+    return y
+
+
+def omp_threads(threads=0):
+    return lib().g4o_omp_threads(int(threads))
 
 
 def w4_linear_f64(x, packed, scales_bf16, group=32):

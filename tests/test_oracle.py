@@ -165,6 +165,59 @@ def test_w4_linear_chunking_does_not_change_values(oracle):
     assert np.array_equal(a, b)
 
 
+def test_w4_linear_threads_bit_identical(oracle):
+    # the all-core CPU leg: chunks over threads, each element's sequence
+    # unchanged, so the bits equal the single-threaded oracle's
+    packed, scales, _ = syn.w4_weights(13, 1000, 1536)
+    _, x = syn.activations(13, 3, 1536)
+    a = oracle.w4_linear(x, packed, scales)
+    for t in (1, 3, 0):
+        b = oracle.w4_linear_mt(x, packed, scales, threads=t)
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+def _run_js_leg(tmp_path, x, packed, scales):
+    import shutil
+    import subprocess
+    node = shutil.which("node")
+    if node is None:
+        pytest.skip("node is not installed")
+    m, k = x.shape
+    n = packed.shape[0]
+    paths = [str(tmp_path / f) for f in ("p.bin", "s.bin", "x.bin", "y.bin")]
+    np.ascontiguousarray(packed).view(np.int32).tofile(paths[0])
+    np.ascontiguousarray(scales).view(np.uint16).tofile(paths[1])
+    np.ascontiguousarray(x, dtype=np.float32).tofile(paths[2])
+    script = os.path.join(os.path.dirname(GOLDEN), "..", "oracle", "w4_linear_cpu.js")
+    p = subprocess.run([node, script, str(m), str(k), str(n)] + paths + ["0"],
+                       stdout=subprocess.PIPE, stderr=subprocess.PIPE, text=True, timeout=120)
+    assert p.returncode == 0, p.stderr
+    assert json.loads(p.stdout.strip().splitlines()[-1])["calls"] >= 1
+    return np.fromfile(paths[3], dtype=np.float32).reshape(m, n)
+
+
+def test_js_cpu_leg_matches_c_oracle(oracle, tmp_path):
+    # the single-threaded JavaScript leg restates the same dequant and
+    # 48-blocked matMul: identical bits, ragged chunk and k-block tails included
+    packed, scales, _ = syn.w4_weights(14, 300, 1568)
+    _, x = syn.activations(14, 2, 1568)
+    got = _run_js_leg(tmp_path, x, packed, scales)
+    want = oracle.w4_linear(x, packed, scales)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def test_js_cpu_leg_block_rounding(oracle, tmp_path):
+    # the 2^24 known answer of test_w4_linear_tfjs_block_rounding, in JS
+    K = 96
+    q = np.zeros((1, K), dtype=np.int64)
+    q[0, 0], q[0, 1], q[0, 48] = 2, 1, 1
+    packed = syn.pack_w4(q)
+    scales = np.full((1, K // 32), 0x3F80, dtype=np.uint16)
+    x = np.zeros((1, K), dtype=np.float32)
+    x[0, 0], x[0, 1], x[0, 48] = 2.0 ** 23, 1.0, 1.0
+    assert _run_js_leg(tmp_path, x, packed, scales)[0, 0] == np.float32(2.0 ** 24)
+
+
 def test_w4_linear_f64_matches_numpy(oracle):
     packed, scales, q = syn.w4_weights(21, 512, 1536)
     _, x = syn.activations(21, 2, 1536)
