@@ -14,11 +14,15 @@ float32 multiply of an exact bf16 value).
 Pinning (tests/test_oracle_layers.py): closed forms and invariants for each
 op (constant-vector RMS, GELU values and limits, RoPE at position 0 and as a
 rotation, single-key and uniform attention, masks against brute force,
-pleMix with zero inputs).  The model forward is pinned by two invariants:
-with every projection zero each layer only scales the residual stream by its
-skip scalar (closed form; a dropped residual add fails it), and a sequence
-fed whole equals the same sequence fed in parts (positions, causal mask,
-KV append and KV sharing).
+pleMix with zero inputs).  The model forward is pinned by a closed form and
+two invariants: one token through a layer of selection-matrix projections
+equals an element-by-element restatement of encodeLayer (planted mistakes -
+gelu(up) * gate, swapped norms, the layer scalar on one term, another
+layer's PLE slice - each fail it); with every projection zero each layer only
+scales the residual stream by its skip scalar (a dropped residual add fails
+it); and a sequence fed whole equals the same sequence fed in parts
+(positions, causal mask, KV append and KV sharing).  DequantModel is pinned
+against Model.
 """
 import numpy as np
 
@@ -214,3 +218,31 @@ class Model:
         lg = self.logits(self.forward(ids, start_pos))
         top_ids, _ = g4oracle.topk(lg, 10)
         return int(top_ids[0]), lg
+
+
+class DequantModel(Model):
+    """Model whose W4 projections dequantize each weight once to float64
+    (q * widened bf16 scale, exact) and multiply with numpy's float64 matmul:
+    the same product as g4o_w4_linear_f64 in another summation order, fast
+    enough for the E2B widths (hidden 1536, hundreds of rows).  Pinned against
+    Model by tests/test_oracle_layers.py."""
+
+    def __init__(self, *a, **kw):
+        super().__init__(*a, **kw)
+        self._deq = {}
+
+    def _w4(self, lin, x):
+        packed, scales = lin
+        key = id(packed)
+        w = self._deq.get(key)
+        if w is None:
+            p = np.asarray(packed).view(np.uint32)
+            n, kw = p.shape
+            shifts = np.arange(8, dtype=np.uint32) * np.uint32(4)
+            q = (((p[:, :, None] >> shifts) & np.uint32(15)).astype(np.int8) - 8).reshape(n, kw * 8)
+            s = g4oracle.bf16_to_f32_array(np.asarray(scales).view(np.uint16)).reshape(n, -1)
+            w = q.astype(F64) * np.repeat(s.astype(F64), 32, axis=1)
+            self._deq[key] = (packed, w)  # keep `packed` alive so its id stays unique
+        else:
+            w = w[1]
+        return np.asarray(x, np.float32).astype(F64) @ w.T

@@ -279,3 +279,192 @@ def test_model_rejects_wrong_append_position():
     m.forward([1, 2], 0)
     with pytest.raises(ValueError, match="KV append position 1 != cache length 2"):
         m.forward([3], 1)
+
+
+# ---- the layer composition in closed form, with planted mistakes -----------------
+#
+# One token at position 0 through one layer whose W4 projections are selection
+# matrices: row o of a projection holds a single nonzero q = m[o] at input
+# column c[o] with scale s (powers of two), so y[o] = x[c[o]] * m[o] * s
+# exactly.  q and k are zero, so the one visible key gets softmax weight 1 and
+# the attention context is the normalised v row.  The expected output follows
+# encodeLayer (gemma4-webgpu.js:224-309) and the top-level PLE mix (317-321)
+# written out element by element below, with the shaders' formulas taken from
+# gpu-runtime.js (RMS 1104-1118, GELU 1139-1173, PLE mix 1250-1263); no oracle
+# function is called to build it.
+
+CF_H, CF_P, CF_V = 64, 32, 4
+
+
+def _selection(n, k, cols, mult, scale_bits):
+    import synthetic as syn
+    q = np.zeros((n, k), np.int8)
+    q[np.arange(n), cols] = mult
+    return syn.pack_w4(q), np.full((n, k // 32), scale_bits, np.uint16)
+
+
+def _cf_setup(seed=7, skip=1.7):
+    import synthetic as syn
+    H, P, V = CF_H, CF_P, CF_V
+    rng = np.random.default_rng(seed)
+    E = syn.bf16_rne(rng.uniform(-1, 1, (V, H)).astype(np.float32))
+    tok_ple = rng.standard_normal((V, P)).astype(np.float32)
+    sels = {}
+    spec = dict(q=(H, H), k=(H, H), v=(H, H), o=(H, H), gate=(H, H), up=(H, H), down=(H, H),
+                ple_gate=(P, H), ple_proj=(H, P))
+    for name, (n, k) in spec.items():
+        cols = rng.integers(0, k, n)
+        mult = np.zeros(n, np.int8) if name in ("q", "k") else rng.integers(1, 8, n).astype(np.int8)
+        sels[name] = (cols, mult)
+    # scales 2^-2 (0x3E80) for gate/up so the GELU sees moderate arguments, else 1
+    scale_bits = {n: (0x3E80 if n in ("gate", "up") else 0x3F80) for n in spec}
+    lin = {n: _selection(spec[n][0], spec[n][1], sels[n][0], sels[n][1], scale_bits[n])
+           for n in spec}
+    top_cols, top_mult = rng.integers(0, H, P), rng.integers(1, 8, P).astype(np.int8)
+    top = _selection(P, H, top_cols, top_mult, 0x3F80)
+    names = ("input", "post_attn", "pre_ffw", "post_ffw", "post_ple")
+    norm = {n: rng.uniform(0.5, 1.5, H).astype(np.float32) for n in names}
+    norm["q"] = rng.uniform(0.5, 1.5, H).astype(np.float32)
+    norm["k"] = rng.uniform(0.5, 1.5, H).astype(np.float32)
+    layer = dict(head_dim=H, intermediate=H, full=0, kv_source=-1, rope_base=1e4, rope_prop=1.0,
+                 linear=lin, norm=norm, skip=skip)
+    ple_norm = rng.uniform(0.5, 1.5, P).astype(np.float32)
+    final = rng.uniform(0.5, 1.5, H).astype(np.float32)
+    parts = dict(E=E, tok_ple=tok_ple, sels=sels, scale={n: 0.25 if n in ("gate", "up") else 1.0
+                                                         for n in spec},
+                 top=(top_cols, top_mult), norm=norm, ple_norm=ple_norm, final=final, skip=skip)
+    return layer, top, parts
+
+
+def _cf_model(layer, top, parts):
+    return lo.Model(CF_H, 1, CF_P, CF_V, [layer], parts["E"],
+                    lambda ids: parts["tok_ple"][np.asarray(ids)], top, parts["ple_norm"],
+                    parts["final"])
+
+
+def _cf_expected(parts, tok):
+    """The layer for one token at position 0, element by element in float64."""
+    H = CF_H
+    f = np.float64
+
+    def rmsn(x, w=None):  # RMS_SHADER: x * inverseSqrt(mean(x*x) + 1e-6) * w
+        y = x / math.sqrt(float(np.mean(x * x)) + 1e-6)
+        return y if w is None else y * w.astype(f)
+
+    def gelu(x):  # GELU_MUL_SHADER / GELU_PLE_SHADER, tanh argument clamped
+        z = 0.7978845608028654 * (x + 0.044715 * x ** 3)
+        return 0.5 * x * (1.0 + np.tanh(np.clip(z, -10, 10)))
+
+    def sel(name, x):
+        cols, mult = parts["sels"][name]
+        return x[cols] * mult.astype(f) * parts["scale"][name]
+
+    nrm = parts["norm"]
+    e = (parts["E"][tok].astype(np.uint32) << 16).view(np.float32).astype(f)
+    h = e * 8.0                                   # scale(embed, sqrt(64))
+    tc, tm = parts["top"]
+    proj = h[tc] * tm.astype(f) * 0.125           # scale(w4(top, hidden), 1/sqrt(64))
+    per = (rmsn(proj, parts["ple_norm"]) + parts["tok_ple"][tok].astype(f) * 16.0) \
+        / math.sqrt(2.0)                          # PLE_MIX_SHADER
+    pre = rmsn(h, nrm["input"])
+    ctx = rmsn(sel("v", pre))                     # one visible key: context = vNorm row
+    an = rmsn(sel("o", ctx), nrm["post_attn"])
+    ares = h + an
+    pf = rmsn(ares, nrm["pre_ffw"])
+    act = gelu(sel("gate", pf)) * sel("up", pf)
+    fres = ares + rmsn(sel("down", act), nrm["post_ffw"])
+    pm = gelu(sel("ple_gate", fres)) * per
+    pn = rmsn(sel("ple_proj", pm), nrm["post_ple"])
+    out = (fres + pn) * parts["skip"]
+    return rmsn(out, parts["final"])
+
+
+def test_layer_composition_matches_closed_form():
+    layer, top, parts = _cf_setup()
+    for tok in range(CF_V):
+        m = _cf_model(layer, top, parts)
+        got = m.forward([tok], 0)
+        np.testing.assert_allclose(got, _cf_expected(parts, tok), rtol=2e-5, atol=1e-6)
+
+
+def _cf_error(layer, top, parts):
+    errs = []
+    for tok in range(CF_V):
+        got = _cf_model(layer, top, parts).forward([tok], 0).astype(np.float64)
+        want = _cf_expected(parts, tok)
+        errs.append(np.linalg.norm(got - want) / np.linalg.norm(want))
+    return max(errs)
+
+
+def test_layer_composition_planted_gelu_operand_swap_is_caught(monkeypatch):
+    layer, top, parts = _cf_setup()
+    assert _cf_error(layer, top, parts) < 1e-5
+    real = lo.gelu_mul
+    monkeypatch.setattr(lo, "gelu_mul", lambda gate, up: real(up, gate))  # gelu(up) * gate
+    assert _cf_error(layer, top, parts) > 1e-2
+
+
+def test_layer_composition_planted_norm_swap_is_caught():
+    layer, top, parts = _cf_setup()
+    swapped = dict(layer, norm=dict(layer["norm"], post_attn=layer["norm"]["pre_ffw"],
+                                    pre_ffw=layer["norm"]["post_attn"]))
+    assert _cf_error(swapped, top, parts) > 1e-2
+    swapped = dict(layer, norm=dict(layer["norm"], post_ffw=layer["norm"]["post_ple"],
+                                    post_ple=layer["norm"]["post_ffw"]))
+    assert _cf_error(swapped, top, parts) > 1e-2
+
+
+@pytest.mark.parametrize("plant", ["skip_on_pn", "skip_on_fres"])
+def test_layer_composition_planted_skip_placement_is_caught(monkeypatch, plant):
+    # out = (fres + pn) * skip; a skip on one term only changes the direction
+    # of out, which the final RMS norm keeps
+    layer, top, parts = _cf_setup()
+    real = lo.add_scale
+
+    def wrong(a, b, s):
+        if s == 1.0:
+            return real(a, b, s)
+        if plant == "skip_on_pn":
+            return real(a, lo.scale(b, s), 1.0)
+        return real(lo.scale(a, s), b, 1.0)
+
+    monkeypatch.setattr(lo, "add_scale", wrong)
+    assert _cf_error(layer, top, parts) > 1e-2
+
+
+def test_layer_composition_planted_ple_layer_index_is_caught(monkeypatch):
+    # a two-layer model reading layer 0's PLE slice at layer 1 differs from
+    # the same model reading its own slice
+    layer, top, parts = _cf_setup()
+    H, P = CF_H, CF_P
+    rng = np.random.default_rng(9)
+    tok_ple2 = rng.standard_normal((CF_V, 2 * P)).astype(np.float32)
+    top2 = _selection(2 * P, H, rng.integers(0, H, 2 * P),
+                      rng.integers(1, 8, 2 * P).astype(np.int8), 0x3F80)
+
+    def run():
+        m = lo.Model(H, 1, P, CF_V, [layer, dict(layer, skip=0.9)], parts["E"],
+                     lambda ids: tok_ple2[np.asarray(ids)], top2, parts["ple_norm"],
+                     parts["final"])
+        return m.forward([1], 0)
+
+    good = run()
+    real = lo.gelu_ple
+    monkeypatch.setattr(lo, "gelu_ple", lambda g, p, rows, layer_i, w, nl: real(g, p, rows, 0, w, nl))
+    bad = run()
+    assert np.linalg.norm(bad - good) / np.linalg.norm(good) > 1e-2
+
+
+def test_dequant_model_equals_model():
+    # the float64 dequantize-once product used for the E2B-width GPU checks
+    # equals the scalar float64 oracle product up to summation order
+    m, _ = _tiny_model(6)
+    d = lo.DequantModel(m.hidden, m.heads, m.ple_dim, m.vocab, m.layers, m.E_bits, m.ple_rows,
+                        m.top, m.ple_norm, m.final_norm, window=m.window)
+    ids = [3, 9, 27, 1, 14, 22]
+    a = m.forward(ids, 0)
+    b = d.forward(ids, 0)
+    np.testing.assert_allclose(b, a, rtol=1e-6, atol=1e-7)
+    a2, b2 = m.forward([5], 6), d.forward([5], 6)
+    np.testing.assert_allclose(b2, a2, rtol=1e-6, atol=1e-7)
+    assert len(d._deq) > 0
