@@ -475,6 +475,9 @@ G4_API int g4_gemma_e2b_config(int max_seq, g4_gemma_config *c) {
   return ok();
 }
 
+// The prefill's norm chains hold one hidden row per block (2048 values).
+constexpr int kMaxHidden = 2048;
+
 G4_API int g4_gemma_create(const g4_gemma_config *cfg, g4_gemma **out) {
   G4_CHECK_INIT();
   G4_CHECK_NOT_ENCODING();
@@ -482,11 +485,11 @@ G4_API int g4_gemma_create(const g4_gemma_config *cfg, g4_gemma **out) {
   *out = nullptr;
   const g4_gemma_config &c = *cfg;
   if (c.layers <= 0 || c.layers > G4_GEMMA_MAX_LAYERS || c.hidden <= 0 || c.hidden % 32 != 0 ||
-      c.hidden > 4096 || c.heads <= 0 || c.heads > 8 || c.ple_dim <= 0 || c.ple_dim % 32 != 0 ||
-      c.vocab <= 0 || c.max_seq <= 0 || c.window <= 0)
+      c.hidden > kMaxHidden || c.heads <= 0 || c.heads > 8 || c.ple_dim <= 0 ||
+      c.ple_dim % 32 != 0 || c.vocab <= 0 || c.max_seq <= 0 || c.window <= 0)
     return fail(G4_E_ARG,
                 "g4_gemma_create: bad config (layers %d <= %d, hidden %d multiple of 32 <= "
-                "4096, heads %d <= 8, ple_dim %d multiple of 32, vocab %d, max_seq %d)",
+                "2048, heads %d <= 8, ple_dim %d multiple of 32, vocab %d, max_seq %d)",
                 c.layers, G4_GEMMA_MAX_LAYERS, c.hidden, c.heads, c.ple_dim, c.vocab, c.max_seq);
   for (int i = 0; i < c.layers; ++i) {
     const int hd = c.head_dim[i];
@@ -737,6 +740,17 @@ G4_API int g4_gemma_reset(g4_gemma *m) {
 G4_API int g4_gemma_cache_length(const g4_gemma *m, int *len) {
   if (!m || !len) return fail(G4_E_ARG, "g4_gemma_cache_length: null argument");
   *len = m->cache_len;
+  return ok();
+}
+
+G4_API int g4_gemma_last_hidden(g4_gemma *m, float *last_hidden) {
+  G4_CHECK_INIT();
+  if (!m || !last_hidden) return fail(G4_E_ARG, "g4_gemma_last_hidden: null argument");
+  if (m->cache_len == 0) return fail(G4_E_STATE, "g4_gemma_last_hidden: no token has run");
+  int rc = check_device_range(last_hidden, (size_t)m->cfg.hidden * 4, "g4_gemma_last_hidden");
+  if (rc) return rc;
+  G4_HIP_TRY(hipMemcpyAsync(last_hidden, m->last, (size_t)m->cfg.hidden * 4,
+                            hipMemcpyDeviceToDevice, stream()));
   return ok();
 }
 

@@ -37,6 +37,9 @@ int cu_count();
 // encoder cannot record: inside an encoder a request beyond the current size
 // fails with G4_E_STATE and `who` in the message (make one call of that size
 // outside the encoder first).  Contents are not preserved across growth.
+// A block outgrown while a finished recording exists stays allocated until
+// the last recording is freed, so replaying an older recording never writes
+// through a stale scratch address into memory handed out since.
 struct Workspace {
   void *mem = nullptr;
   size_t bytes = 0;

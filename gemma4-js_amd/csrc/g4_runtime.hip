@@ -11,6 +11,8 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <vector>
+
 #include "g4_internal.h"
 
 namespace g4 {
@@ -19,6 +21,12 @@ namespace {
 thread_local char g_err[1024] = "";
 hipStream_t g_stream = nullptr;
 bool g_encoding = false;
+// Recordings alive (g4_encoder_finish .. g4_cmdbuf_free), and the scratch
+// blocks a Workspace outgrew while any of them was alive: a recording holds
+// the scratch address it was made with, so those blocks stay allocated until
+// the last recording is freed.
+int g_live_cmdbufs = 0;
+std::vector<void *> g_retired;
 int g_device = -1;
 int g_cu_count = 0;
 
@@ -194,8 +202,12 @@ int Workspace::get(size_t need, void **p, const char *who) {
                 "%s: scratch must grow to %zu bytes; make one call of this size outside a "
                 "command encoder first", who, need);
   if (mem) {
-    int rc = device_free(mem);
-    if (rc) return rc;
+    if (g_live_cmdbufs > 0) {
+      g_retired.push_back(mem);
+    } else {
+      int rc = device_free(mem);
+      if (rc) return rc;
+    }
     mem = nullptr;
     bytes = 0;
   }
@@ -381,6 +393,7 @@ G4_API int g4_encoder_finish(g4_cmdbuf **out) {
     return fail(G4_E_HIP, "hipGraphInstantiate failed: %s", hipGetErrorString(e));
   }
   *out = new g4_cmdbuf{graph, exec};
+  ++g_live_cmdbufs;
   return ok();
 }
 
@@ -400,5 +413,12 @@ G4_API int g4_cmdbuf_free(g4_cmdbuf *cb) {
   (void)hipGraphExecDestroy(cb->exec);
   (void)hipGraphDestroy(cb->graph);
   delete cb;
+  if (--g_live_cmdbufs == 0) {
+    for (void *p : g_retired) {
+      int rc = device_free(p);
+      if (rc) return rc;
+    }
+    g_retired.clear();
+  }
   return ok();
 }

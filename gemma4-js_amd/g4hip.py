@@ -88,6 +88,7 @@ SIGNATURES = {
     "g4_gemma_logits": (_int, [_vp, _vp, _vp]),
     "g4_gemma_greedy": (_int, [_vp, _vp, _int, _int, _c.POINTER(_c.c_int32), _vp]),
     "g4_gemma_decode": (_int, [_vp, _int, _vp]),
+    "g4_gemma_last_hidden": (_int, [_vp, _vp]),
 }
 
 # g4_fill_random kinds
@@ -492,6 +493,10 @@ class Gemma:
         check(lib().g4_gemma_greedy(self.h, ids.ctypes.data, ids.size, start_pos,
                                     ctypes.byref(tok), _f(logits)))
         return tok.value
+
+    def last_hidden(self, out):
+        """The final-norm hidden state of the last token run, into `out` (a Buffer)."""
+        check(lib().g4_gemma_last_hidden(self.h, _f(out)))
 
     def decode(self, steps, want_tokens=True):
         out = np.zeros(max(steps, 1), dtype=np.int32)

@@ -96,7 +96,9 @@ void *g4_stream(void);
  * must wait for the device or move host memory (g4_alloc, g4_free,
  * g4_upload, g4_download, g4_sync, g4_ple_gather with host ids, loads) fail
  * with G4_E_STATE while an encoder is open.  Unlike a WebGPU command buffer,
- * a finished recording may be submitted any number of times. */
+ * a finished recording may be submitted any number of times, also after
+ * later calls made the library's internal scratch grow: scratch outgrown
+ * while a recording exists is kept until the last recording is freed. */
 typedef struct g4_cmdbuf g4_cmdbuf;
 int g4_encoder_begin(void);
 int g4_encoder_finish(g4_cmdbuf **out);
@@ -317,7 +319,7 @@ int g4_fill_random(void *dst, size_t count, int kind, uint64_t seed,
 #define G4_GEMMA_MAX_LAYERS 64
 
 typedef struct {
-  int hidden;                          /* 1536 (HIDDEN)                       */
+  int hidden;                          /* 1536 (HIDDEN); multiple of 32, <= 2048 */
   int heads;                           /* query heads, <= 8; one KV head      */
   int ple_dim;                         /* 256 (PLE)                           */
   int vocab;                           /* 262144                              */
@@ -405,6 +407,12 @@ int g4_gemma_logits(g4_gemma *m, const float *last_hidden, float *logits);
  * (device [vocab]) may be NULL. */
 int g4_gemma_greedy(g4_gemma *m, const int32_t *ids, int n, int start_pos,
                     int32_t *next_token, float *logits);
+
+/* The final-norm hidden state of the last token the model ran (by
+ * g4_gemma_forward, g4_gemma_greedy or a g4_gemma_decode step) into device
+ * [hidden]: forward's lastHidden (gemma4-webgpu.js:394-400) for the decode
+ * loop, whose steps return only the token. */
+int g4_gemma_last_hidden(g4_gemma *m, float *last_hidden);
 
 /* `steps` further greedy tokens, each fed back as the next input (the
  * generation loop of custom-webgpu/main.js), from the state a g4_gemma_greedy

@@ -1,0 +1,163 @@
+"""The decode kernels that the Gemma-4-E2B shapes select, against the oracle.
+
+A 4-layer model at the E2B widths: hidden 1536, 8 query heads, PLE 256, a
+sliding layer (head dim 256, MLP 6144), a global layer (head dim 512, MLP
+6144, RoPE 1e6 / 0.25) and two later layers with MLP 12288 that reuse those
+layers' KV caches, as layers 15-34 of E2B do (gemma4-webgpu.js:65-77).  The
+vocabulary is 8192 rows.  At these widths the one-token step runs the fused
+GEMVs of the 1536-wide input (48 groups per row), the split down projection
+over 4 and 8 input slices, and the one-launch decode attention at head dims
+256 and 512; with max_seq 576 its key splits are 16 (sliding, 512-key window)
+and 24 (global) per head.
+
+A 520-token prompt (past the 512-key window) is prefilled, then 24 tokens
+are decoded by replaying the recorded step (and, separately, by one-token
+calls).  At the prompt and after every step the final-norm hidden state and
+the logits must be within relative L2 1e-3 of the float64 oracle model fed
+the same tokens (layer_oracle.DequantModel, gemma4-webgpu.js:215-481), and
+each chosen token must be the oracle's top-1 unless its top two logits are
+within 1e-3."""
+import copy
+
+import numpy as np
+import pytest
+
+import layer_oracle as lo
+import synthetic as syn
+
+pytestmark = pytest.mark.gpu
+
+H, HEADS, P, V, WINDOW = 1536, 8, 256, 8192, 512
+LAYERS = [
+    dict(head_dim=256, full=0, kv_source=-1, intermediate=6144, rope_base=1e4, rope_prop=1.0),
+    dict(head_dim=512, full=1, kv_source=-1, intermediate=6144, rope_base=1e6, rope_prop=0.25),
+    dict(head_dim=256, full=0, kv_source=0, intermediate=12288, rope_base=1e4, rope_prop=1.0),
+    dict(head_dim=512, full=1, kv_source=1, intermediate=12288, rope_base=1e6, rope_prop=0.25),
+]
+PROMPT, STEPS, MAX_SEQ, RPS = 520, 24, 576, 4096
+
+
+def rel(a, b):
+    a = np.asarray(a, np.float64).ravel()
+    b = np.asarray(b, np.float64).ravel()
+    return np.linalg.norm(a - b) / np.linalg.norm(b)
+
+
+def near_tie(logits, tok, tol=1e-3):
+    return float(np.max(logits) - logits[tok]) <= tol
+
+
+def config(g4):
+    c = g4.GemmaConfig()
+    c.hidden, c.heads, c.ple_dim, c.vocab = H, HEADS, P, V
+    c.layers, c.max_seq, c.window, c.eps, c.softcap = len(LAYERS), MAX_SEQ, WINDOW, 1e-6, 30.0
+    for i, L in enumerate(LAYERS):
+        c.head_dim[i], c.intermediate[i], c.full[i] = L["head_dim"], L["intermediate"], L["full"]
+        c.kv_source[i], c.rope_base[i], c.rope_prop[i] = L["kv_source"], L["rope_base"], L["rope_prop"]
+    return c
+
+
+@pytest.fixture(scope="module")
+def mid(g4):
+    NL = len(LAYERS)
+    rng = np.random.default_rng(1536)
+    E = syn.bf16_rne(rng.standard_normal((V, H), dtype=np.float32) * np.float32(0.03))
+    shards = [syn.ple_shard(17, s, RPS, NL * P) for s in range(V // RPS)]
+    table = np.concatenate(shards)
+    seed = [100]
+
+    def w(n, k):
+        seed[0] += 1
+        return syn.w4_weights(seed[0], n, k)[:2]
+
+    top = w(NL * P, H)
+    layers = []
+    for L in LAYERS:
+        hd, inter, shared = L["head_dim"], L["intermediate"], L["kv_source"] >= 0
+        shapes = dict(q=(HEADS * hd, H), o=(H, HEADS * hd), gate=(inter, H), up=(inter, H),
+                      down=(H, inter), ple_gate=(P, H), ple_proj=(H, P))
+        if not shared:
+            shapes.update(k=(hd, H), v=(hd, H))
+        lin = {name: w(n, k) for name, (n, k) in shapes.items()}
+        norm = {n: rng.uniform(0.9, 1.1, H).astype(np.float32)
+                for n in ("input", "post_attn", "pre_ffw", "post_ffw", "post_ple")}
+        norm["q"] = rng.uniform(0.9, 1.1, hd).astype(np.float32)
+        if not shared:
+            norm["k"] = rng.uniform(0.9, 1.1, hd).astype(np.float32)
+        layers.append(dict(L, linear=lin, norm=norm, skip=float(rng.uniform(0.9, 1.1))))
+    ple_norm = rng.uniform(0.9, 1.1, P).astype(np.float32)
+    final_norm = rng.uniform(0.9, 1.1, H).astype(np.float32)
+
+    def ple_rows(ids):
+        import g4oracle
+        return g4oracle.ple_gather(table, V, NL * P, RPS, ids)
+
+    ref = lo.DequantModel(H, HEADS, P, V, layers, E, ple_rows, top, ple_norm, final_norm,
+                          window=WINDOW)
+    ids = syn.token_ids(21, PROMPT, V)
+    h0 = ref.forward(ids, 0)
+    snapshot = copy.deepcopy((ref.k, ref.v, ref.length))
+
+    # device copies of every weight, shared by the engines of both tests
+    E_dev = g4.Buffer.from_array(E)
+    t = g4.PleTable(V, NL * P, 32, RPS)
+    for s, data in enumerate(shards):
+        t.upload_shard(s, data)
+    w_top = g4.W4Linear(*top)
+    w_layers = [{name: g4.W4Linear(*pw) for name, pw in L["linear"].items()} for L in layers]
+
+    def make_engine():
+        m = g4.Gemma(config(g4))
+        m.set_embedding(E_dev)
+        m.set_ple(t)
+        m.set_linear(-1, "top", w_top)
+        m.set_norm(-1, "ple_projection", ple_norm)
+        m.set_norm(-1, "final", final_norm)
+        for i, L in enumerate(layers):
+            for name, lin in w_layers[i].items():
+                m.set_linear(i, name, lin)
+            for name, v in L["norm"].items():
+                m.set_norm(i, name, v)
+            m.set_layer_scalar(i, L["skip"])
+        return m
+
+    def restore():
+        ref.k, ref.v, ref.length = copy.deepcopy(snapshot)
+
+    return dict(ref=ref, ids=ids, h0=h0, restore=restore, make=make_engine)
+
+
+@pytest.mark.parametrize("mode", ["graph", "eager"])
+def test_e2b_widths_prefill_past_window_then_decode_match_oracle(g4, mid, mode):
+    ref, ids = mid["ref"], mid["ids"]
+    m = mid["make"]()
+    lg = g4.Buffer(V * 4)
+    hb = g4.Buffer(H * 4)
+    tok = m.greedy(ids, 0, lg)
+    m.last_hidden(hb)
+    want_lg = ref.logits(mid["h0"])
+    assert rel(hb.download(np.float32), mid["h0"]) < 1e-3
+    assert rel(lg.download(np.float32), want_lg) < 1e-3
+    assert tok == int(np.argmax(want_lg)) or near_tie(want_lg, tok)
+    mid["restore"]()
+    prev, pos = tok, PROMPT
+    worst = 0.0
+    for s in range(STEPS):
+        if mode == "graph":
+            t = int(m.decode(1)[0])  # replays the step recorded for max_seq keys
+            m.last_hidden(hb)
+            m.logits(hb, lg)
+        else:
+            t = m.greedy([prev], pos, lg)
+            m.last_hidden(hb)
+        got_h, got_lg = hb.download(np.float32), lg.download(np.float32)
+        want_h = ref.forward([prev], pos)
+        want_lg = ref.logits(want_h)
+        eh, el = rel(got_h, want_h), rel(got_lg, want_lg)
+        worst = max(worst, eh, el)
+        assert eh < 1e-3 and el < 1e-3, (mode, s, pos, eh, el)
+        assert t == int(np.argmax(got_lg)), (mode, s, t)  # the step's own argmax
+        assert t == int(np.argmax(want_lg)) or near_tie(want_lg, t), (mode, s, t)
+        prev, pos = t, pos + 1
+    assert m.cache_length() == PROMPT + STEPS
+    print("%s: worst relative L2 over %d steps %.2e" % (mode, STEPS, worst))

@@ -242,6 +242,15 @@ def test_tiny_kv_errors_and_reset(g4, tiny):
     m.greedy(ids, 0)
 
 
+def test_hidden_beyond_the_prefill_row_limit_is_refused_at_create(g4):
+    # a config the prefill could not run fails at creation, before any KV row
+    c = tiny_config(g4)
+    c.hidden = 4096
+    with pytest.raises(g4.G4Error, match="hidden 4096 multiple of 32 <= 2048") as e:
+        g4.Gemma(c)
+    assert e.value.code == g4.G4_E_ARG
+
+
 def test_unset_weights_are_reported(g4):
     m = g4.Gemma(tiny_config(g4))
     with pytest.raises(g4.G4Error, match="not set"):
@@ -284,3 +293,47 @@ def test_e2b_prefill_equals_two_part_prefill(g4, e2b):
     a, b = h1.download(np.float32), h2.download(np.float32)
     assert np.all(np.isfinite(a))
     assert rel(b, a) < 1e-3
+
+
+@pytest.fixture(scope="module")
+def e2b_1024(g4):
+    import e2b
+    cfg = g4.e2b_config(1024)
+    return e2b.build(cfg, seed=4), cfg
+
+
+def test_e2b_config4_prompt512_then_256_graph_steps(g4, e2b_1024):
+    # The benchmark's decode workload at its size: prompt 512, 256 replays of
+    # the step recorded for 1024 keys (16 key splits per sliding head, 32 per
+    # global head), sliding windows past position 512.  Feeding the graph's
+    # own tokens, one-token calls over the first 32 positions, and a 736-token
+    # prefill followed by one-token calls over the last 32, must choose the
+    # same tokens (or a token within 1e-3 of the top logit).
+    m, cfg = e2b_1024
+    V = cfg.vocab
+    ids = syn.token_ids(4, 512, V)
+    m.reset()
+    t0 = m.greedy(ids, 0)
+    graph = m.decode(256)  # fails if a step finds no finite logit
+    assert m.cache_length() == 768
+    hb, lg = g4.Buffer(cfg.hidden * 4), g4.Buffer(V * 4)
+    m.last_hidden(hb)
+    m.logits(hb, lg)
+    assert np.all(np.isfinite(hb.download(np.float32)))
+    assert np.all(np.isfinite(lg.download(np.float32)))
+    fed = np.concatenate([[t0], graph]).astype(np.int32)  # fed[s] runs at position 512 + s
+
+    def check(step, tok):
+        logits = lg.download(np.float32)
+        assert np.all(np.isfinite(logits)), step
+        assert tok == graph[step] or near_tie(logits, int(graph[step])), (step, tok, graph[step])
+
+    m.reset()
+    assert m.greedy(ids, 0) == t0
+    for s in range(32):
+        check(s, m.greedy([fed[s]], 512 + s, lg))
+    m.reset()
+    seq = np.concatenate([ids, fed[:224]]).astype(np.int32)  # positions 0..735
+    check(223, m.greedy(seq, 0, lg))
+    for s in range(224, 256):
+        check(s, m.greedy([fed[s]], 512 + s, lg))

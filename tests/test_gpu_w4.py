@@ -201,6 +201,42 @@ def test_gemm_matches_gemv_path(g4):
         assert rel_l2_rows(big[r:r + 1], ref[r:r + 1]) < 1e-4
 
 
+def test_recording_survives_scratch_growth(g4):
+    # A GEMM-path linear recorded into a command buffer holds the library's
+    # scratch address.  A later, larger eager call grows the scratch; the old
+    # block must not be handed out again while the recording exists, so a
+    # replay still computes the recorded call and touches no newer buffer.
+    n, k, rows, big = 256, 2048, 16, 16384
+    packed, scales, _ = syn.w4_weights(31, n, k)
+    lin = g4.W4Linear(packed, scales)
+    _, x = syn.activations(31, rows, k)
+    xb = g4.Buffer.from_array(x)
+    y_ref, y_rec = g4.Buffer(rows * n * 4), g4.Buffer(rows * n * 4)
+    lin.linear(xb.ptr, g4.F32, rows, y_ref.ptr, g4.F32)
+    with g4.Encoder() as enc:
+        lin.linear(xb.ptr, g4.F32, rows, y_rec.ptr, g4.F32)
+    cb = enc.cmdbuf
+    xbig = g4.Buffer(big * k * 4)
+    xbig.upload(np.tile(x, (big // rows, 1)))
+    ybig = g4.Buffer(big * n * 4)
+    lin.linear(xbig.ptr, g4.F32, big, ybig.ptr, g4.F32)  # grows the scratch
+    pattern = np.full(1 << 20, 0x5A5A5A5A, np.uint32)
+    probes = []
+    for size in (1 << 16, 1 << 20, 1 << 22, 1 << 24, 1 << 25):
+        b = g4.Buffer(size)
+        b.upload(np.resize(pattern, size // 4))
+        probes.append(b)
+    for _ in range(3):
+        cb.submit()
+    got = y_rec.download(np.float32)
+    assert np.array_equal(got.view(np.uint32), y_ref.download(np.float32).view(np.uint32))
+    for b in probes:
+        assert np.all(b.download(np.uint32) == 0x5A5A5A5A)
+    np.testing.assert_array_equal(ybig.download(np.float32).reshape(big, n)[:rows],
+                                  y_ref.download(np.float32).reshape(rows, n))
+    cb.free()
+
+
 def test_errors_are_reported_not_faulted(g4):
     packed, scales, _ = syn.w4_weights(1, 256, 512)
     lin = g4.W4Linear(packed, scales)
