@@ -7,12 +7,13 @@ layers' KV caches, as layers 15-34 of E2B do (gemma4-webgpu.js:65-77).  The
 vocabulary is 8192 rows.  At these widths the one-token step runs the fused
 GEMVs of the 1536-wide input (48 groups per row), the split down projection
 over 4 and 8 input slices, and the one-launch decode attention at head dims
-256 and 512; with max_seq 576 its key splits are 16 (sliding, 512-key window)
-and 24 (global) per head.
+256 and 512, whose key splits per head are 16 (sliding, 512-key window) and
+24 (global, max_seq 576) or 32 (global, max_seq 1024).
 
-A 520-token prompt (past the 512-key window) is prefilled, then 24 tokens
-are decoded by replaying the recorded step (and, separately, by one-token
-calls).  At the prompt and after every step the final-norm hidden state and
+A 520-token prompt (past the 512-key window; max_seq 576) or a 1000-token
+prompt (max_seq 1024, the global layers' longest key range) is prefilled,
+then 24 tokens are decoded by replaying the recorded step (and, separately,
+by one-token calls).  At the prompt and after every step the final-norm hidden state and
 the logits must be within relative L2 1e-3 of the float64 oracle model fed
 the same tokens (layer_oracle.DequantModel, gemma4-webgpu.js:215-481), and
 each chosen token must be the oracle's top-1 unless its top two logits are
@@ -34,7 +35,8 @@ LAYERS = [
     dict(head_dim=256, full=0, kv_source=0, intermediate=12288, rope_base=1e4, rope_prop=1.0),
     dict(head_dim=512, full=1, kv_source=1, intermediate=12288, rope_base=1e6, rope_prop=0.25),
 ]
-PROMPT, STEPS, MAX_SEQ, RPS = 520, 24, 576, 4096
+STEPS, RPS = 24, 4096
+CASES = [(520, 576), (1000, 1024)]  # (prompt, max_seq)
 
 
 def rel(a, b):
@@ -47,10 +49,10 @@ def near_tie(logits, tok, tol=1e-3):
     return float(np.max(logits) - logits[tok]) <= tol
 
 
-def config(g4):
+def config(g4, max_seq):
     c = g4.GemmaConfig()
     c.hidden, c.heads, c.ple_dim, c.vocab = H, HEADS, P, V
-    c.layers, c.max_seq, c.window, c.eps, c.softcap = len(LAYERS), MAX_SEQ, WINDOW, 1e-6, 30.0
+    c.layers, c.max_seq, c.window, c.eps, c.softcap = len(LAYERS), max_seq, WINDOW, 1e-6, 30.0
     for i, L in enumerate(LAYERS):
         c.head_dim[i], c.intermediate[i], c.full[i] = L["head_dim"], L["intermediate"], L["full"]
         c.kv_source[i], c.rope_base[i], c.rope_prop[i] = L["kv_source"], L["rope_base"], L["rope_prop"]
@@ -94,9 +96,22 @@ def mid(g4):
 
     ref = lo.DequantModel(H, HEADS, P, V, layers, E, ple_rows, top, ple_norm, final_norm,
                           window=WINDOW)
-    ids = syn.token_ids(21, PROMPT, V)
-    h0 = ref.forward(ids, 0)
-    snapshot = copy.deepcopy((ref.k, ref.v, ref.length))
+    prefills = {}
+
+    def prefill(prompt):
+        """The oracle after the prompt (computed once per prompt length): the
+        ids, the final-norm hidden state, and a function restoring the state."""
+        if prompt not in prefills:
+            ref.reset()
+            ids = syn.token_ids(21, prompt, V)
+            h0 = ref.forward(ids, 0)
+            prefills[prompt] = (ids, h0, copy.deepcopy((ref.k, ref.v, ref.length)))
+        ids, h0, snap = prefills[prompt]
+
+        def restore():
+            ref.k, ref.v, ref.length = copy.deepcopy(snap)
+
+        return ids, h0, restore
 
     # device copies of every weight, shared by the engines of both tests
     E_dev = g4.Buffer.from_array(E)
@@ -106,8 +121,8 @@ def mid(g4):
     w_top = g4.W4Linear(*top)
     w_layers = [{name: g4.W4Linear(*pw) for name, pw in L["linear"].items()} for L in layers]
 
-    def make_engine():
-        m = g4.Gemma(config(g4))
+    def make_engine(max_seq):
+        m = g4.Gemma(config(g4, max_seq))
         m.set_embedding(E_dev)
         m.set_ple(t)
         m.set_linear(-1, "top", w_top)
@@ -121,26 +136,25 @@ def mid(g4):
             m.set_layer_scalar(i, L["skip"])
         return m
 
-    def restore():
-        ref.k, ref.v, ref.length = copy.deepcopy(snapshot)
-
-    return dict(ref=ref, ids=ids, h0=h0, restore=restore, make=make_engine)
+    return dict(ref=ref, prefill=prefill, make=make_engine)
 
 
 @pytest.mark.parametrize("mode", ["graph", "eager"])
-def test_e2b_widths_prefill_past_window_then_decode_match_oracle(g4, mid, mode):
-    ref, ids = mid["ref"], mid["ids"]
-    m = mid["make"]()
+@pytest.mark.parametrize("prompt,max_seq", CASES)
+def test_e2b_widths_prefill_past_window_then_decode_match_oracle(g4, mid, prompt, max_seq, mode):
+    ref = mid["ref"]
+    ids, h0, restore = mid["prefill"](prompt)
+    m = mid["make"](max_seq)
     lg = g4.Buffer(V * 4)
     hb = g4.Buffer(H * 4)
     tok = m.greedy(ids, 0, lg)
     m.last_hidden(hb)
-    want_lg = ref.logits(mid["h0"])
-    assert rel(hb.download(np.float32), mid["h0"]) < 1e-3
+    want_lg = ref.logits(h0)
+    assert rel(hb.download(np.float32), h0) < 1e-3
     assert rel(lg.download(np.float32), want_lg) < 1e-3
     assert tok == int(np.argmax(want_lg)) or near_tie(want_lg, tok)
-    mid["restore"]()
-    prev, pos = tok, PROMPT
+    restore()
+    prev, pos = tok, prompt
     worst = 0.0
     for s in range(STEPS):
         if mode == "graph":
@@ -159,5 +173,5 @@ def test_e2b_widths_prefill_past_window_then_decode_match_oracle(g4, mid, mode):
         assert t == int(np.argmax(got_lg)), (mode, s, t)  # the step's own argmax
         assert t == int(np.argmax(want_lg)) or near_tie(want_lg, t), (mode, s, t)
         prev, pos = t, pos + 1
-    assert m.cache_length() == PROMPT + STEPS
-    print("%s: worst relative L2 over %d steps %.2e" % (mode, STEPS, worst))
+    assert m.cache_length() == prompt + STEPS
+    print("%s, prompt %d: worst relative L2 over %d steps %.2e" % (mode, prompt, STEPS, worst))

@@ -303,37 +303,40 @@ def e2b_1024(g4):
 
 
 def test_e2b_config4_prompt512_then_256_graph_steps(g4, e2b_1024):
-    # The benchmark's decode workload at its size: prompt 512, 256 replays of
-    # the step recorded for 1024 keys (16 key splits per sliding head, 32 per
-    # global head), sliding windows past position 512.  Feeding the graph's
-    # own tokens, one-token calls over the first 32 positions, and a 736-token
-    # prefill followed by one-token calls over the last 32, must choose the
-    # same tokens (or a token within 1e-3 of the top logit).
+    # The benchmark's decode workload at its size: prompt 512, then 256
+    # replays of the step recorded for 1024 keys (16 key splits per sliding
+    # head, 32 per global head) over positions 512-767, past the 512-key
+    # window.  One-token calls from the same prompt, fed the graph's tokens,
+    # pick their key splits from the actual length instead (24 per global
+    # head here); at every one of the 256 positions they must choose the
+    # graph's token (or one within 1e-3 of their top logit), with logits
+    # within relative L2 5e-3 of the graph's.  (A prefill of the whole
+    # sequence is not compared token by token: in this random-init 35-layer
+    # model the attention logits q.k have a spread of about 16-22 - the
+    # reference applies no 1/sqrt(head_dim) - and amplify the rounding
+    # difference between the prefill GEMM and the decode GEMV to a few percent
+    # of the logits.  The four-layer E2B-width test bounds both paths against
+    # the float64 oracle instead.)
     m, cfg = e2b_1024
     V = cfg.vocab
     ids = syn.token_ids(4, 512, V)
+    hb, lg = g4.Buffer(cfg.hidden * 4), g4.Buffer(V * 4)
     m.reset()
     t0 = m.greedy(ids, 0)
-    graph = m.decode(256)  # fails if a step finds no finite logit
+    graph, glog = [], []
+    for s in range(256):
+        graph.append(int(m.decode(1)[0]))  # fails if a step finds no finite logit
+        m.last_hidden(hb)
+        m.logits(hb, lg)
+        glog.append(lg.download(np.float32))
+        assert np.all(np.isfinite(glog[-1])), s
     assert m.cache_length() == 768
-    hb, lg = g4.Buffer(cfg.hidden * 4), g4.Buffer(V * 4)
-    m.last_hidden(hb)
-    m.logits(hb, lg)
-    assert np.all(np.isfinite(hb.download(np.float32)))
-    assert np.all(np.isfinite(lg.download(np.float32)))
-    fed = np.concatenate([[t0], graph]).astype(np.int32)  # fed[s] runs at position 512 + s
-
-    def check(step, tok):
-        logits = lg.download(np.float32)
-        assert np.all(np.isfinite(logits)), step
-        assert tok == graph[step] or near_tie(logits, int(graph[step])), (step, tok, graph[step])
-
+    fed = [t0] + graph  # fed[s] runs at position 512 + s
     m.reset()
     assert m.greedy(ids, 0) == t0
-    for s in range(32):
-        check(s, m.greedy([fed[s]], 512 + s, lg))
-    m.reset()
-    seq = np.concatenate([ids, fed[:224]]).astype(np.int32)  # positions 0..735
-    check(223, m.greedy(seq, 0, lg))
-    for s in range(224, 256):
-        check(s, m.greedy([fed[s]], 512 + s, lg))
+    for s in range(256):
+        tok = m.greedy([fed[s]], 512 + s, lg)
+        eager = lg.download(np.float32)
+        assert np.all(np.isfinite(eager)), s
+        assert rel(eager, glog[s]) < 5e-3, (s, rel(eager, glog[s]))
+        assert tok == graph[s] or near_tie(eager, graph[s]), (s, tok, graph[s])

@@ -232,8 +232,9 @@ def test_recording_survives_scratch_growth(g4):
     assert np.array_equal(got.view(np.uint32), y_ref.download(np.float32).view(np.uint32))
     for b in probes:
         assert np.all(b.download(np.uint32) == 0x5A5A5A5A)
-    np.testing.assert_array_equal(ybig.download(np.float32).reshape(big, n)[:rows],
-                                  y_ref.download(np.float32).reshape(rows, n))
+    # the large call tiles differently; its rows agree to FP32 rounding
+    ybig_rows = ybig.download(np.float32).reshape(big, n)[:rows].astype(np.float64)
+    assert rel_l2_rows(ybig_rows, y_ref.download(np.float32).reshape(rows, n).astype(np.float64)) < 1e-5
     cb.free()
 
 
