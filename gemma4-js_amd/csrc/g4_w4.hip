@@ -807,15 +807,15 @@ G4_API int g4_w4_linear(const g4_w4 *w, const void *x, int x_dtype, int rows,
   rc = check_device_range(y, (size_t)rows * w->N * ye, "g4_w4_linear y");
   if (rc) return rc;
   const bool f32x = x_dtype == G4_F32;
-  if (gemv_lds_per_row(w->K, f32x) > kGemvLdsBudget)
-    return fail(G4_E_ARG, "g4_w4_linear: in_dim %d exceeds the GEMV staging limit (%s x)",
-                w->K, f32x ? "FP32" : "BF16");
-  if (rows == 1 && has_gemv1_plan(w->G, f32x)) {
+  // The GEMVs stage a whole activation row in LDS; a longer in_dim (like any
+  // row count above kMaxGemvRows) takes the GEMM, which streams x' tiles.
+  const bool gemv_fits = gemv_lds_per_row(w->K, f32x) <= kGemvLdsBudget;
+  if (rows == 1 && gemv_fits && has_gemv1_plan(w->G, f32x)) {
     rc = f32x ? launch_gemv1<true>(w, x, y, y_dtype == G4_BF16)
               : launch_gemv1<false>(w, x, y, y_dtype == G4_BF16);
     return rc ? rc : ok();
   }
-  if (rows > kMaxGemvRows) {
+  if (rows > kMaxGemvRows || !gemv_fits) {
     rc = w4_gemm(w, x, f32x, rows, y, y_dtype == G4_BF16);
     return rc ? rc : ok();
   }
@@ -863,10 +863,9 @@ G4_API int g4_w4_linear_multi(const g4_w4 *const *w, int n, const void *x, int x
   for (int i = 0; i < n; ++i)
     if ((rc = check_device_range(y[i], (size_t)rows * w[i]->N * ye, "g4_w4_linear_multi y")))
       return rc;
-  if (gemv_lds_per_row(w[0]->K, f32x) > kGemvLdsBudget)
-    return fail(G4_E_ARG, "g4_w4_linear_multi: in_dim %d exceeds the GEMV staging limit (%s x)",
-                w[0]->K, f32x ? "FP32" : "BF16");
-  if (rows > 1) {  // more than kMaxGemvRows: one x pre-pass, one GEMM launch when it fills
+  // more than kMaxGemvRows, or an in_dim beyond the GEMV's LDS staging: one
+  // x pre-pass, one GEMM launch when it fills
+  if (rows > 1 || gemv_lds_per_row(w[0]->K, f32x) > kGemvLdsBudget) {
     rc = w4_gemm_multi(w, n, x, f32x, rows, y, y_dtype == G4_BF16);
     return rc ? rc : ok();
   }

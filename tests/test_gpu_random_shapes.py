@@ -62,6 +62,31 @@ def test_random_linear(g4, seed):
                           syn.bf16_rne(got).reshape(rows, n)), (rows, n, k, f32x)
 
 
+@pytest.mark.parametrize("k", [16384, 32768])
+@pytest.mark.parametrize("rows", [1, 3, 40])
+@pytest.mark.parametrize("f32x", [False, True])
+def test_long_in_dim_linear(g4, k, rows, f32x):
+    # in_dims whose activation row no longer fits the GEMVs' LDS staging
+    # (32768 BF16, 16384 and 32768 FP32) take the GEMM at every row count;
+    # the reference's GPUOps.w4 takes any inDim
+    rng = np.random.default_rng([k, rows, f32x])
+    n = 300
+    packed, scales, q = syn.w4_weights(k + rows, n, k)
+    lin = g4.W4Linear(packed, scales)
+    xb, x, xd = activations(g4, rng, rows, k, f32x)
+    y32 = g4.Buffer(rows * n * 4)
+    lin.linear(xb.ptr, xd, rows, y32.ptr, g4.F32)
+    ref = x.astype(np.float64) @ dense(q, scales).T
+    assert rel_l2_rows(y32.download(np.float32).reshape(rows, n), ref) <= 1e-4
+    ys = [g4.Buffer(rows * w * 4) for w in (64, 200)]
+    lins = [g4.W4Linear(*syn.w4_weights(k + w, w, k)[:2]) for w in (64, 200)]
+    g4.W4Linear.linear_multi(lins, xb.ptr, xd, rows, [b.ptr for b in ys], g4.F32)
+    for w, lw, yb in zip((64, 200), lins, ys):
+        _, sc, qq = syn.w4_weights(k + w, w, k)
+        r = x.astype(np.float64) @ dense(qq, sc).T
+        assert rel_l2_rows(yb.download(np.float32).reshape(rows, w), r) <= 1e-4
+
+
 @pytest.mark.parametrize("seed", range(16))
 def test_random_linear_multi(g4, seed):
     rng, rows, _, k, f32x = draw(100 + seed)
