@@ -737,7 +737,7 @@ void xprep_layout(int K, int rows, bool f32x, int *Mp, size_t *eoff, size_t *xen
 }
 
 int gemm_scratch(const g4_w4 *const *w, int nw, bool f32x, int rows, bool prepped,
-                 GemmScratch *sc) {
+                 GemmScratch *sc, const ExtScratch *ext) {
   const g4_w4 *w0 = w[0];
   size_t eoff, xend;
   xprep_layout(w0->K, rows, f32x, &sc->Mp, &eoff, &xend);
@@ -746,6 +746,20 @@ int gemm_scratch(const g4_w4 *const *w, int nw, bool f32x, int rows, bool preppe
   const size_t part_bytes =
       sc->plan.slices > 1 ? sc->plan.slices * splitk_pstride(rows, w0->N) * 4 : 0;
   void *ws = nullptr, *wx = nullptr;
+  if (ext) {
+    // one region: x', exponents, then the K-slice planes (x is never prepared here)
+    if (prepped) return fail(G4_E_ARG, "%s: a prepared x needs the library scratch", ext->who);
+    if (poff + part_bytes > ext->bytes)
+      return fail(G4_E_ARG,
+                  "%s: %d rows of in_dim %d (%s x) into out_dim %d need %zu bytes of scratch; "
+                  "the static scratch holds %zu",
+                  ext->who, rows, w0->K, f32x ? "FP32" : "BF16", w0->N, poff + part_bytes,
+                  ext->bytes);
+    sc->xt = static_cast<uint4 *>(ext->mem);
+    sc->xe = reinterpret_cast<int *>(static_cast<char *>(ext->mem) + eoff);
+    sc->part = reinterpret_cast<float *>(static_cast<char *>(ext->mem) + poff);
+    return G4_OK;
+  }
   if (poff + part_bytes > 0)
     if (int rc = g_ws.get(poff + part_bytes, &ws, "g4_w4_linear (prefill)")) return rc;
   if (prepped) {
@@ -762,7 +776,8 @@ int gemm_scratch(const g4_w4 *const *w, int nw, bool f32x, int rows, bool preppe
 // x == nullptr: x' and the row exponents are already in the scratch
 // (written by the producer after w4_gemm_prepare).
 static int gemm_run(const g4_w4 *const *w, int nw, const void *x, bool f32x, int rows,
-                    void *const *y, bool y_bf16, GemmParts *keep, bool glu = false) {
+                    void *const *y, bool y_bf16, GemmParts *keep, bool glu = false,
+                    const ExtScratch *ext = nullptr) {
   // weights whose joint grid still leaves CUs idle run one by one (each may
   // then split K); not with x' prepared, whose scratch is sized for the joint call
   const int cus = cu_count() > 0 ? cu_count() : 256;
@@ -775,7 +790,7 @@ static int gemm_run(const g4_w4 *const *w, int nw, const void *x, bool f32x, int
   }
   const g4_w4 *w0 = w[0];
   GemmScratch sc;
-  if (int rc = gemm_scratch(w, nw, f32x, rows, !x, &sc)) return rc;
+  if (int rc = gemm_scratch(w, nw, f32x, rows, !x, &sc, ext)) return rc;
   const GemmPlan plan = sc.plan;
   const int Mp = sc.Mp;
   uint4 *xt = sc.xt;
@@ -845,6 +860,11 @@ int w4_gemm(const g4_w4 *w, const void *x, bool f32x, int rows, void *y, bool y_
   return gemm_run(&w, 1, x, f32x, rows, &y, y_bf16, nullptr);
 }
 
+int w4_gemm_ext(const g4_w4 *w, const void *x, bool f32x, int rows, void *y, bool y_bf16,
+                const ExtScratch &ext) {
+  return gemm_run(&w, 1, x, f32x, rows, &y, y_bf16, nullptr, false, &ext);
+}
+
 int w4_gemm_glu(const g4_w4 *gate, const g4_w4 *up, const float *x, int rows, float *act) {
   if (gate->N != up->N || gate->K != up->K)
     return fail(G4_E_ARG, "w4_gemm_glu: gate [%d, %d] and up [%d, %d] differ", gate->N, gate->K,
@@ -873,3 +893,44 @@ int w4_gemm_parts(const g4_w4 *w, const float *x, int rows, float *y, GemmParts 
 }
 
 }  // namespace g4
+
+// ---- allocation-free linear ------------------------------------------------
+// The GEMM scratch of g4_w4_linear_noalloc: one static array per device,
+// allocated with the code object when the library loads on a device and held
+// until the process ends.  Host code must not pass `scratch` itself to a
+// kernel (in host code the name is a host-side stand-in, not a device
+// address): static_scratch_init looks up each device's address once, with
+// that device current, and every launch takes that address.
+constexpr size_t kStaticScratchBytes = size_t(64) << 20;
+constexpr int kMaxScratchDevices = 64;
+static __device__ __align__(256) unsigned char scratch[kStaticScratchBytes];
+
+namespace {
+void *g_static_scratch[kMaxScratchDevices];
+}  // namespace
+
+namespace g4 {
+
+int static_scratch_init(int device) {
+  if (device < 0 || device >= kMaxScratchDevices)
+    return fail(G4_E_ARG, "static scratch: device %d beyond %d", device, kMaxScratchDevices);
+  if (g_static_scratch[device]) return G4_OK;
+  void *p = nullptr;
+  const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+  if (e != hipSuccess || !p)
+    return fail(G4_E_HIP, "hipGetSymbolAddress(scratch) failed: %s", hipGetErrorString(e));
+  g_static_scratch[device] = p;
+  return G4_OK;
+}
+
+}  // namespace g4
+
+G4_API int g4_w4_linear_noalloc(const g4_w4 *w, const void *x, int x_dtype, int rows, void *y,
+                                int y_dtype) {
+  G4_CHECK_INIT();
+  void *mem = g_static_scratch[current_device()];
+  if (!mem) return fail(G4_E_STATE, "g4_w4_linear_noalloc: static scratch not set up");
+  const ExtScratch ext{mem, kStaticScratchBytes, "g4_w4_linear_noalloc"};
+  const int rc = w4_linear_impl(w, x, x_dtype, rows, y, y_dtype, &ext, "g4_w4_linear_noalloc");
+  return rc ? rc : ok();
+}

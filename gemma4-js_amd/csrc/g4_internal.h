@@ -32,6 +32,8 @@ int device_free(void *p);
 
 // Device attribute cache.
 int cu_count();
+// The device g4_init selected.
+int current_device();
 
 // Scratch memory that grows on demand.  Growing allocates, which a command
 // encoder cannot record: inside an encoder a request beyond the current size
@@ -133,6 +135,23 @@ constexpr int kMaxGemvRows = 4;
 // Prefill GEMM (more than kMaxGemvRows rows): y[rows, N] = x[rows, K] . W^T on
 // the matrix cores (g4_gemm.hip).
 int w4_gemm(const g4_w4 *w, const void *x, bool f32x, int rows, void *y, bool y_bf16);
+// Caller-provided scratch for the GEMM (x', row exponents, K-slice planes)
+// instead of the library's growing workspace: nothing is allocated, and a
+// call whose scratch would exceed `bytes` fails with G4_E_ARG naming `who`.
+struct ExtScratch {
+  void *mem;
+  size_t bytes;
+  const char *who;
+};
+int w4_gemm_ext(const g4_w4 *w, const void *x, bool f32x, int rows, void *y, bool y_bf16,
+                const ExtScratch &ext);
+// g4_w4_linear's argument checks and dispatch; with ext set, the GEMM path
+// uses that scratch (the GEMV paths use none).
+int w4_linear_impl(const g4_w4 *w, const void *x, int x_dtype, int rows, void *y, int y_dtype,
+                   const ExtScratch *ext, const char *who);
+// Per-device address of the static GEMM scratch of g4_w4_linear_noalloc,
+// looked up once when the library is initialised on a device.
+int static_scratch_init(int device);
 // nw (1..3) weights of one input dimension over the same x, y[i] receiving
 // weight i's output: one x pre-pass and, when their joint grid fills the CUs,
 // one GEMM launch.

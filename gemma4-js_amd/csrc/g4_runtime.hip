@@ -88,6 +88,7 @@ int ok() {
 hipStream_t stream() { return g_stream; }
 bool initialised() { return g_stream != nullptr; }
 bool encoding() { return g_encoding; }
+int current_device() { return g_device; }
 int cu_count() { return g_cu_count; }
 
 int check_device_range(const void *p, size_t bytes, const char *what) {
@@ -240,6 +241,7 @@ G4_API int g4_init(int device) {
     return fail(G4_E_STATE, "g4_init: device %d is %s; this library is built for gfx950",
                 device, prop.gcnArchName);
   g_cu_count = prop.multiProcessorCount;
+  if (int rc = static_scratch_init(device)) return rc;
   hipStream_t s = nullptr;
   G4_HIP_TRY(hipStreamCreateWithFlags(&s, hipStreamNonBlocking));
   g_stream = s;

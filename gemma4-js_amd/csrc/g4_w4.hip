@@ -791,16 +791,15 @@ G4_API int g4_w4_info(const g4_w4 *w, int *out_dim, int *in_dim, int *group,
   return ok();
 }
 
-G4_API int g4_w4_linear(const g4_w4 *w, const void *x, int x_dtype, int rows,
-                        void *y, int y_dtype) {
-  G4_CHECK_INIT();
-  if (!w) return fail(G4_E_ARG, "g4_w4_linear: null weight handle");
-  if (rows <= 0) return fail(G4_E_ARG, "g4_w4_linear: rows must be positive, got %d", rows);
-  if (x_dtype != G4_F32 && x_dtype != G4_BF16)
-    return fail(G4_E_ARG, "g4_w4_linear: bad x dtype %d", x_dtype);
-  if (y_dtype != G4_F32 && y_dtype != G4_BF16)
-    return fail(G4_E_ARG, "g4_w4_linear: bad y dtype %d", y_dtype);
-  if (!aligned16(x)) return fail(G4_E_ARG, "g4_w4_linear: x must be 16-byte aligned");
+namespace g4 {
+
+int w4_linear_impl(const g4_w4 *w, const void *x, int x_dtype, int rows, void *y, int y_dtype,
+                   const ExtScratch *ext, const char *who) {
+  if (!w) return fail(G4_E_ARG, "%s: null weight handle", who);
+  if (rows <= 0) return fail(G4_E_ARG, "%s: rows must be positive, got %d", who, rows);
+  if (x_dtype != G4_F32 && x_dtype != G4_BF16) return fail(G4_E_ARG, "%s: bad x dtype %d", who, x_dtype);
+  if (y_dtype != G4_F32 && y_dtype != G4_BF16) return fail(G4_E_ARG, "%s: bad y dtype %d", who, y_dtype);
+  if (!aligned16(x)) return fail(G4_E_ARG, "%s: x must be 16-byte aligned", who);
   const size_t xe = x_dtype == G4_F32 ? 4 : 2, ye = y_dtype == G4_F32 ? 4 : 2;
   int rc = check_device_range(x, (size_t)rows * w->K * xe, "g4_w4_linear x");
   if (rc) return rc;
@@ -810,15 +809,12 @@ G4_API int g4_w4_linear(const g4_w4 *w, const void *x, int x_dtype, int rows,
   // The GEMVs stage a whole activation row in LDS; a longer in_dim (like any
   // row count above kMaxGemvRows) takes the GEMM, which streams x' tiles.
   const bool gemv_fits = gemv_lds_per_row(w->K, f32x) <= kGemvLdsBudget;
-  if (rows == 1 && gemv_fits && has_gemv1_plan(w->G, f32x)) {
-    rc = f32x ? launch_gemv1<true>(w, x, y, y_dtype == G4_BF16)
-              : launch_gemv1<false>(w, x, y, y_dtype == G4_BF16);
-    return rc ? rc : ok();
-  }
-  if (rows > kMaxGemvRows || !gemv_fits) {
-    rc = w4_gemm(w, x, f32x, rows, y, y_dtype == G4_BF16);
-    return rc ? rc : ok();
-  }
+  if (rows == 1 && gemv_fits && has_gemv1_plan(w->G, f32x))
+    return f32x ? launch_gemv1<true>(w, x, y, y_dtype == G4_BF16)
+                : launch_gemv1<false>(w, x, y, y_dtype == G4_BF16);
+  if (rows > kMaxGemvRows || !gemv_fits)
+    return ext ? w4_gemm_ext(w, x, f32x, rows, y, y_dtype == G4_BF16, *ext)
+               : w4_gemm(w, x, f32x, rows, y, y_dtype == G4_BF16);
   const int per = gemv_rows_per_launch(w->K, f32x);
   for (int r0 = 0; r0 < rows; r0 += per) {
     const int m = rows - r0 < per ? rows - r0 : per;
@@ -828,7 +824,16 @@ G4_API int g4_w4_linear(const g4_w4 *w, const void *x, int x_dtype, int rows,
               : launch_gemv<false>(w, xr, m, yr, y_dtype == G4_BF16);
     if (rc) return rc;
   }
-  return ok();
+  return G4_OK;
+}
+
+}  // namespace g4
+
+G4_API int g4_w4_linear(const g4_w4 *w, const void *x, int x_dtype, int rows,
+                        void *y, int y_dtype) {
+  G4_CHECK_INIT();
+  const int rc = w4_linear_impl(w, x, x_dtype, rows, y, y_dtype, nullptr, "g4_w4_linear");
+  return rc ? rc : ok();
 }
 
 G4_API int g4_w4_linear_multi(const g4_w4 *const *w, int n, const void *x, int x_dtype,

@@ -52,6 +52,7 @@ SIGNATURES = {
     "g4_w4_info": (_int, [_vp, _c.POINTER(_int), _c.POINTER(_int), _c.POINTER(_int), _c.POINTER(_sz)]),
     "g4_w4_linear": (_int, [_vp, _vp, _int, _int, _vp, _int]),
     "g4_w4_linear_multi": (_int, [_c.POINTER(_vp), _int, _vp, _int, _int, _c.POINTER(_vp), _int]),
+    "g4_w4_linear_noalloc": (_int, [_vp, _vp, _int, _int, _vp, _int]),
     "g4_w4_dequant": (_int, [_vp, _int, _int, _vp, _int]),
     "g4_ple_create": (_int, [_int, _int, _int, _int, _c.POINTER(_vp)]),
     "g4_ple_upload_shard": (_int, [_vp, _int, _vp, _sz]),
@@ -293,6 +294,10 @@ class W4Linear:
 
     def linear(self, x_ptr, x_dtype, rows, y_ptr, y_dtype=F32):
         check(lib().g4_w4_linear(self.h, x_ptr, x_dtype, rows, y_ptr, y_dtype))
+
+    def linear_noalloc(self, x_ptr, x_dtype, rows, y_ptr, y_dtype=F32):
+        """g4_w4_linear_noalloc: the same linear on the library's static scratch."""
+        check(lib().g4_w4_linear_noalloc(self.h, x_ptr, x_dtype, rows, y_ptr, y_dtype))
 
     @staticmethod
     def linear_multi(linears, x_ptr, x_dtype, rows, y_ptrs, y_dtype=F32):

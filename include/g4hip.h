@@ -149,6 +149,21 @@ int g4_w4_info(const g4_w4 *w, int *out_dim, int *in_dim, int *group,
 int g4_w4_linear(const g4_w4 *w, const void *x, int x_dtype, int rows,
                  void *y, int y_dtype);
 
+/* No counterpart in the reference.  g4_w4_linear for callers that cannot
+ * allocate device memory: code under HIP graph capture (a g4 encoder), tight
+ * serving loops, harnesses that forbid hipMalloc.  Same arguments, kernels
+ * and results; the prefill GEMM path (rows > 4, or an in_dim beyond the GEMV
+ * staging) takes its x' staging, row exponents and K-slice partial sums from
+ * a static 64 MiB device array instead of the library's growing scratch, so
+ * the call never allocates or frees.  A call whose scratch would exceed
+ * 64 MiB (e.g. 4096 FP32 rows of in_dim 4096) fails with G4_E_ARG and a
+ * message giving the bytes it needs.  Every call on one GPU shares that
+ * GPU's array: calls whose device work overlaps (replays of recordings made
+ * from it on other streams) race; calls enqueued on the library's one stream
+ * run in order and are safe. */
+int g4_w4_linear_noalloc(const g4_w4 *w, const void *x, int x_dtype, int rows,
+                         void *y, int y_dtype);
+
 /* Consecutive GPUOps.w4 dispatches over one input (gemma4-webgpu.js:225,
  * 237-238 for q/k/v and 280-281 for gate/up): y[i] = x * W[i]^T for i < n,
  * 1 <= n <= 3, every W[i] of the same in_dim, outputs as g4_w4_linear's.
