@@ -195,7 +195,7 @@ def bench_head(reps=20, seed=12):
             "gbs": per * reps / (ms * 1e-3) / 1e9}
 
 
-def bench_gemm(reps=3, seed=3):
+def bench_gemm(reps=20, seed=3):
     res = {}
     for n, k in ((6144, 1536), (1536, 6144)):
         packed, scales, _ = syn.w4_weights(seed, n, k)

@@ -124,8 +124,8 @@ struct g4_w4 {
   uint8_t *mem;      // the one device allocation holding both arrays
   uint4 *packed;     // [N][G] 16-byte groups, compressed-tensors order
   uint16_t *scales;  // [N][G] bf16 bits
+  int16_t *rshift;   // [N]: 2^rshift[o] * 8 * max_g |scale[o, g]| <= 2^15 (FP16 GEMM)
   size_t bytes;
-  int shift;         // 2^shift * 8 * max|scale| <= 2^15 keeps every FP16 q*s exact
 };
 
 namespace g4 {

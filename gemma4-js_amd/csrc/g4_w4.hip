@@ -617,6 +617,52 @@ int launch_gemv1_split(const g4_w4 *w, const float *x, float *parts) {
 
 }  // namespace g4
 
+namespace {
+
+// Per output row, the power-of-two shift of the FP16 path of the prefill
+// GEMM: with 2^shift[o] * 8 * max_g |s[o, g]| <= 2^15 every q * s * 2^shift[o]
+// of the row (<= 11 significant bits) is an exact FP16 value, unless the
+// group's scale is more than 2^26 below the row's largest (then its products
+// may lose bits, each at most 2^-26 of the row's largest product).  Rows are
+// independent, so their magnitudes may differ by any factor.  Rows whose
+// scales are all zero (or not finite) get shift 0.
+__global__ __launch_bounds__(256) void row_shift_kernel(const uint16_t *__restrict__ s, int N,
+                                                        int G, int16_t *__restrict__ shift) {
+  const int o = blockIdx.x * 256 + threadIdx.x;
+  if (o >= N) return;
+  const uint16_t *row = s + (size_t)o * G;
+  uint32_t mx = 0;
+  for (int g = 0; g < G; ++g) {
+    const uint32_t a = row[g] & 0x7fffu;
+    if (a < 0x7f80u && a > mx) mx = a;  // finite magnitudes only
+  }
+  // floor(log2 max|s|) for a normal bf16; -127 for a subnormal one (its
+  // true exponent is lower, so the shift only keeps it further from overflow)
+  shift[o] = mx ? (int16_t)(11 - ((int)(mx >> 7) - 127)) : (int16_t)0;
+}
+
+// One allocation per weight: packed groups, the scales, the row shifts.
+int alloc_weight(g4_w4 *w, size_t qbytes, size_t sbytes) {
+  const size_t soff = (qbytes + 255) & ~size_t(255);
+  const size_t roff = (soff + sbytes + 255) & ~size_t(255);
+  const size_t total = roff + (size_t)w->N * sizeof(int16_t);
+  int rc = device_alloc(total, reinterpret_cast<void **>(&w->mem));
+  if (rc) return rc;
+  w->packed = reinterpret_cast<uint4 *>(w->mem);
+  w->scales = reinterpret_cast<uint16_t *>(w->mem + soff);
+  w->rshift = reinterpret_cast<int16_t *>(w->mem + roff);
+  w->bytes = total;
+  return G4_OK;
+}
+
+hipError_t launch_row_shift(const g4_w4 *w) {
+  hipLaunchKernelGGL(row_shift_kernel, dim3((w->N + 255) / 256), dim3(256), 0, stream(),
+                     w->scales, w->N, w->G, w->rshift);
+  return hipGetLastError();
+}
+
+}  // namespace
+
 G4_API int g4_w4_load(const void *packed, const void *scales, int out_dim,
                       int in_dim, int group, g4_w4 **out) {
   G4_CHECK_INIT();
@@ -640,39 +686,15 @@ G4_API int g4_w4_load(const void *packed, const void *scales, int out_dim,
   w->G = in_dim / 32;
   const size_t qbytes = (size_t)out_dim * in_dim / 2;
   const size_t sbytes = (size_t)out_dim * w->G * 2;
-  const size_t soff = (qbytes + 255) & ~size_t(255);
-  // One allocation: packed groups, then the scales.
-  int rc = device_alloc(soff + sbytes, reinterpret_cast<void **>(&w->mem));
+  int rc = alloc_weight(w, qbytes, sbytes);
   if (rc) {
     delete w;
     return rc;
   }
-  w->packed = reinterpret_cast<uint4 *>(w->mem);
-  w->scales = reinterpret_cast<uint16_t *>(w->mem + soff);
-  w->bytes = soff + sbytes;
-  // Power-of-two shift for the FP16 path of the prefill GEMM: with
-  // 2^shift * 8 * max|s| <= 2^15 every q * s * 2^shift (<= 11 significant
-  // bits) stays an exact FP16 value unless a scale is 2^29 times smaller
-  // than the largest one.
-  {
-    const uint16_t *sb = static_cast<const uint16_t *>(scales);
-    uint32_t maxbits = 0;
-    for (size_t i = 0, n = (size_t)out_dim * w->G; i < n; ++i) {
-      const uint32_t a = sb[i] & 0x7fffu;
-      if (a < 0x7f80u && a > maxbits) maxbits = a;  // finite magnitudes only
-    }
-    int shift = 0;
-    if (maxbits) {
-      const int e = (int)(maxbits >> 7) - 127;  // floor(log2(max|s|)) for normal bf16
-      shift = 11 - e;                           // 8 * 2^(e+1) * 2^shift <= 2^15
-      if (shift > 60) shift = 60;
-      if (shift < -60) shift = -60;
-    }
-    w->shift = shift;
-  }
   hipError_t e = hipMemcpyAsync(w->packed, packed, qbytes, hipMemcpyHostToDevice, stream());
   if (e == hipSuccess)
     e = hipMemcpyAsync(w->scales, scales, sbytes, hipMemcpyHostToDevice, stream());
+  if (e == hipSuccess) e = launch_row_shift(w);
   if (e == hipSuccess) e = hipStreamSynchronize(stream());
   if (e != hipSuccess) {
     device_free(w->mem);
@@ -682,32 +704,6 @@ G4_API int g4_w4_load(const void *packed, const void *scales, int out_dim,
   *out = w;
   return ok();
 }
-
-namespace {
-
-// Largest finite |scale| as bf16 magnitude bits, one block.
-__global__ __launch_bounds__(1024) void scale_maxbits_kernel(const uint16_t *__restrict__ s,
-                                                             size_t n, uint32_t *__restrict__ out) {
-  __shared__ uint32_t red[16];
-  uint32_t m = 0;
-  for (size_t i = threadIdx.x; i < n; i += 1024) {
-    const uint32_t a = s[i] & 0x7fffu;
-    if (a < 0x7f80u && a > m) m = a;
-  }
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    const uint32_t v = __shfl_xor(m, o, 64);
-    m = v > m ? v : m;
-  }
-  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    for (int i = 1; i < 16; ++i) m = red[i] > m ? red[i] : m;
-    *out = m;
-  }
-}
-
-}  // namespace
 
 G4_API int g4_w4_load_dev(const void *packed_dev, const void *scales_dev, int out_dim,
                           int in_dim, int group, g4_w4 **out) {
@@ -734,40 +730,21 @@ G4_API int g4_w4_load_dev(const void *packed_dev, const void *scales_dev, int ou
   w->K = in_dim;
   w->group = group;
   w->G = G;
-  const size_t soff = (qbytes + 255) & ~size_t(255);
-  rc = device_alloc(soff + sbytes + 256, reinterpret_cast<void **>(&w->mem));
+  rc = alloc_weight(w, qbytes, sbytes);
   if (rc) {
     delete w;
     return rc;
   }
-  w->packed = reinterpret_cast<uint4 *>(w->mem);
-  w->scales = reinterpret_cast<uint16_t *>(w->mem + soff);
-  w->bytes = soff + sbytes;
-  uint32_t *maxbits_dev = reinterpret_cast<uint32_t *>(w->mem + ((soff + sbytes + 255) & ~size_t(255)));
-  uint32_t maxbits = 0;
   hipError_t e = hipMemcpyAsync(w->packed, packed_dev, qbytes, hipMemcpyDeviceToDevice, stream());
   if (e == hipSuccess)
     e = hipMemcpyAsync(w->scales, scales_dev, sbytes, hipMemcpyDeviceToDevice, stream());
-  if (e == hipSuccess) {
-    hipLaunchKernelGGL(scale_maxbits_kernel, dim3(1), dim3(1024), 0, stream(), w->scales,
-                       (size_t)out_dim * G, maxbits_dev);
-    e = hipGetLastError();
-  }
-  if (e == hipSuccess)
-    e = hipMemcpyAsync(&maxbits, maxbits_dev, 4, hipMemcpyDeviceToHost, stream());
+  if (e == hipSuccess) e = launch_row_shift(w);
   if (e == hipSuccess) e = hipStreamSynchronize(stream());
   if (e != hipSuccess) {
     device_free(w->mem);
     delete w;
     return fail(G4_E_HIP, "g4_w4_load_dev: copy failed: %s", hipGetErrorString(e));
   }
-  int shift = 0;  // the same rule as g4_w4_load
-  if (maxbits) {
-    shift = 11 - ((int)(maxbits >> 7) - 127);
-    if (shift > 60) shift = 60;
-    if (shift < -60) shift = -60;
-  }
-  w->shift = shift;
   *out = w;
   return ok();
 }

@@ -201,6 +201,34 @@ def test_gemm_matches_gemv_path(g4):
         assert rel_l2_rows(big[r:r + 1], ref[r:r + 1]) < 1e-4
 
 
+@pytest.mark.parametrize("layout", ["by_row", "by_group"])
+@pytest.mark.parametrize("x_dtype_name", ["bf16", "f32"])
+def test_scales_spanning_2e40_stay_exact(g4, layout, x_dtype_name):
+    # One tensor whose group scales span 2^-40 .. 2^0: by output row (each
+    # row's scales within a factor 2 of 2^-40 r / (N - 1)), or independently
+    # per group inside every row.  The prefill GEMM runs on FP16 operands with
+    # a power-of-two shift per output row, so rows of any relative magnitude
+    # keep every bit; inside a row only groups 2^26 below its largest may lose
+    # bits, a negligible share of that row's output.  GEMV rows (1, 3) and
+    # GEMM rows (64) must all stay within 1e-5 of the binary64 product.
+    n, k = 384, 2048
+    G = k // 32
+    rng = np.random.default_rng([40, layout == "by_row"])
+    q = rng.integers(-7, 8, size=(n, k), dtype=np.int8)
+    if layout == "by_row":
+        ex = (-40.0 * np.arange(n) / (n - 1))[:, None] - rng.uniform(0, 1, (n, G))
+    else:
+        ex = rng.uniform(-40, 0, (n, G))
+    scales = syn.bf16_rne(np.exp2(ex).astype(np.float32))
+    lin = g4.W4Linear(syn.pack_w4(q), scales)
+    w = dense(q, scales)
+    xd = g4.BF16 if x_dtype_name == "bf16" else g4.F32
+    for rows in (1, 3, 64):
+        bits, x = syn.activations(41 + rows, rows, k)
+        y = run_linear(g4, lin, bits, x, rows, xd)
+        assert rel_l2_rows(y, x.astype(np.float64) @ w.T) < 1e-5, (layout, rows)
+
+
 def test_recording_survives_scratch_growth(g4):
     # A GEMM-path linear recorded into a command buffer holds the library's
     # scratch address.  A later, larger eager call grows the scratch; the old
