@@ -104,6 +104,66 @@ int launch_gather(const g4_ple *t, const int32_t *ids_dev, int n, void *out, int
   return G4_OK;
 }
 
+// quantize_batch of the builder (tools/build_ple_w4_full.py:48-60), one
+// thread per 32-column group: s = bf16_rne(maxabs / 7) (1.0 for an all-zero
+// group, the float32 division of numpy), q = clip(rint(x / s_bf16), -7, 7)
+// with round half to even, stored as two's-complement nibbles, low nibble
+// first.  Row r goes to shard r / rows_per_shard of a table of `vocab` rows,
+// each shard its packed block then its scales block (130-170).  The 64 input
+// bytes of a group are four 16-byte loads; its 16 packed bytes one store.
+__global__ __launch_bounds__(256) void ple_quantize_kernel(
+    const uint4 *__restrict__ src, int vocab, int width, int rows_per_shard, size_t packed_row,
+    size_t scale_row, size_t full_shard_bytes, uint8_t *__restrict__ table) {
+  const int G = width / 32;
+  const size_t item = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (item >= (size_t)vocab * G) return;
+  const int r = (int)(item / G);
+  const int g = (int)(item - (size_t)r * G);
+  const uint4 *p = src + item * 4;  // 32 bf16 = 4 x 16 bytes
+  float x[32];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    const uint4 v = p[c];
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      x[8 * c + 2 * k] = __uint_as_float(w[k] << 16);
+      x[8 * c + 2 * k + 1] = __uint_as_float(w[k] & 0xffff0000u);
+    }
+  }
+  float maxabs = 0.f;
+#pragma unroll
+  for (int i = 0; i < 32; ++i) maxabs = fmaxf(maxabs, fabsf(x[i]));
+  const float sc = maxabs == 0.f ? 1.f : maxabs / 7.f;  // IEEE division, as numpy's float32
+  const uint32_t sbits = f32_to_bf16_rne(sc);
+  const float stored = bf16_to_f32(sbits);
+  uint32_t packed[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+  for (int i = 0; i < 32; ++i) {
+    const float q = fminf(fmaxf(rintf(x[i] / stored), -7.f), 7.f);
+    packed[i >> 3] |= ((uint32_t)(int)q & 15u) << (4 * (i & 7));
+  }
+  const int shard = r / rows_per_shard;
+  const int local = r - shard * rows_per_shard;
+  const int left = vocab - shard * rows_per_shard;
+  const int rows_in_shard = left < rows_per_shard ? left : rows_per_shard;
+  uint8_t *base = table + (size_t)shard * full_shard_bytes;
+  *reinterpret_cast<uint4 *>(base + (size_t)local * packed_row + (size_t)g * 16) =
+      make_uint4(packed[0], packed[1], packed[2], packed[3]);
+  reinterpret_cast<uint16_t *>(base + (size_t)rows_in_shard * packed_row +
+                               (size_t)local * scale_row)[g] = (uint16_t)sbits;
+}
+
+int launch_quantize(const void *src, int vocab, int width, int rows_per_shard,
+                    size_t full_shard_bytes, uint8_t *table) {
+  const size_t items = (size_t)vocab * (width / 32);
+  hipLaunchKernelGGL(ple_quantize_kernel, dim3((unsigned)((items + 255) / 256)), dim3(256), 0,
+                     stream(), static_cast<const uint4 *>(src), vocab, width, rows_per_shard,
+                     (size_t)width / 2, (size_t)(width / 32) * 2, full_shard_bytes, table);
+  G4_LAUNCH_CHECK("ple_quantize_kernel");
+  return G4_OK;
+}
+
 int check_out(const g4_ple *t, int n, void *out, int out_dtype) {
   if (out_dtype != G4_F32 && out_dtype != G4_BF16)
     return fail(G4_E_ARG, "PLE gather: bad out dtype %d", out_dtype);
@@ -274,5 +334,35 @@ G4_API int g4_ple_gather_dev(const g4_ple *t, const int32_t *ids_dev, int n, voi
   rc = check_out(t, n, out, out_dtype);
   if (rc) return rc;
   rc = launch_gather(t, ids_dev, n, out, out_dtype);
+  return rc ? rc : ok();
+}
+
+G4_API int g4_ple_quantize_rows(const void *rows_bf16, int rows, int width, void *shard_dev) {
+  G4_CHECK_INIT();
+  if (rows < 0 || width <= 0 || width % 32 != 0)
+    return fail(G4_E_ARG, "g4_ple_quantize_rows: %d rows of width %d (a multiple of 32)", rows,
+                width);
+  if (rows == 0) return ok();
+  if ((reinterpret_cast<uintptr_t>(rows_bf16) & 15u) || (reinterpret_cast<uintptr_t>(shard_dev) & 15u))
+    return fail(G4_E_ARG, "g4_ple_quantize_rows: rows and shard must be 16-byte aligned");
+  const size_t packed_row = (size_t)width / 2, scale_row = (size_t)(width / 32) * 2;
+  int rc = check_device_range(rows_bf16, (size_t)rows * width * 2, "g4_ple_quantize_rows rows");
+  if (!rc)
+    rc = check_device_range(shard_dev, (size_t)rows * (packed_row + scale_row),
+                            "g4_ple_quantize_rows shard");
+  if (!rc) rc = launch_quantize(rows_bf16, rows, width, rows, 0, static_cast<uint8_t *>(shard_dev));
+  return rc ? rc : ok();
+}
+
+G4_API int g4_ple_quantize_table(g4_ple *t, const void *dense_bf16) {
+  G4_CHECK_INIT();
+  if (!t) return fail(G4_E_ARG, "g4_ple_quantize_table: null table");
+  if (reinterpret_cast<uintptr_t>(dense_bf16) & 15u)
+    return fail(G4_E_ARG, "g4_ple_quantize_table: rows must be 16-byte aligned");
+  int rc = check_device_range(dense_bf16, (size_t)t->vocab * t->width * 2,
+                              "g4_ple_quantize_table rows");
+  if (!rc)
+    rc = launch_quantize(dense_bf16, t->vocab, t->width, t->rows_per_shard, t->full_shard_bytes,
+                         t->table);
   return rc ? rc : ok();
 }

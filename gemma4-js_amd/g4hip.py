@@ -58,6 +58,8 @@ SIGNATURES = {
     "g4_ple_upload_shard": (_int, [_vp, _int, _vp, _sz]),
     "g4_ple_shard_bytes": (_int, [_vp, _int, _c.POINTER(_int), _c.POINTER(_sz)]),
     "g4_ple_free": (_int, [_vp]),
+    "g4_ple_quantize_rows": (_int, [_vp, _int, _int, _vp]),
+    "g4_ple_quantize_table": (_int, [_vp, _vp]),
     "g4_ple_gather": (_int, [_vp, _vp, _int, _vp, _int]),
     "g4_ple_gather_dev": (_int, [_vp, _vp, _int, _vp, _int]),
     "g4_bf16_head": (_int, [_vp, _vp, _int, _int, _vp, _c.c_float, _c.c_float]),
@@ -348,6 +350,11 @@ class PleTable:
             else np.ascontiguousarray(data).view(np.uint8)
         check(lib().g4_ple_upload_shard(self.h, shard, data.ctypes.data, data.nbytes))
 
+    def quantize_from(self, dense):
+        """g4_ple_quantize_table: build every shard from dense BF16 rows [vocab, width]
+        (a Buffer or device pointer)."""
+        check(lib().g4_ple_quantize_table(self.h, _f(dense)))
+
     def gather(self, ids, out_ptr, out_dtype=F32):
         ids = np.ascontiguousarray(ids, dtype=np.int32)
         check(lib().g4_ple_gather(self.h, ids.ctypes.data, ids.size, out_ptr, out_dtype))
@@ -366,6 +373,11 @@ class PleTable:
                 _lib.g4_ple_free(self.h)
         except Exception:
             pass
+
+
+def ple_quantize_rows(rows_bf16, nrows, width, shard):
+    """g4_ple_quantize_rows: one shard file's bytes from BF16 rows on the device."""
+    check(lib().g4_ple_quantize_rows(_f(rows_bf16), nrows, width, _f(shard)))
 
 
 def bf16_head(x_ptr, E_ptr, rows, in_dim, out_ptr, scale=1.0, softcap=30.0):

@@ -207,6 +207,24 @@ int g4_ple_shard_bytes(const g4_ple *t, int shard, int *num_shards,
 
 int g4_ple_free(g4_ple *t);
 
+/* quantize_batch and the shard layout of the PLE builder
+ * (tools/build_ple_w4_full.py:48-60, 130-170) on the device.  `rows` BF16
+ * rows [rows, width] (device, 16-byte aligned, width a multiple of 32)
+ * become the bytes of one shard file at shard_dev (device, 16-byte aligned,
+ * rows * (width/2 + width/16) bytes): the packed block, q = clip(rint(x / s),
+ * -7, 7) as two's-complement nibbles, low nibble first (rint rounds half to
+ * even), then the scales block, s = bf16_rne(max |x| / 7) per 32-column group
+ * (1.0 for an all-zero group), q computed against that stored BF16 scale.
+ * Finite inputs; stream-ordered, no wait. */
+int g4_ple_quantize_rows(const void *rows_bf16, int rows, int width, void *shard_dev);
+
+/* The whole table from a dense BF16 embed_tokens_per_layer [vocab, width] in
+ * device memory (the builder's source tensor): every shard quantized in
+ * place, the bytes the builder's shard files would hold, so a model that has
+ * only the dense rows (the inputBuffers fallback, gemma4-webgpu.js:198-213)
+ * can gather from a W4 table instead.  Stream-ordered, no wait. */
+int g4_ple_quantize_table(g4_ple *t, const void *dense_bf16);
+
 /* W4PleShardBundle.rowsToGpu (gpu-runtime.js:487-527) with the dequant shader
  * (gpu-runtime.js:218-256) and the oracle LocalPleW4ShardReader.readRows
  * (ple-w4-shard-reader.js:65-103): out[j, i] = q(ids[j], i) * scale, with

@@ -98,11 +98,13 @@ def tiny(g4):
     ref_dense = lo.Model(H, heads, P, V, layers, E, lambda ids: dense_f32[np.asarray(ids)], top,
                          ple_norm, final_norm, window=TINY["window"])
 
-    def make_engine(max_seq=40, dense=False):
+    def make_engine(max_seq=40, dense=False, table=None):
         m = g4.Gemma(tiny_config(g4, max_seq))
         Eb = g4.Buffer.from_array(E)
         m.set_embedding(Eb)
-        if dense:
+        if table is not None:
+            m.set_ple(table)
+        elif dense:
             m.set_ple_dense(g4.Buffer.from_array(dense_bits))
         else:
             t = g4.PleTable(V, NL * P, 32, RPS)
@@ -176,6 +178,32 @@ def test_tiny_dense_ple_rows_match_oracle(g4, tiny):
         want, lg2 = ref.greedy([prev], pos)
         assert t == want or near_tie(lg2, int(t))
         prev, pos = int(t), pos + 1
+
+
+def test_tiny_ple_table_quantized_on_device_from_dense_rows(g4, oracle, tiny):
+    # A model that has only dense BF16 per-layer embeddings builds its W4 table
+    # on the device (the builder's quantizer): its bytes, and so the model's
+    # logits, equal those of the table built from the oracle's shards.
+    _, make = tiny
+    V, NL, P = TINY["vocab"], len(TINY["layers"]), TINY["ple_dim"]
+    rng = np.random.default_rng(77)
+    bits = syn.bf16_rne(rng.standard_normal((V, NL * P), dtype=np.float32) * np.float32(0.3))
+    dev = g4.PleTable(V, NL * P, 32, RPS)
+    dev.quantize_from(g4.Buffer.from_array(bits))
+    host = g4.PleTable(V, NL * P, 32, RPS)
+    x = syn.bf16_to_f32(bits).reshape(V, NL * P)
+    for s in range(host.num_shards):
+        packed, scales = oracle.ple_quantize_rows(x[s * RPS:(s + 1) * RPS])
+        host.upload_shard(s, np.concatenate([packed.reshape(-1),
+                                             scales.astype("<u2").view(np.uint8).reshape(-1)]))
+    ids = syn.token_ids(78, 9, V)
+    out = []
+    for t in (dev, host):
+        m = make(table=t)
+        lg = g4.Buffer(V * 4)
+        out.append((m.greedy(ids, 0, lg), lg.download(np.float32)))
+    assert out[0][0] == out[1][0]
+    assert np.array_equal(out[0][1].view(np.uint32), out[1][1].view(np.uint32))
 
 
 def test_tiny_decode_matches_oracle_step_by_step(g4, tiny):

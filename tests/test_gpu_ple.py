@@ -105,3 +105,74 @@ def test_short_last_shard(g4, oracle):
     with pytest.raises(g4.G4Error):
         t.upload_shard(2, shards[1])  # wrong size for the short shard
     t.free()
+
+
+# ---- the builder's quantizer on the device ---------------------------------------
+
+def quantizer_rows(seed, rows, width):
+    """BF16 rows with the builder's edge cases: all-zero and negative-zero
+    groups, groups whose values sit exactly halfway between two steps (ties
+    to even), and groups of tiny and huge magnitude."""
+    rng = np.random.default_rng(seed)
+    x = rng.standard_normal((rows, width), dtype=np.float32) * np.float32(0.05)
+    x[::97, :32] = 0.0
+    x[5::101, 32:64] = -0.0
+    ties = np.array([7, 0.5, 1.5, 2.5, 3.5, 4.5, 5.5, 6.5, -0.5, -1.5, -2.5, -3.5, -4.5, -5.5,
+                     -6.5, -7] * 2, np.float32)
+    for j, r in enumerate(range(3, rows, 53)):
+        x[r, 64:96] = ties * np.float32(2.0 ** (j % 40 - 20))  # maxabs 7 * 2^k: scale 2^k
+    x[7::89, 96:128] *= np.float32(1e-30)
+    x[11::83, 128:160] *= np.float32(1e30)
+    bits = syn.bf16_rne(x)
+    return bits, syn.bf16_to_f32(bits).reshape(rows, width)
+
+
+def test_quantize_rows_matches_builder_bit_exact(g4, oracle):
+    # quantize_batch + one shard's layout (tools/build_ple_w4_full.py:48-60,
+    # 130-170) on 4096 rows of the table's width, against the oracle's bytes
+    rows = 4096
+    bits, x = quantizer_rows(5, rows, WIDTH)
+    src = g4.Buffer.from_array(bits)
+    shard = g4.Buffer(rows * (WIDTH // 2 + WIDTH // 16))
+    g4.ple_quantize_rows(src, rows, WIDTH, shard)
+    got = shard.download(np.uint8)
+    packed, scales = oracle.ple_quantize_rows(x)
+    want = np.concatenate([packed.reshape(-1), scales.astype("<u2").view(np.uint8).reshape(-1)])
+    assert got.size == want.size
+    bad = np.flatnonzero(got != want)
+    assert bad.size == 0, (bad[:8], got[bad[:8]], want[bad[:8]])
+    # the tie rows decode to the even neighbours
+    deq = oracle.ple_dequant_row(packed[3], scales[3], WIDTH)[64:96] * np.float32(2.0 ** 20)
+    assert deq[:8].tolist() == [7.0, 0.0, 2.0, 2.0, 4.0, 4.0, 6.0, 6.0]  # row 3: scale 2^-20
+
+
+def test_quantize_table_in_place_then_gather(g4, oracle):
+    # a dense [5000, 8960] BF16 table quantized shard by shard in place (the
+    # last shard short), then gathered: bit-exact against the oracle's shards
+    vocab = 5000
+    bits, x = quantizer_rows(6, vocab, WIDTH)
+    dense = g4.Buffer.from_array(bits)
+    t = g4.PleTable(vocab, WIDTH, 32, RPS)
+    t.quantize_from(dense)
+    shards = []
+    for s in range(t.num_shards):
+        packed, scales = oracle.ple_quantize_rows(x[s * RPS:(s + 1) * RPS])
+        shards.append(np.concatenate([packed.reshape(-1),
+                                      scales.astype("<u2").view(np.uint8).reshape(-1)]))
+        assert shards[-1].nbytes == t.shard_bytes(s)
+    ids = np.concatenate([np.arange(0, vocab, 7), [RPS - 1, RPS, vocab - 1]]).astype(np.int32)
+    got = gather(g4, t, ids, g4.F32)
+    want = oracle.ple_gather(np.concatenate(shards), vocab, WIDTH, RPS, ids)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    t.free()
+
+
+def test_quantize_rejects_bad_geometry(g4):
+    src = g4.Buffer(64 * 48 * 2)
+    out = g4.Buffer(64 * 48)
+    with pytest.raises(g4.G4Error) as e:
+        g4.ple_quantize_rows(src, 64, 48, out)  # width not a multiple of 32
+    assert e.value.code == g4.G4_E_ARG
+    with pytest.raises(g4.G4Error) as e:
+        g4.ple_quantize_rows(src, 64, 64, out)  # src too short for 64 x 64
+    assert e.value.code == g4.G4_E_RANGE
