@@ -8,7 +8,8 @@
 // it is exact in FP16 but not in BF16 (rounding it to BF16 alone would cost
 // ~1.6e-3 relative L2 at the E2B shapes).  The GEMM therefore runs
 // v_mfma_f32_16x16x32_f16 with FP32 accumulation on
-//   W' = q * s * 2^shift[n]   (exact FP16; shift per output row, set at load)
+//   W' = q * s * 2^shift[n]   (exact FP16; shift set at load, one per tensor
+//                              unless its rows' scales differ by more than 2^12)
 //   x' = x * 2^-e[m]          (per row; max |x'| in [2^13, 2^14))
 // and writes y = acc * 2^(e[m] - shift[n]), an exact power-of-two rescale.
 // Output rows of any relative magnitude are exact; within a row, a group
@@ -295,8 +296,9 @@ struct GemmSegs {
   const u32x4 *wq[kMaxGemmSegs];
   const uint16_t *ws[kMaxGemmSegs];
   void *y[kMaxGemmSegs];
-  const int16_t *rs[kMaxGemmSegs];  // per-row power-of-two shifts (g4_w4::rshift)
-  int N[kMaxGemmSegs];
+  // per-row power-of-two shifts (g4_w4::rshift), or null: shift[] for the tensor
+  const int16_t *rs[kMaxGemmSegs];
+  int N[kMaxGemmSegs], shift[kMaxGemmSegs];
   int t0[kMaxGemmSegs + 1];
   int n, glu;
 };
@@ -342,7 +344,7 @@ __global__ __launch_bounds__(kThreads, 2) void w4_gemm_kernel(
   const u32x4 *__restrict__ wq = SG.wq[si];
   const uint16_t *__restrict__ ws = SG.ws[si];
   void *__restrict__ y = SG.y[si];
-  const int N = SG.N[si];
+  const int N = SG.N[si], shift = SG.shift[si];
   const int16_t *__restrict__ rsh = SG.rs[si];
   const int m0 = mt * BM, n0 = glu ? ntile * HALF : (ntile - SG.t0[si]) * BN;
 
@@ -377,7 +379,8 @@ __global__ __launch_bounds__(kThreads, 2) void w4_gemm_kernel(
     const int gn = n0 + rn < N ? n0 + rn : N - 1;
     b_src[i] = (up ? SG.wq[1] : wq) + (size_t)gn * G + st0_slice * KS + b_kk[i];
     s_src[i] = (up ? SG.ws[1] : ws) + (size_t)gn * G + st0_slice * KS + (b_kk[i] & ~(SW - 1));
-    b_shift[i] = (up ? SG.rs[1] : rsh)[gn];
+    const int16_t *rsi = up ? SG.rs[1] : rsh;
+    b_shift[i] = rsi ? rsi[gn] : up ? SG.shift[1] : shift;
   }
 
   // Ring of P register slots: stage j is loaded into slot j % P, P - 1
@@ -493,15 +496,39 @@ __global__ __launch_bounds__(kThreads, 2) void w4_gemm_kernel(
   }
   }
 
+  // Every row exponent and column shift is read, and every accumulator
+  // rescaled, before the first output store: vmcnt counts stores too, so a
+  // wait for a load issued (or first used) among the stores would also wait
+  // for the stores before it, one store at a time.
+  {
+    int ev[TM][4], csh[TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int m = m0 + wm * 16 * TM + i * 16 + 4 * lc + r;
+        ev[i][r] = xe[m < M ? m : M - 1];
+      }
+    // this lane's output columns (glu: columns n0 + j * 16 + lr of up for wn = 1,
+    // of gate for wn = 0)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const int n = glu ? n0 + j * 16 + lr : n0 + wn * 16 * TN + j * 16 + lr;
+      const int seg = glu ? (wn == 1 ? 1 : 0) : si;
+      const int16_t *r = SG.rs[seg];
+      csh[j] = r ? r[n < N ? n : N - 1] : SG.shift[seg];
+    }
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[i][j][r] = ldexpf(acc[i][j][r], ev[i][r] - csh[j]);
+  }
+
   // epilogue: lane holds rows 4*lc + r (r = 0..3) of column lr of each tile;
   // one branch-free copy per output type
   auto epilogue = [&](auto *out) {
-    int csh[TN];  // the shifts of this lane's output columns
-#pragma unroll
-    for (int j = 0; j < TN; ++j) {
-      const int n = n0 + wn * 16 * TN + j * 16 + lr;
-      csh[j] = rsh[n < N ? n : N - 1];
-    }
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
 #pragma unroll
@@ -512,7 +539,7 @@ __global__ __launch_bounds__(kThreads, 2) void w4_gemm_kernel(
         for (int j = 0; j < TN; ++j) {
           const int n = n0 + wn * 16 * TN + j * 16 + lr;
           if (n >= N) continue;
-          const float v = ldexpf(acc[i][j][r], xe[m] - csh[j]);
+          const float v = acc[i][j][r];
           if constexpr (sizeof(*out) == 2)
             out[(size_t)m * N + n] = (uint16_t)f32_to_bf16_rne(v);
           else
@@ -528,24 +555,14 @@ __global__ __launch_bounds__(kThreads, 2) void w4_gemm_kernel(
     constexpr int NE = TM * TN * 4;  // accumulator floats per lane
     static_assert(2 * NE * 64 * sizeof(float) <= sizeof(As), "up values must fit the A tile");
     float *upv = reinterpret_cast<float *>(&As[0][0][0][0]);
-    // both halves hold columns n0 + j * 16 + lr: of up (wn = 1), of gate (wn = 0)
-    int csh[TN];
-#pragma unroll
-    for (int j = 0; j < TN; ++j) {
-      const int n = n0 + j * 16 + lr;
-      csh[j] = SG.rs[wn == 1 ? 1 : 0][n < N ? n : N - 1];
-    }
     if (wn == 1) {
 #pragma unroll
       for (int i = 0; i < TM; ++i)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int m = m0 + wm * 16 * TM + i * 16 + 4 * lc + r;
-          const int e = m < M ? xe[m] : 0;
+        for (int r = 0; r < 4; ++r)
 #pragma unroll
           for (int j = 0; j < TN; ++j)
-            upv[(wm * NE + (i * TN + j) * 4 + r) * 64 + lane] = ldexpf(acc[i][j][r], e - csh[j]);
-        }
+            upv[(wm * NE + (i * TN + j) * 4 + r) * 64 + lane] = acc[i][j][r];
     }
     __syncthreads();
     if (wn == 0) {
@@ -560,7 +577,7 @@ __global__ __launch_bounds__(kThreads, 2) void w4_gemm_kernel(
           for (int j = 0; j < TN; ++j) {
             const int n = n0 + j * 16 + lr;
             if (n >= N) continue;
-            const float g = ldexpf(acc[i][j][r], xe[m] - csh[j]);
+            const float g = acc[i][j][r];
             out[(size_t)m * N + n] = gelu_tanh(g) * upv[(wm * NE + (i * TN + j) * 4 + r) * 64 + lane];
           }
         }
@@ -622,7 +639,8 @@ int launch_gemm(const g4_w4 *const *w, int nw, const uint4 *xt, const int *xe, i
     sg.ws[i] = w[i]->scales;
     sg.y[i] = ys[i];
     sg.N[i] = w[i]->N;
-    sg.rs[i] = w[i]->rshift;
+    sg.rs[i] = w[i]->row_shift ? w[i]->rshift : nullptr;
+    sg.shift[i] = w[i]->shift;
     sg.t0[i + 1] = sg.t0[i] + (w[i]->N + BN - 1) / BN;
   }
   sg.glu = glu;

@@ -125,6 +125,8 @@ struct g4_w4 {
   uint4 *packed;     // [N][G] 16-byte groups, compressed-tensors order
   uint16_t *scales;  // [N][G] bf16 bits
   int16_t *rshift;   // [N]: 2^rshift[o] * 8 * max_g |scale[o, g]| <= 2^15 (FP16 GEMM)
+  int shift;         // min_o rshift[o]: one shift for the whole tensor ...
+  bool row_shift;    // ... unless the rows' maxima spread beyond 2^12: then per row
   size_t bytes;
 };
 

@@ -641,12 +641,15 @@ __global__ __launch_bounds__(256) void row_shift_kernel(const uint16_t *__restri
   shift[o] = mx ? (int16_t)(11 - ((int)(mx >> 7) - 127)) : (int16_t)0;
 }
 
+constexpr int kRowShiftSpread = 12;
+
 // One allocation per weight: packed groups, the scales, the row shifts.
 int alloc_weight(g4_w4 *w, size_t qbytes, size_t sbytes) {
   const size_t soff = (qbytes + 255) & ~size_t(255);
   const size_t roff = (soff + sbytes + 255) & ~size_t(255);
-  const size_t total = roff + (size_t)w->N * sizeof(int16_t);
-  int rc = device_alloc(total, reinterpret_cast<void **>(&w->mem));
+  const size_t total = roff + (((size_t)w->N * sizeof(int16_t) + 15) & ~size_t(15));
+  // + 8 bytes past `bytes` for the row-shift range read back at load
+  int rc = device_alloc(total + 8, reinterpret_cast<void **>(&w->mem));
   if (rc) return rc;
   w->packed = reinterpret_cast<uint4 *>(w->mem);
   w->scales = reinterpret_cast<uint16_t *>(w->mem + soff);
@@ -655,10 +658,52 @@ int alloc_weight(g4_w4 *w, size_t qbytes, size_t sbytes) {
   return G4_OK;
 }
 
-hipError_t launch_row_shift(const g4_w4 *w) {
+// Smallest and largest row shift, one block (bounds of a uint32 pair: the
+// shifts biased by 512 so the atomics compare unsigned values).
+__global__ __launch_bounds__(256) void row_shift_range_kernel(const int16_t *__restrict__ shift,
+                                                              int N, uint32_t *__restrict__ out) {
+  uint32_t lo = 0xffffffffu, hi = 0u;
+  for (int o = threadIdx.x; o < N; o += 256) {
+    const uint32_t v = (uint32_t)(shift[o] + 512);
+    lo = v < lo ? v : lo;
+    hi = v > hi ? v : hi;
+  }
+  __shared__ uint32_t slo[256], shi[256];
+  slo[threadIdx.x] = lo;
+  shi[threadIdx.x] = hi;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int i = 1; i < 256; ++i) {
+      lo = slo[i] < lo ? slo[i] : lo;
+      hi = shi[i] > hi ? shi[i] : hi;
+    }
+    out[0] = lo;
+    out[1] = hi;
+  }
+}
+
+// Row shifts into w->rshift, then the tensor shift (the smallest row shift,
+// that of the row with the largest scale) and whether rows need their own:
+// with one shift, a row whose largest scale is 2^d below the tensor's keeps
+// 26 - d bits of headroom below its largest product before FP16 products
+// lose bits; up to d = 12 that is far below what the 1e-3 contract can see,
+// beyond it the GEMM rescales per row (a few percent slower).  Synchronises.
+hipError_t finish_row_shift(g4_w4 *w) {
   hipLaunchKernelGGL(row_shift_kernel, dim3((w->N + 255) / 256), dim3(256), 0, stream(),
                      w->scales, w->N, w->G, w->rshift);
-  return hipGetLastError();
+  uint32_t *range_dev = reinterpret_cast<uint32_t *>(w->mem + w->bytes);
+  hipLaunchKernelGGL(row_shift_range_kernel, dim3(1), dim3(256), 0, stream(), w->rshift, w->N,
+                     range_dev);
+  hipError_t e = hipGetLastError();
+  uint32_t range[2] = {0, 0};
+  if (e == hipSuccess)
+    e = hipMemcpyAsync(range, range_dev, sizeof(range), hipMemcpyDeviceToHost, stream());
+  if (e == hipSuccess) e = hipStreamSynchronize(stream());
+  if (e == hipSuccess) {
+    w->shift = (int)range[0] - 512;
+    w->row_shift = (int)(range[1] - range[0]) > kRowShiftSpread;
+  }
+  return e;
 }
 
 }  // namespace
@@ -694,8 +739,7 @@ G4_API int g4_w4_load(const void *packed, const void *scales, int out_dim,
   hipError_t e = hipMemcpyAsync(w->packed, packed, qbytes, hipMemcpyHostToDevice, stream());
   if (e == hipSuccess)
     e = hipMemcpyAsync(w->scales, scales, sbytes, hipMemcpyHostToDevice, stream());
-  if (e == hipSuccess) e = launch_row_shift(w);
-  if (e == hipSuccess) e = hipStreamSynchronize(stream());
+  if (e == hipSuccess) e = finish_row_shift(w);
   if (e != hipSuccess) {
     device_free(w->mem);
     delete w;
@@ -738,8 +782,7 @@ G4_API int g4_w4_load_dev(const void *packed_dev, const void *scales_dev, int ou
   hipError_t e = hipMemcpyAsync(w->packed, packed_dev, qbytes, hipMemcpyDeviceToDevice, stream());
   if (e == hipSuccess)
     e = hipMemcpyAsync(w->scales, scales_dev, sbytes, hipMemcpyDeviceToDevice, stream());
-  if (e == hipSuccess) e = launch_row_shift(w);
-  if (e == hipSuccess) e = hipStreamSynchronize(stream());
+  if (e == hipSuccess) e = finish_row_shift(w);
   if (e != hipSuccess) {
     device_free(w->mem);
     delete w;
