@@ -337,8 +337,14 @@ def test_e2b_config4_prompt512_then_256_graph_steps(g4, e2b_1024):
     # window.  One-token calls from the same prompt, fed the graph's tokens,
     # pick their key splits from the actual length instead (24 per global
     # head here); at every one of the 256 positions they must choose the
-    # graph's token (or one within 1e-3 of their top logit), with logits
-    # within relative L2 5e-3 of the graph's.  (A prefill of the whole
+    # graph's token (or one whose logit is within twice the largest per-logit
+    # difference of their top, the most that difference can move an argmax),
+    # with logits within relative L2 2e-3 of the graph's over the first 8
+    # positions and 1e-2 over all 256.  The two runs keep their own KV caches,
+    # so the rounding difference of the split layouts compounds over the
+    # positions: it starts near 1e-4 (at most 1.1e-3 over the first 8) and
+    # reaches 4.9e-3 by position 160; a wrong split or a lost partial moves the
+    # logits by 1e-1 or more.  (A prefill of the whole
     # sequence is not compared token by token: in this random-init 35-layer
     # model the attention logits q.k have a spread of about 16-22 - the
     # reference applies no 1/sqrt(head_dim) - and amplify the rounding
@@ -366,5 +372,6 @@ def test_e2b_config4_prompt512_then_256_graph_steps(g4, e2b_1024):
         tok = m.greedy([fed[s]], 512 + s, lg)
         eager = lg.download(np.float32)
         assert np.all(np.isfinite(eager)), s
-        assert rel(eager, glog[s]) < 5e-3, (s, rel(eager, glog[s]))
-        assert tok == graph[s] or near_tie(eager, graph[s]), (s, tok, graph[s])
+        assert rel(eager, glog[s]) < (2e-3 if s < 8 else 1e-2), (s, rel(eager, glog[s]))
+        tol = max(1e-3, 2 * float(np.max(np.abs(eager - glog[s]))))
+        assert tok == graph[s] or near_tie(eager, graph[s], tol), (s, tok, graph[s])
