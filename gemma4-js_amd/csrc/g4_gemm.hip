@@ -49,6 +49,8 @@ using namespace g4;
 
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
 
 constexpr int kThreads = 256;
 constexpr int kRowPad = 128;   // x' rows are padded to a multiple of the largest BM
@@ -591,6 +593,311 @@ __global__ __launch_bounds__(kThreads, 2) void w4_gemm_kernel(
     epilogue(static_cast<float *>(y));
 }
 
+// ---- main kernel, packed weights per wave --------------------------------------
+//
+// The same product, laid out so that every weight is used by one wave only
+// and stays packed (4 bits) until that wave's registers.  The 4 waves of a
+// block sit side by side in N: wave w computes rows [m0, m0 + BM)
+// (BM = 16 TMW) times TNW tiles of 16 columns.  A stage is 64 values of K (2
+// groups, 8 x' chunks).  Every operand of a stage reaches LDS by direct
+// global -> LDS loads, two stages ahead, into one of three buffers:
+//   x'      64 consecutive rows of one chunk per wave instruction;
+//   words   per wave, lane l of instruction d: tile 2d + l / 32, row
+//           (l / 2) % 16, group 2 st + l % 2 (16 bytes);
+//   scales  per wave, lane l: tile l / 16, row l % 16, the 2 scales of the
+//           stage (4 bytes).
+// Lane (c = lane % 16, q = lane / 16) then reads words 2q and 2q + 1 of the
+// stage's 8 words of row c (both in group q / 2, one scale) and dequantizes
+// them; MFMA step j (0, 1) takes word j as its B operand and x' chunk 2q + j
+// of row m as its A operand, so A and B agree on the k order inside every
+// lane's 8 values.  Only the waits for these loads order the main loop: the
+// compiler's own waits for register loads cannot follow a ring across the
+// loop's back edge and would wait for every load in flight.
+//
+// glu: TNW is even and a wave's tiles TNW/2 .. TNW-1 are the up columns of
+// its gate tiles 0 .. TNW/2-1, so gelu(gate) * up needs no exchange.
+// P: stages (LDS buffers) in the ring; MINB: blocks per CU the registers are
+// sized for (1: up to 512 per lane, accumulators in AGPRs).
+template <int TMW, int TNW, int NX, int P, int MINB>
+__global__ __launch_bounds__(kThreads, MINB) void w4_gemm_rb_kernel(
+    const u32x4 *__restrict__ xt, const int *__restrict__ xe, GemmSegs SG, int y_bf16, int M,
+    int Mp, int K, int xcd_map, float *__restrict__ part, size_t pstride) {
+  constexpr int BM = 16 * TMW;
+  constexpr int KC = 8;                 // x' chunks per stage
+  constexpr int AW = KC * BM / 64 / 4;  // x' wave loads per wave, per plane
+  constexpr int BD = (TNW + 1) / 2;     // weight-word wave loads per wave
+  constexpr int SD = (TNW + 3) / 4;     // scale wave loads per wave
+  static_assert(BM % 64 == 0 && AW >= 1, "A rows must come in runs of 64");
+  struct Stage {
+    u32x4 a[NX][KC][BM];
+    u32x4 b[4][BD][64];
+    uint32_t s[4][SD][64];
+  };
+  __shared__ Stage st_lds[P];
+
+  const int G = K >> 5;
+  const int S = G / 2 / (int)gridDim.y;  // stages of this block's slice of K
+  const int st0_slice = (int)blockIdx.y * S;
+  const int t = threadIdx.x;
+  const int lane = t & 63, wave = t >> 6;
+  const int lr = lane & 15, lq = lane >> 4;
+
+  const bool glu = SG.glu != 0;
+  // columns per block: 64 TNW, or 32 TNW gate (+ the same up) columns with glu
+  const int bn = glu ? 32 * TNW : 64 * TNW;
+  const int nn = glu ? (SG.N[0] + bn - 1) / bn : SG.t0[SG.n];
+  int mt, ntile;
+  if (xcd_map) {
+    const int b = blockIdx.x, xcd = b & 7, j = b >> 3;
+    mt = xcd + 8 * (j / nn);
+    ntile = j - (j / nn) * nn;
+  } else {
+    mt = blockIdx.x / nn;
+    ntile = blockIdx.x - mt * nn;
+  }
+  const int si = glu ? 0 : SG.n > 2 && ntile >= SG.t0[2] ? 2 : SG.n > 1 && ntile >= SG.t0[1] ? 1 : 0;
+  const int N = SG.N[si];
+  const int m0 = mt * BM;
+  // this wave's first output column; tile jj covers columns col(jj) .. + 15
+  const int wc0 = glu ? ntile * bn + wave * 8 * TNW : (ntile - SG.t0[si]) * bn + wave * 16 * TNW;
+  auto col = [&](int jj) { return wc0 + 16 * (glu && jj >= TNW / 2 ? jj - TNW / 2 : jj); };
+  // the weight of tile jj, and its row for tile row r (rows past N re-read the last)
+  auto seg_of = [&](int jj) { return glu ? (jj >= TNW / 2 ? 1 : 0) : si; };
+  auto row_of = [&](int jj, int r) {
+    const int gn = col(jj) + r, Nw = SG.N[seg_of(jj)];
+    return gn < Nw ? gn : Nw - 1;
+  };
+
+  // sources of this lane's loads at stage 0 of the slice (tiles past TNW
+  // re-read tile 0 into an unread part of the buffer)
+  const size_t a_stage = (size_t)KC * Mp;
+  const size_t lo_plane = (size_t)(K >> 3) * Mp;
+  const u32x4 *a_src[AW];
+  int a_c[AW], a_r[AW];
+#pragma unroll
+  for (int i = 0; i < AW; ++i) {
+    const int u = wave * AW + i;
+    a_c[i] = u / (BM / 64);
+    a_r[i] = 64 * (u % (BM / 64));
+    a_src[i] = xt + (size_t)(st0_slice * KC + a_c[i]) * Mp + m0 + a_r[i] + lane;
+  }
+  const u32x4 *b_src[BD];
+#pragma unroll
+  for (int d = 0; d < BD; ++d) {
+    int jj = 2 * d + (lane >> 5);
+    jj = jj < TNW ? jj : 0;
+    const int gn = row_of(jj, (lane >> 1) & 15);
+    b_src[d] = SG.wq[seg_of(jj)] + (size_t)gn * G + 2 * st0_slice + (lane & 1);
+  }
+  const uint32_t *s_src[SD];
+#pragma unroll
+  for (int d = 0; d < SD; ++d) {
+    int jj = 4 * d + (lane >> 4);
+    jj = jj < TNW ? jj : 0;
+    const int gn = row_of(jj, lane & 15);
+    s_src[d] = reinterpret_cast<const uint32_t *>(SG.ws[seg_of(jj)] + (size_t)gn * G + 2 * st0_slice);
+  }
+  int b_shift[TNW];
+#pragma unroll
+  for (int jj = 0; jj < TNW; ++jj) {
+    const int seg = seg_of(jj);
+    b_shift[jj] = SG.rs[seg] ? SG.rs[seg][row_of(jj, lr)] : SG.shift[seg];
+  }
+
+  typedef __attribute__((address_space(3))) void *lds_ptr;
+  auto issue = [&](int stg, int slot) {
+    const int sc = stg < S ? stg : S - 1;  // past the last stage: re-read it, never used
+    Stage &L = st_lds[slot];
+#pragma unroll
+    for (int x = 0; x < NX; ++x)
+#pragma unroll
+      for (int i = 0; i < AW; ++i)
+        __builtin_amdgcn_global_load_lds((const void *)(a_src[i] + (x ? lo_plane : 0) + sc * a_stage),
+                                         (lds_ptr)&L.a[x][a_c[i]][a_r[i]], 16, 0, 0);
+#pragma unroll
+    for (int d = 0; d < BD; ++d)
+      __builtin_amdgcn_global_load_lds((const void *)(b_src[d] + 2 * sc), (lds_ptr)&L.b[wave][d][0],
+                                       16, 0, 0);
+#pragma unroll
+    for (int d = 0; d < SD; ++d)
+      __builtin_amdgcn_global_load_lds((const void *)(s_src[d] + sc), (lds_ptr)&L.s[wave][d][0], 4, 0,
+                                       0);
+  };
+
+  f32x4 acc[TMW][TNW];
+#pragma unroll
+  for (int i = 0; i < TMW; ++i)
+#pragma unroll
+    for (int j = 0; j < TNW; ++j) acc[i][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
+
+  uint32_t mask = 0x000F000Fu;
+  asm volatile("" : "+v"(mask));  // keep the mask in a VGPR: lets v_and_or_b32 take the magic
+  auto deq = [&](uint32_t w, int sh, f16x2 s2) {
+    const uint32_t u = ((w >> (4 * sh)) & mask) | 0x64006400u;
+    f16x2 h = __builtin_bit_cast(f16x2, u);
+    const f16x2 off = {(_Float16)1032.f, (_Float16)1032.f};
+    h = (h - off) * s2;
+    return __builtin_bit_cast(uint32_t, h);
+  };
+  // One stage: every LDS read is issued before the first use, and step 1's
+  // operands (A reads, B dequant) are prepared while step 0's MFMAs run.
+  auto compute = [&](int slot) {
+    const Stage &L = st_lds[slot];
+    u32x2 wds[TNW];
+    uint32_t sp[TNW];
+#pragma unroll
+    for (int jj = 0; jj < TNW; ++jj) {
+      const int l = (jj & 1) * 32 + 2 * lr + (lq >> 1);
+      wds[jj] = reinterpret_cast<const u32x2 *>(&L.b[wave][jj >> 1][l])[lq & 1];
+      sp[jj] = L.s[wave][jj >> 2][(jj & 3) * 16 + lr];
+    }
+    f16x8 a0[NX][TMW], a1[NX][TMW];
+#pragma unroll
+    for (int x = 0; x < NX; ++x)
+#pragma unroll
+      for (int i = 0; i < TMW; ++i) a0[x][i] = as_f16x8(L.a[x][2 * lq][i * 16 + lr]);
+    f16x2 s2[TNW];
+#pragma unroll
+    for (int jj = 0; jj < TNW; ++jj) {
+      const uint32_t sb = (lq >> 1) ? sp[jj] >> 16 : sp[jj] & 0xffffu;
+      const _Float16 sh = (_Float16)ldexpf(bf16_to_f32(sb), b_shift[jj]);
+      s2[jj] = (f16x2){sh, sh};
+    }
+    auto deq8 = [&](uint32_t w, f16x2 sc) {
+      return as_f16x8((u32x4){deq(w, 0, sc), deq(w, 1, sc), deq(w, 2, sc), deq(w, 3, sc)});
+    };
+    f16x8 b0[TNW], b1[TNW];
+#pragma unroll
+    for (int jj = 0; jj < TNW; ++jj) b0[jj] = deq8(wds[jj][0], s2[jj]);
+#pragma unroll
+    for (int x = 0; x < NX; ++x)
+#pragma unroll
+      for (int i = 0; i < TMW; ++i) a1[x][i] = as_f16x8(L.a[x][2 * lq + 1][i * 16 + lr]);
+#pragma unroll
+    for (int jj = 0; jj < TNW; ++jj) b1[jj] = deq8(wds[jj][1], s2[jj]);
+#pragma unroll
+    for (int x = 0; x < NX; ++x)
+#pragma unroll
+      for (int i = 0; i < TMW; ++i)
+#pragma unroll
+        for (int jj = 0; jj < TNW; ++jj)
+          acc[i][jj] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0[x][i], b0[jj], acc[i][jj], 0, 0, 0);
+#pragma unroll
+    for (int x = 0; x < NX; ++x)
+#pragma unroll
+      for (int i = 0; i < TMW; ++i)
+#pragma unroll
+        for (int jj = 0; jj < TNW; ++jj)
+          acc[i][jj] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1[x][i], b1[jj], acc[i][jj], 0, 0, 0);
+    // the order above, as scheduling groups: this stage's loads, every LDS
+    // read of step 0, the scales and step 0's dequant, step 1's A reads, then
+    // step 0's MFMAs with step 1's dequant between them, then step 1's MFMAs
+    constexpr int NM = NX * TMW * TNW;  // MFMAs per step
+    __builtin_amdgcn_sched_group_barrier(0x020, NX * AW + BD + SD, 0);
+    __builtin_amdgcn_sched_group_barrier(0x100, 2 * TNW + NX * TMW, 0);
+    __builtin_amdgcn_sched_group_barrier(0x002, 20 * TNW, 0);
+    __builtin_amdgcn_sched_group_barrier(0x100, NX * TMW, 0);
+#pragma unroll
+    for (int k = 0; k < NM; ++k) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x002, (16 * TNW + NM - 1) / NM, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, NM, 0);
+  };
+
+  // Loads of one issue, per thread: they retire in order, so waiting until at
+  // most one issue is outstanding completes the one before it.  The wait and
+  // the barrier are one asm statement with a memory clobber: __syncthreads()
+  // would add a workgroup release, which waits for every load in flight (the
+  // direct-LDS loads count as LDS writes), the next stage's included.
+  constexpr int NI = NX * AW + BD + SD;
+  constexpr int NW = (P - 2) * NI;  // loads that may stay in flight: stages st + 2 .. st + P - 1
+  static_assert(NW < 64, "vmcnt is 6 bits");
+#pragma unroll
+  for (int q = 0; q < P - 1; ++q) issue(q, q);
+  asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(NW) : "memory");
+  for (int st0 = 0; st0 < S; st0 += P) {
+#pragma unroll
+    for (int s = 0; s < P; ++s) {
+      const int stg = st0 + s;
+      if (stg >= S) break;
+      issue(stg + P - 1, (s + P - 1) % P);  // the buffer of stage stg - 1, free after its barrier
+      compute(s);
+      // stage stg + 1 has landed (this wave's loads; after the barrier,
+      // everyone's), and no wave still reads stage stg's buffer; nothing
+      // (the MFMAs included) moves across
+      __builtin_amdgcn_sched_barrier(0);
+      asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(NW) : "memory");
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+  // the re-reads issued past the last stage land before the block may end
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+
+  // rescale before the first store (vmcnt counts stores too)
+  {
+    int ev[TMW][4];
+#pragma unroll
+    for (int i = 0; i < TMW; ++i)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int m = m0 + i * 16 + 4 * lq + r;
+        ev[i][r] = xe[m < M ? m : M - 1];
+      }
+#pragma unroll
+    for (int i = 0; i < TMW; ++i)
+#pragma unroll
+      for (int j = 0; j < TNW; ++j)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[i][j][r] = ldexpf(acc[i][j][r], ev[i][r] - b_shift[j]);
+  }
+
+  if (glu) {
+    float *out = static_cast<float *>(SG.y[0]);
+#pragma unroll
+    for (int i = 0; i < TMW; ++i) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int m = m0 + i * 16 + 4 * lq + r;
+        if (m >= M) continue;
+#pragma unroll
+        for (int j = 0; j < TNW / 2; ++j) {
+          const int n = col(j) + lr;
+          if (n >= N) continue;
+          out[(size_t)m * N + n] = gelu_tanh(acc[i][j][r]) * acc[i][j + TNW / 2][r];
+        }
+      }
+    }
+    return;
+  }
+  auto epilogue = [&](auto *out) {
+#pragma unroll
+    for (int i = 0; i < TMW; ++i) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int m = m0 + i * 16 + 4 * lq + r;
+        if (m >= M) continue;
+#pragma unroll
+        for (int j = 0; j < TNW; ++j) {
+          const int n = col(j) + lr;
+          if (n >= N) continue;
+          const float v = acc[i][j][r];
+          if constexpr (sizeof(*out) == 2)
+            out[(size_t)m * N + n] = (uint16_t)f32_to_bf16_rne(v);
+          else
+            out[(size_t)m * N + n] = v;
+        }
+      }
+    }
+  };
+  if (gridDim.y > 1)
+    epilogue(part + blockIdx.y * pstride);
+  else if (y_bf16)
+    epilogue(static_cast<uint16_t *>(SG.y[si]));
+  else
+    epilogue(static_cast<float *>(SG.y[si]));
+}
+
 // y[i] = sum of part[s * pstride + i] over the slices s in order, as FP32 or
 // BF16.  VEC: four outputs per thread (n a multiple of 4, y 16-byte aligned).
 template <bool VEC>
@@ -671,6 +978,55 @@ int launch_gemm(const g4_w4 *const *w, int nw, const uint4 *xt, const int *xe, i
   return G4_OK;
 }
 
+// The registers-B kernel: BM = 16 TMW rows by BN = 64 TNW columns per block,
+// stages of 64 values of K.
+template <int TMW, int TNW, int NX, int P, int MINB>
+int launch_gemm_rb(const g4_w4 *const *w, int nw, const uint4 *xt, const int *xe, int rows,
+                   int Mp, void *const *ys, bool y_bf16, float *part, int slices, bool sum,
+                   bool glu) {
+  constexpr int BM = 16 * TMW;
+  const int BN = glu ? 32 * TNW : 64 * TNW;  // output columns per block
+  if (Mp % BM != 0 || w[0]->G % (2 * slices) != 0 || (slices > 1 && nw != 1) ||
+      (glu && TNW % 2 != 0))
+    return fail(G4_E_ARG, "w4_gemm: tile %dx%d (%d slices) does not fit rows %d, K %d", BM, BN,
+                slices, rows, w[0]->K);
+  GemmSegs sg{};
+  sg.n = nw;
+  for (int i = 0; i < nw; ++i) {
+    sg.wq[i] = reinterpret_cast<const u32x4 *>(w[i]->packed);
+    sg.ws[i] = w[i]->scales;
+    sg.y[i] = ys[i];
+    sg.N[i] = w[i]->N;
+    sg.rs[i] = w[i]->row_shift ? w[i]->rshift : nullptr;
+    sg.shift[i] = w[i]->shift;
+    sg.t0[i + 1] = sg.t0[i] + (w[i]->N + BN - 1) / BN;
+  }
+  sg.glu = glu;
+  const int nm = (rows + BM - 1) / BM;
+  const int nn = glu ? (w[0]->N + BN - 1) / BN : sg.t0[nw];
+  const int xcd_map = nm % 8 == 0;
+  const size_t pstride = splitk_pstride(rows, w[0]->N);
+  hipLaunchKernelGGL((w4_gemm_rb_kernel<TMW, TNW, NX, P, MINB>), dim3(nm * nn, slices), dim3(kThreads),
+                     0, stream(), reinterpret_cast<const u32x4 *>(xt), xe, sg, (int)y_bf16, rows,
+                     Mp, w[0]->K, xcd_map, part, pstride);
+  G4_LAUNCH_CHECK("w4_gemm_rb_kernel");
+  if (slices > 1 && sum) {
+    void *y = ys[0];
+    const size_t n = (size_t)rows * w[0]->N;
+    const bool vec = n % 4 == 0 && (reinterpret_cast<uintptr_t>(y) & 15u) == 0;
+    const size_t threads = vec ? n / 4 : n;
+    const dim3 grid((unsigned)((threads + kThreads - 1) / kThreads));
+    if (vec)
+      hipLaunchKernelGGL(gemm_splitk_sum_kernel<true>, grid, dim3(kThreads), 0, stream(), part,
+                         slices, pstride, n, y, (int)y_bf16);
+    else
+      hipLaunchKernelGGL(gemm_splitk_sum_kernel<false>, grid, dim3(kThreads), 0, stream(), part,
+                         slices, pstride, n, y, (int)y_bf16);
+    G4_LAUNCH_CHECK("gemm_splitk_sum_kernel");
+  }
+  return G4_OK;
+}
+
 // Tile and K split of one prefill GEMM.  Tile: the largest (128 x 128, BF16
 // x) unless that leaves CUs idle or a ragged last wave; then 128 x 96 or 64 x 96
 // tiles when those fill whole rounds of the CUs (e.g. M 2048, N 1536 -> 256
@@ -687,6 +1043,7 @@ int launch_gemm(const g4_w4 *const *w, int nw, const uint4 *xt, const int *xe, i
 // 21 us instead of 70 / 127 / 25; N 256 at K 1536 10.6 instead of 18.
 struct GemmPlan {
   int tm, tn, ks, slices;
+  int rb;  // the registers-B kernel (tm, tn, ks unused)
 };
 constexpr int kMaxSplitK = 8;
 
@@ -702,6 +1059,19 @@ GemmPlan plan_gemm(const g4_w4 *const *w, int nw, int rows, bool f32x) {
   bool n96 = true;
   for (int i = 0; i < nw; ++i) n96 = n96 && w[i]->N % 96 == 0;
   const int split_ok = nw == 1;  // a K split takes one weight
+  {
+    // registers-B tiles: 128 x 192 (BF16 x) or 64 x 192 (FP32 x), split K
+    // into slices of at least 8 stages while that keeps the grid within two
+    // blocks per CU
+    const long b = blocks(f32x ? 64 : 128, 192);
+    if (b >= cus) return {0, 0, 0, 1, 1};
+    if (split_ok) {
+      int slices = 1;
+      for (int k = 2; k <= kMaxSplitK; ++k)
+        if (S % k == 0 && S / k >= 8 && b * k <= 2L * cus) slices = k;
+      if (b * slices >= cus) return {0, 0, 0, slices, 1};
+    }
+  }
   // FP32 x holds two planes of x' in LDS: 128-row tiles then fit one block
   // per CU, and 64-row tiles run faster (M 512, N 6144: 33 vs 45 us)
   if (!f32x && blocks(128, 128) >= 2L * cus) return {4, 4, 2, 1};
@@ -726,6 +1096,15 @@ int launch_planned(const GemmPlan &pl, const g4_w4 *const *w, int nw, const uint
                    bool sum, bool glu) {
   constexpr int P = 4;
   const int sl = pl.slices;
+  if (pl.rb) {
+    // two blocks per CU, 3 stages; 128 x 192 tiles (64 x 192 with FP32 x,
+    // whose two x' planes double the LDS per row), gate/up 64 x (96 + 96)
+    if (glu)
+      return launch_gemm_rb<4, 4, NX, 3, 2>(w, nw, xt, xe, rows, Mp, y, y_bf16, part, sl, sum,
+                                            glu);
+    return launch_gemm_rb<NX == 1 ? 8 : 4, 3, NX, 3, 2>(w, nw, xt, xe, rows, Mp, y, y_bf16, part,
+                                                       sl, sum, glu);
+  }
 #define G4_GEMM_TILE(TM, TN, KS) \
   return launch_gemm<TM, TN, NX, KS, P>(w, nw, xt, xe, rows, Mp, y, y_bf16, part, sl, sum, glu)
   if (pl.ks == 1) G4_GEMM_TILE(2, 2, 1);

@@ -348,7 +348,8 @@ def test_linear_multi_several_rows(g4, oracle, rows):
 def test_linear_multi_prefill_gemm(g4, shapes):
     # 512 FP32 rows, as the model's prefill: one x pre-pass and one GEMM launch
     # over the weights' tiles; each output against the binary64 product, and
-    # a weight that plans the same tile alone gives identical bits.
+    # the same weight run alone (its own plan: tile, K split) agrees within the
+    # same bound.
     rows, k = 512, shapes[0][1]
     x = np.random.default_rng(31).standard_normal((rows, k)).astype(np.float32)
     xb = g4.Buffer.from_array(x)
@@ -362,9 +363,9 @@ def test_linear_multi_prefill_gemm(g4, shapes):
     for lin, y, ref in zip(lins, ys, refs):
         got = y.download(np.float32).reshape(rows, lin.out_dim)
         assert rel_l2_rows(got, ref) <= 1e-5
-    if shapes[0][0] == 2048:  # q plans 64 x 64 tiles alone and with k, v
+    if shapes[0][0] == 2048:
         alone = run_linear(g4, lins[0], None, x, rows, g4.F32)
-        assert np.array_equal(ys[0].download(np.float32).reshape(rows, 2048), alone)
+        assert rel_l2_rows(ys[0].download(np.float32).reshape(rows, 2048), alone) <= 1e-5
 
 
 @pytest.mark.parametrize("rows", [5, 200, 512])
