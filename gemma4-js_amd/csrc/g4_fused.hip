@@ -980,76 +980,113 @@ __device__ __forceinline__ uint32_t half2_bits(_Float16 a, _Float16 b) {
 // an all-zero or non-finite row), per 8-value chunk c the FP16 pairs (0,4)
 // (1,5) (2,6) (3,7) of x * 2^-xe (hi) and of the rounding remainders (lo) at
 // xt[c * Mp + row] and xt[(width / 8 + c) * Mp + row].  r_out and x_out (FP32)
-// are optional.  Grid: Mp blocks; rows past `rows` write zero chunks.
+// are optional.
+//
+// One wave per row, 4 rows per block: lane l holds whole chunks l, l + 64,
+// ... (up to 4), so the norms and the maximum are wave reductions (no
+// barrier) and each chunk is converted where it was loaded.  Blocks are
+// dealt to the 8 XCDs round-robin; rows go to them in runs of Mp / 8, so the
+// 8 rows that share each 128-byte line of xt[c][m] are written through one
+// XCD's L2.  Grid: Mp / 4 blocks (Mp a multiple of 32); rows past `rows`
+// write zero chunks.
+constexpr int kChainCpl = 4;  // chunks per lane: width <= 64 * 4 * 8 = 2048
 __global__ __launch_bounds__(256) void norm_chain_xprep_kernel(
     const float *__restrict__ a, int a_parts, size_t a_stride, const float *__restrict__ h,
     const float *__restrict__ w1, const float *__restrict__ w2, float c, float eps, int width,
     int rows, float *__restrict__ r_out, float *__restrict__ x_out, uint4 *__restrict__ xt,
     int *__restrict__ xe, int Mp) {
-  __shared__ float red[16];
-  __shared__ float xs[2048];
-  const int row = blockIdx.x;
+  const int lane = threadIdx.x & 63;
+  const int grp = (blockIdx.x & 7) * (Mp >> 5) + (blockIdx.x >> 3);  // 4-row group
+  const int row = 4 * grp + (threadIdx.x >> 6);
   const int nch = width >> 3;
   const size_t lo_plane = (size_t)nch * Mp;
   if (row >= rows) {
-    for (int ch = threadIdx.x; ch < nch; ch += 256) {
+    for (int ch = lane; ch < nch; ch += 64) {
       xt[(size_t)ch * Mp + row] = make_uint4(0u, 0u, 0u, 0u);
       xt[lo_plane + (size_t)ch * Mp + row] = make_uint4(0u, 0u, 0u, 0u);
     }
     return;
   }
   const size_t off = (size_t)row * width;
-  constexpr int U = 8;
-  float av[U], hv[U], w1v[U], w2v[U];
+  // every load first (chunks past the row re-read chunk 0 and are left out)
+  float av[kChainCpl][8], hv[kChainCpl][8], w1v[kChainCpl][8], w2v[kChainCpl][8];
 #pragma unroll
-  for (int u = 0; u < U; ++u) {
-    int i = threadIdx.x + 256 * u;
-    i = i < width ? i : width - 1;
-    av[u] = a[off + i];
-    for (int s = 1; s < a_parts; ++s) av[u] += a[s * a_stride + off + i];
-    hv[u] = h[off + i];
-    w1v[u] = w1[i];
-    w2v[u] = w2 ? w2[i] : 0.f;
+  for (int u = 0; u < kChainCpl; ++u) {
+    int ch = lane + 64 * u;
+    ch = ch < nch ? ch : 0;
+    load8(a + off, ch, av[u]);
+    load8(h + off, ch, hv[u]);
+    load8(w1, ch, w1v[u]);
+    if (w2) load8(w2, ch, w2v[u]);
   }
+  for (int sp = 1; sp < a_parts; ++sp)  // the other partial planes, added in order
+#pragma unroll
+    for (int u = 0; u < kChainCpl; ++u) {
+      int ch = lane + 64 * u;
+      ch = ch < nch ? ch : 0;
+      float t[8];
+      load8(a + sp * a_stride + off, ch, t);
+#pragma unroll
+      for (int q = 0; q < 8; ++q) av[u][q] += t[q];
+    }
   float ss = 0.f;
 #pragma unroll
-  for (int u = 0; u < U; ++u)
-    if (threadIdx.x + 256 * u < width) ss += av[u] * av[u];
-  const float inv1 = 1.f / sqrtf(fblock_sum(ss, red, 4) / (float)width + eps);
-  float r[U], ss2 = 0.f;
+  for (int u = 0; u < kChainCpl; ++u)
+    if (lane + 64 * u < nch)
 #pragma unroll
-  for (int u = 0; u < U; ++u) {
-    r[u] = (hv[u] + av[u] * inv1 * w1v[u]) * c;
-    if (threadIdx.x + 256 * u < width) ss2 += r[u] * r[u];
-  }
-  float xv[U];
+      for (int q = 0; q < 8; ++q) ss += av[u][q] * av[u][q];
+  const float inv1 = 1.f / sqrtf(wave_sum(ss) / (float)width + eps);
+  float r[kChainCpl][8], ss2 = 0.f;
+#pragma unroll
+  for (int u = 0; u < kChainCpl; ++u)
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      r[u][q] = (hv[u][q] + av[u][q] * inv1 * w1v[u][q]) * c;
+      if (lane + 64 * u < nch) ss2 += r[u][q] * r[u][q];
+    }
+  float xv[kChainCpl][8];
   if (w2) {
-    const float inv2 = 1.f / sqrtf(fblock_sum(ss2, red + 4, 4) / (float)width + eps);
+    const float inv2 = 1.f / sqrtf(wave_sum(ss2) / (float)width + eps);
 #pragma unroll
-    for (int u = 0; u < U; ++u) xv[u] = r[u] * inv2 * w2v[u];
+    for (int u = 0; u < kChainCpl; ++u)
+#pragma unroll
+      for (int q = 0; q < 8; ++q) xv[u][q] = r[u][q] * inv2 * w2v[u][q];
   } else {
 #pragma unroll
-    for (int u = 0; u < U; ++u) xv[u] = r[u];
+    for (int u = 0; u < kChainCpl; ++u)
+#pragma unroll
+      for (int q = 0; q < 8; ++q) xv[u][q] = r[u][q];
   }
   float mx = 0.f;
 #pragma unroll
-  for (int u = 0; u < U; ++u) {
-    const int i = threadIdx.x + 256 * u;
-    if (i < width) {
-      if (r_out) r_out[off + i] = r[u];
-      if (x_out) x_out[off + i] = xv[u];
-      xs[i] = xv[u];
-      mx = fmaxf(mx, fabsf(xv[u]));
+  for (int u = 0; u < kChainCpl; ++u) {
+    const int ch = lane + 64 * u;
+    if (ch >= nch) continue;
+    float4 *ro = r_out ? reinterpret_cast<float4 *>(r_out + off) + 2 * ch : nullptr;
+    float4 *xo = x_out ? reinterpret_cast<float4 *>(x_out + off) + 2 * ch : nullptr;
+    if (ro) {
+      ro[0] = make_float4(r[u][0], r[u][1], r[u][2], r[u][3]);
+      ro[1] = make_float4(r[u][4], r[u][5], r[u][6], r[u][7]);
     }
+    if (xo) {
+      xo[0] = make_float4(xv[u][0], xv[u][1], xv[u][2], xv[u][3]);
+      xo[1] = make_float4(xv[u][4], xv[u][5], xv[u][6], xv[u][7]);
+    }
+#pragma unroll
+    for (int q = 0; q < 8; ++q) mx = fmaxf(mx, fabsf(xv[u][q]));
   }
-  mx = fblock_max(mx, red + 8);  // its barrier also publishes xs
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
   const int e = mx > 0.f && mx <= 3.4e38f ? ilogbf(mx) - 13 : 0;
-  if (threadIdx.x == 0) xe[row] = e;
-  for (int ch = threadIdx.x; ch < nch; ch += 256) {
+  if (lane == 0) xe[row] = e;
+#pragma unroll
+  for (int u = 0; u < kChainCpl; ++u) {
+    const int ch = lane + 64 * u;
+    if (ch >= nch) continue;
     _Float16 hh[8], ll[8];
 #pragma unroll
     for (int q = 0; q < 8; ++q) {
-      const float sv = ldexpf(xs[8 * ch + q], -e);
+      const float sv = ldexpf(xv[u][q], -e);
       hh[q] = (_Float16)sv;
       ll[q] = (_Float16)(sv - (float)hh[q]);
     }
@@ -1233,10 +1270,10 @@ int launch_norm_chain(const float *a, const float *h, const float *w1, const flo
 int launch_norm_chain_xprep(const float *a, int a_parts, size_t a_stride, const float *h,
                             const float *w1, const float *w2, float c, float eps, int rows,
                             int width, float *r_out, float *x_out, void *xt, int *xe, int Mp) {
-  if (width > 2048 || width % 8 || rows > Mp)
+  if (width > 64 * kChainCpl * 8 || width % 8 || rows > Mp || Mp % 32)
     return fail(G4_E_ARG, "norm chain with x pre-pass: width %d (<= 2048, multiple of 8), "
-                "rows %d <= %d", width, rows, Mp);
-  hipLaunchKernelGGL(norm_chain_xprep_kernel, dim3(Mp), dim3(256), 0, stream(), a, a_parts,
+                "rows %d <= %d (a multiple of 32)", width, rows, Mp);
+  hipLaunchKernelGGL(norm_chain_xprep_kernel, dim3(Mp / 4), dim3(256), 0, stream(), a, a_parts,
                      a_stride, h, w1, w2, c, eps, width, rows, r_out, x_out,
                      static_cast<uint4 *>(xt), xe, Mp);
   G4_LAUNCH_CHECK("norm_chain_xprep_kernel");
