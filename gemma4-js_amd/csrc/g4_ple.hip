@@ -35,17 +35,20 @@ namespace {
 
 using namespace g4;
 
-// One thread per 16 bytes of output: EPT consecutive elements of one row
-// (4 for FP32, 8 for BF16), so every store instruction of a wave writes 1 KB
-// of consecutive output and the packed reads (EPT/2 bytes per lane) are
-// consecutive too.  The table is only read (1.32 GB, far beyond the caches);
-// the output is written once.
+// One thread per 32 bytes of output: EPT consecutive elements of one row (8
+// for FP32, 16 for BF16), loaded as one 32- or 64-bit word of packed nibbles
+// and one scale (the EPT elements lie in one 32-element group), stored as two
+// 16-byte chunks.  Measured at 2048 ids: 17.4 vs 20.1 us (FP32) and 11.6 vs
+// 13.5 us (BF16) for one 16-byte chunk per thread; four chunks per thread
+// (stores 64 bytes apart across the lanes) took 52.7 us.  The table is only
+// read (1.32 GB, far beyond the caches); the output is written once.
 template <bool BF16OUT>
 __global__ __launch_bounds__(256) void ple_gather_kernel(
     const uint8_t *__restrict__ table, const int32_t *__restrict__ ids, int n,
     void *__restrict__ out, int vocab, int width, int rows_per_shard, size_t packed_row,
     size_t scale_row, size_t full_shard_bytes) {
-  constexpr int EPT = BF16OUT ? 8 : 4;
+  constexpr int EPT = BF16OUT ? 16 : 8;
+  constexpr int NW = EPT / 8;  // packed words per thread
   const int per_row = width / EPT;
   const size_t item = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (item >= (size_t)n * per_row) return;
@@ -63,34 +66,49 @@ __global__ __launch_bounds__(256) void ple_gather_kernel(
     const int rows_in_shard = left < rows_per_shard ? left : rows_per_shard;
     const uint8_t *base = table + (size_t)shard * full_shard_bytes;
     const uint8_t *prow = base + (size_t)local * packed_row;
-    // two's-complement nibbles -> offset binary: n ^ 8 = q + 8
-    uint32_t w = BF16OUT ? *reinterpret_cast<const uint32_t *>(prow + e0 / 2)
-                         : (uint32_t)*reinterpret_cast<const uint16_t *>(prow + e0 / 2);
-    w ^= 0x88888888u;
+    uint32_t w[NW];
+    if constexpr (NW == 1) {
+      w[0] = *reinterpret_cast<const uint32_t *>(prow + e0 / 2);
+    } else {
+      const uint2 x = *reinterpret_cast<const uint2 *>(prow + e0 / 2);
+      w[0] = x.x;
+      w[1] = x.y;
+    }
     const uint16_t sb = reinterpret_cast<const uint16_t *>(
         base + (size_t)rows_in_shard * packed_row + (size_t)local * scale_row)[e0 / 32];
     const float s = bf16_to_f32(sb);
 #pragma unroll
-    for (int i = 0; i < EPT; ++i) v[i] = (float)((int)((w >> (4 * i)) & 15u) - 8) * s;
+    for (int k = 0; k < NW; ++k) {
+      // two's-complement nibbles -> offset binary: n ^ 8 = q + 8
+      const uint32_t ww = w[k] ^ 0x88888888u;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) v[8 * k + i] = (float)((int)((ww >> (4 * i)) & 15u) - 8) * s;
+    }
   }
   const size_t o = (size_t)j * width + e0;
   // streaming stores: the output is written once and not read back here
   if (BF16OUT) {
-    u32x4 p;
 #pragma unroll
-    for (int k = 0; k < 4; ++k)
-      p[k] = f32_to_bf16_rne(v[2 * k]) | (f32_to_bf16_rne(v[2 * k + 1]) << 16);
-    __builtin_nontemporal_store(p, reinterpret_cast<u32x4 *>(static_cast<uint16_t *>(out) + o));
+    for (int k = 0; k < 2; ++k) {
+      u32x4 p;
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        p[q] = f32_to_bf16_rne(v[8 * k + 2 * q]) | (f32_to_bf16_rne(v[8 * k + 2 * q + 1]) << 16);
+      __builtin_nontemporal_store(p, reinterpret_cast<u32x4 *>(static_cast<uint16_t *>(out) + o) + k);
+    }
   } else {
-    const u32x4 p = {__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]),
-                     __float_as_uint(v[3])};
-    __builtin_nontemporal_store(p, reinterpret_cast<u32x4 *>(static_cast<float *>(out) + o));
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      const u32x4 p = {__float_as_uint(v[4 * k]), __float_as_uint(v[4 * k + 1]),
+                       __float_as_uint(v[4 * k + 2]), __float_as_uint(v[4 * k + 3])};
+      __builtin_nontemporal_store(p, reinterpret_cast<u32x4 *>(static_cast<float *>(out) + o) + k);
+    }
   }
 }
 
 int launch_gather(const g4_ple *t, const int32_t *ids_dev, int n, void *out, int out_dtype) {
   const bool bf = out_dtype == G4_BF16;
-  const size_t items = (size_t)n * (t->width / (bf ? 8 : 4));
+  const size_t items = (size_t)n * (t->width / (bf ? 16 : 8));
   const unsigned blocks = (unsigned)((items + 255) / 256);
   if (bf)
     hipLaunchKernelGGL(ple_gather_kernel<true>, dim3(blocks), dim3(256), 0, stream(), t->table,
