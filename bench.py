@@ -452,7 +452,7 @@ def main():
         cpu = cpu_baseline(n, k, args.cpu_seconds)
         log("  ", cpu)
 
-    traffic, traffic_src, kname = None, None, "w4_gemv1_kernel"
+    traffic, traffic_src, kname = None, None, "w4_gemv_r16_kernel"
     tpath = os.path.join(ROOT, "profiles", "w4_gemv_m1_k1536_n6144_traffic.json")
     if os.path.exists(tpath):
         with open(tpath) as f:

@@ -263,31 +263,19 @@ int gemv_rows_per_launch(int K, bool f32x) {
 // GC, TC: the group count and block size when known at compile time (0 =
 // taken from K and blockDim at run time); the E2B shapes use fixed ones.
 //
-// SPLIT: slice blockIdx.y of the input dimension.  The kernel then reads
-// groups [slice * G, slice * G + G) of rows whose length in memory is gstride
-// groups, x from slice * K, and writes FP32 partial sums to y + slice * N.
-//
 // bx: the block's index among the blocks of this weight (blockIdx.x, or the
 // index within its weight's blocks when one launch covers several weights).
-template <int GC, int TC, int IPL, bool F32X, bool SPLIT>
+template <int GC, int TC, int IPL, bool F32X>
 __device__ __forceinline__ void gemv1_body(const void *__restrict__ x,
                                            const uint4 *__restrict__ wq,
                                            const uint16_t *__restrict__ ws, void *__restrict__ y,
-                                           int y_bf16, int K, int N, int RB_, int gstride,
-                                           unsigned bx) {
+                                           int y_bf16, int K, int N, int RB_, unsigned bx) {
   extern __shared__ uint4 lds[];
   const int T = TC ? TC : (int)blockDim.x;
   const int G = GC ? GC : K >> 5;
   const int RB = GC ? TC * IPL / GC : RB_;
   const int nch = 4 * G;
   const int t = threadIdx.x;
-  if (SPLIT) {
-    const int slice = blockIdx.y;
-    x = static_cast<const char *>(x) + (size_t)slice * K * (F32X ? 4 : 2);
-    wq += (size_t)slice * G;
-    ws += (size_t)slice * G;
-    y = static_cast<float *>(y) + (size_t)slice * N;
-  }
 
   // 1. x chunks (L2-resident), issued first
   uint4 xa[IPL], xb[IPL];
@@ -310,15 +298,8 @@ __device__ __forceinline__ void gemv1_body(const void *__restrict__ x,
   uint32_t s[IPL];
 #pragma unroll
   for (int i = 0; i < IPL; ++i) {
-    size_t it;
-    if (SPLIT) {
-      const int li = t + i * T, r = li / G;
-      const int row = (int)bx * RB + r < N ? (int)bx * RB + r : N - 1;
-      it = (size_t)row * gstride + (li - r * G);
-    } else {
-      it = base + t + (size_t)i * T;
-      it = it < last ? it : last;
-    }
+    size_t it = base + t + (size_t)i * T;
+    it = it < last ? it : last;
     q[i] = ld_nt(&wq[it]);
     s[i] = ws[it];
   }
@@ -425,11 +406,11 @@ __device__ __forceinline__ void gemv1_body(const void *__restrict__ x,
   }
 }
 
-template <int GC, int TC, int IPL, bool F32X, bool SPLIT = false>
+template <int GC, int TC, int IPL, bool F32X>
 __global__ __launch_bounds__(TC ? TC : 1024) void w4_gemv1_kernel(
     const void *__restrict__ x, const uint4 *__restrict__ wq, const uint16_t *__restrict__ ws,
-    void *__restrict__ y, int y_bf16, int K, int N, int RB_, int gstride) {
-  gemv1_body<GC, TC, IPL, F32X, SPLIT>(x, wq, ws, y, y_bf16, K, N, RB_, gstride, blockIdx.x);
+    void *__restrict__ y, int y_bf16, int K, int N, int RB_) {
+  gemv1_body<GC, TC, IPL, F32X>(x, wq, ws, y, y_bf16, K, N, RB_, blockIdx.x);
 }
 
 // Up to kMaxLinearSegs weights of one input dimension over the same x in one
@@ -450,15 +431,257 @@ __global__ __launch_bounds__(TC ? TC : 1024) void w4_gemv1_multi_kernel(
     const void *__restrict__ x, Gemv1Segs S, int y_bf16, int K, int RB_) {
   const int b = blockIdx.x;
   const int i = S.n > 2 && b >= S.block0[2] ? 2 : S.n > 1 && b >= S.block0[1] ? 1 : 0;
-  gemv1_body<GC, TC, IPL, F32X, false>(x, S.wq[i], S.ws[i], S.y[i], y_bf16, K, S.N[i], RB_,
-                                       K >> 5, (unsigned)(b - S.block0[i]));
+  gemv1_body<GC, TC, IPL, F32X>(x, S.wq[i], S.ws[i], S.y[i], y_bf16, K, S.N[i], RB_,
+                                (unsigned)(b - S.block0[i]));
+}
+
+// ---------------------------------------------------------------------------
+// Decode GEMV, one row of x, for in_dim 1536 and 2048 (J = 3 or 4 groups of
+// 16 per row): the row split.
+//
+// 16 lanes per output row; lane c of a row takes groups c, c + 16, ...,
+// c + 16 (J - 1), so a block of W waves owns 4 W rows, and at instruction j
+// the 16 lanes of a row read 256 consecutive bytes of it.  x is staged in LDS
+// as in the flat split, then every lane reads its J groups' pairs and group
+// sums into registers right after the staging barrier, before its first
+// weight use.  The row sum is a 16-lane DPP reduction: once the weights land,
+// nothing goes back through LDS and no barrier sits between the last load and
+// the store.  The arithmetic and its order are the flat split's (each group
+// partial rounded, then added c, c + 16, ... before the 16-lane sum), so the
+// two give bit-identical outputs.
+//
+// gstride: row length in memory, in groups (J * 16, or the full width when a
+// split launch reads one slice of longer rows).  bx: the block's index among
+// the blocks of this weight.
+// ---------------------------------------------------------------------------
+template <int J, int W, bool F32X>
+__device__ __forceinline__ void gemv_r16_body(const void *__restrict__ x,
+                                              const uint4 *__restrict__ wq,
+                                              const uint16_t *__restrict__ ws,
+                                              void *__restrict__ y, int y_bf16, int N,
+                                              int gstride, unsigned bx) {
+  constexpr int G = 16 * J, T = 64 * W, nch = 4 * G;
+  constexpr int XI = (nch + T - 1) / T;  // x chunks per thread
+  constexpr int JL = F32X ? J : 1;
+  __shared__ uint4 hi[4 * G];
+  __shared__ uint4 lo[F32X ? 4 * G : 1];
+  __shared__ float sx[G];
+  const int t = threadIdx.x;
+  const int c16 = t & 15;
+  const int row = (int)bx * (4 * W) + (t >> 4);
+  const int rr = row < N ? row : N - 1;  // rows past N re-read the last row, store nothing
+  const uint4 *x4 = static_cast<const uint4 *>(x);
+
+  // 1. x chunks (L2-resident), issued before the weights
+  uint4 xa[XI], xb[XI];
+#pragma unroll
+  for (int i = 0; i < XI; ++i) {
+    const int ct = t + i * T;
+    const int cc = ct < nch ? ct : nch - 1;
+    if (F32X) {
+      xa[i] = x4[2 * cc];
+      xb[i] = x4[2 * cc + 1];
+    } else {
+      xa[i] = x4[cc];
+    }
+  }
+
+  // 2. the lane's J weight groups (HBM)
+  uint4 q[J];
+  uint32_t s[J];
+#pragma unroll
+  for (int j = 0; j < J; ++j) {
+    const size_t it = (size_t)rr * gstride + c16 + 16 * j;
+    q[j] = ld_nt(&wq[it]);
+    s[j] = ws[it];
+  }
+
+  // 3. stage x: bf16 pairs of each chunk (hi, and lo for FP32 x), 136 * group sum
+#pragma unroll
+  for (int i = 0; i < XI; ++i) {
+    const int ct = t + i * T;
+    uint32_t h[8], l[8];
+    float sum = 0.f;
+    if (F32X) {
+      const float v[8] = {__uint_as_float(xa[i].x), __uint_as_float(xa[i].y),
+                          __uint_as_float(xa[i].z), __uint_as_float(xa[i].w),
+                          __uint_as_float(xb[i].x), __uint_as_float(xb[i].y),
+                          __uint_as_float(xb[i].z), __uint_as_float(xb[i].w)};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        h[e] = f32_to_bf16_rne(v[e]);
+        l[e] = f32_to_bf16_rne(v[e] - bf16_to_f32(h[e]));
+        sum += bf16_to_f32(h[e]) + bf16_to_f32(l[e]);
+      }
+    } else {
+      const uint32_t w[4] = {xa[i].x, xa[i].y, xa[i].z, xa[i].w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        h[2 * e] = w[e] & 0xffffu;
+        h[2 * e + 1] = w[e] >> 16;
+        sum += bf16_to_f32(h[2 * e]) + bf16_to_f32(h[2 * e + 1]);
+      }
+    }
+    sum += dpp_f32<0xB1>(sum);  // chunks 4g..4g+3 of a group sit in one lane quad
+    sum += dpp_f32<0x4E>(sum);
+    if (ct < nch) {
+      const int g = ct >> 2, c = ct & 3;
+      hi[c * G + g] = make_uint4(bf16_pair(h[0], h[4]), bf16_pair(h[1], h[5]),
+                                 bf16_pair(h[2], h[6]), bf16_pair(h[3], h[7]));
+      if (F32X)
+        lo[c * G + g] = make_uint4(bf16_pair(l[0], l[4]), bf16_pair(l[1], l[5]),
+                                   bf16_pair(l[2], l[6]), bf16_pair(l[3], l[7]));
+      if (c == 0) sx[g] = kPairBias * sum;
+    }
+  }
+  // keep the weight arithmetic below the barrier: otherwise the compiler may
+  // hoist the first group's unpacking above it, and the barrier waits for HBM
+  __builtin_amdgcn_sched_barrier(0);
+  __syncthreads();
+
+  // 4. the lane's x groups into registers, all reads issued before any weight use
+  uint4 xh[J][4], xl[JL][4];
+  float sxr[J];
+#pragma unroll
+  for (int j = 0; j < J; ++j) {
+    const int g = c16 + 16 * j;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      xh[j][c] = hi[c * G + g];
+      if (F32X) xl[j < JL ? j : 0][c] = lo[c * G + g];
+    }
+    sxr[j] = sx[g];
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
+  // 5. group partials, the row sum over 16 lanes, the store
+  uint32_t mask = 0x000F000Fu;
+  asm volatile("" : "+v"(mask));  // keep the mask in a VGPR: lets v_and_or_b32 take the magic
+  float v = 0.f;
+#pragma unroll
+  for (int j = 0; j < J; ++j) {
+    const uint32_t wd[4] = {q[j].x, q[j].y, q[j].z, q[j].w};
+    float d0 = 0.f, d1 = 0.f;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const uint32_t p0 = (wd[c] & mask) | kPairMagic;
+      const uint32_t p1 = ((wd[c] >> 4) & mask) | kPairMagic;
+      const uint32_t p2 = ((wd[c] >> 8) & mask) | kPairMagic;
+      const uint32_t p3 = ((wd[c] >> 12) & mask) | kPairMagic;
+      const uint4 xp = xh[j][c];
+      d0 = dot2_bf16(xp.x, p0, d0);
+      d1 = dot2_bf16(xp.y, p1, d1);
+      d0 = dot2_bf16(xp.z, p2, d0);
+      d1 = dot2_bf16(xp.w, p3, d1);
+      if (F32X) {
+        const uint4 xq = xl[j < JL ? j : 0][c];
+        d0 = dot2_bf16(xq.x, p0, d0);
+        d1 = dot2_bf16(xq.y, p1, d1);
+        d0 = dot2_bf16(xq.z, p2, d0);
+        d1 = dot2_bf16(xq.w, p3, d1);
+      }
+    }
+    float pj = bf16_to_f32(s[j]) * ((d0 + d1) - sxr[j]);
+    asm volatile("" : "+v"(pj));  // rounded on its own (no FMA into the row sum)
+    v += pj;
+  }
+  v = team_sum<16>(v);
+  if (c16 == 0 && row < N) {
+    if (y_bf16)
+      static_cast<uint16_t *>(y)[row] = (uint16_t)f32_to_bf16_rne(v);
+    else  // written through to memory (sc0 sc1): 3.06 against 3.09 us at N 6144
+      __hip_atomic_store(static_cast<float *>(y) + row, v, __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_SYSTEM);
+  }
+}
+
+// SPLIT: slice blockIdx.y of the input dimension (16 J groups of rows
+// gstride groups long), x from slice * 512 J, FP32 partial sums to
+// y + slice * N.
+template <int J, int W, bool F32X, bool SPLIT>
+__global__ __launch_bounds__(64 * W) void w4_gemv_r16_kernel(
+    const void *__restrict__ x, const uint4 *__restrict__ wq, const uint16_t *__restrict__ ws,
+    void *__restrict__ y, int y_bf16, int N, int gstride) {
+  if (SPLIT) {
+    const int slice = blockIdx.y;
+    x = static_cast<const char *>(x) + (size_t)slice * 512 * J * (F32X ? 4 : 2);
+    wq += (size_t)slice * 16 * J;
+    ws += (size_t)slice * 16 * J;
+    y = static_cast<float *>(y) + (size_t)slice * N;
+  }
+  gemv_r16_body<J, W, F32X>(x, wq, ws, y, y_bf16, N, gstride, blockIdx.x);
+}
+
+template <int J, int W, bool F32X>
+__global__ __launch_bounds__(64 * W) void w4_gemv_r16_multi_kernel(const void *__restrict__ x,
+                                                                   Gemv1Segs S, int y_bf16) {
+  const int b = blockIdx.x;
+  const int i = S.n > 2 && b >= S.block0[2] ? 2 : S.n > 1 && b >= S.block0[1] ? 1 : 0;
+  gemv_r16_body<J, W, F32X>(x, S.wq[i], S.ws[i], S.y[i], y_bf16, S.N[i], 16 * J,
+                            (unsigned)(b - S.block0[i]));
+}
+
+// Waves per block of the row split: 4 (16 rows) from 4096 rows on, else 2
+// (measured at in_dim 1536, cold weights: N 6144 3.09 us with 4 waves against
+// 3.34 with 2; N 2048 2.46 us with 2 against 2.49 with 4).
+inline int r16_waves(int rows) { return rows >= 4096 ? 4 : 2; }
+
+inline bool has_r16(int G) { return G == 48 || G == 64; }
+
+template <int J, int W, bool F32X>
+int launch_r16_i(const g4_w4 *w, const void *x, void *y, int y_bf16) {
+  hipLaunchKernelGGL((w4_gemv_r16_kernel<J, W, F32X, false>),
+                     dim3((w->N + 4 * W - 1) / (4 * W)), dim3(64 * W), 0, stream(), x, w->packed,
+                     w->scales, y, y_bf16, w->N, w->G);
+  G4_LAUNCH_CHECK("w4_gemv_r16_kernel");
+  return G4_OK;
+}
+
+template <bool F32X>
+int launch_r16(const g4_w4 *w, const void *x, void *y, int y_bf16) {
+  const bool w4 = r16_waves(w->N) == 4;
+  if (w->G == 48)
+    return w4 ? launch_r16_i<3, 4, F32X>(w, x, y, y_bf16) : launch_r16_i<3, 2, F32X>(w, x, y, y_bf16);
+  return w4 ? launch_r16_i<4, 4, F32X>(w, x, y, y_bf16) : launch_r16_i<4, 2, F32X>(w, x, y, y_bf16);
+}
+
+template <int J, int W, bool F32X>
+int launch_r16_multi_i(const g4_w4 *const *w, int n, const void *x, void *const *y,
+                       int y_bf16) {
+  Gemv1Segs S{};
+  int blocks = 0;
+  for (int i = 0; i < n; ++i) {
+    S.wq[i] = w[i]->packed;
+    S.ws[i] = w[i]->scales;
+    S.y[i] = y[i];
+    S.N[i] = w[i]->N;
+    S.block0[i] = blocks;
+    blocks += (w[i]->N + 4 * W - 1) / (4 * W);
+  }
+  S.n = n;
+  hipLaunchKernelGGL((w4_gemv_r16_multi_kernel<J, W, F32X>), dim3(blocks), dim3(64 * W), 0,
+                     stream(), x, S, y_bf16);
+  G4_LAUNCH_CHECK("w4_gemv_r16_multi_kernel");
+  return G4_OK;
+}
+
+template <bool F32X>
+int launch_r16_multi(const g4_w4 *const *w, int n, const void *x, void *const *y, int y_bf16) {
+  int rows = 0;
+  for (int i = 0; i < n; ++i) rows += w[i]->N;
+  const bool w4 = r16_waves(rows) == 4;
+  if (w[0]->G == 48)
+    return w4 ? launch_r16_multi_i<3, 4, F32X>(w, n, x, y, y_bf16)
+              : launch_r16_multi_i<3, 2, F32X>(w, n, x, y, y_bf16);
+  return w4 ? launch_r16_multi_i<4, 4, F32X>(w, n, x, y, y_bf16)
+            : launch_r16_multi_i<4, 2, F32X>(w, n, x, y, y_bf16);
 }
 
 template <int GC, int TC, int IPL, bool F32X>
 int launch_gemv1_i(const g4_w4 *w, const Gemv1Plan &p, const void *x, void *y, int y_bf16) {
   const int blocks = (w->N + p.RB - 1) / p.RB;
   hipLaunchKernelGGL((w4_gemv1_kernel<GC, TC, IPL, F32X>), dim3(blocks), dim3(p.T), p.lds,
-                     stream(), x, w->packed, w->scales, y, y_bf16, w->K, w->N, p.RB, w->G);
+                     stream(), x, w->packed, w->scales, y, y_bf16, w->K, w->N, p.RB);
   G4_LAUNCH_CHECK("w4_gemv1_kernel");
   return G4_OK;
 }
@@ -479,27 +702,18 @@ int gemv1_plan(const g4_w4 *w, Gemv1Plan *p) {
   const int min_rb = F32X && w->K >= 4096 ? 8 : 4;
   if (!plan_gemv1(w->G, F32X, p, min_rb) && !plan_gemv1(w->G, F32X, p))
     return fail(G4_E_ARG, "g4_w4_linear: no decode GEMV plan for in_dim %d", w->K);
-  if (w->G == 48) {
-    // K = 1536: 8 rows per 192-thread block, two groups per thread (measured
-    // 3.21 vs 3.26 us at N 6144 and 4.02 vs 4.57 us at N 12288, cold weights)
-    p->T = 192;
-    p->IPL = 2;
-    p->RB = 8;
-    p->lds = (size_t)48 * 4 * 16 * (F32X ? 2 : 1) + 48 * 4 + (size_t)8 * 48 * 4;
-  }
   return G4_OK;
 }
 
 template <bool F32X>
 int launch_gemv1(const g4_w4 *w, const void *x, void *y, int y_bf16) {
+  if (has_r16(w->G)) return launch_r16<F32X>(w, x, y, y_bf16);
   Gemv1Plan p;
   if (int rc = gemv1_plan<F32X>(w, &p)) return rc;
   // compile-time variants for the plans of the Gemma-4-E2B projections
 #define G4_GEMV1_FIXED(GG, TT, II)                                      \
   if (w->G == GG && p.T == TT && p.IPL == II)                           \
     return launch_gemv1_i<GG, TT, II, F32X>(w, p, x, y, y_bf16);
-  G4_GEMV1_FIXED(48, 192, 2)    // K = 1536
-  G4_GEMV1_FIXED(64, 256, 1)    // K = 2048
   G4_GEMV1_FIXED(128, 512, 1)   // K = 4096
   G4_GEMV1_FIXED(192, 768, 1)   // K = 6144
   G4_GEMV1_FIXED(384, 768, 2)   // K = 12288
@@ -540,10 +754,9 @@ int launch_gemv1_multi_i(const g4_w4 *const *w, int n, const Gemv1Plan &p, const
 template <bool F32X>
 int launch_gemv1_multi(const g4_w4 *const *w, int n, const void *x, void *const *y,
                        int y_bf16) {
+  if (has_r16(w[0]->G)) return launch_r16_multi<F32X>(w, n, x, y, y_bf16);
   Gemv1Plan p;
   if (int rc = gemv1_plan<F32X>(w[0], &p)) return rc;
-  if (w[0]->G == 48 && p.T == 192 && p.IPL == 2)  // K = 1536: q/k/v, gate/up
-    return launch_gemv1_multi_i<48, 192, 2, F32X>(w, n, p, x, y, y_bf16);
   switch (p.IPL) {
     case 1: return launch_gemv1_multi_i<0, 0, 1, F32X>(w, n, p, x, y, y_bf16);
     case 2: return launch_gemv1_multi_i<0, 0, 2, F32X>(w, n, p, x, y, y_bf16);
@@ -597,21 +810,23 @@ bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 namespace g4 {
 
 // Split-K decode GEMV for one FP32 row: parts[s][n] = sum over inputs
-// [1536 s, 1536 s + 1536) of x[k] * W[n, k], each slice on the K = 1536 plan
-// (8 rows per 192-thread block).  A long input row then needs neither the
-// whole row staged per block nor fewer blocks than CUs; the consumer adds the
-// slices in order.  Returns the slice count, 0 when K is not a multiple of
-// 1536 of at least two slices (nothing launched), or a negative status.
+// [1536 s, 1536 s + 1536) of x[k] * W[n, k], each slice on the in_dim 1536
+// row split with 16 rows per block (E2B decode step, down 1536 x 6144:
+// 1.243 ms/token against 1.259 with 8 rows and 1.267 with 4).  A long input
+// row then needs neither the whole row staged per block nor fewer blocks than
+// CUs; the consumer adds the slices in order.
+// Returns the slice count, 0 when K is not a multiple of 1536 of at least two
+// slices (nothing launched), or a negative status.
 int launch_gemv1_split(const g4_w4 *w, const float *x, float *parts) {
-  constexpr int kSliceK = 1536, G = kSliceK / 32, T = 192, IPL = 2, RB = 8;
+  constexpr int kSliceK = 1536, W = 4;
   if (w->K % kSliceK || w->K / kSliceK < 2) return 0;
   const int slices = w->K / kSliceK;
-  const size_t lds = (size_t)G * 4 * 16 * 2 + G * 4 + (size_t)RB * G * 4;
-  hipLaunchKernelGGL((w4_gemv1_kernel<G, T, IPL, true, true>),
-                     dim3((w->N + RB - 1) / RB, slices), dim3(T), lds, stream(), x, w->packed,
-                     w->scales, parts, 0, kSliceK, w->N, RB, w->G);
+  hipLaunchKernelGGL((w4_gemv_r16_kernel<kSliceK / 512, W, true, true>),
+                     dim3((w->N + 4 * W - 1) / (4 * W), slices), dim3(64 * W), 0, stream(), x,
+                     w->packed, w->scales, parts, 0, w->N, w->G);
   const hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return -fail(G4_E_HIP, "w4_gemv1_kernel (split): %s", hipGetErrorString(e));
+  if (e != hipSuccess)
+    return -fail(G4_E_HIP, "w4_gemv_r16_kernel (split): %s", hipGetErrorString(e));
   return slices;
 }
 
