@@ -122,91 +122,65 @@ __device__ __forceinline__ const FusedSeg &seg_for(const FusedArgs &A, int rg, i
   return S;
 }
 
-// Block b owns row groups b, b + grid, ..., IT of them (ngroups in total).
-// Every weight load of those groups is issued at the start, before the
-// prologue: the prologue's chain of dependent steps (activation loads, two
-// block reductions, staging) then overlaps one HBM round trip instead of
-// delaying the later groups' loads.
-template <int GC, int TC, int IPL, int IT, int PRO, int EPI>
-__global__ __launch_bounds__(TC ? TC : 1024) void fused_gemv_kernel(FusedArgs A, int RB_,
-                                                                    int ngroups) {
-  extern __shared__ uint4 lds[];
-  const int T = TC ? TC : (int)blockDim.x;
-  const int G = GC ? GC : A.K >> 5;
-  const int RB = GC ? TC * IPL / GC : RB_;
-  const int nch = 4 * G;
-  const int t = threadIdx.x;
-  const int nwaves = (T + 63) >> 6;
-
-  // The prologue runs on the first pw waves only (the 4G chunks of 8 inputs,
-  // XI per lane): the other waves skip it and meet them at the barriers, so
-  // the SIMDs are not busy with copies of the same element-wise work.
-  const int wave = t >> 6;
-  const int pw = ((nch + 63) >> 6) < nwaves ? ((nch + 63) >> 6) : nwaves;
-  const bool pro = wave < pw;  // uniform per wave
-  const int cstride = 64 * pw;
-  constexpr int XI = (GC && TC) ? (4 * GC + 63) / 64 <= TC / 64 ? 1 : (4 * GC + TC - 1) / TC : IPL;
-
-  // 1. activation chunks, issued before the weight stream.  With kProRes, a
-  // may come as up to kMaxParts partial vectors (split-K sums of the previous
-  // GEMV): all are loaded here (past a_parts the last is re-read) and added
-  // in order in the prologue.
-  constexpr int NPART = PRO == kProRes ? kMaxParts : 1;
+// The activation inputs of one prologue lane: XI chunks of 8 of each vector.
+// With kProRes, a may come as up to kMaxParts partial vectors (split-K sums of
+// the previous GEMV).
+template <int XI, int PRO>
+struct ProIn {
+  static constexpr int NPART = PRO == kProRes ? kMaxParts : 1;
   float av[XI][8], hv[XI][8], w1v[XI][8], w2v[XI][8], apv[NPART > 1 ? NPART - 1 : 1][XI][8];
-  if (pro) {
+};
+
+// Step 1 of a fused launch: the prologue lanes load their activation chunks
+// (chunk t + i * cstride), before the weight stream.  All partial vectors are
+// loaded here (past a_parts the last is re-read) and added in order later.
+template <int XI, int PRO>
+__device__ __forceinline__ void pro_load(const FusedArgs &A, int t, int cstride, int nch,
+                                         bool pro, ProIn<XI, PRO> &in) {
+  if (!pro) return;
 #pragma unroll
-    for (int i = 0; i < XI; ++i) {
-      const int ct = t + i * cstride;
-      const int cc = ct < nch ? ct : nch - 1;
-      load8(A.a, cc, av[i]);
+  for (int i = 0; i < XI; ++i) {
+    const int ct = t + i * cstride;
+    const int cc = ct < nch ? ct : nch - 1;
+    load8(A.a, cc, in.av[i]);
 #pragma unroll
-      for (int pp = 1; pp < NPART; ++pp) {
-        const int pc = pp < A.a_parts ? pp : A.a_parts - 1;
-        load8(A.a + (size_t)pc * A.K, cc, apv[pp - 1][i]);
-      }
-      if (PRO != kProNone) load8(A.w1, cc, w1v[i]);
-      if (PRO == kProRes || PRO == kProResNorm) load8(A.h, cc, hv[i]);
-      if (PRO == kProResNorm) load8(A.w2, cc, w2v[i]);
+    for (int pp = 1; pp < ProIn<XI, PRO>::NPART; ++pp) {
+      const int pc = pp < A.a_parts ? pp : A.a_parts - 1;
+      load8(A.a + (size_t)pc * A.K, cc, in.apv[pp - 1][i]);
     }
+    if (PRO != kProNone) load8(A.w1, cc, in.w1v[i]);
+    if (PRO == kProRes || PRO == kProResNorm) load8(A.h, cc, in.hv[i]);
+    if (PRO == kProResNorm) load8(A.w2, cc, in.w2v[i]);
   }
+}
 
-  // 2. weights of all the block's row groups (groups past the last re-read it
-  // and store nothing; rows past N re-read the last group)
-  uint4 q[IT][IPL];
-  uint32_t s[IT][IPL];
-#pragma unroll
-  for (int k = 0; k < IT; ++k) {
-    const int rg = blockIdx.x + k * (int)gridDim.x;
-    load_rows<IPL, EPI>(A, rg < ngroups ? rg : ngroups - 1, G, RB, T, t, q[k], s[k]);
-  }
-
-  // 3. prologue
-  constexpr int CH = 2;  // FP32 activations: hi and lo
-  uint4 *hi = lds;
-  uint4 *lo = lds + 4 * G;
-  float *sx = reinterpret_cast<float *>(lds + 4 * G * CH);
-  float *part = sx + G;              // [IT * RB][G]
-  float *rs = part + IT * RB * G;    // row sums [IT * RB] (kEpiGeluUp)
-  float *red = rs + IT * RB;         // 2 x 16 wave sums
-  // Everything element-wise stays inside `if (pro)`; the reductions are
-  // called by every wave.
+// Steps 3 and 4: the prologue (norms, residual; block 0 writes r) and the x
+// staging: hi/lo bf16 pairs per chunk in hi[c * G + g], lo[...], and
+// 136 * group sum in sx[g].  Every wave of the block must call it (the
+// reductions are block-wide); the element-wise work stays on the pw
+// prologue waves.  red: 32 floats.  Ends with the block barrier after which
+// the staged x may be read.
+template <int XI, int PRO>
+__device__ __forceinline__ void pro_stage(const FusedArgs &A, ProIn<XI, PRO> &in, int t,
+                                          int cstride, int nch, int pw, bool pro, int G,
+                                          uint4 *hi, uint4 *lo, float *sx, float *red) {
   float xv[XI][8];
   if (PRO == kProNone) {
     if (pro) {
 #pragma unroll
       for (int i = 0; i < XI; ++i)
 #pragma unroll
-        for (int e = 0; e < 8; ++e) xv[i][e] = av[i][e];
+        for (int e = 0; e < 8; ++e) xv[i][e] = in.av[i][e];
     }
   } else {
-    if (NPART > 1 && pro) {
+    if (ProIn<XI, PRO>::NPART > 1 && pro) {
 #pragma unroll
-      for (int pp = 1; pp < NPART; ++pp)
+      for (int pp = 1; pp < ProIn<XI, PRO>::NPART; ++pp)
         if (pp < A.a_parts)
 #pragma unroll
           for (int i = 0; i < XI; ++i)
 #pragma unroll
-            for (int e = 0; e < 8; ++e) av[i][e] += apv[pp - 1][i][e];
+            for (int e = 0; e < 8; ++e) in.av[i][e] += in.apv[pp - 1][i][e];
     }
     float ss = 0.f;
     if (pro) {
@@ -214,7 +188,7 @@ __global__ __launch_bounds__(TC ? TC : 1024) void fused_gemv_kernel(FusedArgs A,
       for (int i = 0; i < XI; ++i)
         if (t + i * cstride < nch)
 #pragma unroll
-          for (int e = 0; e < 8; ++e) ss += av[i][e] * av[i][e];
+          for (int e = 0; e < 8; ++e) ss += in.av[i][e] * in.av[i][e];
     }
     const float tot1 = pro_sum(ss, red, pw, pro);
     float r[XI][8];
@@ -225,13 +199,13 @@ __global__ __launch_bounds__(TC ? TC : 1024) void fused_gemv_kernel(FusedArgs A,
 #pragma unroll
         for (int i = 0; i < XI; ++i)
 #pragma unroll
-          for (int e = 0; e < 8; ++e) xv[i][e] = av[i][e] * inv1 * w1v[i][e];
+          for (int e = 0; e < 8; ++e) xv[i][e] = in.av[i][e] * inv1 * in.w1v[i][e];
       } else {
 #pragma unroll
         for (int i = 0; i < XI; ++i)
 #pragma unroll
           for (int e = 0; e < 8; ++e) {
-            r[i][e] = (hv[i][e] + av[i][e] * inv1 * w1v[i][e]) * A.c;
+            r[i][e] = (in.hv[i][e] + in.av[i][e] * inv1 * in.w1v[i][e]) * A.c;
             if (t + i * cstride < nch) ss2 += r[i][e] * r[i][e];
           }
         if (blockIdx.x == 0) {
@@ -260,12 +234,11 @@ __global__ __launch_bounds__(TC ? TC : 1024) void fused_gemv_kernel(FusedArgs A,
 #pragma unroll
         for (int i = 0; i < XI; ++i)
 #pragma unroll
-          for (int e = 0; e < 8; ++e) xv[i][e] = r[i][e] * inv2 * w2v[i][e];
+          for (int e = 0; e < 8; ++e) xv[i][e] = r[i][e] * inv2 * in.w2v[i][e];
       }
     }
   }
 
-  // 4. stage x: hi/lo bf16 pairs per chunk, 136 * group sum
   if (pro) {
 #pragma unroll
     for (int i = 0; i < XI; ++i) {
@@ -291,6 +264,56 @@ __global__ __launch_bounds__(TC ? TC : 1024) void fused_gemv_kernel(FusedArgs A,
     }
   }
   __syncthreads();
+}
+
+// Block b owns row groups b, b + grid, ..., IT of them (ngroups in total).
+// Every weight load of those groups is issued at the start, before the
+// prologue: the prologue's chain of dependent steps (activation loads, two
+// block reductions, staging) then overlaps one HBM round trip instead of
+// delaying the later groups' loads.
+template <int GC, int TC, int IPL, int IT, int PRO, int EPI>
+__global__ __launch_bounds__(TC ? TC : 1024) void fused_gemv_kernel(FusedArgs A, int RB_,
+                                                                    int ngroups) {
+  extern __shared__ uint4 lds[];
+  const int T = TC ? TC : (int)blockDim.x;
+  const int G = GC ? GC : A.K >> 5;
+  const int RB = GC ? TC * IPL / GC : RB_;
+  const int nch = 4 * G;
+  const int t = threadIdx.x;
+  const int nwaves = (T + 63) >> 6;
+
+  // The prologue runs on the first pw waves only (the 4G chunks of 8 inputs,
+  // XI per lane): the other waves skip it and meet them at the barriers, so
+  // the SIMDs are not busy with copies of the same element-wise work.
+  const int wave = t >> 6;
+  const int pw = ((nch + 63) >> 6) < nwaves ? ((nch + 63) >> 6) : nwaves;
+  const bool pro = wave < pw;  // uniform per wave
+  const int cstride = 64 * pw;
+  constexpr int XI = (GC && TC) ? (4 * GC + 63) / 64 <= TC / 64 ? 1 : (4 * GC + TC - 1) / TC : IPL;
+
+  // 1. activation chunks, issued before the weight stream
+  ProIn<XI, PRO> in;
+  pro_load<XI, PRO>(A, t, cstride, nch, pro, in);
+
+  // 2. weights of all the block's row groups (groups past the last re-read it
+  // and store nothing; rows past N re-read the last group)
+  uint4 q[IT][IPL];
+  uint32_t s[IT][IPL];
+#pragma unroll
+  for (int k = 0; k < IT; ++k) {
+    const int rg = blockIdx.x + k * (int)gridDim.x;
+    load_rows<IPL, EPI>(A, rg < ngroups ? rg : ngroups - 1, G, RB, T, t, q[k], s[k]);
+  }
+
+  // 3-4. prologue and x staging
+  constexpr int CH = 2;  // FP32 activations: hi and lo
+  uint4 *hi = lds;
+  uint4 *lo = lds + 4 * G;
+  float *sx = reinterpret_cast<float *>(lds + 4 * G * CH);
+  float *part = sx + G;              // [IT * RB][G]
+  float *rs = part + IT * RB * G;    // row sums [IT * RB] (kEpiGeluUp)
+  float *red = rs + IT * RB;         // 2 x 16 wave sums
+  pro_stage<XI, PRO>(A, in, t, cstride, nch, pw, pro, G, hi, lo, sx, red);
 
   // 5. one partial per group, for every row group of the block
   uint32_t mask = 0x000F000Fu;
@@ -365,6 +388,116 @@ __global__ __launch_bounds__(TC ? TC : 1024) void fused_gemv_kernel(FusedArgs A,
   }
 }
 
+// Row split of a fused launch at in_dim 1536 (48 groups per row): 16 lanes per
+// output row, lane c taking groups c, c + 16 and c + 32, as in
+// w4_gemv_r16_kernel.  A block of W waves owns row groups of 4 W rows, IT of
+// them as in fused_gemv_kernel.  The prologue and staging are the flat
+// kernel's; after the staging barrier every lane reads its groups' x pairs
+// into registers and each row sum is a 16-lane DPP reduction: no LDS
+// partials and no barrier after the weights land.  The group partials and
+// their order are the flat kernel's, so the outputs are bit-identical.  (No
+// gelu(gate) * up epilogue: gate/up keeps the flat split.)
+template <int EPI>
+__device__ __forceinline__ const FusedSeg &r16_row(const FusedArgs &A, int rg, int team, int W,
+                                                   int *o) {
+  int o0;
+  const FusedSeg &S = seg_for<EPI>(A, rg, 4 * W, &o0);
+  *o = o0 + team;
+  return S;
+}
+
+template <int W, int IT, int PRO, int EPI>
+__global__ __launch_bounds__(64 * W) void fused_r16_kernel(FusedArgs A, int ngroups) {
+  static_assert(EPI != kEpiGeluUp, "gate/up takes the flat split");
+  constexpr int J = 3, G = 16 * J, nch = 4 * G;
+  constexpr int PW = (nch + 63) / 64 < W ? (nch + 63) / 64 : W;  // prologue waves
+  constexpr int XI = (nch + 64 * PW - 1) / (64 * PW);
+  __shared__ uint4 hi[4 * G], lo[4 * G];
+  __shared__ float sx[G], red[32];
+  const int t = threadIdx.x, c16 = t & 15, team = t >> 4;
+  const bool pro = (t >> 6) < PW;  // uniform per wave
+
+  // 1. activation chunks, issued before the weight stream
+  ProIn<XI, PRO> in;
+  pro_load<XI, PRO>(A, t, 64 * PW, nch, pro, in);
+
+  // 2. the lane's groups of its row in every row group (groups past the last
+  // re-read it, rows past N the last row; neither is stored)
+  uint4 q[IT][J];
+  uint32_t s[IT][J];
+#pragma unroll
+  for (int k = 0; k < IT; ++k) {
+    const int rg = blockIdx.x + k * (int)gridDim.x;
+    int o;
+    const FusedSeg &S = r16_row<EPI>(A, rg < ngroups ? rg : ngroups - 1, team, W, &o);
+    const int rr = o < S.N ? o : S.N - 1;
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+      const size_t it = (size_t)rr * G + c16 + 16 * j;
+      q[k][j] = ld_nt(&S.wq[it]);
+      s[k][j] = S.ws[it];
+    }
+  }
+
+  // 3-4. prologue and x staging; keep the weight arithmetic below its barriers
+  __builtin_amdgcn_sched_barrier(0);
+  pro_stage<XI, PRO>(A, in, t, 64 * PW, nch, PW, pro, G, hi, lo, sx, red);
+
+  // 5. the lane's x groups into registers, all reads issued before any weight use
+  uint4 xh[J][4], xl[J][4];
+  float sxr[J];
+#pragma unroll
+  for (int j = 0; j < J; ++j) {
+    const int g = c16 + 16 * j;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      xh[j][c] = hi[c * G + g];
+      xl[j][c] = lo[c * G + g];
+    }
+    sxr[j] = sx[g];
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
+  // 6. per row group: group partials, the 16-lane row sum, the epilogue
+  uint32_t mask = 0x000F000Fu;
+  asm volatile("" : "+v"(mask));  // keep the mask in a VGPR: lets v_and_or_b32 take the magic
+#pragma unroll
+  for (int k = 0; k < IT; ++k) {
+    float v = 0.f;
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+      const uint32_t wd[4] = {q[k][j].x, q[k][j].y, q[k][j].z, q[k][j].w};
+      float d0 = 0.f, d1 = 0.f;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const uint32_t p0 = (wd[c] & mask) | kPairMagic;
+        const uint32_t p1 = ((wd[c] >> 4) & mask) | kPairMagic;
+        const uint32_t p2 = ((wd[c] >> 8) & mask) | kPairMagic;
+        const uint32_t p3 = ((wd[c] >> 12) & mask) | kPairMagic;
+        const uint4 xp = xh[j][c];
+        const uint4 xq = xl[j][c];
+        d0 = dot2_bf16(xp.x, p0, d0);
+        d1 = dot2_bf16(xp.y, p1, d1);
+        d0 = dot2_bf16(xp.z, p2, d0);
+        d1 = dot2_bf16(xp.w, p3, d1);
+        d0 = dot2_bf16(xq.x, p0, d0);
+        d1 = dot2_bf16(xq.y, p1, d1);
+        d0 = dot2_bf16(xq.z, p2, d0);
+        d1 = dot2_bf16(xq.w, p3, d1);
+      }
+      float pj = bf16_to_f32(s[k][j]) * ((d0 + d1) - sxr[j]);
+      asm volatile("" : "+v"(pj));  // rounded on its own (no FMA into the row sum)
+      v += pj;
+    }
+    v = team_sum<16>(v);
+    const int rg = blockIdx.x + k * (int)gridDim.x;
+    int o;
+    const FusedSeg &S = r16_row<EPI>(A, rg < ngroups ? rg : ngroups - 1, team, W, &o);
+    if (c16 == 0 && rg < ngroups && o < S.N)
+      S.y[o] = EPI == kEpiGeluMul ? gelu_tanh(v) * A.mul[o] : v;
+  }
+}
+
 // LDS of a fused launch: x hi/lo pairs, group sums, IT * RB rows of partials
 // and row sums, the reduction scratch.
 size_t fused_lds(int G, int RB, int IT) {
@@ -417,9 +550,43 @@ bool plan_fused(int G, int total_rows, Gemv1Plan *p) {
   return false;
 }
 
+template <int W, int IT, int PRO, int EPI>
+int launch_fused_r16_it(const FusedArgs &a, int groups) {
+  hipLaunchKernelGGL((fused_r16_kernel<W, IT, PRO, EPI>), dim3((groups + IT - 1) / IT),
+                     dim3(64 * W), 0, stream(), a, groups);
+  G4_LAUNCH_CHECK("fused_r16_kernel");
+  return G4_OK;
+}
+
+// Row groups of 4 W rows; up to 3 per block once they outnumber the CUs, as
+// in launch_fused_i.
+template <int W, int PRO, int EPI>
+int launch_fused_r16(FusedArgs a) {
+  int groups = 0;
+  for (int i = 0; i < a.nseg; ++i) {
+    a.seg[i].block0 = groups;
+    groups += (a.seg[i].N + 4 * W - 1) / (4 * W);
+  }
+  const int cap = cu_count() > 0 ? cu_count() : 256;
+  int it = (groups + cap - 1) / cap;
+  it = it < 1 ? 1 : it > 3 ? 3 : it;
+  switch (it) {
+    case 1: return launch_fused_r16_it<W, 1, PRO, EPI>(a, groups);
+    case 2: return launch_fused_r16_it<W, 2, PRO, EPI>(a, groups);
+    default: return launch_fused_r16_it<W, 3, PRO, EPI>(a, groups);
+  }
+}
+
 template <int PRO, int EPI>
 int launch_fused(FusedArgs a) {
   const int G = a.K / 32;
+  // The PLE gate (256 rows at in_dim 1536) takes the row split with 12 rows
+  // per block: E2B decode 1.253 ms/token against 1.260 with the flat split.
+  // q/k/v and gate/up keep the flat split, whose 12-wave blocks give each
+  // lane one group (the row split's three groups per lane measured 1.265).
+  if constexpr (EPI == kEpiGeluMul) {
+    if (a.K == 1536) return launch_fused_r16<3, PRO, EPI>(a);
+  }
   int total_rows = 0;
   for (int i = 0; i < a.nseg; ++i) total_rows += a.seg[i].N;
   Gemv1Plan p;
