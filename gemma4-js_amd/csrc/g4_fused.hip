@@ -324,14 +324,12 @@ __global__ __launch_bounds__(TC ? TC : 1024) void fused_gemv_kernel(FusedArgs A,
     for (int i = 0; i < IPL; ++i) {
       const int li = t + i * T;
       const int g = li % G;
-      const uint32_t wd[4] = {q[k][i].x, q[k][i].y, q[k][i].z, q[k][i].w};
+      uint32_t pr[4][4];
+      group_pairs(q[k][i], mask, pr);
       float d0 = 0.f, d1 = 0.f;
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
-        const uint32_t p0 = (wd[c] & mask) | kPairMagic;
-        const uint32_t p1 = ((wd[c] >> 4) & mask) | kPairMagic;
-        const uint32_t p2 = ((wd[c] >> 8) & mask) | kPairMagic;
-        const uint32_t p3 = ((wd[c] >> 12) & mask) | kPairMagic;
+        const uint32_t p0 = pr[c][0], p1 = pr[c][1], p2 = pr[c][2], p3 = pr[c][3];
         const uint4 xp = hi[c * G + g];
         const uint4 xl = lo[c * G + g];
         d0 = dot2_bf16(xp.x, p0, d0);
@@ -466,14 +464,12 @@ __global__ __launch_bounds__(64 * W) void fused_r16_kernel(FusedArgs A, int ngro
     float v = 0.f;
 #pragma unroll
     for (int j = 0; j < J; ++j) {
-      const uint32_t wd[4] = {q[k][j].x, q[k][j].y, q[k][j].z, q[k][j].w};
+      uint32_t pr[4][4];
+      group_pairs(q[k][j], mask, pr);
       float d0 = 0.f, d1 = 0.f;
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
-        const uint32_t p0 = (wd[c] & mask) | kPairMagic;
-        const uint32_t p1 = ((wd[c] >> 4) & mask) | kPairMagic;
-        const uint32_t p2 = ((wd[c] >> 8) & mask) | kPairMagic;
-        const uint32_t p3 = ((wd[c] >> 12) & mask) | kPairMagic;
+        const uint32_t p0 = pr[c][0], p1 = pr[c][1], p2 = pr[c][2], p3 = pr[c][3];
         const uint4 xp = xh[j][c];
         const uint4 xq = xl[j][c];
         d0 = dot2_bf16(xp.x, p0, d0);

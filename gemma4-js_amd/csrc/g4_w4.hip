@@ -143,12 +143,13 @@ __global__ __launch_bounds__(256) void w4_gemv_kernel(
 #pragma unroll
     for (int i = 0; i < B; ++i) {
       const int g = tl + L * (b0 + i);
-      const uint32_t wd[4] = {q[i].x, q[i].y, q[i].z, q[i].w};
+      uint32_t pr[4][4];
+      group_pairs(q[i], mask, pr);
       uint32_t wp[16];
 #pragma unroll
       for (int c = 0; c < 4; ++c)
 #pragma unroll
-        for (int t = 0; t < 4; ++t) wp[4 * c + t] = ((wd[c] >> (4 * t)) & mask) | kPairMagic;
+        for (int t = 0; t < 4; ++t) wp[4 * c + t] = pr[c][t];
       const float sc = bf16_to_f32(s[i]);
 #pragma unroll
       for (int m = 0; m < kMaxGemvRows; ++m) {
@@ -357,14 +358,12 @@ __device__ __forceinline__ void gemv1_body(const void *__restrict__ x,
   for (int i = 0; i < IPL; ++i) {
     const int li = t + i * T;
     const int g = li % G;
-    const uint32_t wd[4] = {q[i].x, q[i].y, q[i].z, q[i].w};
+    uint32_t pr[4][4];
+    group_pairs(q[i], mask, pr);
     float d0 = 0.f, d1 = 0.f;
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
-      const uint32_t p0 = (wd[c] & mask) | kPairMagic;
-      const uint32_t p1 = ((wd[c] >> 4) & mask) | kPairMagic;
-      const uint32_t p2 = ((wd[c] >> 8) & mask) | kPairMagic;
-      const uint32_t p3 = ((wd[c] >> 12) & mask) | kPairMagic;
+      const uint32_t p0 = pr[c][0], p1 = pr[c][1], p2 = pr[c][2], p3 = pr[c][3];
       const uint4 xp = hi[c * G + g];
       d0 = dot2_bf16(xp.x, p0, d0);
       d1 = dot2_bf16(xp.y, p1, d1);
@@ -560,14 +559,12 @@ __device__ __forceinline__ void gemv_r16_body(const void *__restrict__ x,
   float v = 0.f;
 #pragma unroll
   for (int j = 0; j < J; ++j) {
-    const uint32_t wd[4] = {q[j].x, q[j].y, q[j].z, q[j].w};
+    uint32_t pr[4][4];
+    group_pairs(q[j], mask, pr);
     float d0 = 0.f, d1 = 0.f;
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
-      const uint32_t p0 = (wd[c] & mask) | kPairMagic;
-      const uint32_t p1 = ((wd[c] >> 4) & mask) | kPairMagic;
-      const uint32_t p2 = ((wd[c] >> 8) & mask) | kPairMagic;
-      const uint32_t p3 = ((wd[c] >> 12) & mask) | kPairMagic;
+      const uint32_t p0 = pr[c][0], p1 = pr[c][1], p2 = pr[c][2], p3 = pr[c][3];
       const uint4 xp = xh[j][c];
       d0 = dot2_bf16(xp.x, p0, d0);
       d1 = dot2_bf16(xp.y, p1, d1);
