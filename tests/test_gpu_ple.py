@@ -88,6 +88,51 @@ def test_device_ids_out_of_range_give_nan_rows(g4, oracle, table):
     assert np.isnan(got[[1, 3]]).all()
 
 
+@pytest.mark.parametrize("n", [127, 128, 129, 700, 1023, 1024, 1500])
+def test_gather_counts_across_kernel_choices(g4, oracle, table, n):
+    # 128 ids and more take the one-block-per-row kernel (512 threads for FP32;
+    # BF16: 512 below 1024 ids, 128 from there on); 127 the element kernel
+    t, host = table
+    ids = syn.token_ids(40 + n, n, VOCAB)
+    ids[:7] = [0, VOCAB - 1, RPS - 1, RPS, 63 * RPS, 5 * RPS + 17, 0]
+    ids[-1] = ids[3]
+    want = oracle.ple_gather(host, VOCAB, WIDTH, RPS, ids)
+    got = gather(g4, t, ids, g4.F32)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    got16 = gather(g4, t, ids, g4.BF16)
+    assert np.array_equal(got16.reshape(-1), oracle.f32_to_bf16_array(want))
+
+
+def test_row_kernel_bad_device_ids_and_short_last_shard(g4, oracle):
+    # 300 ids (the one-block-per-row kernel) over a table whose last shard is
+    # short, with device ids outside [0, vocab) that must give NaN rows
+    vocab, rps, width = 9000, 4096, 8960
+    shards = syn.ple_table(11, vocab, width, rps, threads=4)
+    t = g4.PleTable(vocab, width, 32, rps)
+    for i, s in enumerate(shards):
+        t.upload_shard(i, s)
+    host = np.concatenate(shards)
+    ids = syn.token_ids(12, 300, vocab)
+    ids[:4] = [8192, 8999, 4095, 0]
+    bad = np.array([5, 77, 150, 299])
+    ids[bad] = [-1, vocab, -(2 ** 31), 2 ** 31 - 1]
+    for dtype in (g4.F32, g4.BF16):
+        dev = g4.Buffer.from_array(ids)
+        out = g4.Buffer(ids.size * width * (4 if dtype == g4.F32 else 2))
+        t.gather_dev(dev.ptr, ids.size, out.ptr, dtype)
+        ok = np.setdiff1d(np.arange(ids.size), bad)
+        want = oracle.ple_gather(host, vocab, width, rps, ids[ok])
+        if dtype == g4.F32:
+            got = out.download(np.float32).reshape(ids.size, width)
+            assert np.array_equal(got[ok].view(np.uint32), want.view(np.uint32))
+            assert np.isnan(got[bad]).all()
+        else:
+            got = out.download(np.uint16).reshape(ids.size, width)
+            assert np.array_equal(got[ok].reshape(-1), oracle.f32_to_bf16_array(want))
+            assert (got[bad] == 0x7fc0).all()  # bf16 of the quiet NaN
+    t.free()
+
+
 def test_short_last_shard(g4, oracle):
     # vocab not a multiple of rows_per_shard: the last shard's scales block
     # starts after its own (shorter) packed block.
