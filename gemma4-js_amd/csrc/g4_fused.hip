@@ -105,7 +105,7 @@ __device__ __forceinline__ void load_rows(const FusedArgs &A, int rg, int G, int
     }
     idx = idx < last ? idx : last;
     q[i] = ld_nt(&wq[idx]);
-    s[i] = ws[idx];
+    s[i] = ld_nt_u16(&ws[idx]);
   }
 }
 
@@ -433,7 +433,7 @@ __global__ __launch_bounds__(64 * W) void fused_r16_kernel(FusedArgs A, int ngro
     for (int j = 0; j < J; ++j) {
       const size_t it = (size_t)rr * G + c16 + 16 * j;
       q[k][j] = ld_nt(&S.wq[it]);
-      s[k][j] = S.ws[it];
+      s[k][j] = ld_nt_u16(&S.ws[it]);
     }
   }
 

@@ -56,6 +56,11 @@ __device__ __forceinline__ uint4 ld_nt(const uint4 *p) {
   const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p));
   return make_uint4(v.x, v.y, v.z, v.w);
 }
+// A weight scale: streamed like the packed words it belongs to (3.01 -> 2.92 us
+// for the M1 K1536 N6144 GEMV, cold weights, against plain loads).
+__device__ __forceinline__ uint32_t ld_nt_u16(const uint16_t *p) {
+  return __builtin_nontemporal_load(p);
+}
 __device__ __forceinline__ void st_nt(uint4 *p, uint4 v) {
   const u32x4 u = {v.x, v.y, v.z, v.w};
   __builtin_nontemporal_store(u, reinterpret_cast<u32x4 *>(p));

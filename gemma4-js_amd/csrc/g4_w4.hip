@@ -111,7 +111,7 @@ __global__ __launch_bounds__(256) void w4_gemv_kernel(
 #pragma unroll
   for (int i = 0; i < B; ++i) {
     q[i] = ld_nt(&wq[rbase + (size_t)L * i]);
-    s[i] = ws[rbase + (size_t)L * i];
+    s[i] = ld_nt_u16(&ws[rbase + (size_t)L * i]);
   }
 
   // 2. stage x (L2) into LDS
@@ -137,7 +137,7 @@ __global__ __launch_bounds__(256) void w4_gemv_kernel(
 #pragma unroll
       for (int i = 0; i < B; ++i) {
         q[i] = ld_nt(&wq[rbase + (size_t)L * (b0 + i)]);
-        s[i] = ws[rbase + (size_t)L * (b0 + i)];
+        s[i] = ld_nt_u16(&ws[rbase + (size_t)L * (b0 + i)]);
       }
     }
 #pragma unroll
@@ -302,7 +302,7 @@ __device__ __forceinline__ void gemv1_body(const void *__restrict__ x,
     size_t it = base + t + (size_t)i * T;
     it = it < last ? it : last;
     q[i] = ld_nt(&wq[it]);
-    s[i] = ws[it];
+    s[i] = ld_nt_u16(&ws[it]);
   }
 
   // 3. stage x into LDS: hi[4][G], lo[4][G] (FP32 x), sx[G], then partials
@@ -492,7 +492,7 @@ __device__ __forceinline__ void gemv_r16_body(const void *__restrict__ x,
   for (int j = 0; j < J; ++j) {
     const size_t it = (size_t)rr * gstride + c16 + 16 * j;
     q[j] = ld_nt(&wq[it]);
-    s[j] = ws[it];
+    s[j] = ld_nt_u16(&ws[it]);
   }
 
   // 3. stage x: bf16 pairs of each chunk (hi, and lo for FP32 x), 136 * group sum
