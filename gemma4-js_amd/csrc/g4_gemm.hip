@@ -639,7 +639,9 @@ __global__ __launch_bounds__(kThreads, MINB) void w4_gemm_rb_kernel(
   const int S = G / 2 / (int)gridDim.y;  // stages of this block's slice of K
   const int st0_slice = (int)blockIdx.y * S;
   const int t = threadIdx.x;
-  const int lane = t & 63, wave = t >> 6;
+  // wave index in a scalar register: the LDS destinations of the direct loads
+  // are then scalar arithmetic (no readfirstlane per load)
+  const int lane = t & 63, wave = __builtin_amdgcn_readfirstlane(t >> 6);
   const int lr = lane & 15, lq = lane >> 4;
 
   const bool glu = SG.glu != 0;
@@ -672,14 +674,18 @@ __global__ __launch_bounds__(kThreads, MINB) void w4_gemm_rb_kernel(
   // re-read tile 0 into an unread part of the buffer)
   const size_t a_stage = (size_t)KC * Mp;
   const size_t lo_plane = (size_t)(K >> 3) * Mp;
-  const u32x4 *a_src[AW];
+  // x' sources: a uniform base (this slice's first stage, this block's rows)
+  // plus a 32-bit per-lane byte offset, so the loads take a scalar base and
+  // the stage advance is scalar arithmetic
+  const u32x4 *a_base = xt + (size_t)(st0_slice * KC) * Mp + m0;
+  uint32_t a_off[AW];
   int a_c[AW], a_r[AW];
 #pragma unroll
   for (int i = 0; i < AW; ++i) {
     const int u = wave * AW + i;
     a_c[i] = u / (BM / 64);
     a_r[i] = 64 * (u % (BM / 64));
-    a_src[i] = xt + (size_t)(st0_slice * KC + a_c[i]) * Mp + m0 + a_r[i] + lane;
+    a_off[i] = (uint32_t)((a_c[i] * Mp + a_r[i] + lane) * 16);
   }
   const u32x4 *b_src[BD];
 #pragma unroll
@@ -712,8 +718,10 @@ __global__ __launch_bounds__(kThreads, MINB) void w4_gemm_rb_kernel(
     for (int x = 0; x < NX; ++x)
 #pragma unroll
       for (int i = 0; i < AW; ++i)
-        __builtin_amdgcn_global_load_lds((const void *)(a_src[i] + (x ? lo_plane : 0) + sc * a_stage),
-                                         (lds_ptr)&L.a[x][a_c[i]][a_r[i]], 16, 0, 0);
+        __builtin_amdgcn_global_load_lds(
+            (const void *)(reinterpret_cast<const char *>(a_base + (x ? lo_plane : 0) + sc * a_stage) +
+                           a_off[i]),
+            (lds_ptr)&L.a[x][a_c[i]][a_r[i]], 16, 0, 0);
 #pragma unroll
     for (int d = 0; d < BD; ++d)
       __builtin_amdgcn_global_load_lds((const void *)(b_src[d] + 2 * sc), (lds_ptr)&L.b[wave][d][0],
@@ -763,18 +771,38 @@ __global__ __launch_bounds__(kThreads, MINB) void w4_gemm_rb_kernel(
       const _Float16 sh = (_Float16)ldexpf(bf16_to_f32(sb), b_shift[jj]);
       s2[jj] = (f16x2){sh, sh};
     }
-    auto deq8 = [&](uint32_t w, f16x2 sc) {
-      return as_f16x8((u32x4){deq(w, 0, sc), deq(w, 1, sc), deq(w, 2, sc), deq(w, 3, sc)});
+    // the nibbles of both words at shifts 4, 8, 12 from three 64-bit shifts
+    // (the low word's top bits then come from the high word and fall outside
+    // the mask)
+    uint32_t sh_lo[TNW][4], sh_hi[TNW][4];
+#pragma unroll
+    for (int jj = 0; jj < TNW; ++jj) {
+      const uint64_t u = ((uint64_t)wds[jj][1] << 32) | wds[jj][0];
+      uint64_t s4, s8, s12;
+      asm("v_lshrrev_b64 %0, 4, %1" : "=v"(s4) : "v"(u));
+      asm("v_lshrrev_b64 %0, 8, %1" : "=v"(s8) : "v"(u));
+      asm("v_lshrrev_b64 %0, 12, %1" : "=v"(s12) : "v"(u));
+      sh_lo[jj][0] = wds[jj][0];
+      sh_lo[jj][1] = (uint32_t)s4;
+      sh_lo[jj][2] = (uint32_t)s8;
+      sh_lo[jj][3] = (uint32_t)s12;
+      sh_hi[jj][0] = wds[jj][1];
+      sh_hi[jj][1] = (uint32_t)(s4 >> 32);
+      sh_hi[jj][2] = (uint32_t)(s8 >> 32);
+      sh_hi[jj][3] = (uint32_t)(s12 >> 32);
+    }
+    auto deq8 = [&](const uint32_t (&w)[4], f16x2 sc) {
+      return as_f16x8((u32x4){deq(w[0], 0, sc), deq(w[1], 0, sc), deq(w[2], 0, sc), deq(w[3], 0, sc)});
     };
     f16x8 b0[TNW], b1[TNW];
 #pragma unroll
-    for (int jj = 0; jj < TNW; ++jj) b0[jj] = deq8(wds[jj][0], s2[jj]);
+    for (int jj = 0; jj < TNW; ++jj) b0[jj] = deq8(sh_lo[jj], s2[jj]);
 #pragma unroll
     for (int x = 0; x < NX; ++x)
 #pragma unroll
       for (int i = 0; i < TMW; ++i) a1[x][i] = as_f16x8(L.a[x][2 * lq + 1][i * 16 + lr]);
 #pragma unroll
-    for (int jj = 0; jj < TNW; ++jj) b1[jj] = deq8(wds[jj][1], s2[jj]);
+    for (int jj = 0; jj < TNW; ++jj) b1[jj] = deq8(sh_hi[jj], s2[jj]);
 #pragma unroll
     for (int x = 0; x < NX; ++x)
 #pragma unroll
@@ -800,7 +828,7 @@ __global__ __launch_bounds__(kThreads, MINB) void w4_gemm_rb_kernel(
 #pragma unroll
     for (int k = 0; k < NM; ++k) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x002, (16 * TNW + NM - 1) / NM, 0);
+      __builtin_amdgcn_sched_group_barrier(0x002, (12 * TNW + NM - 1) / NM, 0);
     }
     __builtin_amdgcn_sched_group_barrier(0x008, NM, 0);
   };
