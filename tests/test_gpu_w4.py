@@ -187,6 +187,22 @@ def test_gemm_split_k_prefill_shapes(g4, rows, n, k):
     assert np.array_equal(yb, syn.bf16_rne(y).reshape(rows, n))
 
 
+@pytest.mark.parametrize("rows,n,k", [(1900, 6100, 1536), (1800, 1500, 6144), (2100, 6144, 1536)])
+def test_gemm_large_ragged_bf16(g4, rows, n, k):
+    # Prefill-sized BF16 GEMMs off the tile grid: rows that are not a multiple
+    # of the 128-row tile, a ragged last column tile, a K split (N 1500) and
+    # grids of more than two rounds of the CUs; BF16 output is the RNE of the
+    # FP32 output.
+    packed, scales, q = syn.w4_weights(31, n, k)
+    x_bits, x = syn.activations(31, rows, k)
+    lin = g4.W4Linear(packed, scales)
+    y = run_linear(g4, lin, x_bits, x, rows, g4.BF16)
+    ref = x.astype(np.float64) @ dense(q, scales).T
+    assert rel_l2_rows(y, ref) <= TOL
+    yb = run_linear(g4, lin, x_bits, x, rows, g4.BF16, g4.BF16)
+    assert np.array_equal(yb, syn.bf16_rne(y).reshape(rows, n))
+
+
 def test_gemm_matches_gemv_path(g4):
     # Rows 1..4 take the streaming GEMV, more rows the MFMA GEMM: the row a
     # caller computes must not depend on how many rows come with it.
