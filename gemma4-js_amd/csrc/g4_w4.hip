@@ -855,19 +855,49 @@ __global__ __launch_bounds__(256) void row_shift_kernel(const uint16_t *__restri
 
 constexpr int kRowShiftSpread = 12;
 
-// One allocation per weight: packed groups, the scales, the row shifts.
+// One allocation per weight: packed groups, the scales, the row shifts and
+// (even G) the tile-major copy of the words and scales for the GEMM.
 int alloc_weight(g4_w4 *w, size_t qbytes, size_t sbytes) {
   const size_t soff = (qbytes + 255) & ~size_t(255);
   const size_t roff = (soff + sbytes + 255) & ~size_t(255);
-  const size_t total = roff + (((size_t)w->N * sizeof(int16_t) + 15) & ~size_t(15));
+  size_t total = roff + (((size_t)w->N * sizeof(int16_t) + 15) & ~size_t(15));
+  const bool tiles = w->G % 2 == 0;
+  const size_t Np = ((size_t)w->N + 15) / 16 * 16;
+  const size_t tqoff = (total + 255) & ~size_t(255);
+  const size_t tsoff = (tqoff + Np * w->G * 16 + 255) & ~size_t(255);
+  if (tiles) total = tsoff + Np * w->G * 2;
   // + 8 bytes past `bytes` for the row-shift range read back at load
   int rc = device_alloc(total + 8, reinterpret_cast<void **>(&w->mem));
   if (rc) return rc;
   w->packed = reinterpret_cast<uint4 *>(w->mem);
   w->scales = reinterpret_cast<uint16_t *>(w->mem + soff);
   w->rshift = reinterpret_cast<int16_t *>(w->mem + roff);
+  w->tpacked = tiles ? reinterpret_cast<uint4 *>(w->mem + tqoff) : nullptr;
+  w->tscales = tiles ? reinterpret_cast<uint32_t *>(w->mem + tsoff) : nullptr;
   w->bytes = total;
   return G4_OK;
+}
+
+// The tile-major copy (g4_w4::tpacked, ::tscales) from the row-major arrays:
+// one thread per 16-byte word group, and per scale pair.
+__global__ __launch_bounds__(256) void tile_weight_kernel(const uint4 *__restrict__ packed,
+                                                          const uint32_t *__restrict__ spairs,
+                                                          int N, int G, uint4 *__restrict__ tq,
+                                                          uint32_t *__restrict__ ts) {
+  const int S2 = G / 2;
+  const size_t nq = ((size_t)N + 15) / 16 * 16 * G;  // tile-major word groups (Np * G)
+  const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= nq) return;
+  // word group i = ((t * S2 + st) * 16 + r) * 2 + h
+  const int h = (int)(i & 1);
+  const int r = (int)((i >> 1) & 15);
+  const size_t ts_i = i >> 5;  // t * S2 + st
+  const int st = (int)(ts_i % S2);
+  const size_t t = ts_i / S2;
+  size_t row = t * 16 + r;
+  row = row < (size_t)N ? row : (size_t)N - 1;
+  tq[i] = packed[row * G + 2 * st + h];
+  if (h == 0) ts[(ts_i * 16) + r] = spairs[row * S2 + st];
 }
 
 // Smallest and largest row shift, one block (bounds of a uint32 pair: the
@@ -894,13 +924,20 @@ __global__ __launch_bounds__(256) void row_shift_range_kernel(const int16_t *__r
   }
 }
 
-// Row shifts into w->rshift, then the tensor shift (the smallest row shift,
-// that of the row with the largest scale) and whether rows need their own:
+// The tile-major copy (even G), the row shifts into w->rshift, then the
+// tensor shift (the smallest row shift, that of the row with the largest
+// scale) and whether rows need their own:
 // with one shift, a row whose largest scale is 2^d below the tensor's keeps
 // 26 - d bits of headroom below its largest product before FP16 products
 // lose bits; up to d = 12 that is far below what the 1e-3 contract can see,
 // beyond it the GEMM rescales per row (a few percent slower).  Synchronises.
 hipError_t finish_row_shift(g4_w4 *w) {
+  if (w->tpacked) {
+    const size_t nq = ((size_t)w->N + 15) / 16 * 16 * w->G;
+    hipLaunchKernelGGL(tile_weight_kernel, dim3((unsigned)((nq + 255) / 256)), dim3(256), 0,
+                       stream(), w->packed, reinterpret_cast<const uint32_t *>(w->scales), w->N,
+                       w->G, w->tpacked, w->tscales);
+  }
   hipLaunchKernelGGL(row_shift_kernel, dim3((w->N + 255) / 256), dim3(256), 0, stream(),
                      w->scales, w->N, w->G, w->rshift);
   uint32_t *range_dev = reinterpret_cast<uint32_t *>(w->mem + w->bytes);
