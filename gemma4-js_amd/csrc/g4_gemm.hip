@@ -642,7 +642,16 @@ __global__ __launch_bounds__(kThreads, MINB) void w4_gemm_rb_kernel(
     u32x4 b[4][BD][64];
     uint32_t s[4][SD][64];
   };
-  __shared__ Stage st_lds[P];
+  // one LDS object: the stage ring and the block's row exponents (loaded
+  // with the first stages).  A second __shared__ array makes the compiler
+  // wait for every direct load in flight before each LDS read of the ring.
+  struct Smem {
+    Stage st[P];
+    int xe[BM];
+  };
+  __shared__ Smem smem;
+  Stage *const st_lds = smem.st;
+  int *const xe_lds = smem.xe;
 
   const int G = K >> 5;
   const int S = G / 2 / (int)gridDim.y;  // stages of this block's slice of K
@@ -856,6 +865,14 @@ __global__ __launch_bounds__(kThreads, MINB) void w4_gemm_rb_kernel(
   constexpr int NI = NX * AW + BD + SD;
   constexpr int NW = (P - 2) * NI;  // loads that may stay in flight: stages st + 2 .. st + P - 1
   static_assert(NW < 64, "vmcnt is 6 bits");
+  // the row exponents first (older than every stage load, so each wait below
+  // completes them too): the epilogue then reads them from LDS instead of
+  // waiting on a global load after the main loop
+  if (wave < BM / 64) {
+    const int m = m0 + wave * 64 + lane;
+    __builtin_amdgcn_global_load_lds((const void *)(xe + (m < M ? m : M - 1)),
+                                     (lds_ptr)&xe_lds[wave * 64], 4, 0, 0);
+  }
 #pragma unroll
   for (int q = 0; q < P - 1; ++q) issue(q, q);
   asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(NW) : "memory");
@@ -884,8 +901,7 @@ __global__ __launch_bounds__(kThreads, MINB) void w4_gemm_rb_kernel(
     for (int i = 0; i < TMW; ++i)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int m = m0 + i * 16 + 4 * lq + r;
-        ev[i][r] = xe[m < M ? m : M - 1];
+        ev[i][r] = xe_lds[i * 16 + 4 * lq + r];
       }
 #pragma unroll
     for (int i = 0; i < TMW; ++i)
