@@ -297,9 +297,8 @@ constexpr int kMaxGemmSegs = 3;
 struct GemmSegs {
   const u32x4 *wq[kMaxGemmSegs];
   const uint16_t *ws[kMaxGemmSegs];
-  // tile-major copies (g4_w4::tpacked, ::tscales), read by the packed-weight kernel
-  const u32x4 *tq[kMaxGemmSegs];
-  const uint32_t *ts[kMaxGemmSegs];
+  // stage-major tile copies (g4_w4::tiles), read by the packed-weight kernel
+  const u32x4 *tw[kMaxGemmSegs];
   void *y[kMaxGemmSegs];
   // per-row power-of-two shifts (g4_w4::rshift), or null: shift[] for the tensor
   const int16_t *rs[kMaxGemmSegs];
@@ -605,16 +604,14 @@ __global__ __launch_bounds__(kThreads, 2) void w4_gemm_kernel(
 // groups, 8 x' chunks).  Every operand of a stage reaches LDS by direct
 // global -> LDS loads, two stages ahead, into one of three buffers:
 //   x'      64 consecutive rows of one chunk per wave instruction;
-//   words   per wave, lane l of instruction d: tile 2d + l / 32, row
-//           (l / 2) % 16, group 2 st + l % 2 (16 bytes);
-//   scales  per wave, lane l: tile l / 16, row l % 16, the 2 scales of the
-//           stage (4 bytes).
-// Words and scales come from the weight's tile-major copy (g4_w4::tpacked,
-// ::tscales), where a stage of a 16-row tile is 512 contiguous bytes of words
-// and 64 of scales: from the row-major arrays each of those instructions
-// touched 32-48 cache lines, and their loads, not the MFMAs, held the main
-// loop (M 2048 N 6144 K 1536: 51.1 -> 44.5 us with the same addresses made
-// contiguous).
+//   weights per wave, the stage's 576-byte blocks of its TNW tiles from the
+//           weight's stage-major tile copy (g4_w4::tiles): 512 bytes of
+//           words (row r, group 2 st + h at 32 r + 16 h) and the 16 rows'
+//           scale pairs, 16 bytes per lane, so words and scales of 3 tiles
+//           take 2 load instructions.
+// From the row-major arrays each word or scale load instruction touched 32-48
+// cache lines, and those loads, not the MFMAs, held the main loop (M 2048 N
+// 6144 K 1536: 51.1 -> 44.5 us with the same addresses made contiguous).
 // Lane (c = lane % 16, q = lane / 16) then reads words 2q and 2q + 1 of the
 // stage's 8 words of row c (both in group q / 2, one scale) and dequantizes
 // them; MFMA step j (0, 1) takes word j as its B operand and x' chunk 2q + j
@@ -634,13 +631,18 @@ __global__ __launch_bounds__(kThreads, MINB) void w4_gemm_rb_kernel(
   constexpr int BM = 16 * TMW;
   constexpr int KC = 8;                 // x' chunks per stage
   constexpr int AW = KC * BM / 64 / 4;  // x' wave loads per wave, per plane
-  constexpr int BD = (TNW + 1) / 2;     // weight-word wave loads per wave
-  constexpr int SD = (TNW + 3) / 4;     // scale wave loads per wave
+  constexpr int TU = 36;                    // 16-byte units of a tile's stage block
+  constexpr int WU = TNW * TU;              // units of a wave's stage stream
+  constexpr int NB = (WU + 63) / 64;        // weight wave loads per wave
   static_assert(BM % 64 == 0 && AW >= 1, "A rows must come in runs of 64");
+  static_assert(WU >= 64, "a wave's weight stream fills at least one load");
+  // load d covers units w0(d) .. + 63: the last one ends at the stream's end,
+  // overlapping the one before (those units are written twice, with the same
+  // bytes), so the LDS region is the stream itself
+  auto w0 = [](int d) { return 64 * d < WU - 64 ? 64 * d : WU - 64; };
   struct Stage {
     u32x4 a[NX][KC][BM];
-    u32x4 b[4][BD][64];
-    uint32_t s[4][SD][64];
+    u32x4 w[4][WU];  // per wave: its tiles' stage blocks, TU units each
   };
   // one LDS object: the stage ring and the block's row exponents (loaded
   // with the first stages).  A second __shared__ array makes the compiler
@@ -705,27 +707,20 @@ __global__ __launch_bounds__(kThreads, MINB) void w4_gemm_rb_kernel(
     a_r[i] = 64 * (u % (BM / 64));
     a_off[i] = (uint32_t)((a_c[i] * Mp + a_r[i] + lane) * 16);
   }
-  // weight words and scales from the tile-major copies: a stage of tile
-  // gn / 16 is 32 word groups and 16 scale pairs, row gn % 16 at 2 (gn % 16)
-  // and gn % 16, so each load instruction reads 512 (words) or 64 (scales)
-  // contiguous bytes per tile
-  const int S2 = G / 2;
-  const u32x4 *b_src[BD];
+  // weight words and scales from the stage-major tile copies: unit u of the
+  // wave's stream is unit u % TU of tile u / TU's block; tiles past N (a
+  // ragged last block) read the last tile.  The stage stride is the same for
+  // every tile of a block (gate and up share N).
+  const int Tn = (SG.N[seg_of(0)] + 15) >> 4;
+  const size_t w_stage = (size_t)Tn * TU;
+  const u32x4 *w_src[NB];
 #pragma unroll
-  for (int d = 0; d < BD; ++d) {
-    int jj = 2 * d + (lane >> 5);
-    jj = jj < TNW ? jj : 0;
-    const int gn = row_of(jj, (lane >> 1) & 15);
-    b_src[d] = SG.tq[seg_of(jj)] + ((size_t)(gn >> 4) * S2 + st0_slice) * 32 + (gn & 15) * 2 +
-               (lane & 1);
-  }
-  const uint32_t *s_src[SD];
-#pragma unroll
-  for (int d = 0; d < SD; ++d) {
-    int jj = 4 * d + (lane >> 4);
-    jj = jj < TNW ? jj : 0;
-    const int gn = row_of(jj, lane & 15);
-    s_src[d] = SG.ts[seg_of(jj)] + ((size_t)(gn >> 4) * S2 + st0_slice) * 16 + (gn & 15);
+  for (int d = 0; d < NB; ++d) {
+    const int u = w0(d) + lane;
+    const int jj = u / TU, e = u - jj * TU;
+    int tile = col(jj) >> 4;
+    tile = tile < Tn ? tile : Tn - 1;
+    w_src[d] = SG.tw[seg_of(jj)] + ((size_t)st0_slice * Tn + tile) * TU + e;
   }
   int b_shift[TNW];
 #pragma unroll
@@ -747,13 +742,9 @@ __global__ __launch_bounds__(kThreads, MINB) void w4_gemm_rb_kernel(
                            a_off[i]),
             (lds_ptr)&L.a[x][a_c[i]][a_r[i]], 16, 0, 0);
 #pragma unroll
-    for (int d = 0; d < BD; ++d)
-      __builtin_amdgcn_global_load_lds((const void *)(b_src[d] + 32 * sc),
-                                       (lds_ptr)&L.b[wave][d][0], 16, 0, 0);
-#pragma unroll
-    for (int d = 0; d < SD; ++d)
-      __builtin_amdgcn_global_load_lds((const void *)(s_src[d] + 16 * sc),
-                                       (lds_ptr)&L.s[wave][d][0], 4, 0, 0);
+    for (int d = 0; d < NB; ++d)
+      __builtin_amdgcn_global_load_lds((const void *)(w_src[d] + sc * w_stage),
+                                       (lds_ptr)&L.w[wave][w0(d)], 16, 0, 0);
   };
 
   f32x4 acc[TMW][TNW];
@@ -777,11 +768,11 @@ __global__ __launch_bounds__(kThreads, MINB) void w4_gemm_rb_kernel(
     const Stage &L = st_lds[slot];
     u32x2 wds[TNW];
     uint32_t sp[TNW];
+    const char *wb = reinterpret_cast<const char *>(&L.w[wave][0]);
 #pragma unroll
     for (int jj = 0; jj < TNW; ++jj) {
-      const int l = (jj & 1) * 32 + 2 * lr + (lq >> 1);
-      wds[jj] = reinterpret_cast<const u32x2 *>(&L.b[wave][jj >> 1][l])[lq & 1];
-      sp[jj] = L.s[wave][jj >> 2][(jj & 3) * 16 + lr];
+      wds[jj] = *reinterpret_cast<const u32x2 *>(wb + jj * TU * 16 + 32 * lr + 8 * lq);
+      sp[jj] = *reinterpret_cast<const uint32_t *>(wb + jj * TU * 16 + 512 + 4 * lr);
     }
     f16x8 a0[NX][TMW], a1[NX][TMW];
 #pragma unroll
@@ -845,7 +836,7 @@ __global__ __launch_bounds__(kThreads, MINB) void w4_gemm_rb_kernel(
     // read of step 0, the scales and step 0's dequant, step 1's A reads, then
     // step 0's MFMAs with step 1's dequant between them, then step 1's MFMAs
     constexpr int NM = NX * TMW * TNW;  // MFMAs per step
-    __builtin_amdgcn_sched_group_barrier(0x020, NX * AW + BD + SD, 0);
+    __builtin_amdgcn_sched_group_barrier(0x020, NX * AW + NB, 0);
     __builtin_amdgcn_sched_group_barrier(0x100, 2 * TNW + NX * TMW, 0);
     __builtin_amdgcn_sched_group_barrier(0x002, 20 * TNW, 0);
     __builtin_amdgcn_sched_group_barrier(0x100, NX * TMW, 0);
@@ -862,7 +853,7 @@ __global__ __launch_bounds__(kThreads, MINB) void w4_gemm_rb_kernel(
   // the barrier are one asm statement with a memory clobber: __syncthreads()
   // would add a workgroup release, which waits for every load in flight (the
   // direct-LDS loads count as LDS writes), the next stage's included.
-  constexpr int NI = NX * AW + BD + SD;
+  constexpr int NI = NX * AW + NB;
   constexpr int NW = (P - 2) * NI;  // loads that may stay in flight: stages st + 2 .. st + P - 1
   static_assert(NW < 64, "vmcnt is 6 bits");
   // the row exponents first (older than every stage load, so each wait below
@@ -1052,13 +1043,12 @@ int launch_gemm_rb(const g4_w4 *const *w, int nw, const uint4 *xt, const int *xe
   GemmSegs sg{};
   sg.n = nw;
   for (int i = 0; i < nw; ++i) {
-    if (!w[i]->tpacked)
+    if (!w[i]->tiles)
       return fail(G4_E_ARG, "w4_gemm: no tile-major copy of a weight with odd group count %d",
                   w[i]->G);
     sg.wq[i] = reinterpret_cast<const u32x4 *>(w[i]->packed);
     sg.ws[i] = w[i]->scales;
-    sg.tq[i] = reinterpret_cast<const u32x4 *>(w[i]->tpacked);
-    sg.ts[i] = w[i]->tscales;
+    sg.tw[i] = reinterpret_cast<const u32x4 *>(w[i]->tiles);
     sg.y[i] = ys[i];
     sg.N[i] = w[i]->N;
     sg.rs[i] = w[i]->row_shift ? w[i]->rshift : nullptr;

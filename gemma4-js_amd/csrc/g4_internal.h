@@ -130,14 +130,14 @@ struct g4_w4 {
   uint4 *packed;     // [N][G] 16-byte groups, compressed-tensors order
   uint16_t *scales;  // [N][G] bf16 bits
   int16_t *rshift;   // [N]: 2^rshift[o] * 8 * max_g |scale[o, g]| <= 2^15 (FP16 GEMM)
-  // The same words and scales by 16-row tile and GEMM stage (two groups), for
-  // the packed-weight GEMM (even G only, else null): tile t, stage st, tile
-  // row r (rows past N repeat row N - 1) holds
-  //   tpacked[((t * G/2 + st) * 16 + r) * 2 + h] = packed[row * G + 2 st + h]
-  //   tscales[(t * G/2 + st) * 16 + r] = the bf16 pair scales[row * G + 2 st ..]
-  // so one stage of a tile is 512 contiguous bytes of words and 64 of scales.
-  uint4 *tpacked;
-  uint32_t *tscales;
+  // The same words and scales by GEMM stage (two groups) and 16-row tile, for
+  // the packed-weight GEMM (even G only, else null).  Stage st of tile t
+  // (T = ceil(N / 16) tiles; rows past N repeat row N - 1) is a 576-byte
+  // block at tiles + (st * T + t) * 36 (in 16-byte units): the words of
+  // rows r = 0..15, groups 2 st and 2 st + 1, at r * 2 + h, then the bf16
+  // scale pairs of the 16 rows as 16 u32 (units 32..35).  A stage of
+  // consecutive tiles is contiguous.
+  uint4 *tiles;
   int shift;         // min_o rshift[o]: one shift for the whole tensor ...
   bool row_shift;    // ... unless the rows' maxima spread beyond 2^12: then per row
   size_t bytes;

@@ -856,48 +856,50 @@ __global__ __launch_bounds__(256) void row_shift_kernel(const uint16_t *__restri
 constexpr int kRowShiftSpread = 12;
 
 // One allocation per weight: packed groups, the scales, the row shifts and
-// (even G) the tile-major copy of the words and scales for the GEMM.
+// (even G) the stage-major tile copy of the words and scales for the GEMM.
 int alloc_weight(g4_w4 *w, size_t qbytes, size_t sbytes) {
   const size_t soff = (qbytes + 255) & ~size_t(255);
   const size_t roff = (soff + sbytes + 255) & ~size_t(255);
   size_t total = roff + (((size_t)w->N * sizeof(int16_t) + 15) & ~size_t(15));
   const bool tiles = w->G % 2 == 0;
   const size_t Np = ((size_t)w->N + 15) / 16 * 16;
-  const size_t tqoff = (total + 255) & ~size_t(255);
-  const size_t tsoff = (tqoff + Np * w->G * 16 + 255) & ~size_t(255);
-  if (tiles) total = tsoff + Np * w->G * 2;
+  const size_t toff = (total + 255) & ~size_t(255);
+  if (tiles) total = toff + Np * w->G * 18;  // per row and stage: 32 B of words, 4 of scales
   // + 8 bytes past `bytes` for the row-shift range read back at load
   int rc = device_alloc(total + 8, reinterpret_cast<void **>(&w->mem));
   if (rc) return rc;
   w->packed = reinterpret_cast<uint4 *>(w->mem);
   w->scales = reinterpret_cast<uint16_t *>(w->mem + soff);
   w->rshift = reinterpret_cast<int16_t *>(w->mem + roff);
-  w->tpacked = tiles ? reinterpret_cast<uint4 *>(w->mem + tqoff) : nullptr;
-  w->tscales = tiles ? reinterpret_cast<uint32_t *>(w->mem + tsoff) : nullptr;
+  w->tiles = tiles ? reinterpret_cast<uint4 *>(w->mem + toff) : nullptr;
   w->bytes = total;
   return G4_OK;
 }
 
-// The tile-major copy (g4_w4::tpacked, ::tscales) from the row-major arrays:
-// one thread per 16-byte word group, and per scale pair.
+// The stage-major tile copy (g4_w4::tiles) from the row-major arrays: one
+// thread per 16-byte unit.
 __global__ __launch_bounds__(256) void tile_weight_kernel(const uint4 *__restrict__ packed,
                                                           const uint32_t *__restrict__ spairs,
-                                                          int N, int G, uint4 *__restrict__ tq,
-                                                          uint32_t *__restrict__ ts) {
+                                                          int N, int G, uint4 *__restrict__ tw) {
   const int S2 = G / 2;
-  const size_t nq = ((size_t)N + 15) / 16 * 16 * G;  // tile-major word groups (Np * G)
+  const size_t T = ((size_t)N + 15) / 16;
   const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
-  if (i >= nq) return;
-  // word group i = ((t * S2 + st) * 16 + r) * 2 + h
-  const int h = (int)(i & 1);
-  const int r = (int)((i >> 1) & 15);
-  const size_t ts_i = i >> 5;  // t * S2 + st
-  const int st = (int)(ts_i % S2);
-  const size_t t = ts_i / S2;
-  size_t row = t * 16 + r;
-  row = row < (size_t)N ? row : (size_t)N - 1;
-  tq[i] = packed[row * G + 2 * st + h];
-  if (h == 0) ts[(ts_i * 16) + r] = spairs[row * S2 + st];
+  if (i >= (size_t)S2 * T * 36) return;
+  const size_t blk = i / 36;  // st * T + t
+  const int e = (int)(i - blk * 36);
+  const int st = (int)(blk / T);
+  const size_t t = blk - (size_t)st * T;
+  auto row = [&](int r) {
+    const size_t o = t * 16 + r;
+    return o < (size_t)N ? o : (size_t)N - 1;
+  };
+  if (e < 32) {
+    tw[i] = packed[row(e >> 1) * G + 2 * st + (e & 1)];
+  } else {
+    const int r0 = 4 * (e - 32);
+    tw[i] = make_uint4(spairs[row(r0) * S2 + st], spairs[row(r0 + 1) * S2 + st],
+                       spairs[row(r0 + 2) * S2 + st], spairs[row(r0 + 3) * S2 + st]);
+  }
 }
 
 // Smallest and largest row shift, one block (bounds of a uint32 pair: the
@@ -924,7 +926,7 @@ __global__ __launch_bounds__(256) void row_shift_range_kernel(const int16_t *__r
   }
 }
 
-// The tile-major copy (even G), the row shifts into w->rshift, then the
+// The stage-major tile copy (even G), the row shifts into w->rshift, then the
 // tensor shift (the smallest row shift, that of the row with the largest
 // scale) and whether rows need their own:
 // with one shift, a row whose largest scale is 2^d below the tensor's keeps
@@ -932,11 +934,11 @@ __global__ __launch_bounds__(256) void row_shift_range_kernel(const int16_t *__r
 // lose bits; up to d = 12 that is far below what the 1e-3 contract can see,
 // beyond it the GEMM rescales per row (a few percent slower).  Synchronises.
 hipError_t finish_row_shift(g4_w4 *w) {
-  if (w->tpacked) {
-    const size_t nq = ((size_t)w->N + 15) / 16 * 16 * w->G;
-    hipLaunchKernelGGL(tile_weight_kernel, dim3((unsigned)((nq + 255) / 256)), dim3(256), 0,
+  if (w->tiles) {
+    const size_t nu = (size_t)(w->G / 2) * ((w->N + 15) / 16) * 36;
+    hipLaunchKernelGGL(tile_weight_kernel, dim3((unsigned)((nu + 255) / 256)), dim3(256), 0,
                        stream(), w->packed, reinterpret_cast<const uint32_t *>(w->scales), w->N,
-                       w->G, w->tpacked, w->tscales);
+                       w->G, w->tiles);
   }
   hipLaunchKernelGGL(row_shift_kernel, dim3((w->N + 255) / 256), dim3(256), 0, stream(),
                      w->scales, w->N, w->G, w->rshift);
