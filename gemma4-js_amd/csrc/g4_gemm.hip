@@ -1044,7 +1044,7 @@ int launch_gemm_rb(const g4_w4 *const *w, int nw, const uint4 *xt, const int *xe
   sg.n = nw;
   for (int i = 0; i < nw; ++i) {
     if (!w[i]->tiles)
-      return fail(G4_E_ARG, "w4_gemm: no tile-major copy of a weight with odd group count %d",
+      return fail(G4_E_ARG, "w4_gemm: no tile copy of a weight with odd group count %d",
                   w[i]->G);
     sg.wq[i] = reinterpret_cast<const u32x4 *>(w[i]->packed);
     sg.ws[i] = w[i]->scales;
