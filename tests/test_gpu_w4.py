@@ -187,19 +187,27 @@ def test_gemm_split_k_prefill_shapes(g4, rows, n, k):
     assert np.array_equal(yb, syn.bf16_rne(y).reshape(rows, n))
 
 
-@pytest.mark.parametrize("rows,n,k", [(1900, 6100, 1536), (1800, 1500, 6144), (2100, 6144, 1536)])
-def test_gemm_large_ragged_bf16(g4, rows, n, k):
-    # Prefill-sized BF16 GEMMs off the tile grid: rows that are not a multiple
-    # of the 128-row tile, a ragged last column tile, a K split (N 1500) and
-    # grids of more than two rounds of the CUs; BF16 output is the RNE of the
-    # FP32 output.
+@pytest.mark.parametrize("rows,n,k,x_dtype_name", [(1900, 6100, 1536, "bf16"),
+                                                   (1800, 1500, 6144, "bf16"),
+                                                   (2100, 6144, 1536, "bf16"),
+                                                   (1000, 6100, 1536, "f32"),
+                                                   (700, 1500, 6144, "f32")])
+def test_gemm_large_ragged(g4, rows, n, k, x_dtype_name):
+    # Prefill-sized GEMMs off the tile grid: rows that are not a multiple of
+    # the 128-row (BF16 x) or 64-row (FP32 x, two x' planes) tile, a ragged
+    # last column tile (the weight's tile copy repeats its last row there), a
+    # K split (N 1500) and grids of more than two rounds of the CUs; BF16
+    # output is the RNE of the FP32 output.
     packed, scales, q = syn.w4_weights(31, n, k)
     x_bits, x = syn.activations(31, rows, k)
+    if x_dtype_name == "f32":
+        x = np.random.default_rng(31).standard_normal((rows, k)).astype(np.float32)
+    xd = g4.BF16 if x_dtype_name == "bf16" else g4.F32
     lin = g4.W4Linear(packed, scales)
-    y = run_linear(g4, lin, x_bits, x, rows, g4.BF16)
+    y = run_linear(g4, lin, x_bits, x, rows, xd)
     ref = x.astype(np.float64) @ dense(q, scales).T
-    assert rel_l2_rows(y, ref) <= TOL
-    yb = run_linear(g4, lin, x_bits, x, rows, g4.BF16, g4.BF16)
+    assert rel_l2_rows(y, ref) <= (TOL if x_dtype_name == "bf16" else 1e-5)
+    yb = run_linear(g4, lin, x_bits, x, rows, xd, g4.BF16)
     assert np.array_equal(yb, syn.bf16_rne(y).reshape(rows, n))
 
 
