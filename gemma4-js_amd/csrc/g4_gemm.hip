@@ -713,10 +713,10 @@ __global__ __launch_bounds__(kThreads, MINB) void w4_gemm_rb_kernel(
   // every tile of a block (gate and up share N).
   const int Tn = (SG.N[seg_of(0)] + 15) >> 4;
   const size_t w_stage = (size_t)Tn * TU;
-  // With an odd TNW (never gate/up) a block reads one weight: its loads take
-  // a uniform base and 32-bit per-lane byte offsets, like the x' loads (the
-  // cheaper form to issue); gate/up tiles come from two weights and keep
-  // per-lane pointers.
+  // With an odd TNW (never gate/up) a block reads one weight: its loads are
+  // written as a uniform base and 32-bit per-lane byte offsets, like the x'
+  // loads (measured slightly faster); gate/up tiles come from two weights and
+  // keep per-lane pointers.
   constexpr bool ONE_W = TNW % 2 != 0;
   const u32x4 *w_base = SG.tw[seg_of(0)] + (size_t)st0_slice * w_stage;
   const u32x4 *w_src[NB];
