@@ -713,14 +713,7 @@ __global__ __launch_bounds__(kThreads, MINB) void w4_gemm_rb_kernel(
   // every tile of a block (gate and up share N).
   const int Tn = (SG.N[seg_of(0)] + 15) >> 4;
   const size_t w_stage = (size_t)Tn * TU;
-  // With an odd TNW (never gate/up) a block reads one weight: its loads are
-  // written as a uniform base and 32-bit per-lane byte offsets, like the x'
-  // loads (measured slightly faster); gate/up tiles come from two weights and
-  // keep per-lane pointers.
-  constexpr bool ONE_W = TNW % 2 != 0;
-  const u32x4 *w_base = SG.tw[seg_of(0)] + (size_t)st0_slice * w_stage;
   const u32x4 *w_src[NB];
-  uint32_t w_off[NB];
 #pragma unroll
   for (int d = 0; d < NB; ++d) {
     const int u = w0(d) + lane;
@@ -728,7 +721,6 @@ __global__ __launch_bounds__(kThreads, MINB) void w4_gemm_rb_kernel(
     int tile = col(jj) >> 4;
     tile = tile < Tn ? tile : Tn - 1;
     w_src[d] = SG.tw[seg_of(jj)] + ((size_t)st0_slice * Tn + tile) * TU + e;
-    w_off[d] = (uint32_t)((tile * TU + e) * 16);
   }
   int b_shift[TNW];
 #pragma unroll
@@ -750,15 +742,9 @@ __global__ __launch_bounds__(kThreads, MINB) void w4_gemm_rb_kernel(
                            a_off[i]),
             (lds_ptr)&L.a[x][a_c[i]][a_r[i]], 16, 0, 0);
 #pragma unroll
-    for (int d = 0; d < NB; ++d) {
-      if constexpr (ONE_W)
-        __builtin_amdgcn_global_load_lds(
-            (const void *)(reinterpret_cast<const char *>(w_base + sc * w_stage) + w_off[d]),
-            (lds_ptr)&L.w[wave][w0(d)], 16, 0, 0);
-      else
-        __builtin_amdgcn_global_load_lds((const void *)(w_src[d] + sc * w_stage),
-                                         (lds_ptr)&L.w[wave][w0(d)], 16, 0, 0);
-    }
+    for (int d = 0; d < NB; ++d)
+      __builtin_amdgcn_global_load_lds((const void *)(w_src[d] + sc * w_stage),
+                                       (lds_ptr)&L.w[wave][w0(d)], 16, 0, 0);
   };
 
   f32x4 acc[TMW][TNW];
