@@ -191,6 +191,27 @@ def test_quantize_rows_matches_builder_bit_exact(g4, oracle):
     assert deq[:8].tolist() == [7.0, 0.0, 2.0, 2.0, 4.0, 4.0, 6.0, 6.0]  # row 3: scale 2^-20
 
 
+def test_quantize_rows_divides_by_the_stored_scale(g4, oracle):
+    # rows whose elements lie between the stored-BF16-scale and FP32-scale
+    # rounding boundaries (tools/build_ple_w4_full.py:54-56): the device codes
+    # must be the brute-force nearest k * s_bf16 (ties to even), and equal the
+    # oracle's bytes
+    import quantizer_cases as qc
+    rows = 64
+    bits, x, differs = qc.divisor_rows(31, rows, WIDTH)
+    src = g4.Buffer.from_array(bits)
+    shard = g4.Buffer(rows * (WIDTH // 2 + WIDTH // 16))
+    g4.ple_quantize_rows(src, rows, WIDTH, shard)
+    got = shard.download(np.uint8)
+    packed = got[:rows * WIDTH // 2].reshape(rows, WIDTH // 2)
+    scales = got[rows * WIDTH // 2:].view("<u2").reshape(rows, WIDTH // 32)
+    assert differs.sum() > x.size // 16
+    s = syn.bf16_to_f32(scales).reshape(rows, WIDTH // 32)
+    assert np.array_equal(qc.codes_of(packed), qc.best_codes(x, s))
+    want_p, want_s = oracle.ple_quantize_rows(x)
+    assert np.array_equal(packed, want_p) and np.array_equal(scales, want_s)
+
+
 def test_quantize_table_in_place_then_gather(g4, oracle):
     # a dense [5000, 8960] BF16 table quantized shard by shard in place (the
     # last shard short), then gathered: bit-exact against the oracle's shards

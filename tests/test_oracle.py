@@ -337,6 +337,37 @@ def test_ple_quantizer_properties(oracle):
     assert np.all(err <= np.repeat(s, 32, axis=1) * 0.5 + np.abs(x) * 2.0 ** -7)
 
 
+def test_ple_quantizer_divides_by_the_stored_bf16_scale(oracle):
+    # tools/build_ple_w4_full.py:54-56 quantizes against the STORED BF16
+    # scale.  Every group's FP32 seventh of its maximum differs from its BF16
+    # rounding, and most elements lie between the two scales' rounding
+    # boundaries, so a divisor of maxabs / 7 in FP32 gives other codes there.
+    # The codes must equal the brute-force nearest k * s_bf16 (ties to even),
+    # found without division or rint.
+    import quantizer_cases as qc
+    rows, width = 64, 1024
+    _, x, differs = qc.divisor_rows(23, rows, width)
+    packed, scales = oracle.ple_quantize_rows(x)
+    maxabs = np.abs(x.reshape(rows, width // 32, 32)).max(axis=2)
+    assert np.array_equal(scales, syn.bf16_rne((maxabs / np.float32(7)).astype(np.float32)))
+    s_stored = syn.bf16_to_f32(scales).reshape(rows, width // 32)
+    assert differs.sum() > x.size // 16  # about 13% of the elements
+    assert np.array_equal(qc.codes_of(packed), qc.best_codes(x, s_stored))
+
+
+def test_ple_quantizer_brute_force_codes_on_random_rows(oracle):
+    # the same brute-force characterisation on ordinary rows (normal values,
+    # zero groups), where the divisor rarely matters
+    import quantizer_cases as qc
+    rng = np.random.default_rng(29)
+    x = syn.bf16_to_f32(syn.bf16_rne(rng.standard_normal((32, 512)).astype(np.float32) * 0.2))
+    x = x.reshape(32, 512).copy()
+    x[4, 64:96] = 0.0
+    packed, scales = oracle.ple_quantize_rows(x)
+    s = syn.bf16_to_f32(scales).reshape(32, 16)
+    assert np.array_equal(qc.codes_of(packed), qc.best_codes(x, s))
+
+
 def test_ple_quantizer_rounds_half_to_even(oracle):
     x = np.zeros((1, 32), dtype=np.float32)
     x[0, :5] = [7.0, 2.5, 3.5, -2.5, 0.5]  # maxabs 7 -> scale exactly 1.0
