@@ -87,7 +87,7 @@ def bench_gemv(n, k, steps, warmup, seed=0, copies=None):
     if copies is None:
         copies = max(2, int(math.ceil(COLD_BYTES / per)))
         copies = min(copies, 128) if per > 4e6 else copies
-    lins = [g4hip.W4Linear(packed, scales) for _ in range(copies)]
+    lins = [g4hip.W4Linear(packed, scales, gemm_tiles=False) for _ in range(copies)]
     # at least 120 launches per recorded step, cycling through the copies
     order = [lins[i % copies] for i in range(max(copies, 120))]
     x_bits, _ = syn.activations(seed, 1, k)
@@ -127,7 +127,7 @@ def bench_layer(reps=50, seed=1):
             for i, (name, n, k) in enumerate(E2B_SLIDING_LAYER)}
     layer_bytes = sum(w4_bytes(n, k) for _, n, k in mats.values())
     copies = int(math.ceil(COLD_BYTES / layer_bytes))
-    layers = [{name: g4hip.W4Linear(*ps) for name, (ps, _, _) in mats.items()}
+    layers = [{name: g4hip.W4Linear(*ps, gemm_tiles=False) for name, (ps, _, _) in mats.items()}
               for _ in range(copies)]
     xs = {k: g4hip.Buffer.from_array(syn.activations(seed, 1, k)[0]) for k in (1536, 2048, 6144)}
     ys = {name: g4hip.Buffer(n * 4) for name, (_, n, _) in mats.items()}

@@ -1104,6 +1104,8 @@ constexpr int kMaxSplitK = 8;
 GemmPlan plan_gemm(const g4_w4 *const *w, int nw, int rows, bool f32x) {
   const int cus = cu_count() > 0 ? cu_count() : 256;
   if (w[0]->G % 2 != 0) return {2, 2, 1, 1};
+  bool tiled = true;  // the packed-weight kernel reads every weight's tile copy
+  for (int i = 0; i < nw; ++i) tiled = tiled && w[i]->tiles != nullptr;
   const int S = w[0]->G / 2;
   auto blocks = [&](int bm, int bn) {
     long tiles = 0;
@@ -1118,8 +1120,8 @@ GemmPlan plan_gemm(const g4_w4 *const *w, int nw, int rows, bool f32x) {
     // into slices of at least 8 stages while that keeps the grid within two
     // blocks per CU
     const long b = blocks(f32x ? 64 : 128, 192);
-    if (b >= cus) return {0, 0, 0, 1, 1};
-    if (split_ok) {
+    if (tiled && b >= cus) return {0, 0, 0, 1, 1};
+    if (tiled && split_ok) {
       int slices = 1;
       for (int k = 2; k <= kMaxSplitK; ++k)
         if (S % k == 0 && S / k >= 8 && b * k <= 2L * cus) slices = k;

@@ -45,6 +45,7 @@ int current_device();
 struct Workspace {
   void *mem = nullptr;
   size_t bytes = 0;
+  bool captured = false;  // handed out while an encoder was recording
   int get(size_t need, void **p, const char *who);
 };
 

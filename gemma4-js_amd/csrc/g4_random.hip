@@ -7,6 +7,8 @@
 //   W4 packed words: 8 nibbles, each uniform in [1, 15] (q = nibble - 8 in
 //     [-7, 7], compressed-tensors offset binary);
 //   PLE packed bytes: 2 two's-complement nibbles, each q uniform in [-7, 7];
+//   the _FULL kinds: every nibble uniform over all 16 values (q in [-8, 7],
+//     the format's whole range: W4 nibble 0 and PLE nibble 8 are q = -8);
 //   BF16 |N(0,1)| * sigma (scales) and N(0,1) * sigma (embeddings), rounded
 //   to nearest even; FP32 N(0,1) * sigma.
 #include <math.h>
@@ -58,6 +60,14 @@ __global__ __launch_bounds__(256) void fill_kernel(void *__restrict__ dst, size_
         static_cast<uint32_t *>(dst)[i] = w;
         break;
       }
+      case G4_RAND_W4_PACKED_FULL: {  // 8 uniform nibbles = 32 uniform bits
+        static_cast<uint32_t *>(dst)[i] = (uint32_t)splitmix64(base + i);
+        break;
+      }
+      case G4_RAND_PLE_PACKED_FULL: {  // 2 uniform nibbles = a uniform byte
+        static_cast<uint8_t *>(dst)[i] = (uint8_t)splitmix64(base + i);
+        break;
+      }
       case G4_RAND_PLE_PACKED: {
         const uint64_t r = splitmix64(base + i);
         const uint32_t lo = (uniform15(r, 0) + 9u) & 15u;  // q + 16 mod 16, q in [-7, 7]
@@ -82,8 +92,10 @@ __global__ __launch_bounds__(256) void fill_kernel(void *__restrict__ dst, size_
 
 size_t elem_bytes(int kind) {
   switch (kind) {
-    case G4_RAND_W4_PACKED: return 4;
-    case G4_RAND_PLE_PACKED: return 1;
+    case G4_RAND_W4_PACKED:
+    case G4_RAND_W4_PACKED_FULL: return 4;
+    case G4_RAND_PLE_PACKED:
+    case G4_RAND_PLE_PACKED_FULL: return 1;
     case G4_RAND_BF16_ABS_NORMAL:
     case G4_RAND_BF16_NORMAL: return 2;
     case G4_RAND_F32_NORMAL: return 4;

@@ -195,6 +195,7 @@ int device_free(void *p) {
 
 int Workspace::get(size_t need, void **p, const char *who) {
   if (need <= bytes) {
+    if (g_encoding) captured = true;
     *p = mem;
     return G4_OK;
   }
@@ -203,7 +204,8 @@ int Workspace::get(size_t need, void **p, const char *who) {
                 "%s: scratch must grow to %zu bytes; make one call of this size outside a "
                 "command encoder first", who, need);
   if (mem) {
-    if (g_live_cmdbufs > 0) {
+    // only a block that a recording may hold must outlive the recordings
+    if (captured && g_live_cmdbufs > 0) {
       g_retired.push_back(mem);
     } else {
       int rc = device_free(mem);
@@ -211,6 +213,7 @@ int Workspace::get(size_t need, void **p, const char *who) {
     }
     mem = nullptr;
     bytes = 0;
+    captured = false;
   }
   int rc = device_alloc(need, &mem);
   if (rc) return rc;
@@ -416,11 +419,13 @@ G4_API int g4_cmdbuf_free(g4_cmdbuf *cb) {
   (void)hipGraphDestroy(cb->graph);
   delete cb;
   if (--g_live_cmdbufs == 0) {
+    int first = G4_OK;
     for (void *p : g_retired) {
-      int rc = device_free(p);
-      if (rc) return rc;
+      const int rc = device_free(p);
+      if (rc && !first) first = rc;
     }
-    g_retired.clear();
+    g_retired.clear();  // even after a failed free: no pointer is freed twice
+    if (first) return first;
   }
   return ok();
 }

@@ -837,7 +837,12 @@ namespace {
 // group's scale is more than 2^26 below the row's largest (then its products
 // may lose bits, each at most 2^-26 of the row's largest product).  Rows are
 // independent, so their magnitudes may differ by any factor.  Rows whose
-// scales are all zero (or not finite) get shift 0.
+// scales are all zero (or not finite) have no constraint: they get kNoShift
+// here and the tensor shift once the range is known (row_shift_range_kernel),
+// so a pruned or padding row neither lowers the tensor shift nor forces the
+// per-row path.
+constexpr int16_t kNoShift = -32768;
+
 __global__ __launch_bounds__(256) void row_shift_kernel(const uint16_t *__restrict__ s, int N,
                                                         int G, int16_t *__restrict__ shift) {
   const int o = blockIdx.x * 256 + threadIdx.x;
@@ -850,18 +855,18 @@ __global__ __launch_bounds__(256) void row_shift_kernel(const uint16_t *__restri
   }
   // floor(log2 max|s|) for a normal bf16; -127 for a subnormal one (its
   // true exponent is lower, so the shift only keeps it further from overflow)
-  shift[o] = mx ? (int16_t)(11 - ((int)(mx >> 7) - 127)) : (int16_t)0;
+  shift[o] = mx ? (int16_t)(11 - ((int)(mx >> 7) - 127)) : kNoShift;
 }
 
 constexpr int kRowShiftSpread = 12;
 
 // One allocation per weight: packed groups, the scales, the row shifts and
 // (even G) the stage-major tile copy of the words and scales for the GEMM.
-int alloc_weight(g4_w4 *w, size_t qbytes, size_t sbytes) {
+int alloc_weight(g4_w4 *w, size_t qbytes, size_t sbytes, bool want_tiles) {
   const size_t soff = (qbytes + 255) & ~size_t(255);
   const size_t roff = (soff + sbytes + 255) & ~size_t(255);
   size_t total = roff + (((size_t)w->N * sizeof(int16_t) + 15) & ~size_t(15));
-  const bool tiles = w->G % 2 == 0;
+  const bool tiles = want_tiles && w->G % 2 == 0;
   const size_t Np = ((size_t)w->N + 15) / 16 * 16;
   const size_t toff = (total + 255) & ~size_t(255);
   if (tiles) total = toff + Np * w->G * 18;  // per row and stage: 32 B of words, 4 of scales
@@ -902,12 +907,15 @@ __global__ __launch_bounds__(256) void tile_weight_kernel(const uint4 *__restric
   }
 }
 
-// Smallest and largest row shift, one block (bounds of a uint32 pair: the
-// shifts biased by 512 so the atomics compare unsigned values).
-__global__ __launch_bounds__(256) void row_shift_range_kernel(const int16_t *__restrict__ shift,
+// Smallest and largest row shift over the rows that have one, one block
+// (a uint32 pair, the shifts biased by 512 so they compare unsigned); then
+// every kNoShift row takes the smallest (the tensor shift; 0 if no row has
+// a non-zero scale).
+__global__ __launch_bounds__(256) void row_shift_range_kernel(int16_t *__restrict__ shift,
                                                               int N, uint32_t *__restrict__ out) {
   uint32_t lo = 0xffffffffu, hi = 0u;
   for (int o = threadIdx.x; o < N; o += 256) {
+    if (shift[o] == kNoShift) continue;
     const uint32_t v = (uint32_t)(shift[o] + 512);
     lo = v < lo ? v : lo;
     hi = v > hi ? v : hi;
@@ -921,9 +929,15 @@ __global__ __launch_bounds__(256) void row_shift_range_kernel(const int16_t *__r
       lo = slo[i] < lo ? slo[i] : lo;
       hi = shi[i] > hi ? shi[i] : hi;
     }
+    if (hi < lo) lo = hi = 512u;  // no row with a scale: shift 0
+    slo[0] = lo;
     out[0] = lo;
     out[1] = hi;
   }
+  __syncthreads();
+  const int16_t fill = (int16_t)((int)slo[0] - 512);
+  for (int o = threadIdx.x; o < N; o += 256)
+    if (shift[o] == kNoShift) shift[o] = fill;
 }
 
 // The stage-major tile copy (even G), the row shifts into w->rshift, then the
@@ -959,88 +973,79 @@ hipError_t finish_row_shift(g4_w4 *w) {
 
 }  // namespace
 
-G4_API int g4_w4_load(const void *packed, const void *scales, int out_dim,
-                      int in_dim, int group, g4_w4 **out) {
-  G4_CHECK_INIT();
-  G4_CHECK_NOT_ENCODING();
-  if (!out) return fail(G4_E_ARG, "g4_w4_load: null output handle");
+namespace {
+
+// g4_w4_load / g4_w4_load_dev / g4_w4_load_opts: validation as
+// official-w4a16.js:56-61, one allocation, the bytes copied in unchanged,
+// then the GEMM's tile copy and row shifts.  Synchronises.
+int load_weight(const void *packed, const void *scales, int out_dim, int in_dim, int group,
+                bool from_device, bool tiles, const char *who, g4_w4 **out) {
+  if (!out) return fail(G4_E_ARG, "%s: null output handle", who);
   *out = nullptr;
-  if (!packed || !scales) return fail(G4_E_ARG, "g4_w4_load: null weight pointer");
+  if (!packed || !scales) return fail(G4_E_ARG, "%s: null weight pointer", who);
   if (out_dim <= 0 || in_dim <= 0)
-    return fail(G4_E_ARG, "g4_w4_load: bad shape [%d, %d]", out_dim, in_dim);
-  // official-w4a16.js:56-61
+    return fail(G4_E_ARG, "%s: bad shape [%d, %d]", who, out_dim, in_dim);
   if (in_dim % 8 != 0) return fail(G4_E_ARG, "inDim must be divisible by 8.");
   if (group <= 0 || in_dim % group != 0)
     return fail(G4_E_ARG, "inDim must be divisible by groupSize.");
   if (group != 32)
-    return fail(G4_E_ARG, "g4_w4_load: group size %d unsupported (the checkpoint uses 32)",
-                group);
+    return fail(G4_E_ARG, "%s: group size %d unsupported (the checkpoint uses 32)", who, group);
+  const int G = in_dim / 32;
+  const size_t qbytes = (size_t)out_dim * in_dim / 2;
+  const size_t sbytes = (size_t)out_dim * G * 2;
+  if (from_device) {
+    int rc = check_device_range(packed, qbytes, "weight packed");
+    if (!rc) rc = check_device_range(scales, sbytes, "weight scales");
+    if (rc) return rc;
+  }
   g4_w4 *w = new g4_w4();
   w->N = out_dim;
   w->K = in_dim;
   w->group = group;
-  w->G = in_dim / 32;
-  const size_t qbytes = (size_t)out_dim * in_dim / 2;
-  const size_t sbytes = (size_t)out_dim * w->G * 2;
-  int rc = alloc_weight(w, qbytes, sbytes);
+  w->G = G;
+  int rc = alloc_weight(w, qbytes, sbytes, tiles);
   if (rc) {
     delete w;
     return rc;
   }
-  hipError_t e = hipMemcpyAsync(w->packed, packed, qbytes, hipMemcpyHostToDevice, stream());
-  if (e == hipSuccess)
-    e = hipMemcpyAsync(w->scales, scales, sbytes, hipMemcpyHostToDevice, stream());
+  const hipMemcpyKind kind = from_device ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice;
+  hipError_t e = hipMemcpyAsync(w->packed, packed, qbytes, kind, stream());
+  if (e == hipSuccess) e = hipMemcpyAsync(w->scales, scales, sbytes, kind, stream());
   if (e == hipSuccess) e = finish_row_shift(w);
   if (e != hipSuccess) {
     device_free(w->mem);
     delete w;
-    return fail(G4_E_HIP, "g4_w4_load: upload failed: %s", hipGetErrorString(e));
+    return fail(G4_E_HIP, "%s: copy failed: %s", who, hipGetErrorString(e));
   }
   *out = w;
   return ok();
+}
+
+}  // namespace
+
+G4_API int g4_w4_load(const void *packed, const void *scales, int out_dim,
+                      int in_dim, int group, g4_w4 **out) {
+  G4_CHECK_INIT();
+  G4_CHECK_NOT_ENCODING();
+  return load_weight(packed, scales, out_dim, in_dim, group, false, true, "g4_w4_load", out);
 }
 
 G4_API int g4_w4_load_dev(const void *packed_dev, const void *scales_dev, int out_dim,
                           int in_dim, int group, g4_w4 **out) {
   G4_CHECK_INIT();
   G4_CHECK_NOT_ENCODING();
-  if (!out) return fail(G4_E_ARG, "g4_w4_load_dev: null output handle");
-  *out = nullptr;
-  if (out_dim <= 0 || in_dim <= 0)
-    return fail(G4_E_ARG, "g4_w4_load_dev: bad shape [%d, %d]", out_dim, in_dim);
-  if (in_dim % 8 != 0) return fail(G4_E_ARG, "inDim must be divisible by 8.");
-  if (group <= 0 || in_dim % group != 0)
-    return fail(G4_E_ARG, "inDim must be divisible by groupSize.");
-  if (group != 32)
-    return fail(G4_E_ARG, "g4_w4_load_dev: group size %d unsupported (the checkpoint uses 32)",
-                group);
-  const int G = in_dim / 32;
-  const size_t qbytes = (size_t)out_dim * in_dim / 2;
-  const size_t sbytes = (size_t)out_dim * G * 2;
-  int rc = check_device_range(packed_dev, qbytes, "g4_w4_load_dev packed");
-  if (!rc) rc = check_device_range(scales_dev, sbytes, "g4_w4_load_dev scales");
-  if (rc) return rc;
-  g4_w4 *w = new g4_w4();
-  w->N = out_dim;
-  w->K = in_dim;
-  w->group = group;
-  w->G = G;
-  rc = alloc_weight(w, qbytes, sbytes);
-  if (rc) {
-    delete w;
-    return rc;
-  }
-  hipError_t e = hipMemcpyAsync(w->packed, packed_dev, qbytes, hipMemcpyDeviceToDevice, stream());
-  if (e == hipSuccess)
-    e = hipMemcpyAsync(w->scales, scales_dev, sbytes, hipMemcpyDeviceToDevice, stream());
-  if (e == hipSuccess) e = finish_row_shift(w);
-  if (e != hipSuccess) {
-    device_free(w->mem);
-    delete w;
-    return fail(G4_E_HIP, "g4_w4_load_dev: copy failed: %s", hipGetErrorString(e));
-  }
-  *out = w;
-  return ok();
+  return load_weight(packed_dev, scales_dev, out_dim, in_dim, group, true, true,
+                     "g4_w4_load_dev", out);
+}
+
+G4_API int g4_w4_load_opts(const void *packed, const void *scales, int out_dim, int in_dim,
+                           int group, int flags, g4_w4 **out) {
+  G4_CHECK_INIT();
+  G4_CHECK_NOT_ENCODING();
+  if (flags & ~(G4_W4_SRC_DEVICE | G4_W4_NO_GEMM_TILES))
+    return fail(G4_E_ARG, "g4_w4_load_opts: unknown flags 0x%x", flags);
+  return load_weight(packed, scales, out_dim, in_dim, group, (flags & G4_W4_SRC_DEVICE) != 0,
+                     (flags & G4_W4_NO_GEMM_TILES) == 0, "g4_w4_load_opts", out);
 }
 
 G4_API int g4_w4_free(g4_w4 *w) {

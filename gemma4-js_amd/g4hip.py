@@ -74,6 +74,7 @@ SIGNATURES = {
     "g4_embed": (_int, [_vp, _int, _int, _vp, _int, _c.c_float, _vp]),
     "g4_argmax": (_int, [_vp, _int, _vp]),
     "g4_w4_load_dev": (_int, [_vp, _vp, _int, _int, _int, _c.POINTER(_vp)]),
+    "g4_w4_load_opts": (_int, [_vp, _vp, _int, _int, _int, _int, _c.POINTER(_vp)]),
     "g4_ple_upload_shard_dev": (_int, [_vp, _int, _vp, _sz]),
     "g4_fill_random": (_int, [_vp, _sz, _int, _c.c_uint64, _c.c_float]),
     "g4_gemma_e2b_config": (_int, [_int, _vp]),
@@ -95,7 +96,8 @@ SIGNATURES = {
 }
 
 # g4_fill_random kinds
-RAND_W4_PACKED, RAND_PLE_PACKED, RAND_BF16_ABS_NORMAL, RAND_BF16_NORMAL, RAND_F32_NORMAL = range(5)
+(RAND_W4_PACKED, RAND_PLE_PACKED, RAND_BF16_ABS_NORMAL, RAND_BF16_NORMAL, RAND_F32_NORMAL,
+ RAND_W4_PACKED_FULL, RAND_PLE_PACKED_FULL) = range(7)
 # g4_gemma projections and norms
 PROJ = dict(q=0, k=1, v=2, o=3, gate=4, up=5, down=6, ple_gate=7, ple_proj=8, top=9)
 NORM = dict(input=0, post_attn=1, pre_ffw=2, post_ffw=3, post_ple=4, q=5, k=6,
@@ -266,10 +268,15 @@ class Event:
             pass
 
 
-class W4Linear:
-    """GPUW4Linear: compressed-tensors W4A16 weights resident on the device."""
+# g4_w4_load_opts flags
+W4_SRC_DEVICE, W4_NO_GEMM_TILES = 1, 2
 
-    def __init__(self, packed, scales, group=32):
+
+class W4Linear:
+    """GPUW4Linear: compressed-tensors W4A16 weights resident on the device.
+    gemm_tiles=False skips the prefill GEMM's tile copy (decode-only weights)."""
+
+    def __init__(self, packed, scales, group=32, gemm_tiles=True):
         packed = np.ascontiguousarray(packed).view(np.uint32)
         scales = np.ascontiguousarray(scales).view(np.uint16)
         if packed.ndim != 2 or scales.ndim != 2:
@@ -278,8 +285,12 @@ class W4Linear:
         self.in_dim = packed.shape[1] * 8
         self.group = group
         h = _vp()
-        check(lib().g4_w4_load(packed.ctypes.data, scales.ctypes.data, self.out_dim,
-                               self.in_dim, group, ctypes.byref(h)))
+        if gemm_tiles:
+            check(lib().g4_w4_load(packed.ctypes.data, scales.ctypes.data, self.out_dim,
+                                   self.in_dim, group, ctypes.byref(h)))
+        else:
+            check(lib().g4_w4_load_opts(packed.ctypes.data, scales.ctypes.data, self.out_dim,
+                                        self.in_dim, group, W4_NO_GEMM_TILES, ctypes.byref(h)))
         self.h = h.value
 
     @classmethod

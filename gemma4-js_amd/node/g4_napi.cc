@@ -1434,7 +1434,9 @@ napi_value Init(napi_env env, napi_value exports) {
   const struct { const char *name; int value; } kinds[] = {
       {"RAND_W4_PACKED", G4_RAND_W4_PACKED}, {"RAND_PLE_PACKED", G4_RAND_PLE_PACKED},
       {"RAND_BF16_ABS_NORMAL", G4_RAND_BF16_ABS_NORMAL},
-      {"RAND_BF16_NORMAL", G4_RAND_BF16_NORMAL}, {"RAND_F32_NORMAL", G4_RAND_F32_NORMAL}};
+      {"RAND_BF16_NORMAL", G4_RAND_BF16_NORMAL}, {"RAND_F32_NORMAL", G4_RAND_F32_NORMAL},
+      {"RAND_W4_PACKED_FULL", G4_RAND_W4_PACKED_FULL},
+      {"RAND_PLE_PACKED_FULL", G4_RAND_PLE_PACKED_FULL}};
   for (const auto &k : kinds) {
     napi_create_int32(env, k.value, &v);
     napi_set_named_property(env, exports, k.name, v);

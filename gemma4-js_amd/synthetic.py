@@ -6,12 +6,17 @@ kernels seeded data with the distributions of the measured workloads:
 * W4A16 linear: q uniform integer in [-7, 7], stored as the offset nibble q+8,
   8 per little-endian u32 along K, low nibble first (compressed-tensors,
   official-w4a16.js:1-19); per-group (32 along K) scales bf16(|N(0,1)|*0.02).
+  With full_range, q is uniform over the format's whole [-8, 7] (stored
+  nibbles 0..15; official-w4a16.js:15-19) and every group holds q = -8
+  (nibble 0) at least once.
 * activations: bf16(N(0,1)), handed to the kernels as bf16 bits or as the
   exactly equal FP32 values.
 * PLE table: q uniform integer in [-7, 7] as two's-complement nibbles, two per
   byte, low nibble first; scales bf16(|N(0,1)|*0.05) per 32-column group; each
   shard laid out packed block then scales block as the builder writes it
-  (tools/build_ple_w4_full.py:130-170).
+  (tools/build_ple_w4_full.py:130-170).  With full_range, q is uniform over
+  [-8, 7] (all 16 nibbles; nibble 8 is -8, ple-w4-shard-reader.js:92) and
+  every group holds nibble 8 at least once.
 * token ids: uniform in [0, vocab).
 
 bf16 conversion is round-to-nearest-even (official-w4a16.js:34-48).
@@ -48,10 +53,22 @@ def unpack_w4(packed):
     return (nib.astype(np.int16) - 8).astype(np.int8).reshape(n, kw * 8)
 
 
-def w4_weights(seed, n, k, scale_mult=0.02):
+def _force_in_every_group(rng, q, value, group=32):
+    """Set one random element of every `group`-wide group of q to `value`."""
+    r, w = q.shape
+    g = w // group
+    pos = rng.integers(0, group, size=(r, g)) + np.arange(g) * group
+    q[np.arange(r)[:, None], pos] = value
+    return q
+
+
+def w4_weights(seed, n, k, scale_mult=0.02, full_range=False):
     """(packed u32 [n, k/8], scales bf16 bits [n, k/32], q int8 [n, k])."""
-    rng = np.random.default_rng([seed, n, k, 0x57])
-    q = rng.integers(-7, 8, size=(n, k), dtype=np.int8)
+    rng = np.random.default_rng([seed, n, k, 0x57 if not full_range else 0x58])
+    if full_range:
+        q = _force_in_every_group(rng, rng.integers(-8, 8, size=(n, k), dtype=np.int8), -8)
+    else:
+        q = rng.integers(-7, 8, size=(n, k), dtype=np.int8)
     s = np.abs(rng.standard_normal((n, k // 32), dtype=np.float32)) * np.float32(scale_mult)
     return pack_w4(q), bf16_rne(s), q
 
@@ -75,26 +92,31 @@ _PAIR = np.arange(225)
 _PLE_PAIR_LUT = ((((_PAIR % 15) - 7) & 15) | ((((_PAIR // 15) - 7) & 15) << 4)).astype(np.uint8)
 
 
-def ple_shard(seed, shard, rows, width=8960, scale_mult=0.05):
+def ple_shard(seed, shard, rows, width=8960, scale_mult=0.05, full_range=False):
     """One shard file's bytes (packed block then scales block) as uint8.
 
     Each byte holds two independent q uniform in [-7, 7] (a pair drawn
-    uniformly from the 225 combinations)."""
-    rng = np.random.default_rng([seed, shard, width, 0x91])
-    packed = _PLE_PAIR_LUT[rng.integers(0, 225, size=(rows, width // 2), dtype=np.uint8)]
+    uniformly from the 225 combinations), or with full_range two q uniform in
+    [-8, 7] (a uniform byte) with q = -8 in every 32-column group."""
+    rng = np.random.default_rng([seed, shard, width, 0x91 if not full_range else 0x92])
+    if full_range:
+        q = rng.integers(-8, 8, size=(rows, width), dtype=np.int8)
+        packed = pack_ple(_force_in_every_group(rng, q, -8))
+    else:
+        packed = _PLE_PAIR_LUT[rng.integers(0, 225, size=(rows, width // 2), dtype=np.uint8)]
     s = np.abs(rng.standard_normal((rows, width // 32), dtype=np.float32)) * np.float32(scale_mult)
     scales = bf16_rne(s).astype("<u2")
     return np.concatenate([packed.reshape(-1), scales.view(np.uint8).reshape(-1)])
 
 
-def ple_table(seed, vocab=262144, width=8960, rows_per_shard=4096, threads=8):
+def ple_table(seed, vocab=262144, width=8960, rows_per_shard=4096, threads=8, full_range=False):
     """All shard files of a table, generated in parallel: list of uint8 arrays."""
     from concurrent.futures import ThreadPoolExecutor
     nshards = (vocab + rows_per_shard - 1) // rows_per_shard
 
     def one(si):
         rows = min(rows_per_shard, vocab - si * rows_per_shard)
-        return ple_shard(seed, si, rows, width)
+        return ple_shard(seed, si, rows, width, full_range=full_range)
 
     with ThreadPoolExecutor(max(1, threads)) as ex:
         return list(ex.map(one, range(nshards)))

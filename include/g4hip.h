@@ -133,6 +133,20 @@ int g4_w4_load(const void *packed, const void *scales, int out_dim, int in_dim,
 int g4_w4_load_dev(const void *packed_dev, const void *scales_dev, int out_dim,
                    int in_dim, int group, g4_w4 **out);
 
+/* g4_w4_load / g4_w4_load_dev with options (no reference counterpart; the
+ * reference keeps one buffer per tensor, gpu-runtime.js:1385-1392):
+ *   G4_W4_SRC_DEVICE     packed and scales are device pointers
+ *   G4_W4_NO_GEMM_TILES  do not build the prefill GEMM's stage-major tile copy
+ *                        of the words and scales (about half the handle's
+ *                        device bytes).  For weights that only ever run the
+ *                        decode GEMV; a prefill call on such a weight takes the
+ *                        row-major MFMA kernel instead (same results to FP32
+ *                        rounding, slower at large row counts). */
+#define G4_W4_SRC_DEVICE 1
+#define G4_W4_NO_GEMM_TILES 2
+int g4_w4_load_opts(const void *packed, const void *scales, int out_dim, int in_dim,
+                    int group, int flags, g4_w4 **out);
+
 /* GPUW4Linear.dispose(). */
 int g4_w4_free(g4_w4 *w);
 
@@ -332,12 +346,18 @@ int g4_argmax(const float *x, int n, int32_t *out_dev);
  *   G4_RAND_PLE_PACKED       bytes, 2 two's-complement nibbles in [-7, 7]
  *   G4_RAND_BF16_ABS_NORMAL  bf16 |N(0,1)| * sigma (group scales)
  *   G4_RAND_BF16_NORMAL      bf16 N(0,1) * sigma (embeddings)
- *   G4_RAND_F32_NORMAL       float N(0,1) * sigma */
+ *   G4_RAND_F32_NORMAL       float N(0,1) * sigma
+ *   G4_RAND_W4_PACKED_FULL   uint32 words, 8 nibbles uniform in [0, 15]: the
+ *                            format's whole q range [-8, 7] (nibble 0 = -8)
+ *   G4_RAND_PLE_PACKED_FULL  bytes, 2 nibbles uniform in [0, 15]: q in
+ *                            [-8, 7] (two's-complement nibble 8 = -8) */
 #define G4_RAND_W4_PACKED 0
 #define G4_RAND_PLE_PACKED 1
 #define G4_RAND_BF16_ABS_NORMAL 2
 #define G4_RAND_BF16_NORMAL 3
 #define G4_RAND_F32_NORMAL 4
+#define G4_RAND_W4_PACKED_FULL 5
+#define G4_RAND_PLE_PACKED_FULL 6
 int g4_fill_random(void *dst, size_t count, int kind, uint64_t seed,
                    float sigma);
 

@@ -174,24 +174,25 @@ int g4o_w4_linear_mt(const float *x, int M, const int32_t *packed,
   {
     float *wchunk = (float *)malloc((size_t)chunk * K * sizeof(float));
     float *ychunk = (float *)malloc((size_t)M * chunk * sizeof(float));
-    if (!wchunk || !ychunk) {
-      rc |= 1 << 8;
-    } else {
+    const int have = wchunk && ychunk;
+    if (!have) rc |= 1 << 8;
+    /* every thread of the team reaches the worksharing loop (its implicit
+     * barrier); a thread without buffers only skips the loop bodies */
 #pragma omp for schedule(dynamic, 1)
-      for (int c = 0; c < nchunks; ++c) {
-        const int rowStart = c * chunk;
-        const int rowCount = chunk < N - rowStart ? chunk : N - rowStart;
-        int r = g4o_w4_dequant_rows(packed, (size_t)N * (K / 8), scales, nscales, N, K,
-                                    rowStart, rowCount, groupSize, wchunk);
-        if (r) {
-          rc |= r;
-          continue;
-        }
-        tfjs_matmul_xwT(x, M, wchunk, rowCount, K, ychunk, rowCount);
-        for (int i = 0; i < M; ++i)
-          memcpy(&y[(size_t)i * N + rowStart], &ychunk[(size_t)i * rowCount],
-                 (size_t)rowCount * sizeof(float));
+    for (int c = 0; c < nchunks; ++c) {
+      if (!have) continue;
+      const int rowStart = c * chunk;
+      const int rowCount = chunk < N - rowStart ? chunk : N - rowStart;
+      int r = g4o_w4_dequant_rows(packed, (size_t)N * (K / 8), scales, nscales, N, K,
+                                  rowStart, rowCount, groupSize, wchunk);
+      if (r) {
+        rc |= r;
+        continue;
       }
+      tfjs_matmul_xwT(x, M, wchunk, rowCount, K, ychunk, rowCount);
+      for (int i = 0; i < M; ++i)
+        memcpy(&y[(size_t)i * N + rowStart], &ychunk[(size_t)i * rowCount],
+               (size_t)rowCount * sizeof(float));
     }
     free(wchunk);
     free(ychunk);

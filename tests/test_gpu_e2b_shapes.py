@@ -59,18 +59,32 @@ def config(g4, max_seq):
     return c
 
 
-@pytest.fixture(scope="module")
-def mid(g4):
+def spread_gate(packed, scales, q):
+    """The same weight with its group scales multiplied by 2^(-24 r / (N - 1))
+    on output row r, so that the rows' largest scales spread far beyond 2^12
+    and the prefill GEMM shifts each output row on its own."""
+    n = scales.shape[0]
+    f = np.exp2(-24.0 * np.arange(n) / (n - 1)).astype(np.float32)[:, None]
+    return packed, syn.bf16_rne(syn.bf16_to_f32(scales).reshape(scales.shape) * f)
+
+
+def build_model(g4, full_range=False):
+    """A 4-layer model at the E2B widths and its float64 oracle.  With
+    full_range every W4 weight and the PLE table draw q over all of [-8, 7]
+    (W4 nibble 0 and PLE nibble 8 in every group), and each gate weight has
+    row-spread scales (spread_gate), so the prefill's gate/up GEMM (one
+    launch, gelu(gate) * up in its epilogue) runs with per-row shifts."""
     NL = len(LAYERS)
     rng = np.random.default_rng(1536)
     E = syn.bf16_rne(rng.standard_normal((V, H), dtype=np.float32) * np.float32(0.03))
-    shards = [syn.ple_shard(17, s, RPS, NL * P) for s in range(V // RPS)]
+    shards = [syn.ple_shard(17, s, RPS, NL * P, full_range=full_range) for s in range(V // RPS)]
     table = np.concatenate(shards)
     seed = [100]
 
-    def w(n, k):
+    def w(n, k, gate=False):
         seed[0] += 1
-        return syn.w4_weights(seed[0], n, k)[:2]
+        pw = syn.w4_weights(seed[0], n, k, full_range=full_range)
+        return spread_gate(*pw) if gate and full_range else pw[:2]
 
     top = w(NL * P, H)
     layers = []
@@ -80,7 +94,7 @@ def mid(g4):
                       down=(H, inter), ple_gate=(P, H), ple_proj=(H, P))
         if not shared:
             shapes.update(k=(hd, H), v=(hd, H))
-        lin = {name: w(n, k) for name, (n, k) in shapes.items()}
+        lin = {name: w(n, k, name == "gate") for name, (n, k) in shapes.items()}
         norm = {n: rng.uniform(0.9, 1.1, H).astype(np.float32)
                 for n in ("input", "post_attn", "pre_ffw", "post_ffw", "post_ple")}
         norm["q"] = rng.uniform(0.9, 1.1, hd).astype(np.float32)
@@ -139,9 +153,30 @@ def mid(g4):
     return dict(ref=ref, prefill=prefill, make=make_engine)
 
 
+@pytest.fixture(scope="module")
+def mid(g4):
+    return build_model(g4)
+
+
+@pytest.fixture(scope="module")
+def mid_full(g4):
+    return build_model(g4, full_range=True)
+
+
 @pytest.mark.parametrize("mode", ["graph", "eager"])
 @pytest.mark.parametrize("prompt,max_seq", CASES)
 def test_e2b_widths_prefill_past_window_then_decode_match_oracle(g4, mid, prompt, max_seq, mode):
+    run_against_oracle(g4, mid, prompt, max_seq, mode)
+
+
+def test_e2b_widths_full_nibble_range_match_oracle(g4, mid_full):
+    # every weight and the PLE table over the formats' whole q range, gate
+    # weights with row-spread scales: prefill (the packed-weight gate/up GEMM
+    # with per-row shifts) and recorded decode steps against the oracle
+    run_against_oracle(g4, mid_full, 520, 576, "graph")
+
+
+def run_against_oracle(g4, mid, prompt, max_seq, mode):
     ref = mid["ref"]
     ids, h0, restore = mid["prefill"](prompt)
     m = mid["make"](max_seq)

@@ -5,6 +5,8 @@ even of the exact value (BF16); matmul outputs within max-over-rows relative
 L2 error 1e-3 of the reference's FP32 dequant-then-matMul (the oracle), and
 of the binary64 product.
 """
+import ctypes
+
 import numpy as np
 import pytest
 
@@ -431,3 +433,27 @@ def test_linear_multi_errors(g4):
     with pytest.raises(g4.G4Error) as e:  # second output too short
         g4.W4Linear.linear_multi([a, a], x.ptr, g4.F32, 1, [ys[0].ptr, short.ptr])
     assert e.value.code == g4.G4_E_RANGE
+
+
+@pytest.mark.parametrize("rows,n,k", [(2048, 6144, 1536), (512, 1536, 6144), (1, 6144, 1536)])
+def test_weight_without_gemm_tiles(g4, rows, n, k):
+    # g4_w4_load_opts(G4_W4_NO_GEMM_TILES): a decode-only weight holds no tile
+    # copy (about half the device bytes); a prefill call on it takes the
+    # row-major MFMA kernel, the decode GEMV is unchanged (identical bits)
+    packed, scales, q = syn.w4_weights(61, n, k)
+    a = g4.W4Linear(packed, scales)
+    b = g4.W4Linear(packed, scales, gemm_tiles=False)
+    assert b.info()["device_bytes"] < 0.6 * a.info()["device_bytes"]
+    x = np.random.default_rng(61).standard_normal((rows, k)).astype(np.float32)
+    xb = g4.Buffer.from_array(x)
+    ya = run_linear(g4, a, None, x, rows, g4.F32)
+    yb = run_linear(g4, b, None, x, rows, g4.F32)
+    ref = x.astype(np.float64) @ dense(q, scales).T
+    assert rel_l2_rows(yb, ref) <= 1e-5
+    if rows == 1:
+        assert np.array_equal(ya, yb)
+    h = ctypes.c_void_p()
+    with pytest.raises(g4.G4Error) as e:  # an unknown flag
+        g4.check(g4.lib().g4_w4_load_opts(packed.ctypes.data, scales.ctypes.data, n, k, 32, 8,
+                                          ctypes.byref(h)))
+    assert e.value.code == g4.G4_E_ARG and not h.value
