@@ -805,28 +805,37 @@ __device__ __forceinline__ void store_halves(float *p, int lane, const float (&a
   }
 }
 
-// x = rms(x) * scale (SCALE), then (ROPE) the rotation of the pairs
-// (t, t + hd/2) for t < angles: the arithmetic of rope_qkv_kernel.  Every
-// load is unconditional (clamped index) so that none waits inside a branch.
-template <int DH, bool SCALE, bool ROPE>
-__device__ __forceinline__ void norm_rope_wave(float (&a)[DH], float (&b)[DH],
-                                               const float *scale, const float2 *rope,
-                                               int angles, float eps, int lane) {
-  constexpr int HALF = 64 * DH;
+// The norm weights and RoPE factors of one lane (dims lane * DH + j and
+// their partners hd/2 + ...), loaded once at kernel start.
+template <int DH>
+struct NormRope {
   float sa[DH], sb[DH];
   float2 r[DH];
+};
+
+template <int DH, bool SCALE, bool ROPE>
+__device__ __forceinline__ void load_norm_rope(NormRope<DH> &n, const float *scale,
+                                               const float2 *rope, int angles, int lane) {
+  constexpr int HALF = 64 * DH;
 #pragma unroll
   for (int j = 0; j < DH; ++j) {
     const int t = lane * DH + j;
     if (SCALE) {
-      sa[j] = scale[t];
-      sb[j] = scale[HALF + t];
+      n.sa[j] = scale[t];
+      n.sb[j] = scale[HALF + t];
     }
-    if (ROPE) {
-      r[j] = rope[t < angles ? t : (angles > 0 ? angles - 1 : 0)];
-      asm volatile("" ::"v"(r[j].x), "v"(r[j].y));  // load here, not in a branch below
-    }
+    if (ROPE) n.r[j] = rope[t < angles ? t : (angles > 0 ? angles - 1 : 0)];
   }
+}
+
+// x = rms(x) * scale (SCALE), then (ROPE) the rotation of the pairs
+// (t, t + hd/2) for t < angles: the arithmetic of rope_qkv_kernel, on
+// factors loaded beforehand.
+template <int DH, bool SCALE, bool ROPE>
+__device__ __forceinline__ void norm_rope_wave(float (&a)[DH], float (&b)[DH],
+                                               const NormRope<DH> &n, int angles, float eps,
+                                               int lane) {
+  constexpr int HALF = 64 * DH;
   float ss = 0.f;
 #pragma unroll
   for (int j = 0; j < DH; ++j) ss += a[j] * a[j] + b[j] * b[j];
@@ -834,12 +843,12 @@ __device__ __forceinline__ void norm_rope_wave(float (&a)[DH], float (&b)[DH],
 #pragma unroll
   for (int j = 0; j < DH; ++j) {
     const int t = lane * DH + j;
-    const float an = SCALE ? a[j] * inv * sa[j] : a[j] * inv;
-    const float bn = SCALE ? b[j] * inv * sb[j] : b[j] * inv;
+    const float an = SCALE ? a[j] * inv * n.sa[j] : a[j] * inv;
+    const float bn = SCALE ? b[j] * inv * n.sb[j] : b[j] * inv;
     if (ROPE) {
       const bool rot = t < angles;
-      a[j] = rot ? an * r[j].x - bn * r[j].y : an;
-      b[j] = rot ? bn * r[j].x + an * r[j].y : bn;
+      a[j] = rot ? an * n.r[j].x - bn * n.r[j].y : an;
+      b[j] = rot ? bn * n.r[j].x + an * n.r[j].y : bn;
     } else {
       a[j] = an;
       b[j] = bn;
@@ -857,19 +866,32 @@ __global__ __launch_bounds__(256) void attn_rope_dec_kernel(AttnRopeArgs A) {
   __shared__ int last_sh;
   const int h = blockIdx.x / A.S, s = blockIdx.x - h * A.S;
   const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
-  // q, its norm weights and the RoPE table do not depend on the position:
-  // their loads go out first
-  float qa[DH], qb[DH];
-  load_halves<DH>(A.qraw + (size_t)h * HD, lane, qa, qb);
+  // Only the key range needs the position (a scalar load).  q and its norm
+  // weights and RoPE factors (a table of the current position) go out first,
+  // so that the q norm runs while the k/v rows are in flight; the wave that
+  // builds the new key loads its k/v row and norm weights before its k/v rows.
   const int pos = *A.pos_dev;
+  float qa[DH], qb[DH], na[DH], nb[DH], va[DH], vb[DH];
+  load_halves<DH>(A.qraw + (size_t)h * HD, lane, qa, qb);
+  NormRope<DH> qn, kn;
+  load_norm_rope<DH, true, true>(qn, A.qnorm, A.rope, A.angles, lane);
   int lo = A.sliding ? pos - A.window + 1 : 0;
   lo = lo > 0 ? lo : 0;
   const int kps = (pos - lo + A.S) / A.S;  // ceil((pos - lo + 1) / S)
   const int k0 = lo + s * kps;
   const int k1 = k0 + kps < pos + 1 ? k0 + kps : pos + 1;  // [k0, k1), maybe empty
+  // the new key at pos (own-KV layers): built by the wave that owns it
+  const bool has_new = A.own && k0 <= pos && pos < k1 && ((pos - k0) & 3) == wave;
+  if (has_new) {
+    load_halves<DH>(A.kraw, lane, na, nb);
+    load_halves<DH>(A.vraw, lane, va, vb);
+    load_norm_rope<DH, true, false>(kn, A.knorm, nullptr, 0, lane);
+#pragma unroll
+    for (int j = 0; j < DH; ++j) kn.r[j] = qn.r[j];
+  }
 
-  // k/v rows of the wave's first KC keys, issued before everything else
-  // (clamped to valid rows; keys past k1 are not used)
+  // k/v rows of the wave's first KC keys (clamped to valid rows; keys past k1
+  // are not used)
   float ka[KC][DH], kb[KC][DH], xa[KC][DH], xb[KC][DH];
   int base = k0 + wave;
   auto load_chunk = [&](int b0) {
@@ -883,16 +905,11 @@ __global__ __launch_bounds__(256) void attn_rope_dec_kernel(AttnRopeArgs A) {
   };
   load_chunk(base);
 
-  norm_rope_wave<DH, true, true>(qa, qb, A.qnorm, A.rope, A.angles, A.eps, lane);
+  norm_rope_wave<DH, true, true>(qa, qb, qn, A.angles, A.eps, lane);
 
-  // the new key at pos (own-KV layers): built by the wave that owns it
-  const bool has_new = A.own && k0 <= pos && pos < k1 && ((pos - k0) & 3) == wave;
-  float na[DH], nb[DH], va[DH], vb[DH];
   if (has_new) {
-    load_halves<DH>(A.kraw, lane, na, nb);
-    load_halves<DH>(A.vraw, lane, va, vb);
-    norm_rope_wave<DH, true, true>(na, nb, A.knorm, A.rope, A.angles, A.eps, lane);
-    norm_rope_wave<DH, false, false>(va, vb, nullptr, nullptr, 0, A.eps, lane);
+    norm_rope_wave<DH, true, true>(na, nb, kn, A.angles, A.eps, lane);
+    norm_rope_wave<DH, false, false>(va, vb, kn, 0, A.eps, lane);
     if (h == 0) {
       store_halves<DH>(A.kc + (size_t)pos * HD, lane, na, nb);
       store_halves<DH>(A.vc + (size_t)pos * HD, lane, va, vb);
@@ -930,7 +947,8 @@ __global__ __launch_bounds__(256) void attn_rope_dec_kernel(AttnRopeArgs A) {
     }
 #pragma unroll
     for (int c = 0; c < KC; ++c) {
-      if (base + 4 * c >= k1) break;  // wave-uniform; the clamped rows are not used
+      const int key = base + 4 * c;
+      if (key >= k1) break;  // wave-uniform; the clamped rows are not used
       const float p = expf(d[c] - mc);
       l += p;
 #pragma unroll
@@ -987,8 +1005,9 @@ __global__ __launch_bounds__(256) void attn_rope_dec_kernel(AttnRopeArgs A) {
                                      __HIP_MEMORY_SCOPE_AGENT) == A.S - 1;
   __syncthreads();
   if (!last_sh) return;
-  // wave w merges splits w, w + 4, ... (up to 8 each, all loads in flight
-  // together; lanes hold the dims as above), then the 4 waves merge in LDS
+  // wave w merges splits w, w + 4, ... (up to SMAX / 4 each, all loads in
+  // flight together; lanes hold the dims as above), then the 4 waves merge
+  // in LDS
   constexpr int SW = SMAX / 4;  // splits per wave
   float pm[SW], pl[SW], pa[SW][DH], pb[SW][DH];
 #pragma unroll
