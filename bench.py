@@ -382,6 +382,144 @@ def cpu_baseline(n, k, budget_s=5.0, seed=0):
             "legs": legs}
 
 
+def _node_leg(script, args, budget_s):
+    """One single-threaded JS restatement under Node: (parsed result, node version)."""
+    import shutil
+    import subprocess
+    node = shutil.which("node")
+    if node is None:
+        return None, None
+    p = subprocess.run([node, os.path.join(ROOT, "oracle", script)] + [str(a) for a in args]
+                       + [str(budget_s)], stdout=subprocess.PIPE, stderr=subprocess.PIPE,
+                       text=True, timeout=budget_s * 10 + 60)
+    if p.returncode != 0:
+        raise RuntimeError("JS CPU leg %s failed: %s" % (script, p.stderr[-2000:]))
+    ver = subprocess.run([node, "--version"], stdout=subprocess.PIPE, text=True).stdout.strip()
+    return json.loads(p.stdout.strip().splitlines()[-1]), ver
+
+
+def cpu_configs(budget_s=2.0, seed=0):
+    """The reference's CPU path beside the PLE gather (1 and 2048 ids), the E2B
+    sliding layer's 7 GEMVs and the two M2048 prefill GEMMs, each restated
+    three ways and timed on this host: single-threaded JS under Node, the C
+    oracle on one core, the C oracle over every core this process may use.
+    Every leg's output is checked bit-equal to the single-core C oracle.  The
+    GEMMs are timed on a bounded sample of their 2048 rows (the CPU's time
+    is linear in the rows); the rate is per FLOP of the rows computed."""
+    import tempfile
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import g4oracle
+    threads, nproc = _cpu_share()
+    nthr = g4oracle.omp_threads(threads)
+    out = {"threads_all": nthr, "nproc": nproc, "seconds_per_leg": budget_s}
+
+    # config 1: PLE readRows over the whole [262144, 8960] table
+    vocab, width, rps = 262144, 8960, 4096
+    table = np.concatenate(syn.ple_table(2024, vocab, width, rps, threads=threads))
+    ple = {}
+    for n in (1, 2048):
+        ids = syn.token_ids(seed + n, n, vocab)
+        ref = g4oracle.ple_gather(table, vocab, width, rps, ids)
+        per = n * (width // 2 + (width // 32) * 2 + 4) + n * width * 4
+        legs = {}
+        calls, el = _time_leg(lambda: g4oracle.ple_gather(table, vocab, width, rps, ids), budget_s)
+        legs["c_1core"] = {"threads": 1, "us_per_call": el / calls * 1e6,
+                           "gbs": per * calls / el / 1e9}
+        got = [None]
+
+        def mt():
+            got[0] = g4oracle.ple_gather_mt(table, vocab, width, rps, ids, threads)
+
+        calls, el = _time_leg(mt, budget_s)
+        assert np.array_equal(got[0].view(np.uint32), ref.view(np.uint32)), "PLE all-core leg"
+        legs["c_allcores"] = {"threads": nthr, "us_per_call": el / calls * 1e6,
+                              "gbs": per * calls / el / 1e9}
+        # the JS leg gets each id's packed row and scale row, already read;
+        # at 2048 ids it runs the first 128 (its time is linear in the ids)
+        js_ids = ids[:128]
+        recs = []
+        for tid in js_ids:
+            po, so = g4oracle.ple_row_offsets(vocab, width, rps, int(tid) // rps, int(tid) % rps)
+            recs.append(table[po:po + width // 2])
+            recs.append(table[so:so + width // 16])
+        with tempfile.TemporaryDirectory() as td:
+            rp, op = os.path.join(td, "rows.bin"), os.path.join(td, "out.bin")
+            np.concatenate(recs).tofile(rp)
+            r, ver = _node_leg("ple_rows_cpu.js", [js_ids.size, width, rp, op], budget_s)
+            if r is not None:
+                y = np.fromfile(op, dtype=np.float32).reshape(js_ids.size, width)
+                assert np.array_equal(y.view(np.uint32), ref[:js_ids.size].view(np.uint32)), \
+                    "PLE JS leg"
+                scale = n / js_ids.size
+                legs["js_1core"] = {"threads": 1, "ids_timed": int(js_ids.size),
+                                    "us_per_call": r["ms_per_call"] * 1e3 * scale,
+                                    "gbs": per * r["calls"] / (r["seconds"] * scale) / 1e9,
+                                    "node": ver,
+                                    "note": "the reader's per-row dequant loop on rows already "
+                                            "read (no File.slice)"}
+        ple["ids%d_f32" % n] = legs
+    del table
+    out["ple_gather"] = ple
+
+    def linear_legs(shapes, m, with_js=True):
+        """C 1-core, C all-core and JS 1-core time of the GEMVs/GEMMs `shapes`
+        [(n, k)] at m rows, as one sequence per call."""
+        mats = [(syn.w4_weights(seed + i, n, k)[:2], n, k) for i, (n, k) in enumerate(shapes)]
+        xs = {k: np.random.default_rng([seed, k]).standard_normal((m, k)).astype(np.float32)
+              for _, k in shapes}
+        refs = [g4oracle.w4_linear(xs[k], pk, sc) for (pk, sc), n, k in mats]
+        legs = {}
+        calls, el = _time_leg(lambda: [g4oracle.w4_linear(xs[k], pk, sc)
+                                       for (pk, sc), n, k in mats], budget_s)
+        legs["c_1core"] = {"threads": 1, "ms_per_call": el / calls * 1e3}
+        got = [None]
+
+        def mt():
+            got[0] = [g4oracle.w4_linear_mt(xs[k], pk, sc, threads) for (pk, sc), n, k in mats]
+
+        calls, el = _time_leg(mt, budget_s)
+        for a, b in zip(got[0], refs):
+            assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), "all-core leg"
+        legs["c_allcores"] = {"threads": nthr, "ms_per_call": el / calls * 1e3}
+        if with_js:
+            total_ms, ver = 0.0, None
+            with tempfile.TemporaryDirectory() as td:
+                for i, ((pk, sc), n, k) in enumerate(mats):
+                    paths = [os.path.join(td, "%s%d.bin" % (f, i)) for f in "psxy"]
+                    np.ascontiguousarray(pk).view(np.int32).tofile(paths[0])
+                    np.ascontiguousarray(sc).view(np.uint16).tofile(paths[1])
+                    xs[k].tofile(paths[2])
+                    r, ver = _node_leg("w4_linear_cpu.js", [m, k, n] + paths,
+                                       budget_s / len(mats))
+                    if r is None:
+                        break
+                    y = np.fromfile(paths[3], dtype=np.float32).reshape(m, n)
+                    assert np.array_equal(y.view(np.uint32), refs[i].view(np.uint32)), "JS leg"
+                    total_ms += r["ms_per_call"]
+                else:
+                    legs["js_1core"] = {"threads": 1, "ms_per_call": total_ms, "node": ver}
+        return legs
+
+    # config 2: one E2B sliding layer's 7 GEMVs at one row
+    lb = sum(w4_bytes(n, k) for _, n, k in E2B_SLIDING_LAYER)
+    legs = linear_legs([(n, k) for _, n, k in E2B_SLIDING_LAYER], 1)
+    for v in legs.values():
+        v["gbs"] = lb / (v["ms_per_call"] * 1e-3) / 1e9
+    out["layer_e2b_sliding_7gemv"] = legs
+
+    # config 3: the M2048 GEMMs on a sample of rows
+    gemm = {}
+    for n, k in ((6144, 1536), (1536, 6144)):
+        rows = 16
+        legs = linear_legs([(n, k)], rows)
+        for v in legs.values():
+            v["gflops"] = 2.0 * rows * n * k / (v["ms_per_call"] * 1e-3) / 1e9
+            v["ms_per_2048_rows"] = v["ms_per_call"] * 2048 / rows
+        gemm["M2048_N%d_K%d" % (n, k)] = {"rows_timed": rows, "legs": legs}
+    out["gemm_prefill"] = gemm
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -391,6 +529,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=5.0, help="seconds per CPU leg")
+    ap.add_argument("--cpu-config-seconds", type=float, default=2.0,
+                    help="seconds per CPU leg beside the PLE, layer and GEMM configurations")
     ap.add_argument("--skip-decode", action="store_true",
                     help="leave out the E2B decode extra")
     ap.add_argument("--decode-only", action="store_true",
@@ -464,6 +604,9 @@ def main():
         log("CPU baseline (JS 1 core, C 1 core, C all cores) ...")
         cpu = cpu_baseline(n, k, args.cpu_seconds)
         log("  ", cpu)
+        log("CPU legs beside the PLE gather, the E2B layer and the M2048 GEMMs ...")
+        cpu["configs"] = cpu_configs(args.cpu_config_seconds)
+        log("  ", cpu["configs"])
 
     traffic, traffic_src, kname = None, None, "w4_gemv_r16_kernel"
     tpath = os.path.join(ROOT, "profiles", "w4_gemv_m1_k1536_n6144_traffic.json")

@@ -284,6 +284,32 @@ int g4o_ple_gather(const uint8_t *table, int vocab, int width,
   return 0;
 }
 
+int g4o_ple_gather_mt(const uint8_t *table, int vocab, int width, int rows_per_shard,
+                      const int32_t *ids, int n, float *out, int threads) {
+  /* g4o_ple_gather with the ids over OpenMP threads (the all-core CPU
+   * baseline): every row is the same computation, so the result is too */
+  for (int j = 0; j < n; ++j)
+    if (g4o_ple_locate(ids[j], vocab, rows_per_shard, NULL, NULL)) return -1 - j;
+  int rc = 0;
+#pragma omp parallel num_threads(g4o_omp_threads(threads)) reduction(| : rc)
+  {
+    uint16_t *sb = (uint16_t *)malloc((size_t)(width / 32) * 2);
+    if (!sb) rc |= 1;
+#pragma omp for schedule(static)
+    for (int j = 0; j < n; ++j) {
+      if (!sb) continue;
+      int shard, local;
+      g4o_ple_locate(ids[j], vocab, rows_per_shard, &shard, &local);
+      size_t po, so;
+      g4o_ple_row_offsets(vocab, width, rows_per_shard, shard, local, &po, &so);
+      memcpy(sb, table + so, (size_t)(width / 32) * 2);
+      g4o_ple_dequant_row(table + po, sb, width, out + (size_t)j * width);
+    }
+    free(sb);
+  }
+  return rc ? -1 - n : 0;
+}
+
 void g4o_ple_quantize_rows(const float *rows, int nrows, int width,
                            uint8_t *packed, uint16_t *scale_bits) {
   /* tools/build_ple_w4_full.py:48-60 */

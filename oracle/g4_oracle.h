@@ -104,6 +104,10 @@ void g4o_ple_row_offsets(int vocab, int width, int rows_per_shard, int shard,
  * out-of-range id at position j (the reference throws there). */
 int g4o_ple_gather(const uint8_t *table, int vocab, int width,
                    int rows_per_shard, const int32_t *ids, int n, float *out);
+/* g4o_ple_gather with the ids spread over OpenMP threads (0: all); the same
+ * output.  Every id is range-checked first. */
+int g4o_ple_gather_mt(const uint8_t *table, int vocab, int width, int rows_per_shard,
+                      const int32_t *ids, int n, float *out, int threads);
 
 /* quantize_batch (tools/build_ple_w4_full.py:48-60): per 32-column group
  * s = maxabs/7 (1.0 when maxabs == 0), stored as bf16 (RNE), then

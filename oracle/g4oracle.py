@@ -39,6 +39,7 @@ _SIGS = {
     "g4o_ple_locate": (_i, [_c.c_longlong, _i, _i, _c.POINTER(_i), _c.POINTER(_i)]),
     "g4o_ple_row_offsets": (None, [_i, _i, _i, _i, _i, _c.POINTER(_z), _c.POINTER(_z)]),
     "g4o_ple_gather": (_i, [_p, _i, _i, _i, _p, _i, _p]),
+    "g4o_ple_gather_mt": (_i, [_p, _i, _i, _i, _p, _i, _p, _i]),
     "g4o_ple_quantize_rows": (None, [_p, _i, _i, _p, _p]),
     "g4o_bf16_head": (None, [_p, _p, _i, _i, _c.c_float, _c.c_float, _p]),
     "g4o_topk": (_i, [_p, _i, _i, _p, _p]),
@@ -189,6 +190,18 @@ def ple_gather(table, vocab, width, rows_per_shard, ids):
     ids = np.ascontiguousarray(ids, dtype=np.int32)
     out = np.empty((ids.size, width), dtype=np.float32)
     rc = lib().g4o_ple_gather(_ptr(table), vocab, width, rows_per_shard, _ptr(ids), ids.size, _ptr(out))
+    if rc:
+        raise IndexError("PLE token out of range at position %d" % (-1 - rc))
+    return out
+
+
+def ple_gather_mt(table, vocab, width, rows_per_shard, ids, threads=0):
+    """ple_gather with the ids over `threads` OpenMP threads (0: all); the same output."""
+    table = np.ascontiguousarray(table, dtype=np.uint8)
+    ids = np.ascontiguousarray(ids, dtype=np.int32)
+    out = np.empty((ids.size, width), dtype=np.float32)
+    rc = lib().g4o_ple_gather_mt(_ptr(table), vocab, width, rows_per_shard, _ptr(ids), ids.size,
+                                 _ptr(out), int(threads))
     if rc:
         raise IndexError("PLE token out of range at position %d" % (-1 - rc))
     return out

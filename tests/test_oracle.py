@@ -218,6 +218,45 @@ def test_js_cpu_leg_block_rounding(oracle, tmp_path):
     assert _run_js_leg(tmp_path, x, packed, scales)[0, 0] == np.float32(2.0 ** 24)
 
 
+def test_js_ple_rows_leg_matches_c_oracle(oracle, tmp_path):
+    # the JS restatement of readRows' per-row loop (the CPU baseline beside
+    # the PLE gather) on rows holding every nibble value, nibble 8 (-8) in
+    # every group: identical bits to the C oracle's gather
+    import shutil
+    import subprocess
+    node = shutil.which("node")
+    if node is None:
+        pytest.skip("node is not installed")
+    vocab, width, rps = 9000, 512, 4096
+    table = np.concatenate(syn.ple_table(3, vocab, width, rps, threads=2, full_range=True))
+    ids = np.array([0, 4095, 4096, 8999, 17, 17], dtype=np.int32)
+    recs = []
+    for t in ids:
+        po, so = oracle.ple_row_offsets(vocab, width, rps, int(t) // rps, int(t) % rps)
+        recs += [table[po:po + width // 2], table[so:so + width // 16]]
+    rp, op = str(tmp_path / "rows.bin"), str(tmp_path / "out.bin")
+    np.concatenate(recs).tofile(rp)
+    script = os.path.join(os.path.dirname(GOLDEN), "..", "oracle", "ple_rows_cpu.js")
+    p = subprocess.run([node, script, str(ids.size), str(width), rp, op, "0"],
+                       stdout=subprocess.PIPE, stderr=subprocess.PIPE, text=True, timeout=120)
+    assert p.returncode == 0, p.stderr
+    got = np.fromfile(op, dtype=np.float32).reshape(ids.size, width)
+    want = oracle.ple_gather(table, vocab, width, rps, ids)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def test_ple_gather_mt_matches_single_thread(oracle):
+    vocab, width, rps = 9000, 512, 4096
+    table = np.concatenate(syn.ple_table(4, vocab, width, rps, threads=2, full_range=True))
+    ids = syn.token_ids(5, 700, vocab)
+    want = oracle.ple_gather(table, vocab, width, rps, ids)
+    for t in (1, 3, 0):
+        got = oracle.ple_gather_mt(table, vocab, width, rps, ids, threads=t)
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    with pytest.raises(IndexError):
+        oracle.ple_gather_mt(table, vocab, width, rps, np.array([1, vocab], np.int32))
+
+
 def test_w4_linear_f64_matches_numpy(oracle):
     packed, scales, q = syn.w4_weights(21, 512, 1536)
     _, x = syn.activations(21, 2, 1536)
