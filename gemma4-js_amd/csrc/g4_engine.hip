@@ -278,12 +278,43 @@ int linear_parts(const g4_w4 *w, const float *x, int rows, float *y, GemmParts *
 
 // Enqueue the forward of `rows` tokens whose ids are in m->ids and whose first
 // position is *m->pos; leaves the final-norm last row in m->last.
-int run_layers(g4_gemma *m, int rows, bool graph) {
-  if (rows == 1) return run_token(m, graph);
+// The diagnostic read-outs of forward(ids, pos, {diagnostic: true})
+// (gemma4-webgpu.js:311-397): device buffers, each optional.
+struct Diag {
+  float *top_hidden = nullptr;  // [rows, hidden]: the scaled embedding rows
+  float *top_ple = nullptr;     // [rows, layers * ple_dim]: pleMix's per-layer inputs
+  float *layers = nullptr;      // [layers, rows, hidden]: every layer's output rows
+  int stage_layer = -1;         // the layer whose encodeLayer stages go to `stages`
+  float *stages = nullptr;      // the stages at the offsets of diag_stage_offsets
+  size_t off[G4_STAGES + 1] = {};
+};
+
+// Floats of each encodeLayer stage of `layer` at `rows` rows (the reference's
+// probe counts, gemma4-webgpu.js:224-309; the k/v stages of a shared-KV layer
+// are empty) and their offsets in a stage buffer.
+void diag_stage_offsets(const g4_gemma *m, int layer, int rows, size_t *off) {
+  const g4_gemma_config &c = m->cfg;
+  const Layer &l = m->L[layer];
+  const size_t R = (size_t)rows, H = c.hidden, QD = (size_t)c.heads * l.hd;
+  const size_t kv = l.kv_src < 0 ? R * l.hd : 0;
+  const size_t n[G4_STAGES] = {R * H, R * QD, R * QD, kv, kv, kv, kv, R * QD, R * H, R * H,
+                               R * H, R * H, R * l.inter, R * l.inter, R * l.inter, R * H, R * H,
+                               R * H, R * c.ple_dim, R * c.ple_dim, R * H, R * H, R * H};
+  off[0] = 0;
+  for (int i = 0; i < G4_STAGES; ++i) off[i + 1] = off[i] + n[i];
+}
+
+int run_layers(g4_gemma *m, int rows, bool graph, const Diag *dg = nullptr) {
+  if (rows == 1 && !dg) return run_token(m, graph);
   const g4_gemma_config &c = m->cfg;
   const int H = c.hidden, P = c.ple_dim, NL = c.layers;
   const float eps = c.eps;
   int rc;
+  auto cp = [&](float *dst, const float *src, size_t n) -> int {
+    const hipError_t e =
+        hipMemcpyAsync(dst, src, n * 4, hipMemcpyDeviceToDevice, stream());
+    return e == hipSuccess ? G4_OK : fail(G4_E_HIP, "diagnostic copy: %s", hipGetErrorString(e));
+  };
   // Top level (gemma4-webgpu.js:316-323): scaled embedding, PLE rows,
   // per-layer projection, pleMix.
   if ((rc = launch_embed(m->E, c.vocab, H, m->ids, rows, (float)sqrt((double)H), m->h[0])))
@@ -293,6 +324,8 @@ int run_layers(g4_gemma *m, int rows, bool graph) {
   if ((rc = launch_ple_mix(m->proj, (float)(1.0 / sqrt((double)H)), m->ple_norm, m->tokple,
                            rows, P, NL, 1e-6f, 16.f, 0.7071067811865476f, m->perlayer)))
     return rc;
+  if (dg && dg->top_hidden && (rc = cp(dg->top_hidden, m->h[0], (size_t)rows * H))) return rc;
+  if (dg && dg->top_ple && (rc = cp(dg->top_ple, m->perlayer, (size_t)rows * NL * P))) return rc;
 
   const int keylen_host = m->cache_len + rows;  // prefill calls know it; graphs read *pos
   const int max_keylen = graph ? c.max_seq : keylen_host;
@@ -307,13 +340,20 @@ int run_layers(g4_gemma *m, int rows, bool graph) {
   // feeds a GEMM (q/k/v, gate/up, PLE gate) also write it as the GEMM's x'
   // (launch_norm_chain_xprep after w4_gemm_prepare), so those GEMMs skip
   // their x pre-pass.
-  const bool gemm = rows > kMaxGemvRows;
+  // (the diagnostic forward keeps every stage as its own buffer)
+  const bool gemm = rows > kMaxGemvRows && !dg;
   if ((rc = launch_rms(m->h[0], rows, H, m->L[0].norm[G4_NORM_INPUT], eps, m->pre, nullptr)))
     return rc;
   bool pre_prepped = false;  // x' of m->pre already in the GEMM's prepared scratch
   for (int i = 0; i < NL; ++i) {
     const Layer &l = m->L[i];
     float *hid = m->h[cur], *out = m->h[cur ^ 1];
+    // this layer's stage buffer (diagnostic forward), or null
+    float *sb = dg && dg->stages && i == dg->stage_layer ? dg->stages : nullptr;
+    auto stage = [&](int st, const float *src) -> int {
+      const size_t n = dg->off[st + 1] - dg->off[st];
+      return n ? cp(sb + dg->off[st], src, n) : G4_OK;
+    };
     // encodeLayer (gemma4-webgpu.js:215-301); m->pre holds rms(hid) * input norm
     // q, and k/v for a layer with its own cache, from one pre-pass and launch
     const g4_w4 *qkv[3] = {l.w[G4_PROJ_Q], l.w[G4_PROJ_K], l.w[G4_PROJ_V]};
@@ -324,9 +364,12 @@ int run_layers(g4_gemma *m, int rows, bool graph) {
     else
       rc = g4_w4_linear_multi(qkv, nqkv, m->pre, G4_F32, rows, qkv_out, G4_F32);
     if (rc) return rc;
+    if (sb && ((rc = stage(G4_STAGE_PRE_ATTENTION, m->pre)) || (rc = stage(G4_STAGE_Q_RAW, m->qraw))))
+      return rc;
     if ((rc = launch_norm_rope(m->qraw, rows, c.heads, l.hd, 0, m->pos, l.norm[G4_NORM_Q],
                                l.rope_angles, l.rope_base, eps, m->q, false)))
       return rc;
+    if (sb && (rc = stage(G4_STAGE_Q_NORM_ROPE, m->q))) return rc;
     const Layer &src = l.kv_src >= 0 ? m->L[l.kv_src] : l;
     if (l.kv_src < 0) {
       // KVCache.append: rows go straight to positions pos .. pos + rows - 1
@@ -334,12 +377,30 @@ int run_layers(g4_gemma *m, int rows, bool graph) {
                                  l.rope_angles, l.rope_base, eps, l.kc, true)))
         return rc;
       if ((rc = launch_rms(m->vraw, rows, l.hd, nullptr, eps, l.vc, m->pos))) return rc;
+      if (sb) {
+        const size_t at = (size_t)m->cache_len * l.hd;  // the appended rows
+        if ((rc = stage(G4_STAGE_K_RAW, m->kraw)) || (rc = stage(G4_STAGE_V_RAW, m->vraw)) ||
+            (rc = stage(G4_STAGE_K_NORM_ROPE, l.kc + at)) || (rc = stage(G4_STAGE_V_NORM, l.vc + at)))
+          return rc;
+      }
     }
     if ((rc = launch_attention(m->q, src.kc, src.vc, rows, c.heads, l.hd, keylen_host, 0, m->pos,
                                max_keylen, !l.full, c.window, kpw, m->part, m->ctx)))
       return rc;
+    if (sb && (rc = stage(G4_STAGE_ATTENTION_CONTEXT, m->ctx))) return rc;
     GemmParts op;
-    if ((rc = linear_parts(l.w[G4_PROJ_O], m->ctx, rows, m->attn, &op))) return rc;
+    if (dg) {  // the projection whole (no K slices left for the chain to add)
+      if ((rc = g4_w4_linear(l.w[G4_PROJ_O], m->ctx, G4_F32, rows, m->attn, G4_F32))) return rc;
+      op = {m->attn, 1, 0};
+    } else if ((rc = linear_parts(l.w[G4_PROJ_O], m->ctx, rows, m->attn, &op))) {
+      return rc;
+    }
+    if (sb) {
+      float *pan = sb + dg->off[G4_STAGE_POST_ATTENTION_NORM];
+      if ((rc = stage(G4_STAGE_ATTENTION_OUTPUT, m->attn)) ||
+          (rc = launch_rms(m->attn, rows, H, l.norm[G4_NORM_POST_ATTN], eps, pan, nullptr)))
+        return rc;
+    }
     const g4_w4 *gu[2] = {l.w[G4_PROJ_GATE], l.w[G4_PROJ_UP]};
     if (gemm) {  // gate, up and gelu(gate) * up in one GEMM launch on the chain's x'
       GemmXPrep xp;
@@ -358,8 +419,23 @@ int run_layers(g4_gemma *m, int rows, bool graph) {
       if ((rc = g4_w4_linear_multi(gu, 2, m->pf, G4_F32, rows, gu_out, G4_F32))) return rc;
       if ((rc = launch_gelu_mul(m->gate, m->up, (size_t)rows * l.inter, m->act))) return rc;
     }
+    if (sb && ((rc = stage(G4_STAGE_ATTENTION_RESIDUAL, m->ares)) ||
+               (rc = stage(G4_STAGE_PRE_FFW, m->pf)) || (rc = stage(G4_STAGE_MLP_GATE, m->gate)) ||
+               (rc = stage(G4_STAGE_MLP_UP, m->up)) || (rc = stage(G4_STAGE_MLP_ACTIVATED, m->act))))
+      return rc;
     GemmParts dp;
-    if ((rc = linear_parts(l.w[G4_PROJ_DOWN], m->act, rows, m->down, &dp))) return rc;
+    if (dg) {
+      if ((rc = g4_w4_linear(l.w[G4_PROJ_DOWN], m->act, G4_F32, rows, m->down, G4_F32))) return rc;
+      dp = {m->down, 1, 0};
+    } else if ((rc = linear_parts(l.w[G4_PROJ_DOWN], m->act, rows, m->down, &dp))) {
+      return rc;
+    }
+    if (sb) {
+      float *pfn = sb + dg->off[G4_STAGE_POST_FFW_NORM];
+      if ((rc = stage(G4_STAGE_FFW_OUTPUT, m->down)) ||
+          (rc = launch_rms(m->down, rows, H, l.norm[G4_NORM_POST_FFW], eps, pfn, nullptr)))
+        return rc;
+    }
     const g4_w4 *pgw = l.w[G4_PROJ_PLE_GATE];
     if (gemm) {  // the residual itself is the PLE gate's input
       GemmXPrep xp;
@@ -378,6 +454,14 @@ int run_layers(g4_gemma *m, int rows, bool graph) {
     if ((rc = launch_gelu_ple(m->pg, m->perlayer, rows, i, P, NL, m->pm))) return rc;
     if ((rc = g4_w4_linear(l.w[G4_PROJ_PLE_PROJ], m->pm, G4_F32, rows, m->pp, G4_F32)))
       return rc;
+    if (sb) {
+      float *pln = sb + dg->off[G4_STAGE_PLE_NORMALIZED];
+      if ((rc = stage(G4_STAGE_FFW_RESIDUAL, m->fres)) || (rc = stage(G4_STAGE_PLE_GATE, m->pg)) ||
+          (rc = stage(G4_STAGE_PLE_MODULATED, m->pm)) ||
+          (rc = stage(G4_STAGE_PLE_PROJECTED, m->pp)) ||
+          (rc = launch_rms(m->pp, rows, H, l.norm[G4_NORM_POST_PLE], eps, pln, nullptr)))
+        return rc;
+    }
     const bool last = i + 1 == NL;
     pre_prepped = gemm && !last;
     if (pre_prepped) {  // the next layer's q/k/v input, as that GEMM's x'
@@ -394,6 +478,9 @@ int run_layers(g4_gemma *m, int rows, bool graph) {
                                        eps, rows, H, out, last ? nullptr : m->pre))) {
       return rc;
     }
+    if (sb && (rc = stage(G4_STAGE_OUTPUT, out))) return rc;
+    if (dg && dg->layers && (rc = cp(dg->layers + (size_t)i * rows * H, out, (size_t)rows * H)))
+      return rc;
     cur ^= 1;
   }
   // final norm of the last row (gemma4-webgpu.js:394-400)
@@ -769,6 +856,50 @@ G4_API int g4_gemma_forward(g4_gemma *m, const int32_t *ids, int n, int start_po
   if (last_hidden)
     G4_HIP_TRY(hipMemcpyAsync(last_hidden, m->last, (size_t)m->cfg.hidden * 4,
                               hipMemcpyDeviceToDevice, stream()));
+  return ok();
+}
+
+G4_API int g4_gemma_diag_stages(const g4_gemma *m, int layer, int n, size_t *offsets) {
+  if (!m || !offsets) return fail(G4_E_ARG, "g4_gemma_diag_stages: null argument");
+  if (layer < 0 || layer >= m->cfg.layers || n <= 0)
+    return fail(G4_E_ARG, "g4_gemma_diag_stages: layer %d / %d rows out of range", layer, n);
+  diag_stage_offsets(m, layer, n, offsets);
+  return ok();
+}
+
+G4_API int g4_gemma_forward_diag(g4_gemma *m, const int32_t *ids, int n, int start_pos,
+                                 float *last_hidden, float *top_hidden, float *top_ple,
+                                 float *layer_hidden, int stage_layer, float *stages) {
+  G4_CHECK_INIT();
+  G4_CHECK_NOT_ENCODING();
+  if (!m || !ids) return fail(G4_E_ARG, "g4_gemma_forward_diag: null argument");
+  const g4_gemma_config &c = m->cfg;
+  Diag dg;
+  dg.top_hidden = top_hidden;
+  dg.top_ple = top_ple;
+  dg.layers = layer_hidden;
+  dg.stages = stages;
+  dg.stage_layer = stages ? stage_layer : -1;
+  int rc = check_ready(m);
+  if (!rc && n <= 0) rc = fail(G4_E_ARG, "g4_gemma: token count must be positive, got %d", n);
+  if (!rc && stages && (stage_layer < 0 || stage_layer >= c.layers))
+    rc = fail(G4_E_ARG, "g4_gemma_forward_diag: stage layer %d out of range", stage_layer);
+  if (!rc && stages) diag_stage_offsets(m, stage_layer, n, dg.off);
+  const size_t R = n > 0 ? (size_t)n : 0, H = c.hidden;
+  if (!rc && last_hidden) rc = check_device_range(last_hidden, H * 4, "forward_diag last_hidden");
+  if (!rc && top_hidden) rc = check_device_range(top_hidden, R * H * 4, "forward_diag top_hidden");
+  if (!rc && top_ple)
+    rc = check_device_range(top_ple, R * c.layers * c.ple_dim * 4, "forward_diag top_ple");
+  if (!rc && layer_hidden)
+    rc = check_device_range(layer_hidden, (size_t)c.layers * R * H * 4,
+                            "forward_diag layer_hidden");
+  if (!rc && stages) rc = check_device_range(stages, dg.off[G4_STAGES] * 4, "forward_diag stages");
+  if (!rc) rc = stage_ids(m, ids, n, start_pos);
+  if (!rc) rc = run_layers(m, n, false, &dg);
+  if (rc) return rc;
+  m->cache_len += n;
+  if (last_hidden)
+    G4_HIP_TRY(hipMemcpyAsync(last_hidden, m->last, H * 4, hipMemcpyDeviceToDevice, stream()));
   return ok();
 }
 

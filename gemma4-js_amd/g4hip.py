@@ -93,6 +93,8 @@ SIGNATURES = {
     "g4_gemma_greedy": (_int, [_vp, _vp, _int, _int, _c.POINTER(_c.c_int32), _vp]),
     "g4_gemma_decode": (_int, [_vp, _int, _vp]),
     "g4_gemma_last_hidden": (_int, [_vp, _vp]),
+    "g4_gemma_forward_diag": (_int, [_vp, _vp, _int, _int, _vp, _vp, _vp, _vp, _int, _vp]),
+    "g4_gemma_diag_stages": (_int, [_vp, _int, _int, _c.POINTER(_sz)]),
 }
 
 # g4_fill_random kinds
@@ -103,6 +105,13 @@ PROJ = dict(q=0, k=1, v=2, o=3, gate=4, up=5, down=6, ple_gate=7, ple_proj=8, to
 NORM = dict(input=0, post_attn=1, pre_ffw=2, post_ffw=3, post_ple=4, q=5, k=6,
             ple_projection=7, final=8)
 GEMMA_MAX_LAYERS = 64
+# g4_gemma_forward_diag stages, encodeLayer's probe names (gemma4-webgpu.js:224-309)
+STAGE_NAMES = ["preAttention", "qRaw", "qNormRoPE", "kRaw", "vRaw", "kNormRoPE", "vNorm",
+               "attentionContext", "attentionOutput", "postAttentionNorm", "attentionResidual",
+               "preFfw", "mlpGate", "mlpUp", "mlpActivated", "ffwOutput", "postFfwNorm",
+               "ffwResidual", "pleGate", "pleModulated", "pleProjected", "pleNormalized",
+               "output"]
+STAGES = len(STAGE_NAMES)
 
 
 class GemmaConfig(_c.Structure):
@@ -511,6 +520,21 @@ class Gemma:
         ids = np.ascontiguousarray(ids, dtype=np.int32)
         check(lib().g4_gemma_forward(self.h, ids.ctypes.data, ids.size, start_pos,
                                      _f(last_hidden)))
+
+    def forward_diag(self, ids, start_pos, last_hidden=None, top_hidden=None, top_ple=None,
+                     layer_hidden=None, stage_layer=-1, stages=None):
+        """forward(tokenIds, startPos, {diagnostic: true}) read-outs into the
+        given device buffers (g4_gemma_forward_diag)."""
+        ids = np.ascontiguousarray(ids, dtype=np.int32)
+        check(lib().g4_gemma_forward_diag(self.h, ids.ctypes.data, ids.size, start_pos,
+                                          _f(last_hidden), _f(top_hidden), _f(top_ple),
+                                          _f(layer_hidden), stage_layer, _f(stages)))
+
+    def diag_stages(self, layer, rows):
+        """Float offsets of layer's G4_STAGE_* buffers at `rows` rows."""
+        off = (_sz * (STAGES + 1))()
+        check(lib().g4_gemma_diag_stages(self.h, layer, rows, off))
+        return list(off)
 
     def logits(self, last_hidden, out):
         check(lib().g4_gemma_logits(self.h, _f(last_hidden), _f(out)))

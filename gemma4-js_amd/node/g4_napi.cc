@@ -1306,6 +1306,50 @@ napi_value Engine_forward(napi_env env, napi_callback_info info) {
   return undefined(env);
 }
 
+// e.forwardDiag(ids, startPos, lastHidden?, topHidden?, topPle?, layerHidden?,
+//               stageLayer, stages?)   the buffers DeviceBuffers or null
+napi_value Engine_forwardDiag(napi_env env, napi_callback_info info) {
+  napi_value a[8], self;
+  if (!get_args(env, info, 8, a, &self)) return nullptr;
+  Engine *e = unwrap_engine(env, self);
+  std::vector<int32_t> ids;
+  int64_t start, stage_layer;
+  void *last, *top, *ple, *layers, *stages;
+  if (!e || !id_list(env, a[0], &ids) || !to_i64(env, a[1], &start, "startPos") ||
+      !dev_or_null(env, a[2], "lastHidden", &last) || !dev_or_null(env, a[3], "topHidden", &top) ||
+      !dev_or_null(env, a[4], "topPle", &ple) || !dev_or_null(env, a[5], "layerHidden", &layers) ||
+      !to_i64(env, a[6], &stage_layer, "stageLayer") || !dev_or_null(env, a[7], "stages", &stages))
+    return nullptr;
+  if (ids.empty()) {
+    napi_throw_range_error(env, nullptr, "forward needs at least one token id");
+    return nullptr;
+  }
+  G4_CALL(env, g4_gemma_forward_diag(e->h, ids.data(), (int)ids.size(), (int)start,
+                                     static_cast<float *>(last), static_cast<float *>(top),
+                                     static_cast<float *>(ple), static_cast<float *>(layers),
+                                     (int)stage_layer, static_cast<float *>(stages)));
+  return undefined(env);
+}
+
+// e.diagStages(layer, rows) -> [offsets] (G4_STAGES + 1 float offsets)
+napi_value Engine_diagStages(napi_env env, napi_callback_info info) {
+  napi_value a[2], self, arr;
+  if (!get_args(env, info, 2, a, &self)) return nullptr;
+  Engine *e = unwrap_engine(env, self);
+  int64_t layer, rows;
+  if (!e || !to_i64(env, a[0], &layer, "layer") || !to_i64(env, a[1], &rows, "rows"))
+    return nullptr;
+  size_t off[G4_STAGES + 1];
+  G4_CALL(env, g4_gemma_diag_stages(e->h, (int)layer, (int)rows, off));
+  napi_create_array_with_length(env, G4_STAGES + 1, &arr);
+  for (int i = 0; i <= G4_STAGES; ++i) {
+    napi_value v;
+    napi_create_double(env, (double)off[i], &v);
+    napi_set_element(env, arr, i, v);
+  }
+  return arr;
+}
+
 // e.logits(lastHidden, logits)   both DeviceBuffers
 napi_value Engine_logits(napi_env env, napi_callback_info info) {
   napi_value a[2], self;
@@ -1411,7 +1455,8 @@ napi_value Init(napi_env env, napi_value exports) {
       METHOD("setLayerScalar", Engine_setLayerScalar), METHOD("setEmbedding", Engine_setEmbedding),
       METHOD("setPle", Engine_setPle), METHOD("setPleDense", Engine_setPleDense),
       METHOD("reset", Engine_reset), METHOD("cacheLength", Engine_cacheLength),
-      METHOD("forward", Engine_forward), METHOD("logits", Engine_logits),
+      METHOD("forward", Engine_forward), METHOD("forwardDiag", Engine_forwardDiag),
+      METHOD("diagStages", Engine_diagStages), METHOD("logits", Engine_logits),
       METHOD("greedy", Engine_greedy), METHOD("decode", Engine_decode),
       METHOD("dispose", Engine_dispose)};
   if (!define_class(env, exports, "GemmaEngine", Engine_new, engine_props,

@@ -16,6 +16,13 @@ const rt = require('./hip-runtime.js');
 
 const U = rt.GPUBufferUsage;
 
+// encodeLayer's probe names (gemma4-webgpu.js:224-309), the order of the
+// engine's diagnostic stage buffers (G4_STAGE_*)
+const STAGE_NAMES = ['preAttention', 'qRaw', 'qNormRoPE', 'kRaw', 'vRaw', 'kNormRoPE', 'vNorm',
+  'attentionContext', 'attentionOutput', 'postAttentionNorm', 'attentionResidual', 'preFfw',
+  'mlpGate', 'mlpUp', 'mlpActivated', 'ffwOutput', 'postFfwNorm', 'ffwResidual', 'pleGate',
+  'pleModulated', 'pleProjected', 'pleNormalized', 'output'];
+
 // spec(i) of gemma4-webgpu.js:65-77: every 5th layer global (head_dim 512,
 // RoPE base 1e6 on a quarter of the pairs), intermediate 12288 from layer 15,
 // layers >= 15 reuse the KV caches of layers 13 (sliding) and 14 (global).
@@ -45,6 +52,61 @@ function layerNames(i, s) {
     names.v = `${root}.self_attn.v_proj`;
   }
   return names;
+}
+
+// The diagnostic statistics of gemma4-webgpu.js:15-63: counts of finite, NaN
+// and infinite values, and min / max / mean / std of the finite ones.
+function finiteStats(a) {
+  let finite = 0, nan = 0, inf = 0, min = Infinity, max = -Infinity, sum = 0, sumSq = 0;
+  for (let i = 0; i < a.length; i++) {
+    const v = a[i];
+    if (Number.isNaN(v)) { nan++; continue; }
+    if (!Number.isFinite(v)) { inf++; continue; }
+    finite++;
+    if (v < min) min = v;
+    if (v > max) max = v;
+    sum += v;
+    sumSq += v * v;
+  }
+  const mean = finite > 0 ? sum / finite : NaN;
+  const variance = finite > 0 ? Math.max(0, sumSq / finite - mean * mean) : NaN;
+  return {
+    count: a.length, finite, nan, inf,
+    min: finite > 0 ? min : NaN, max: finite > 0 ? max : NaN,
+    mean, std: Number.isFinite(variance) ? Math.sqrt(variance) : NaN,
+  };
+}
+
+function formatStats(s) {
+  const e = (x) => Number(x).toExponential(3);
+  return `finite=${s.finite}/${s.count} nan=${s.nan} inf=${s.inf} ` +
+    `min=${e(s.min)} max=${e(s.max)} mean=${e(s.mean)} std=${e(s.std)}`;
+}
+
+// forward's diagnostic lines for the layer-1 stages and a layer's hidden
+// state (gemma4-webgpu.js:342-372, 376-389); both throw at the first
+// non-finite value, as the reference does.
+function logStages(log, probes) {
+  log('[diag layer 01 stages]');
+  for (const p of probes) {
+    const stats = finiteStats(p.values);
+    log(`  ${p.name.padEnd(20)} ${formatStats(stats)}`);
+    if (stats.nan > 0 || stats.inf > 0) throw new Error(`First non-finite Layer 1 stage: ${p.name}.`);
+  }
+}
+
+function logLayer(log, i, values) {
+  const stats = finiteStats(values);
+  log(`[diag layer ${String(i).padStart(2, '0')}] ` + formatStats(stats));
+  if (stats.nan > 0 || stats.inf > 0) {
+    throw new Error(`First non-finite hidden state detected at layer ${i}.`);
+  }
+}
+
+// logits' diagnostic lines (gemma4-webgpu.js:419-428)
+function logLogits(log, out) {
+  log(`[diag logits] ${formatStats(finiteStats(out))}`);
+  log('[diag logits first 16] ' + Array.from(out.slice(0, 16)).map((x) => Number(x).toExponential(4)).join(' '));
 }
 
 async function scaleBuffer(device, reader, name) {
@@ -158,21 +220,29 @@ class Gemma4Hip {
   }
 
   // encodeLayer (gemma4-webgpu.js:215-301): one decoder layer, every op output
-  // a fresh buffer that goes on `garbage` once consumed.
-  encodeLayer(encoder, layer, hidden, perLayer, rows, startPos, garbage) {
+  // a fresh buffer that goes on `garbage` once consumed.  With `probes` (an
+  // array) each stage's buffer is listed under the reference's probe name.
+  encodeLayer(encoder, layer, hidden, perLayer, rows, startPos, garbage, probes = null) {
     const ops = this.ops, s = layer.s, L = layer.linear, N = layer.norm, H = this.hidden;
-    const nHidden = rows * H;
+    const nHidden = rows * H, QD = rows * this.heads * s.headDim;
     const trash = (x) => { if (x) garbage.push(x); return x; };
-    const pre = ops.rms(encoder, hidden, rows, H, N.input, garbage);
+    const probe = (name, buffer, count) => {
+      if (probes) probes.push({ name, buffer, count });
+      return buffer;
+    };
+    const pre = probe('preAttention', ops.rms(encoder, hidden, rows, H, N.input, garbage), nHidden);
     const [qRaw, kRaw, vRaw] = ops.w4Multi(encoder, s.shared ? [L.q] : [L.q, L.k, L.v], pre, rows, garbage);
-    const q = ops.normRope(encoder, trash(qRaw), rows, this.heads, s.headDim, startPos, N.q, s.ropeProp, s.ropeBase, garbage);
+    probe('qRaw', qRaw, QD);
+    const q = probe('qNormRoPE', ops.normRope(encoder, trash(qRaw), rows, this.heads, s.headDim, startPos, N.q, s.ropeProp, s.ropeBase, garbage), QD);
     let cache;
     if (s.shared) {
       cache = this.shared[s.attentionType];
       if (!cache) throw new Error(`Missing shared ${s.attentionType} KV cache at layer ${layer.i}`);
     } else {
-      const k = ops.normRope(encoder, trash(kRaw), rows, 1, s.headDim, startPos, N.k, s.ropeProp, s.ropeBase, garbage);
-      const v = ops.rms(encoder, trash(vRaw), rows, s.headDim, null, garbage);
+      probe('kRaw', kRaw, rows * s.headDim);
+      probe('vRaw', vRaw, rows * s.headDim);
+      const k = probe('kNormRoPE', ops.normRope(encoder, trash(kRaw), rows, 1, s.headDim, startPos, N.k, s.ropeProp, s.ropeBase, garbage), rows * s.headDim);
+      const v = probe('vNorm', ops.rms(encoder, trash(vRaw), rows, s.headDim, null, garbage), rows * s.headDim);
       cache = this.caches[layer.i];
       cache.append(encoder, k, v, rows, startPos);
       trash(k);
@@ -180,24 +250,33 @@ class Gemma4Hip {
       if (s.storeShared) this.shared[s.attentionType] = cache;
     }
     trash(pre);
-    const context = trash(ops.attention(encoder, q, cache.k, cache.v, rows, this.heads, s.headDim, startPos + rows, startPos, !s.full, this.window, garbage));
+    const context = probe('attentionContext', trash(ops.attention(encoder, q, cache.k, cache.v, rows, this.heads, s.headDim, startPos + rows, startPos, !s.full, this.window, garbage)), QD);
     trash(q);
-    const attnNorm = trash(ops.rms(encoder, trash(ops.w4(encoder, L.o, context, rows, garbage)), rows, H, N.postAttn, garbage));
-    const attnResidual = ops.addScale(encoder, hidden, attnNorm, nHidden, 1, garbage);
+    const attnProj = probe('attentionOutput', trash(ops.w4(encoder, L.o, context, rows, garbage)), nHidden);
+    const attnNorm = probe('postAttentionNorm', trash(ops.rms(encoder, attnProj, rows, H, N.postAttn, garbage)), nHidden);
+    const attnResidual = probe('attentionResidual', ops.addScale(encoder, hidden, attnNorm, nHidden, 1, garbage), nHidden);
     trash(hidden);
-    const preFfw = trash(ops.rms(encoder, attnResidual, rows, H, N.preFfw, garbage));
+    const preFfw = probe('preFfw', trash(ops.rms(encoder, attnResidual, rows, H, N.preFfw, garbage)), nHidden);
     const [gate, up] = ops.w4Multi(encoder, [L.gate, L.up], preFfw, rows, garbage).map(trash);
-    const act = trash(ops.geluMul(encoder, gate, up, rows * s.intermediate, garbage));
-    const ffwNorm = trash(ops.rms(encoder, trash(ops.w4(encoder, L.down, act, rows, garbage)), rows, H, N.postFfw, garbage));
-    const ffwResidual = trash(ops.addScale(encoder, attnResidual, ffwNorm, nHidden, 1, garbage));
+    probe('mlpGate', gate, rows * s.intermediate);
+    probe('mlpUp', up, rows * s.intermediate);
+    const act = probe('mlpActivated', trash(ops.geluMul(encoder, gate, up, rows * s.intermediate, garbage)), rows * s.intermediate);
+    const down = probe('ffwOutput', trash(ops.w4(encoder, L.down, act, rows, garbage)), nHidden);
+    const ffwNorm = probe('postFfwNorm', trash(ops.rms(encoder, down, rows, H, N.postFfw, garbage)), nHidden);
+    const ffwResidual = probe('ffwResidual', trash(ops.addScale(encoder, attnResidual, ffwNorm, nHidden, 1, garbage)), nHidden);
     trash(attnResidual);
-    const pm = trash(ops.geluPle(encoder, trash(ops.w4(encoder, L.pleGate, ffwResidual, rows, garbage)), perLayer, rows, layer.i, garbage));
-    const pn = trash(ops.rms(encoder, trash(ops.w4(encoder, L.pleProj, pm, rows, garbage)), rows, H, N.postPle, garbage));
-    return ops.addScale(encoder, ffwResidual, pn, nHidden, layer.skipScale, garbage);
+    const pg = probe('pleGate', trash(ops.w4(encoder, L.pleGate, ffwResidual, rows, garbage)), rows * this.pleDim);
+    const pm = probe('pleModulated', trash(ops.geluPle(encoder, pg, perLayer, rows, layer.i, garbage)), rows * this.pleDim);
+    const pp = probe('pleProjected', trash(ops.w4(encoder, L.pleProj, pm, rows, garbage)), nHidden);
+    const pn = probe('pleNormalized', trash(ops.rms(encoder, pp, rows, H, N.postPle, garbage)), nHidden);
+    return probe('output', ops.addScale(encoder, ffwResidual, pn, nHidden, layer.skipScale, garbage), nHidden);
   }
 
-  // forward (gemma4-webgpu.js:303-402); returns the final-norm last row [hidden]
-  async forward(tokenIds, startPos) {
+  // forward (gemma4-webgpu.js:303-402); returns the final-norm last row [hidden].
+  // With {diagnostic: true} it logs the statistics of the top-level hidden
+  // and PLE rows, of every layer-1 stage and of every layer's hidden state,
+  // and throws at the first non-finite one.
+  async forward(tokenIds, startPos, { diagnostic = false } = {}) {
     if (!this.loaded) throw new Error('Model not loaded.');
     const rows = tokenIds.length, H = this.hidden, P = this.pleDim, NL = this.numLayers;
     const inp = await this.inputBuffers(tokenIds);
@@ -210,12 +289,25 @@ class Gemma4Hip {
     garbage.push(inp.embed, inp.ple, projected, projectedScaled);
     this.device.queue.submit([encoder.finish()]);
     for (const b of garbage) b.destroy();
+    if (diagnostic) {
+      this.log(`[diag top hidden] ${formatStats(finiteStats(await rt.readF32(this.device, hidden, rows * H)))}`);
+      this.log(`[diag top PLE]    ${formatStats(finiteStats(await rt.readF32(this.device, perLayer, rows * NL * P)))}`);
+    }
     for (const layer of this.layers) {
       encoder = this.device.createCommandEncoder();
       garbage = [];
-      hidden = this.encodeLayer(encoder, layer, hidden, perLayer, rows, startPos, garbage);
+      const stageProbes = diagnostic && layer.i === 1 ? [] : null;
+      hidden = this.encodeLayer(encoder, layer, hidden, perLayer, rows, startPos, garbage, stageProbes);
       this.device.queue.submit([encoder.finish()]);
-      for (const b of garbage) b.destroy();
+      try {
+        if (stageProbes) {
+          for (const p of stageProbes) p.values = await rt.readF32(this.device, p.buffer, p.count);
+          logStages(this.log, stageProbes);
+        }
+      } finally {
+        for (const b of garbage) b.destroy();
+      }
+      if (diagnostic) logLayer(this.log, layer.i, await rt.readF32(this.device, hidden, rows * H));
     }
     perLayer.destroy();
     encoder = this.device.createCommandEncoder();
@@ -229,14 +321,16 @@ class Gemma4Hip {
     return last;
   }
 
-  // logits (gemma4-webgpu.js:404-431)
-  async logits(lastHidden) {
+  // logits (gemma4-webgpu.js:404-431); {diagnostic: true} logs their statistics
+  // and the first 16 values
+  async logits(lastHidden, { diagnostic = false } = {}) {
     const logits = this.ops.emptyF32(this.vocab, 'logits');
     const encoder = this.device.createCommandEncoder();
     for (const c of this.lmChunks) this.ops.headChunk(encoder, lastHidden, c.buffer, logits, c.start, c.rows, null, this.hidden);
     this.device.queue.submit([encoder.finish()]);
     const out = await rt.readF32(this.device, logits, this.vocab);
     logits.destroy();
+    if (diagnostic) logLogits(this.log, out);
     return out;
   }
 
@@ -396,23 +490,61 @@ class Gemma4HipEngine {
   check() { if (!this.loaded) throw new Error('Model not loaded.'); }
 
   // forward (gemma4-webgpu.js:303-402): the final-norm last row [hidden] in a
-  // new device buffer the caller destroys.
-  async forward(tokenIds, startPos) {
+  // new device buffer the caller destroys.  {diagnostic: true} runs the
+  // engine's diagnostic forward (the op-by-op path, every stage kept) and logs
+  // the reference's lines: the top-level hidden and PLE rows, the layer-1
+  // stages, every layer's hidden state; it throws at the first non-finite one.
+  async forward(tokenIds, startPos, { diagnostic = false } = {}) {
     this.check();
     const last = rt.createBuffer(this.device, this.hidden * 4, U.STORAGE | U.COPY_SRC, 'last-hidden');
+    if (!diagnostic) {
+      try {
+        this.engine.forward(Int32Array.from(tokenIds), startPos, last);
+      } catch (e) { last.destroy(); throw e; }
+      return last;
+    }
+    const rows = tokenIds.length, H = this.hidden, NL = this.numLayers, P = this.pleDim;
+    const mk = (n, label) => rt.createBuffer(this.device, n * 4, U.STORAGE | U.COPY_SRC, label);
+    const stageLayer = NL > 1 ? 1 : -1;
+    const off = stageLayer >= 0 ? this.engine.diagStages(stageLayer, rows) : null;
+    const top = mk(rows * H, 'diag-top-hidden'), ple = mk(rows * NL * P, 'diag-top-ple');
+    const layers = mk(NL * rows * H, 'diag-layers');
+    const stages = off ? mk(off[off.length - 1], 'diag-stages') : null;
     try {
-      this.engine.forward(Int32Array.from(tokenIds), startPos, last);
-    } catch (e) { last.destroy(); throw e; }
+      this.engine.forwardDiag(Int32Array.from(tokenIds), startPos, last, top, ple, layers, stageLayer, stages);
+      this.log(`[diag top hidden] ${formatStats(finiteStats(await rt.readF32(this.device, top, rows * H)))}`);
+      this.log(`[diag top PLE]    ${formatStats(finiteStats(await rt.readF32(this.device, ple, rows * NL * P)))}`);
+      const all = await rt.readF32(this.device, layers, NL * rows * H);
+      const st = stages ? await rt.readF32(this.device, stages, off[off.length - 1]) : null;
+      for (let i = 0; i < NL; i++) {
+        if (i === stageLayer) {
+          const probes = [];
+          for (let k = 0; k < STAGE_NAMES.length; k++) {
+            if (off[k + 1] > off[k]) probes.push({ name: STAGE_NAMES[k], values: st.subarray(off[k], off[k + 1]) });
+          }
+          logStages(this.log, probes);
+        }
+        logLayer(this.log, i, all.subarray(i * rows * H, (i + 1) * rows * H));
+      }
+    } catch (e) {
+      last.destroy();
+      throw e;
+    } finally {
+      for (const b of [top, ple, layers, stages]) if (b) b.destroy();
+    }
     return last;
   }
 
-  // logits (gemma4-webgpu.js:404-431)
-  async logits(lastHidden) {
+  // logits (gemma4-webgpu.js:404-431); {diagnostic: true} logs their statistics
+  // and the first 16 values
+  async logits(lastHidden, { diagnostic = false } = {}) {
     this.check();
     const buf = rt.createBuffer(this.device, this.vocab * 4, U.STORAGE | U.COPY_SRC, 'logits');
     try {
       this.engine.logits(lastHidden, buf);
-      return await rt.readF32(this.device, buf, this.vocab);
+      const out = await rt.readF32(this.device, buf, this.vocab);
+      if (diagnostic) logLogits(this.log, out);
+      return out;
     } finally { buf.destroy(); }
   }
 
@@ -467,4 +599,6 @@ function withPleBundle(reader, bundle) {
   return r;
 }
 
-module.exports = { Gemma4Hip, Gemma4HipEngine, KVCache, e2bSpec, withPleBundle };
+module.exports = {
+  Gemma4Hip, Gemma4HipEngine, KVCache, e2bSpec, withPleBundle, finiteStats, formatStats, STAGE_NAMES,
+};

@@ -452,6 +452,49 @@ int g4_gemma_cache_length(const g4_gemma *m, int *len);
 int g4_gemma_forward(g4_gemma *m, const int32_t *ids, int n, int start_pos,
                      float *last_hidden);
 
+/* forward(tokenIds, startPos, {diagnostic: true}) (gemma4-webgpu.js:311-397):
+ * g4_gemma_forward, taking the op-by-op path whatever the row count, and in
+ * addition, into device buffers (each optional, NULL to skip):
+ *   top_hidden   [n, hidden]               the scaled embedding rows
+ *   top_ple      [n, layers * ple_dim]     the per-layer inputs (pleMix)
+ *   layer_hidden [layers, n, hidden]       each layer's output rows
+ *   stages       the G4_STAGE_* buffers of encodeLayer (224-309) for layer
+ *                stage_layer, at the float offsets g4_gemma_diag_stages gives
+ * The reference probes layer 1's stages (its diagnostic loop, 342-372). */
+#define G4_STAGE_PRE_ATTENTION 0
+#define G4_STAGE_Q_RAW 1
+#define G4_STAGE_Q_NORM_ROPE 2
+#define G4_STAGE_K_RAW 3
+#define G4_STAGE_V_RAW 4
+#define G4_STAGE_K_NORM_ROPE 5
+#define G4_STAGE_V_NORM 6
+#define G4_STAGE_ATTENTION_CONTEXT 7
+#define G4_STAGE_ATTENTION_OUTPUT 8
+#define G4_STAGE_POST_ATTENTION_NORM 9
+#define G4_STAGE_ATTENTION_RESIDUAL 10
+#define G4_STAGE_PRE_FFW 11
+#define G4_STAGE_MLP_GATE 12
+#define G4_STAGE_MLP_UP 13
+#define G4_STAGE_MLP_ACTIVATED 14
+#define G4_STAGE_FFW_OUTPUT 15
+#define G4_STAGE_POST_FFW_NORM 16
+#define G4_STAGE_FFW_RESIDUAL 17
+#define G4_STAGE_PLE_GATE 18
+#define G4_STAGE_PLE_MODULATED 19
+#define G4_STAGE_PLE_PROJECTED 20
+#define G4_STAGE_PLE_NORMALIZED 21
+#define G4_STAGE_OUTPUT 22
+#define G4_STAGES 23
+int g4_gemma_forward_diag(g4_gemma *m, const int32_t *ids, int n, int start_pos,
+                          float *last_hidden, float *top_hidden, float *top_ple,
+                          float *layer_hidden, int stage_layer, float *stages);
+
+/* Float offsets of layer `layer`'s G4_STAGE_* buffers at n rows in a stage
+ * buffer: offsets[s] .. offsets[s + 1] (G4_STAGES + 1 entries; the reference's
+ * probe counts, gemma4-webgpu.js:224-309; the k/v stages of a layer without
+ * its own KV are empty). */
+int g4_gemma_diag_stages(const g4_gemma *m, int layer, int n, size_t *offsets);
+
 /* logits(lastHidden) (gemma4-webgpu.js:404-431) into device [vocab]. */
 int g4_gemma_logits(g4_gemma *m, const float *last_hidden, float *logits);
 

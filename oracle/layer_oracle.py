@@ -173,7 +173,11 @@ class Model:
         packed, scales = lin
         return g4oracle.w4_linear_f64(np.asarray(x, np.float32), packed, scales)
 
-    def forward(self, ids, start_pos):
+    def forward(self, ids, start_pos, probes=None, probe_layer=1):
+        """forward; with a dict `probes`, also the diagnostic read-outs of
+        forward(..., {diagnostic: true}) (gemma4-webgpu.js:311-397): "top
+        hidden", "top PLE", "layer i" (each layer's output) and, for layer
+        probe_layer, every encodeLayer stage under its probe name (224-309)."""
         ids = np.asarray(ids)
         rows, H, P, NL = len(ids), self.hidden, self.ple_dim, len(self.layers)
         if start_pos != self.length:
@@ -183,31 +187,48 @@ class Model:
         projs = scale(proj, np.float32(1.0 / np.sqrt(H)))
         tokple = self.ple_rows(ids)
         perlayer = ple_mix(projs, self.ple_norm, tokple, rows, P, NL)
+        if probes is not None:
+            probes["top hidden"], probes["top PLE"] = hidden, perlayer
         for i, L in enumerate(self.layers):
+            st = {}  # this layer's stages
             hd, heads = L["head_dim"], self.heads
             angles = int(np.floor(np.float32(L["rope_prop"]) * hd / 2))
-            pre = rms(hidden, H, L["norm"]["input"], self.eps)
-            q = norm_rope(self._w4(L["linear"]["q"], pre), rows, heads, hd, start_pos,
-                          L["norm"]["q"], angles, L["rope_base"], self.eps)
+            pre = st["preAttention"] = rms(hidden, H, L["norm"]["input"], self.eps)
+            st["qRaw"] = self._w4(L["linear"]["q"], pre)
+            q = st["qNormRoPE"] = norm_rope(st["qRaw"], rows, heads, hd, start_pos,
+                                            L["norm"]["q"], angles, L["rope_base"], self.eps)
             src = i if L["kv_source"] < 0 else L["kv_source"]
             if L["kv_source"] < 0:
-                k = norm_rope(self._w4(L["linear"]["k"], pre), rows, 1, hd, start_pos,
-                              L["norm"]["k"], angles, L["rope_base"], self.eps)
-                v = rms(self._w4(L["linear"]["v"], pre), hd, None, self.eps)
+                st["kRaw"] = self._w4(L["linear"]["k"], pre)
+                st["vRaw"] = self._w4(L["linear"]["v"], pre)
+                k = st["kNormRoPE"] = norm_rope(st["kRaw"], rows, 1, hd, start_pos,
+                                                L["norm"]["k"], angles, L["rope_base"], self.eps)
+                v = st["vNorm"] = rms(st["vRaw"], hd, None, self.eps)
                 self.k[i] = np.concatenate([self.k.get(i, np.zeros((0, hd), np.float32)), k])
                 self.v[i] = np.concatenate([self.v.get(i, np.zeros((0, hd), np.float32)), v])
             keylen = start_pos + rows
-            ctx = attention(q, self.k[src], self.v[src], rows, heads, hd, keylen, start_pos,
-                            not L["full"], self.window)
-            an = rms(self._w4(L["linear"]["o"], ctx), H, L["norm"]["post_attn"], self.eps)
-            ares = add_scale(hidden, an, 1.0)
-            pf = rms(ares, H, L["norm"]["pre_ffw"], self.eps)
-            act = gelu_mul(self._w4(L["linear"]["gate"], pf), self._w4(L["linear"]["up"], pf))
-            fn = rms(self._w4(L["linear"]["down"], act), H, L["norm"]["post_ffw"], self.eps)
-            fres = add_scale(ares, fn, 1.0)
-            pm = gelu_ple(self._w4(L["linear"]["ple_gate"], fres), perlayer, rows, i, P, NL)
-            pn = rms(self._w4(L["linear"]["ple_proj"], pm), H, L["norm"]["post_ple"], self.eps)
-            hidden = add_scale(fres, pn, L["skip"])
+            ctx = st["attentionContext"] = attention(q, self.k[src], self.v[src], rows, heads, hd,
+                                                     keylen, start_pos, not L["full"], self.window)
+            st["attentionOutput"] = self._w4(L["linear"]["o"], ctx)
+            an = st["postAttentionNorm"] = rms(st["attentionOutput"], H, L["norm"]["post_attn"],
+                                               self.eps)
+            ares = st["attentionResidual"] = add_scale(hidden, an, 1.0)
+            pf = st["preFfw"] = rms(ares, H, L["norm"]["pre_ffw"], self.eps)
+            st["mlpGate"] = self._w4(L["linear"]["gate"], pf)
+            st["mlpUp"] = self._w4(L["linear"]["up"], pf)
+            act = st["mlpActivated"] = gelu_mul(st["mlpGate"], st["mlpUp"])
+            st["ffwOutput"] = self._w4(L["linear"]["down"], act)
+            fn = st["postFfwNorm"] = rms(st["ffwOutput"], H, L["norm"]["post_ffw"], self.eps)
+            fres = st["ffwResidual"] = add_scale(ares, fn, 1.0)
+            st["pleGate"] = self._w4(L["linear"]["ple_gate"], fres)
+            pm = st["pleModulated"] = gelu_ple(st["pleGate"], perlayer, rows, i, P, NL)
+            st["pleProjected"] = self._w4(L["linear"]["ple_proj"], pm)
+            pn = st["pleNormalized"] = rms(st["pleProjected"], H, L["norm"]["post_ple"], self.eps)
+            hidden = st["output"] = add_scale(fres, pn, L["skip"])
+            if probes is not None:
+                probes["layer %d" % i] = hidden
+                if i == probe_layer:
+                    probes["stages"] = st
         self.length += rows
         return rms(hidden[-1:], H, self.final_norm, self.eps)[0]
 

@@ -210,3 +210,47 @@ def run_against_oracle(g4, mid, prompt, max_seq, mode):
         prev, pos = t, pos + 1
     assert m.cache_length() == prompt + STEPS
     print("%s, prompt %d: worst relative L2 over %d steps %.2e" % (mode, prompt, STEPS, worst))
+
+
+def test_e2b_widths_diagnostic_read_outs_match_oracle(g4, mid):
+    # g4_gemma_forward_diag on 6 prompt rows: the top-level hidden and PLE
+    # rows, every layer's output and all 23 encodeLayer stages of layer 1
+    # (gemma4-webgpu.js:224-309, 311-397) against the oracle's read-outs,
+    # each within relative L2 1e-3; the final-norm row equals the plain
+    # forward's to 1e-5
+    ref = mid["ref"]
+    n, NL = 6, len(LAYERS)
+    ids = syn.token_ids(33, n, V)
+    ref.reset()
+    probes = {}
+    want_last = ref.forward(ids, 0, probes=probes)
+    m = mid["make"](576)
+    off = m.diag_stages(1, n)
+    assert len(off) == g4.STAGES + 1
+    top, tple = g4.Buffer(n * H * 4), g4.Buffer(n * NL * P * 4)
+    lay, st, last = g4.Buffer(NL * n * H * 4), g4.Buffer(off[-1] * 4), g4.Buffer(H * 4)
+    m.forward_diag(ids, 0, last, top, tple, lay, 1, st)
+    assert m.cache_length() == n
+    assert rel(top.download(np.float32), probes["top hidden"]) < 1e-5
+    assert rel(tple.download(np.float32), probes["top PLE"]) < 1e-3
+    layers = lay.download(np.float32).reshape(NL, n, H)
+    for i in range(NL):
+        assert rel(layers[i], probes["layer %d" % i]) < 1e-3, i
+    stages = st.download(np.float32)
+    for k, name in enumerate(g4.STAGE_NAMES):
+        assert off[k + 1] - off[k] == np.asarray(probes["stages"][name]).size, name
+        got = stages[off[k]:off[k + 1]]
+        assert rel(got, probes["stages"][name]) < 1e-3, name
+    assert rel(last.download(np.float32), want_last) < 1e-3
+    m2 = mid["make"](576)
+    last2 = g4.Buffer(H * 4)
+    m2.forward(ids, 0, last2)
+    assert rel(last.download(np.float32), last2.download(np.float32)) < 1e-5
+    # a layer without its own KV has empty k/v stages
+    off3 = m.diag_stages(2, n)
+    for k in range(3, 7):
+        assert off3[k + 1] == off3[k]
+    with pytest.raises(g4.G4Error):
+        m.forward_diag(ids, n, None, None, None, None, NL, st)  # stage layer out of range
+    m.free()
+    m2.free()

@@ -247,6 +247,77 @@ def test_js_model_driver_matches_oracle(tmp_path, oracle, driver):
         assert res["decoded"] == toks[1:]
 
 
+def _stats_of(line):
+    """The numbers of one formatStats line (gemma4-webgpu.js:59-63)."""
+    import re
+    m = re.search(r"finite=(\d+)/(\d+) nan=(\d+) inf=(\d+) min=(\S+) max=(\S+) mean=(\S+) "
+                  r"std=(\S+)$", line)
+    assert m, line
+    f, c, nan, inf = (int(m.group(i)) for i in range(1, 5))
+    return dict(finite=f, count=c, nan=nan, inf=inf, min=float(m.group(5)),
+                max=float(m.group(6)), mean=float(m.group(7)), std=float(m.group(8)))
+
+
+def _assert_stats(line, values, what):
+    got = _stats_of(line)
+    a = np.asarray(values, np.float64).ravel()
+    assert got["count"] == a.size and got["finite"] == a.size, (what, line)
+    assert got["nan"] == 0 and got["inf"] == 0, (what, line)
+    want = dict(min=a.min(), max=a.max(), mean=a.mean(), std=a.std())
+    for k, v in want.items():
+        # 4 significant digits printed; FP32 against binary64 underneath
+        tol = 2e-3 * max(abs(v), want["std"], 1e-30)
+        assert abs(got[k] - v) <= tol, (what, k, got[k], v)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("driver", ["ops", "engine"])
+def test_js_diagnostic_lines_match_oracle(tmp_path, oracle, driver):
+    """forward(prompt, 0, {diagnostic: true}) and logits(h, {diagnostic: true})
+    (gemma4-webgpu.js:311-440) log the reference's lines in its order: top
+    hidden, top PLE, then per layer its hidden state, with layer 1's 23
+    encodeLayer stages before it, then the logits and their first 16 values.
+    Every statistic is checked against the same read-out of the oracle model.
+    A NaN planted in layer 1's post-attention norm weight must stop the
+    forward at that stage, with the reference's message."""
+    cfg, ref = small_checkpoint(tmp_path)
+    ckpt, cfgp = str(tmp_path / "core.safetensors"), str(tmp_path / "cfg.json")
+    res = run_node("diag_parity.js", ckpt, cfgp, driver, timeout=300)
+    assert res["error"] is None, res["error"]
+    probes = {}
+    last = ref.forward(cfg["prompt"], 0, probes=probes)
+    lines = res["lines"]
+    NL = len(cfg["specs"])
+    assert lines[0].startswith("[diag top hidden] ")
+    _assert_stats(lines[0], probes["top hidden"], "top hidden")
+    assert lines[1].startswith("[diag top PLE]    ")
+    _assert_stats(lines[1], probes["top PLE"], "top PLE")
+    i = 2
+    for layer in range(NL):
+        if layer == 1:
+            assert lines[i] == "[diag layer 01 stages]"
+            i += 1
+            names = list(probes["stages"])
+            assert len(names) == 23
+            for name in names:
+                assert lines[i].startswith("  " + name.ljust(20) + " "), (lines[i], name)
+                _assert_stats(lines[i], probes["stages"][name], name)
+                i += 1
+        assert lines[i].startswith("[diag layer %02d] " % layer)
+        _assert_stats(lines[i], probes["layer %d" % layer], "layer %d" % layer)
+        i += 1
+    lg = ref.logits(last)
+    assert lines[i].startswith("[diag logits] ")
+    _assert_stats(lines[i], lg, "logits")
+    first = [float(v) for v in lines[i + 1][len("[diag logits first 16] "):].split()]
+    assert len(first) == 16 and np.allclose(first, lg[:16], rtol=1e-3, atol=1e-4 * np.abs(lg).max())
+    assert len(lines) == i + 2
+    bad = run_node("diag_parity.js", ckpt, cfgp, driver,
+                   "model.language_model.layers.1.post_attention_layernorm.weight", timeout=300)
+    assert bad["error"] == "First non-finite Layer 1 stage: postAttentionNorm."
+    assert bad["lines"][-1].startswith("  postAttentionNorm    ") and "nan=0 " not in bad["lines"][-1]
+
+
 def reference_decode(tj, ids, skip_special):
     """standalone-tokenizer.js decode on a Gemma-layout tokenizer.json: ids to
     token texts (special added tokens dropped when skip_special), "▁" to
