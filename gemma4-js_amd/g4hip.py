@@ -454,18 +454,24 @@ def fill_random(buf, count, kind, seed, sigma=1.0):
     check(lib().g4_fill_random(_f(buf), count, kind, seed, sigma))
 
 
-def w4_random(n, k, seed, scale_sigma=0.02):
+def w4_random(n, k, seed, scale_sigma=0.02, keep_host=False):
     """A W4Linear of random weights generated on the device (q uniform in
-    [-7, 7], scales bf16 |N(0,1)| * sigma)."""
+    [-7, 7], scales bf16 |N(0,1)| * sigma).  keep_host: also return the
+    generated bytes, (packed uint32 [n, k/8], scales uint16 [n, k/32])."""
     packed = Buffer(n * k // 2)
     scales = Buffer(n * (k // 32) * 2)
     fill_random(packed, n * k // 8, RAND_W4_PACKED, seed)
     fill_random(scales, n * (k // 32), RAND_BF16_ABS_NORMAL, seed ^ 0x5CA1E, scale_sigma)
     h = _vp()
     check(lib().g4_w4_load_dev(packed.ptr, scales.ptr, n, k, 32, ctypes.byref(h)))
+    host = None
+    if keep_host:
+        host = (packed.download(np.uint32).reshape(n, k // 8),
+                scales.download(np.uint16).reshape(n, k // 32))
     packed.free()
     scales.free()
-    return W4Linear._from_handle(h.value, n, k)
+    lin = W4Linear._from_handle(h.value, n, k)
+    return (lin, host) if keep_host else lin
 
 
 def e2b_config(max_seq):

@@ -375,3 +375,53 @@ def test_e2b_config4_prompt512_then_256_graph_steps(g4, e2b_1024):
         assert rel(eager, glog[s]) < (2e-3 if s < 8 else 1e-2), (s, rel(eager, glog[s]))
         tol = max(1e-3, 2 * float(np.max(np.abs(eager - glog[s]))))
         assert tok == graph[s] or near_tie(eager, graph[s], tol), (s, tok, graph[s])
+
+
+@pytest.fixture(scope="module")
+def e2b_host(g4):
+    import e2b
+    cfg = g4.e2b_config(64)
+    host = {}
+    m = e2b.build(cfg, seed=7, host=host)
+    yield m, cfg, host
+    m.free()
+
+
+def test_e2b_full_size_matches_oracle(g4, oracle, e2b_host):
+    # Config 4's model at its full size - 35 layers, hidden 1536, head dims
+    # 256/512, MLP 6144/12288, vocabulary 262144 with the tied BF16 head, W4
+    # projections and the W4 PLE table - against the oracle model on host
+    # copies of the same bytes (binary64 products, gemma4-webgpu.js:215-481):
+    # a 6-token prompt (the prefill GEMM path), then 3 steps of the recorded
+    # decode graph.  Final-norm hidden state and logits within relative L2
+    # 1e-3 at every position, each chosen token the oracle's top-1 unless its
+    # top two are within 1e-3.  (A short prompt: over hundreds of keys this
+    # random-init model's unscaled attention logits amplify rounding, see the
+    # config-4 test above.)
+    m, cfg, host = e2b_host
+    V, H, NL, P = cfg.vocab, cfg.hidden, cfg.layers, cfg.ple_dim
+    table = host["table"]
+    ref = lo.Model(H, cfg.heads, P, V, host["layers"], host["E"],
+                   lambda ids: oracle.ple_gather(table, V, NL * P, 4096, ids),
+                   host["top"], host["ple_norm"], host["final_norm"], window=cfg.window)
+    ids = syn.token_ids(8, 6, V)
+    hb, lg = g4.Buffer(H * 4), g4.Buffer(V * 4)
+    m.reset()
+    tok = m.greedy(ids, 0, lg)
+    m.last_hidden(hb)
+    want_h = ref.forward(ids, 0)
+    want_lg = ref.logits(want_h)
+    assert rel(hb.download(np.float32), want_h) < 1e-3
+    assert rel(lg.download(np.float32), want_lg) < 1e-3
+    assert tok == int(np.argmax(want_lg)) or near_tie(want_lg, tok)
+    prev, pos = tok, len(ids)
+    for s in range(3):
+        t = int(m.decode(1)[0])
+        m.last_hidden(hb)
+        m.logits(hb, lg)
+        want_h = ref.forward([prev], pos)
+        want_lg = ref.logits(want_h)
+        eh, el = rel(hb.download(np.float32), want_h), rel(lg.download(np.float32), want_lg)
+        assert eh < 1e-3 and el < 1e-3, (s, eh, el)
+        assert t == int(np.argmax(want_lg)) or near_tie(want_lg, t), (s, t)
+        prev, pos = t, pos + 1
