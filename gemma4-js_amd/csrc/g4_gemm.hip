@@ -606,9 +606,10 @@ __global__ __launch_bounds__(kThreads, 2) void w4_gemm_kernel(
 //   x'      64 consecutive rows of one chunk per wave instruction;
 //   weights per wave, the stage's 576-byte blocks of its TNW tiles from the
 //           weight's stage-major tile copy (g4_w4::tiles): 512 bytes of
-//           words (row r, group 2 st + h at 32 r + 16 h) and the 16 rows'
-//           scale pairs, 16 bytes per lane, so words and scales of 3 tiles
-//           take 2 load instructions.
+//           words, in the order the lanes read them (lane l's two words at
+//           8 l, so the 64 lanes' 8-byte reads hit every bank once), and the
+//           16 rows' scale pairs, 16 bytes per lane, so words and scales of
+//           3 tiles take 2 load instructions.
 // From the row-major arrays each word or scale load instruction touched 32-48
 // cache lines, and those loads, not the MFMAs, held the main loop (M 2048 N
 // 6144 K 1536: 51.1 -> 44.5 us with the same addresses made contiguous).
@@ -771,7 +772,7 @@ __global__ __launch_bounds__(kThreads, MINB) void w4_gemm_rb_kernel(
     const char *wb = reinterpret_cast<const char *>(&L.w[wave][0]);
 #pragma unroll
     for (int jj = 0; jj < TNW; ++jj) {
-      wds[jj] = *reinterpret_cast<const u32x2 *>(wb + jj * TU * 16 + 32 * lr + 8 * lq);
+      wds[jj] = *reinterpret_cast<const u32x2 *>(wb + jj * TU * 16 + 8 * lane);
       sp[jj] = *reinterpret_cast<const uint32_t *>(wb + jj * TU * 16 + 512 + 4 * lr);
     }
     f16x8 a0[NX][TMW], a1[NX][TMW];

@@ -134,10 +134,10 @@ struct g4_w4 {
   // The same words and scales by GEMM stage (two groups) and 16-row tile, for
   // the packed-weight GEMM (even G only, else null).  Stage st of tile t
   // (T = ceil(N / 16) tiles; rows past N repeat row N - 1) is a 576-byte
-  // block at tiles + (st * T + t) * 36 (in 16-byte units): the words of
-  // rows r = 0..15, groups 2 st and 2 st + 1, at r * 2 + h, then the bf16
-  // scale pairs of the 16 rows as 16 u32 (units 32..35).  A stage of
-  // consecutive tiles is contiguous.
+  // block at tiles + (st * T + t) * 36 (in 16-byte units): 64 word pairs of
+  // 8 bytes, pair c + 16 q holding words 2 q and 2 q + 1 of the stage's 8 words
+  // of row c (group 2 st + q / 2), then the bf16 scale pairs of the 16 rows as
+  // 16 u32 (units 32..35).  A stage of consecutive tiles is contiguous.
   uint4 *tiles;
   int shift;         // min_o rshift[o]: one shift for the whole tensor ...
   bool row_shift;    // ... unless the rows' maxima spread beyond 2^12: then per row

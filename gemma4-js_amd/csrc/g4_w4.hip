@@ -899,7 +899,12 @@ __global__ __launch_bounds__(256) void tile_weight_kernel(const uint4 *__restric
     return o < (size_t)N ? o : (size_t)N - 1;
   };
   if (e < 32) {
-    tw[i] = packed[row(e >> 1) * G + 2 * st + (e & 1)];
+    // unit e: the 8-byte word pairs (2 q, 2 q + 1) of rows c and c + 1, q = e / 8,
+    // c = 2 (e % 8); both pairs come from group 2 st + q / 2
+    const int q = e >> 3, c = 2 * (e & 7);
+    const uint4 a = packed[row(c) * G + 2 * st + (q >> 1)];
+    const uint4 b = packed[row(c + 1) * G + 2 * st + (q >> 1)];
+    tw[i] = (q & 1) ? make_uint4(a.z, a.w, b.z, b.w) : make_uint4(a.x, a.y, b.x, b.y);
   } else {
     const int r0 = 4 * (e - 32);
     tw[i] = make_uint4(spairs[row(r0) * S2 + st], spairs[row(r0 + 1) * S2 + st],
