@@ -110,6 +110,59 @@ def bench_gemv(n, k, steps, warmup, seed=0, copies=None):
             "gbs": per * launches / (ms * 1e-3) / 1e9}
 
 
+def bench_gemv_stamps(n=6144, k=1536, seed=0, replays=3):
+    """Where the time of one headline GEMV goes, from inside the launch: the
+    same cold rotation as bench_gemv, recorded with g4_w4_gemv_stamps (the
+    row-split kernel writing 5 real-time clock stamps per wave: start, x
+    staged, staging barrier passed, weights landed, store issued; the stamp
+    after the weights waits for all of them).  Medians over the launches of
+    the last replay, in us; times of one launch are taken from the launch's
+    first wave start (t0 min over waves), the gap from the previous launch's
+    last store issue."""
+    packed, scales, _ = syn.w4_weights(seed, n, k)
+    per = w4_bytes(n, k)
+    copies = min(128, max(2, int(math.ceil(COLD_BYTES / per))))
+    lins = [g4hip.W4Linear(packed, scales, gemm_tiles=False) for _ in range(copies)]
+    order = [lins[i % copies] for i in range(max(copies, 120))]
+    x_bits, _ = syn.activations(seed, 1, k)
+    x = g4hip.Buffer.from_array(x_bits)
+    y = g4hip.Buffer(n * 4)
+    waves = lins[0].stamp_waves()
+    st = g4hip.Buffer(len(order) * waves * 5 * 8)
+
+    def rotation():
+        for i, lin in enumerate(order):
+            lin.gemv_stamps(x.ptr, g4hip.BF16, y.ptr, st.ptr + i * waves * 5 * 8)
+
+    cb = record(rotation)
+    time_cmdbufs([cb], max(1, replays - 1))
+    g4hip.sync()
+    ms = time_cmdbufs([cb], 1)
+    s = st.download(np.uint64).reshape(len(order), waves, 5).astype(np.int64)
+    for lin in lins:
+        lin.free()
+    tick_us = 0.01  # 100 MHz
+    base = s[:, :, 0].min(axis=1)  # first wave start per launch
+    rel = (s - base[:, None, None]) * tick_us
+    gaps = (s[1:, :, 0].min(axis=1) - s[:-1, :, 4].max(axis=1)) * tick_us
+
+    def med(a):
+        return round(float(np.median(a)), 3)
+
+    return {
+        "launches": len(order), "waves_per_launch": waves,
+        "us_per_launch_events": round(ms * 1e3 / len(order), 3),
+        "span_first_start_to_last_store": med(rel[:, :, 4].max(axis=1)),
+        "last_wave_start": med(rel[:, :, 0].max(axis=1)),
+        "x_staged_after_wave_start": med(np.median(s[:, :, 1] - s[:, :, 0], axis=1) * tick_us),
+        "barrier_passed_after_wave_start": med(np.median(s[:, :, 2] - s[:, :, 0], axis=1) * tick_us),
+        "weights_landed_after_wave_start": med(np.median(s[:, :, 3] - s[:, :, 0], axis=1) * tick_us),
+        "weights_landed_last": med(rel[:, :, 3].max(axis=1)),
+        "store_after_weights_landed": med(np.median(s[:, :, 4] - s[:, :, 3], axis=1) * tick_us),
+        "gap_to_next_launch": med(gaps),
+    }
+
+
 E2B_SLIDING_LAYER = [("q", 2048, 1536), ("k", 256, 1536), ("v", 256, 1536), ("o", 1536, 2048),
                      ("gate", 6144, 1536), ("up", 6144, 1536), ("down", 1536, 6144)]
 
@@ -579,6 +632,8 @@ def main():
             "label": "MALL-warm: 4 weight copies (21 MB) in rotation, not cold",
             "us_per_launch": w["us_per_launch"], "gbs": w["gbs"], "launches": w["launches"]}
         log("GEMV, MALL-warm (4 copies):", extra["gemv_m1_k1536_n6144_mall_warm"])
+        extra["gemv_stamps_us"] = bench_gemv_stamps(n, k)
+        log("GEMV clock stamps (us):", extra["gemv_stamps_us"])
         log("E2B sliding layer, 7 GEMVs at M=1 ...")
         extra["layer_e2b_sliding_7gemv"] = bench_layer()
         log("  ", extra["layer_e2b_sliding_7gemv"])

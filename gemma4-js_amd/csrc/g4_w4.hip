@@ -453,12 +453,21 @@ __global__ __launch_bounds__(TC ? TC : 1024) void w4_gemv1_multi_kernel(
 // split launch reads one slice of longer rows).  bx: the block's index among
 // the blocks of this weight.
 // ---------------------------------------------------------------------------
-template <int J, int W, bool F32X>
+//
+// STAMP (the clock-stamp diagnostic, g4_w4_gemv_stamps): lane 0 of every wave
+// writes 5 real-time clock values (100 MHz) to stamps[wave][0..4]: the wave's
+// start, x staged, the staging barrier passed, every weight load landed (a
+// full wait inserted there, so group j's arithmetic no longer overlaps the
+// later groups' loads), and the store issued.
+template <int J, int W, bool F32X, bool STAMP = false>
 __device__ __forceinline__ void gemv_r16_body(const void *__restrict__ x,
                                               const uint4 *__restrict__ wq,
                                               const uint16_t *__restrict__ ws,
                                               void *__restrict__ y, int y_bf16, int N,
-                                              int gstride, unsigned bx) {
+                                              int gstride, unsigned bx,
+                                              uint64_t *__restrict__ stamps = nullptr) {
+  uint64_t st[5];
+  if (STAMP) st[0] = __builtin_amdgcn_s_memrealtime();
   constexpr int G = 16 * J, T = 64 * W, nch = 4 * G;
   constexpr int XI = (nch + T - 1) / T;  // x chunks per thread
   constexpr int JL = F32X ? J : 1;
@@ -536,7 +545,9 @@ __device__ __forceinline__ void gemv_r16_body(const void *__restrict__ x,
   // keep the weight arithmetic below the barrier: otherwise the compiler may
   // hoist the first group's unpacking above it, and the barrier waits for HBM
   __builtin_amdgcn_sched_barrier(0);
+  if (STAMP) st[1] = __builtin_amdgcn_s_memrealtime();
   __syncthreads();
+  if (STAMP) st[2] = __builtin_amdgcn_s_memrealtime();
 
   // 4. the lane's x groups into registers, all reads issued before any weight use
   uint4 xh[J][4], xl[JL][4];
@@ -552,6 +563,11 @@ __device__ __forceinline__ void gemv_r16_body(const void *__restrict__ x,
     sxr[j] = sx[g];
   }
   __builtin_amdgcn_sched_barrier(0);
+  if (STAMP) {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    st[3] = __builtin_amdgcn_s_memrealtime();
+    __builtin_amdgcn_sched_barrier(0);
+  }
 
   // 5. group partials, the row sum over 16 lanes, the store
   uint32_t mask = 0x000F000Fu;
@@ -590,6 +606,23 @@ __device__ __forceinline__ void gemv_r16_body(const void *__restrict__ x,
       __hip_atomic_store(static_cast<float *>(y) + row, v, __ATOMIC_RELAXED,
                          __HIP_MEMORY_SCOPE_SYSTEM);
   }
+  if (STAMP) {
+    st[4] = __builtin_amdgcn_s_memrealtime();
+    if ((t & 63) == 0) {
+      uint64_t *o = stamps + ((size_t)bx * W + (t >> 6)) * 5;
+#pragma unroll
+      for (int k = 0; k < 5; ++k) o[k] = st[k];
+    }
+  }
+}
+
+// The row split with clock stamps (BF16 or FP32 x, one weight); stamps:
+// [blocks * W waves][5].
+template <int J, int W, bool F32X>
+__global__ __launch_bounds__(64 * W) void w4_gemv_r16_stamp_kernel(
+    const void *__restrict__ x, const uint4 *__restrict__ wq, const uint16_t *__restrict__ ws,
+    void *__restrict__ y, int y_bf16, int N, uint64_t *__restrict__ stamps) {
+  gemv_r16_body<J, W, F32X, true>(x, wq, ws, y, y_bf16, N, 16 * J, blockIdx.x, stamps);
 }
 
 // SPLIT: slice blockIdx.y of the input dimension (16 J groups of rows
@@ -1157,6 +1190,57 @@ G4_API int g4_w4_linear_multi(const g4_w4 *const *w, int n, const void *x, int x
   }
   rc = f32x ? launch_gemv1_multi<true>(w, n, x, y, y_dtype == G4_BF16)
             : launch_gemv1_multi<false>(w, n, x, y, y_dtype == G4_BF16);
+  return rc ? rc : ok();
+}
+
+namespace g4 {
+namespace {
+
+template <int J, int W, bool F32X>
+int launch_r16_stamps(const g4_w4 *w, const void *x, void *y, int y_bf16, uint64_t *stamps) {
+  hipLaunchKernelGGL((w4_gemv_r16_stamp_kernel<J, W, F32X>), dim3((w->N + 4 * W - 1) / (4 * W)),
+                     dim3(64 * W), 0, stream(), x, w->packed, w->scales, y, y_bf16, w->N, stamps);
+  G4_LAUNCH_CHECK("w4_gemv_r16_stamp_kernel");
+  return G4_OK;
+}
+
+}  // namespace
+}  // namespace g4
+
+G4_API int g4_w4_gemv_stamps(const g4_w4 *w, const void *x, int x_dtype, void *y, int y_dtype,
+                             uint64_t *stamps, int *waves) {
+  G4_CHECK_INIT();
+  if (!w || !waves) return fail(G4_E_ARG, "g4_w4_gemv_stamps: null weight or wave count");
+  if (!has_r16(w->G))
+    return fail(G4_E_ARG, "g4_w4_gemv_stamps: in_dim %d does not take the row split "
+                          "(1536 or 2048)", w->K);
+  const int W = r16_waves(w->N);
+  const int nw = (w->N + 4 * W - 1) / (4 * W) * W;
+  *waves = nw;
+  if (!stamps) return ok();
+  if (x_dtype != G4_F32 && x_dtype != G4_BF16)
+    return fail(G4_E_ARG, "g4_w4_gemv_stamps: bad x dtype %d", x_dtype);
+  if (y_dtype != G4_F32 && y_dtype != G4_BF16)
+    return fail(G4_E_ARG, "g4_w4_gemv_stamps: bad y dtype %d", y_dtype);
+  if (!aligned16(x)) return fail(G4_E_ARG, "g4_w4_gemv_stamps: x must be 16-byte aligned");
+  const bool f32x = x_dtype == G4_F32;
+  int rc = check_device_range(x, (size_t)w->K * (f32x ? 4 : 2), "g4_w4_gemv_stamps x");
+  if (!rc) rc = check_device_range(y, (size_t)w->N * (y_dtype == G4_F32 ? 4 : 2),
+                                   "g4_w4_gemv_stamps y");
+  if (!rc) rc = check_device_range(stamps, (size_t)nw * 5 * sizeof(uint64_t),
+                                   "g4_w4_gemv_stamps stamps");
+  if (rc) return rc;
+  const int yb = y_dtype == G4_BF16;
+  if (w->G == 48)
+    rc = f32x ? (W == 4 ? launch_r16_stamps<3, 4, true>(w, x, y, yb, stamps)
+                        : launch_r16_stamps<3, 2, true>(w, x, y, yb, stamps))
+              : (W == 4 ? launch_r16_stamps<3, 4, false>(w, x, y, yb, stamps)
+                        : launch_r16_stamps<3, 2, false>(w, x, y, yb, stamps));
+  else
+    rc = f32x ? (W == 4 ? launch_r16_stamps<4, 4, true>(w, x, y, yb, stamps)
+                        : launch_r16_stamps<4, 2, true>(w, x, y, yb, stamps))
+              : (W == 4 ? launch_r16_stamps<4, 4, false>(w, x, y, yb, stamps)
+                        : launch_r16_stamps<4, 2, false>(w, x, y, yb, stamps));
   return rc ? rc : ok();
 }
 

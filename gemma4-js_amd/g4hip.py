@@ -53,6 +53,7 @@ SIGNATURES = {
     "g4_w4_linear": (_int, [_vp, _vp, _int, _int, _vp, _int]),
     "g4_w4_linear_multi": (_int, [_c.POINTER(_vp), _int, _vp, _int, _int, _c.POINTER(_vp), _int]),
     "g4_w4_linear_noalloc": (_int, [_vp, _vp, _int, _int, _vp, _int]),
+    "g4_w4_gemv_stamps": (_int, [_vp, _vp, _int, _vp, _int, _vp, _c.POINTER(_int)]),
     "g4_w4_dequant": (_int, [_vp, _int, _int, _vp, _int]),
     "g4_ple_create": (_int, [_int, _int, _int, _int, _c.POINTER(_vp)]),
     "g4_ple_upload_shard": (_int, [_vp, _int, _vp, _sz]),
@@ -316,6 +317,20 @@ class W4Linear:
 
     def linear(self, x_ptr, x_dtype, rows, y_ptr, y_dtype=F32):
         check(lib().g4_w4_linear(self.h, x_ptr, x_dtype, rows, y_ptr, y_dtype))
+
+    def stamp_waves(self):
+        """Waves of the row-split decode GEMV launch (g4_w4_gemv_stamps size query)."""
+        n = _c.c_int()
+        check(lib().g4_w4_gemv_stamps(self.h, None, BF16, None, F32, None, _c.byref(n)))
+        return n.value
+
+    def gemv_stamps(self, x_ptr, x_dtype, y_ptr, stamps_ptr, y_dtype=F32):
+        """g4_w4_gemv_stamps: one row through the row-split GEMV, 5 clock stamps
+        per wave into stamps_ptr (device, stamp_waves() * 5 uint64)."""
+        n = _c.c_int()
+        check(lib().g4_w4_gemv_stamps(self.h, x_ptr, x_dtype, y_ptr, y_dtype, stamps_ptr,
+                                      _c.byref(n)))
+        return n.value
 
     def linear_noalloc(self, x_ptr, x_dtype, rows, y_ptr, y_dtype=F32):
         """g4_w4_linear_noalloc: the same linear on the library's static scratch."""

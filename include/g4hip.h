@@ -188,6 +188,19 @@ int g4_w4_linear_noalloc(const g4_w4 *w, const void *x, int x_dtype, int rows,
 int g4_w4_linear_multi(const g4_w4 *const *w, int n, const void *x, int x_dtype,
                        int rows, void *const *y, int y_dtype);
 
+/* No counterpart in the reference: a diagnostic of the decode GEMV.  One
+ * activation row through the row-split kernel that g4_w4_linear(rows = 1)
+ * runs for in_dim 1536 and 2048, with the same output, plus clock stamps:
+ * lane 0 of every wave writes 5 values of the 100 MHz real-time clock to
+ * stamps[wave * 5 + 0..4]: the wave's start, its x chunks staged in LDS, the
+ * staging barrier passed, all of its weight loads landed (the stamp waits
+ * for them, so group j's arithmetic no longer overlaps the later groups'
+ * loads), and its output store issued.  *waves receives the launch's wave
+ * count; with stamps null nothing is launched (a size query).  Other in_dims
+ * fail with G4_E_ARG. */
+int g4_w4_gemv_stamps(const g4_w4 *w, const void *x, int x_dtype, void *y, int y_dtype,
+                      uint64_t *stamps, int *waves);
+
 /* dequantizeOfficialW4A16Rows (official-w4a16.js:50-101) on the device:
  * out[r, k] = (nibble - 8) * scale for rows row_start..row_start+row_count-1,
  * as FP32 (exact) or as BF16 rounded to nearest even, which is

@@ -457,3 +457,39 @@ def test_weight_without_gemm_tiles(g4, rows, n, k):
         g4.check(g4.lib().g4_w4_load_opts(packed.ctypes.data, scales.ctypes.data, n, k, 32, 8,
                                           ctypes.byref(h)))
     assert e.value.code == g4.G4_E_ARG and not h.value
+
+
+@pytest.mark.parametrize("n,k,xd", [(6144, 1536, "bf16"), (2048, 1536, "f32"), (1536, 2048, "bf16")])
+def test_gemv_stamps_same_output_and_ordered_stamps(g4, n, k, xd):
+    # g4_w4_gemv_stamps runs the row-split decode GEMV with clock stamps: its
+    # output must be the plain launch's, bit for bit, and every wave's five
+    # stamps must be set and in order (start <= staged <= barrier <= weights
+    # landed <= store issued)
+    packed, scales, _ = syn.w4_weights(61, n, k, full_range=True)
+    lin = g4.W4Linear(packed, scales, gemm_tiles=False)
+    x_bits, x_f32 = syn.activations(62, 1, k)
+    dt = g4.BF16 if xd == "bf16" else g4.F32
+    xb = g4.Buffer.from_array(x_bits if xd == "bf16" else x_f32.astype(np.float32))
+    y0, y1 = g4.Buffer(n * 4), g4.Buffer(n * 4)
+    lin.linear(xb.ptr, dt, 1, y0.ptr, g4.F32)
+    waves = lin.stamp_waves()
+    assert n <= 4 * waves < n + 16  # 4 rows per wave, blocks of 2 or 4 waves
+    st = g4.Buffer(waves * 5 * 8)
+    assert lin.gemv_stamps(xb.ptr, dt, y1.ptr, st.ptr) == waves
+    g4.sync()
+    assert np.array_equal(y0.download(np.uint32), y1.download(np.uint32))
+    s = st.download(np.uint64).reshape(waves, 5).astype(np.int64)
+    assert (s > 0).all()
+    assert (np.diff(s, axis=1) >= 0).all()
+    # one launch spans microseconds, not seconds (100 MHz clock)
+    assert s[:, 4].max() - s[:, 0].min() < 100_000
+    lin.free()
+
+
+def test_gemv_stamps_refuses_other_widths(g4):
+    packed, scales, _ = syn.w4_weights(63, 256, 256)
+    lin = g4.W4Linear(packed, scales, gemm_tiles=False)
+    with pytest.raises(g4.G4Error) as e:
+        lin.stamp_waves()
+    assert "row split" in str(e.value)
+    lin.free()
