@@ -99,6 +99,19 @@ bool to_i64(napi_env env, napi_value v, int64_t *out, const char *what) {
   return true;
 }
 
+// An integer argument that the C ABI takes as int: outside the int32 range it
+// throws a RangeError instead of wrapping around in the cast.
+bool to_int(napi_env env, napi_value v, int64_t *out, const char *what) {
+  if (!to_i64(env, v, out, what)) return false;
+  if (*out < INT32_MIN || *out > INT32_MAX) {
+    char msg[128];
+    snprintf(msg, sizeof msg, "%s is out of the int range", what);
+    napi_throw_range_error(env, nullptr, msg);
+    return false;
+  }
+  return true;
+}
+
 bool to_f64(napi_env env, napi_value v, double *out, const char *what) {
   napi_valuetype t;
   napi_typeof(env, v, &t);
@@ -331,8 +344,8 @@ napi_value W4_new(napi_env env, napi_callback_info info) {
   napi_value argv[5], self;
   if (!get_args(env, info, 5, argv, &self)) return nullptr;
   int64_t out_dim, in_dim, group;
-  if (!to_i64(env, argv[2], &out_dim, "outDim") || !to_i64(env, argv[3], &in_dim, "inDim") ||
-      !to_i64(env, argv[4], &group, "groupSize"))
+  if (!to_int(env, argv[2], &out_dim, "outDim") || !to_int(env, argv[3], &in_dim, "inDim") ||
+      !to_int(env, argv[4], &group, "groupSize"))
     return nullptr;
   if (is_instance(env, argv[0], g_devbuf_ctor)) {
     void *pk, *sc;
@@ -383,8 +396,8 @@ napi_value W4_linear(napi_env env, napi_callback_info info) {
   if (!buf_at(env, argv[0], argv[5], "x", &x)) return nullptr;
   if (!buf_at(env, argv[3], argv[6], "y", &y)) return nullptr;
   int64_t xd, rows, yd;
-  if (!to_i64(env, argv[1], &xd, "xDtype") || !to_i64(env, argv[2], &rows, "rows") ||
-      !to_i64(env, argv[4], &yd, "yDtype"))
+  if (!to_int(env, argv[1], &xd, "xDtype") || !to_int(env, argv[2], &rows, "rows") ||
+      !to_int(env, argv[4], &yd, "yDtype"))
     return nullptr;
   G4_CALL(env, g4_w4_linear(w->h, x, (int)xd, (int)rows, y, (int)yd));
   return undefined(env);
@@ -424,8 +437,8 @@ napi_value F_linearMulti(napi_env env, napi_callback_info info) {
   void *x;
   if (!dev(env, argv[1], "x", &x)) return nullptr;
   int64_t xd, rows, yd;
-  if (!to_i64(env, argv[2], &xd, "xDtype") || !to_i64(env, argv[3], &rows, "rows") ||
-      !to_i64(env, argv[5], &yd, "yDtype"))
+  if (!to_int(env, argv[2], &xd, "xDtype") || !to_int(env, argv[3], &rows, "rows") ||
+      !to_int(env, argv[5], &yd, "yDtype"))
     return nullptr;
   G4_CALL(env, g4_w4_linear_multi(ws, (int)n, x, (int)xd, (int)rows, ys, (int)yd));
   return undefined(env);
@@ -438,8 +451,8 @@ napi_value W4_dequant(napi_env env, napi_callback_info info) {
   W4 *w = unwrap_w4(env, self);
   if (!w) return nullptr;
   int64_t r0, rc, dt;
-  if (!to_i64(env, argv[0], &r0, "rowStart") || !to_i64(env, argv[1], &rc, "rowCount") ||
-      !to_i64(env, argv[3], &dt, "dtype"))
+  if (!to_int(env, argv[0], &r0, "rowStart") || !to_int(env, argv[1], &rc, "rowCount") ||
+      !to_int(env, argv[3], &dt, "dtype"))
     return nullptr;
   void *out;
   if (!buf_at(env, argv[2], argv[4], "out", &out)) return nullptr;
@@ -513,8 +526,8 @@ napi_value Ple_new(napi_env env, napi_callback_info info) {
   napi_value argv[4], self;
   if (!get_args(env, info, 4, argv, &self)) return nullptr;
   int64_t vocab, width, group, rps;
-  if (!to_i64(env, argv[0], &vocab, "vocab") || !to_i64(env, argv[1], &width, "width") ||
-      !to_i64(env, argv[2], &group, "groupSize") || !to_i64(env, argv[3], &rps, "rowsPerShard"))
+  if (!to_int(env, argv[0], &vocab, "vocab") || !to_int(env, argv[1], &width, "width") ||
+      !to_int(env, argv[2], &group, "groupSize") || !to_int(env, argv[3], &rps, "rowsPerShard"))
     return nullptr;
   g4_ple *h = nullptr;
   G4_CALL(env, g4_ple_create((int)vocab, (int)width, (int)group, (int)rps, &h));
@@ -535,7 +548,7 @@ napi_value Ple_shardBytes(napi_env env, napi_callback_info info) {
   Ple *t = unwrap_ple(env, self);
   if (!t) return nullptr;
   int64_t i;
-  if (!to_i64(env, argv[0], &i, "shard")) return nullptr;
+  if (!to_int(env, argv[0], &i, "shard")) return nullptr;
   size_t bytes;
   int ns;
   G4_CALL(env, g4_ple_shard_bytes(t->h, (int)i, &ns, &bytes));
@@ -551,7 +564,7 @@ napi_value Ple_uploadShard(napi_env env, napi_callback_info info) {
   Ple *t = unwrap_ple(env, self);
   if (!t) return nullptr;
   int64_t i;
-  if (!to_i64(env, argv[0], &i, "shard")) return nullptr;
+  if (!to_int(env, argv[0], &i, "shard")) return nullptr;
   void *p;
   size_t n;
   if (is_instance(env, argv[1], g_devbuf_ctor)) {  // the shard's bytes on the device
@@ -595,7 +608,7 @@ napi_value Ple_gather(napi_env env, napi_callback_info info) {
   void *out;
   if (!buf_at(env, argv[1], argv[3], "out", &out)) return nullptr;
   int64_t dt;
-  if (!to_i64(env, argv[2], &dt, "dtype")) return nullptr;
+  if (!to_int(env, argv[2], &dt, "dtype")) return nullptr;
   G4_CALL(env, g4_ple_gather(t->h, static_cast<const int32_t *>(ids), (int)n, out, (int)dt));
   return undefined(env);
 }
@@ -610,7 +623,7 @@ napi_value Ple_gatherDev(napi_env env, napi_callback_info info) {
   if (!buf_at(env, argv[0], argv[4], "ids", &ids)) return nullptr;
   if (!buf_at(env, argv[2], argv[5], "out", &out)) return nullptr;
   int64_t n, dt;
-  if (!to_i64(env, argv[1], &n, "n") || !to_i64(env, argv[3], &dt, "dtype")) return nullptr;
+  if (!to_int(env, argv[1], &n, "n") || !to_int(env, argv[3], &dt, "dtype")) return nullptr;
   G4_CALL(env, g4_ple_gather_dev(t->h, static_cast<const int32_t *>(ids), (int)n, out, (int)dt));
   return undefined(env);
 }
@@ -695,7 +708,7 @@ napi_value F_init(napi_env env, napi_callback_info info) {
   int64_t dev = 0;
   napi_valuetype t;
   napi_typeof(env, argv[0], &t);
-  if (t != napi_undefined && !to_i64(env, argv[0], &dev, "device")) return nullptr;
+  if (t != napi_undefined && !to_int(env, argv[0], &dev, "device")) return nullptr;
   G4_CALL(env, g4_init((int)dev));
   return undefined(env);
 }
@@ -752,7 +765,7 @@ napi_value F_bf16Head(napi_env env, napi_callback_info info) {
   if (!buf_at(env, argv[4], argv[8], "out", &out)) return nullptr;
   int64_t rows, k;
   double scale, softcap;
-  if (!to_i64(env, argv[2], &rows, "rows") || !to_i64(env, argv[3], &k, "inDim") ||
+  if (!to_int(env, argv[2], &rows, "rows") || !to_int(env, argv[3], &k, "inDim") ||
       !to_f64(env, argv[5], &scale, "scale") || !to_f64(env, argv[6], &softcap, "softcap"))
     return nullptr;
   G4_CALL(env, g4_bf16_head(static_cast<const float *>(x), E, (int)rows, (int)k,
@@ -817,7 +830,7 @@ napi_value F_timeMs(napi_env env, napi_callback_info info) {
 bool ints(napi_env env, napi_value *argv, const int *idx, int64_t *out, int n,
           const char *const *names) {
   for (int i = 0; i < n; ++i)
-    if (!to_i64(env, argv[idx[i]], &out[i], names[i])) return false;
+    if (!to_int(env, argv[idx[i]], &out[i], names[i])) return false;
   return true;
 }
 
@@ -828,8 +841,8 @@ napi_value F_rms(napi_env env, napi_callback_info info) {
   void *x, *sc, *y;
   int64_t rows, width;
   double eps;
-  if (!dev(env, a[0], "x", &x) || !to_i64(env, a[1], &rows, "rows") ||
-      !to_i64(env, a[2], &width, "width") || !dev_or_null(env, a[3], "scale", &sc) ||
+  if (!dev(env, a[0], "x", &x) || !to_int(env, a[1], &rows, "rows") ||
+      !to_int(env, a[2], &width, "width") || !dev_or_null(env, a[3], "scale", &sc) ||
       !to_f64(env, a[4], &eps, "eps") || !dev(env, a[5], "y", &y))
     return nullptr;
   G4_CALL(env, g4_rms((const float *)x, (int)rows, (int)width, (const float *)sc, (float)eps,
@@ -904,7 +917,7 @@ napi_value F_normRope(napi_env env, napi_callback_info info) {
   static const int idx[4] = {1, 2, 3, 4};
   static const char *const names[4] = {"rows", "heads", "hd", "pos0"};
   if (!dev(env, a[0], "x", &x) || !ints(env, a, idx, v, 4, names) ||
-      !dev(env, a[5], "scale", &sc) || !to_i64(env, a[6], &angles, "ropeAngles") ||
+      !dev(env, a[5], "scale", &sc) || !to_int(env, a[6], &angles, "ropeAngles") ||
       !to_f64(env, a[7], &base, "base") || !to_f64(env, a[8], &eps, "eps") ||
       !dev(env, a[9], "y", &y))
     return nullptr;
@@ -958,7 +971,7 @@ napi_value F_fillRandom(napi_env env, napi_callback_info info) {
   double sigma = 1.0;
   napi_valuetype t;
   if (!buf_at(env, a[0], a[5], "buffer", &p) || !to_i64(env, a[1], &count, "count") ||
-      !to_i64(env, a[2], &kind, "kind") || !to_i64(env, a[3], &seed, "seed"))
+      !to_int(env, a[2], &kind, "kind") || !to_i64(env, a[3], &seed, "seed"))
     return nullptr;
   napi_typeof(env, a[4], &t);
   if (t != napi_undefined && !to_f64(env, a[4], &sigma, "sigma")) return nullptr;
@@ -976,7 +989,7 @@ napi_value F_argmax(napi_env env, napi_callback_info info) {
   if (!get_args(env, info, 3, a, &self)) return nullptr;
   void *x, *o;
   int64_t n;
-  if (!dev(env, a[0], "x", &x) || !to_i64(env, a[1], &n, "n") || !dev(env, a[2], "out", &o))
+  if (!dev(env, a[0], "x", &x) || !to_int(env, a[1], &n, "n") || !dev(env, a[2], "out", &o))
     return nullptr;
   G4_CALL(env, g4_argmax((const float *)x, (int)n, (int32_t *)o));
   return undefined(env);
@@ -1124,7 +1137,7 @@ napi_value F_e2bConfig(napi_env env, napi_callback_info info) {
   napi_value a[1], self;
   if (!get_args(env, info, 1, a, &self)) return nullptr;
   int64_t max_seq;
-  if (!to_i64(env, a[0], &max_seq, "maxSeq")) return nullptr;
+  if (!to_int(env, a[0], &max_seq, "maxSeq")) return nullptr;
   g4_gemma_config c;
   G4_CALL(env, g4_gemma_e2b_config((int)max_seq, &c));
   return config_object(env, c);
@@ -1187,7 +1200,7 @@ napi_value Engine_setLinear(napi_env env, napi_callback_info info) {
   if (!get_args(env, info, 3, a, &self)) return nullptr;
   Engine *e = unwrap_engine(env, self);
   int64_t layer, which;
-  if (!e || !to_i64(env, a[0], &layer, "layer") || !to_i64(env, a[1], &which, "which"))
+  if (!e || !to_int(env, a[0], &layer, "layer") || !to_int(env, a[1], &which, "which"))
     return nullptr;
   W4 *w = unwrap_w4(env, a[2]);
   if (!w) return nullptr;
@@ -1201,7 +1214,7 @@ napi_value Engine_setNorm(napi_env env, napi_callback_info info) {
   if (!get_args(env, info, 3, a, &self)) return nullptr;
   Engine *e = unwrap_engine(env, self);
   int64_t layer, which;
-  if (!e || !to_i64(env, a[0], &layer, "layer") || !to_i64(env, a[1], &which, "which"))
+  if (!e || !to_int(env, a[0], &layer, "layer") || !to_int(env, a[1], &which, "which"))
     return nullptr;
   bool is = false;
   napi_is_typedarray(env, a[2], &is);
@@ -1226,7 +1239,7 @@ napi_value Engine_setLayerScalar(napi_env env, napi_callback_info info) {
   Engine *e = unwrap_engine(env, self);
   int64_t layer;
   double s;
-  if (!e || !to_i64(env, a[0], &layer, "layer") || !to_f64(env, a[1], &s, "scalar"))
+  if (!e || !to_int(env, a[0], &layer, "layer") || !to_f64(env, a[1], &s, "scalar"))
     return nullptr;
   G4_CALL(env, g4_gemma_set_layer_scalar(e->h, (int)layer, (float)s));
   return undefined(env);
@@ -1294,7 +1307,7 @@ napi_value Engine_forward(napi_env env, napi_callback_info info) {
   std::vector<int32_t> ids;
   int64_t start;
   void *out;
-  if (!e || !id_list(env, a[0], &ids) || !to_i64(env, a[1], &start, "startPos") ||
+  if (!e || !id_list(env, a[0], &ids) || !to_int(env, a[1], &start, "startPos") ||
       !dev_or_null(env, a[2], "lastHidden", &out))
     return nullptr;
   if (ids.empty()) {
@@ -1315,10 +1328,10 @@ napi_value Engine_forwardDiag(napi_env env, napi_callback_info info) {
   std::vector<int32_t> ids;
   int64_t start, stage_layer;
   void *last, *top, *ple, *layers, *stages;
-  if (!e || !id_list(env, a[0], &ids) || !to_i64(env, a[1], &start, "startPos") ||
+  if (!e || !id_list(env, a[0], &ids) || !to_int(env, a[1], &start, "startPos") ||
       !dev_or_null(env, a[2], "lastHidden", &last) || !dev_or_null(env, a[3], "topHidden", &top) ||
       !dev_or_null(env, a[4], "topPle", &ple) || !dev_or_null(env, a[5], "layerHidden", &layers) ||
-      !to_i64(env, a[6], &stage_layer, "stageLayer") || !dev_or_null(env, a[7], "stages", &stages))
+      !to_int(env, a[6], &stage_layer, "stageLayer") || !dev_or_null(env, a[7], "stages", &stages))
     return nullptr;
   if (ids.empty()) {
     napi_throw_range_error(env, nullptr, "forward needs at least one token id");
@@ -1337,7 +1350,7 @@ napi_value Engine_diagStages(napi_env env, napi_callback_info info) {
   if (!get_args(env, info, 2, a, &self)) return nullptr;
   Engine *e = unwrap_engine(env, self);
   int64_t layer, rows;
-  if (!e || !to_i64(env, a[0], &layer, "layer") || !to_i64(env, a[1], &rows, "rows"))
+  if (!e || !to_int(env, a[0], &layer, "layer") || !to_int(env, a[1], &rows, "rows"))
     return nullptr;
   size_t off[G4_STAGES + 1];
   G4_CALL(env, g4_gemma_diag_stages(e->h, (int)layer, (int)rows, off));
@@ -1369,7 +1382,7 @@ napi_value Engine_greedy(napi_env env, napi_callback_info info) {
   std::vector<int32_t> ids;
   int64_t start;
   void *lg;
-  if (!e || !id_list(env, a[0], &ids) || !to_i64(env, a[1], &start, "startPos") ||
+  if (!e || !id_list(env, a[0], &ids) || !to_int(env, a[1], &start, "startPos") ||
       !dev_or_null(env, a[2], "logits", &lg))
     return nullptr;
   if (ids.empty()) {

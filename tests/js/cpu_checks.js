@@ -32,6 +32,12 @@ check('buffers before init throw the C ABI error', () => {
   assert.throws(() => new rt.native.DeviceBuffer(16), e => e.code === 'G4_STATUS_3' && /g4_init/.test(e.message));
 });
 
+check('int arguments outside the int32 range throw instead of wrapping', () => {
+  // checked in the addon before the C ABI call, so no device is needed
+  assert.throws(() => rt.native.init(2 ** 32), e => e instanceof RangeError && /device is out of the int range/.test(e.message));
+  assert.throws(() => rt.native.init(-(2 ** 31) - 1), e => e instanceof RangeError);
+});
+
 check('topK: largest first, finite only, ties keep the lower index', () => {
   const brute = (a, k) => Array.from(a.keys()).filter(i => Number.isFinite(a[i]))
     .sort((x, y) => (a[y] - a[x]) || (x - y)).slice(0, k);

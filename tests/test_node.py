@@ -35,7 +35,7 @@ def run_node(script, *args, timeout=120):
 
 def test_js_runtime_host_logic(tmp_path):
     res = run_node("cpu_checks.js", str(tmp_path), os.path.join(ROOT, "tests", "golden", "ple_w4_layout.json"))
-    assert res["ok"] and len(res["checks"]) == 6
+    assert res["ok"] and len(res["checks"]) == 7
 
 
 def write_safetensors(path, tensors):
