@@ -293,21 +293,28 @@ class Gemma4Hip {
       this.log(`[diag top hidden] ${formatStats(finiteStats(await rt.readF32(this.device, hidden, rows * H)))}`);
       this.log(`[diag top PLE]    ${formatStats(finiteStats(await rt.readF32(this.device, perLayer, rows * NL * P)))}`);
     }
-    for (const layer of this.layers) {
-      encoder = this.device.createCommandEncoder();
-      garbage = [];
-      const stageProbes = diagnostic && layer.i === 1 ? [] : null;
-      hidden = this.encodeLayer(encoder, layer, hidden, perLayer, rows, startPos, garbage, stageProbes);
-      this.device.queue.submit([encoder.finish()]);
-      try {
-        if (stageProbes) {
-          for (const p of stageProbes) p.values = await rt.readF32(this.device, p.buffer, p.count);
-          logStages(this.log, stageProbes);
+    try {
+      for (const layer of this.layers) {
+        encoder = this.device.createCommandEncoder();
+        garbage = [];
+        const stageProbes = diagnostic && layer.i === 1 ? [] : null;
+        hidden = this.encodeLayer(encoder, layer, hidden, perLayer, rows, startPos, garbage, stageProbes);
+        this.device.queue.submit([encoder.finish()]);
+        try {
+          if (stageProbes) {
+            for (const p of stageProbes) p.values = await rt.readF32(this.device, p.buffer, p.count);
+            logStages(this.log, stageProbes);
+          }
+        } finally {
+          for (const b of garbage) b.destroy();
         }
-      } finally {
-        for (const b of garbage) b.destroy();
+        if (diagnostic) logLayer(this.log, layer.i, await rt.readF32(this.device, hidden, rows * H));
       }
-      if (diagnostic) logLayer(this.log, layer.i, await rt.readF32(this.device, hidden, rows * H));
+    } catch (e) {
+      // a diagnostic stop: the live hidden state and PLE rows go too
+      hidden.destroy();
+      perLayer.destroy();
+      throw e;
     }
     perLayer.destroy();
     encoder = this.device.createCommandEncoder();
