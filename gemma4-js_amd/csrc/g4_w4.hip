@@ -438,9 +438,12 @@ __global__ __launch_bounds__(TC ? TC : 1024) void w4_gemv1_multi_kernel(
 // Decode GEMV, one row of x, for in_dim 1536 and 2048 (J = 3 or 4 groups of
 // 16 per row): the row split.
 //
-// 16 lanes per output row; lane c of a row takes groups c, c + 16, ...,
+// 16 lanes per output row (LPR); lane c of a row takes groups c, c + 16, ...,
 // c + 16 (J - 1), so a block of W waves owns 4 W rows, and at instruction j
-// the 16 lanes of a row read 256 consecutive bytes of it.  x is staged in LDS
+// the 16 lanes of a row read 256 consecutive bytes of it.  In_dim 6144 and
+// 12288 take LPR = 64 (one row per wave, lane c taking groups c, c + 64, ...,
+// J = 3 or 6): the same work per lane, a wave-wide row sum, and none of the
+// flat split's LDS partials and second barrier.  x is staged in LDS
 // as in the flat split, then every lane reads its J groups' pairs and group
 // sums into registers right after the staging barrier, before its first
 // weight use.  The row sum is a 16-lane DPP reduction: once the weights land,
@@ -459,7 +462,7 @@ __global__ __launch_bounds__(TC ? TC : 1024) void w4_gemv1_multi_kernel(
 // start, x staged, the staging barrier passed, every weight load landed (a
 // full wait inserted there, so group j's arithmetic no longer overlaps the
 // later groups' loads), and the store issued.
-template <int J, int W, bool F32X, bool STAMP = false>
+template <int J, int W, bool F32X, bool STAMP = false, int LPR = 16>
 __device__ __forceinline__ void gemv_r16_body(const void *__restrict__ x,
                                               const uint4 *__restrict__ wq,
                                               const uint16_t *__restrict__ ws,
@@ -468,15 +471,16 @@ __device__ __forceinline__ void gemv_r16_body(const void *__restrict__ x,
                                               uint64_t *__restrict__ stamps = nullptr) {
   uint64_t st[5];
   if (STAMP) st[0] = __builtin_amdgcn_s_memrealtime();
-  constexpr int G = 16 * J, T = 64 * W, nch = 4 * G;
+  constexpr int G = LPR * J, T = 64 * W, nch = 4 * G;
+  constexpr int RPW = 64 / LPR;  // rows per wave
   constexpr int XI = (nch + T - 1) / T;  // x chunks per thread
   constexpr int JL = F32X ? J : 1;
   __shared__ uint4 hi[4 * G];
   __shared__ uint4 lo[F32X ? 4 * G : 1];
   __shared__ float sx[G];
   const int t = threadIdx.x;
-  const int c16 = t & 15;
-  const int row = (int)bx * (4 * W) + (t >> 4);
+  const int c16 = t & (LPR - 1);  // the lane's place in its row's team
+  const int row = (int)bx * (RPW * W) + t / LPR;
   const int rr = row < N ? row : N - 1;  // rows past N re-read the last row, store nothing
   const uint4 *x4 = static_cast<const uint4 *>(x);
 
@@ -499,7 +503,7 @@ __device__ __forceinline__ void gemv_r16_body(const void *__restrict__ x,
   uint32_t s[J];
 #pragma unroll
   for (int j = 0; j < J; ++j) {
-    const size_t it = (size_t)rr * gstride + c16 + 16 * j;
+    const size_t it = (size_t)rr * gstride + c16 + LPR * j;
     q[j] = ld_nt(&wq[it]);
     s[j] = ld_nt_u16(&ws[it]);
   }
@@ -554,7 +558,7 @@ __device__ __forceinline__ void gemv_r16_body(const void *__restrict__ x,
   float sxr[J];
 #pragma unroll
   for (int j = 0; j < J; ++j) {
-    const int g = c16 + 16 * j;
+    const int g = c16 + LPR * j;
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
       xh[j][c] = hi[c * G + g];
@@ -598,7 +602,7 @@ __device__ __forceinline__ void gemv_r16_body(const void *__restrict__ x,
     asm volatile("" : "+v"(pj));  // rounded on its own (no FMA into the row sum)
     v += pj;
   }
-  v = team_sum<16>(v);
+  v = team_sum<LPR>(v);
   if (c16 == 0 && row < N) {
     if (y_bf16)
       static_cast<uint16_t *>(y)[row] = (uint16_t)f32_to_bf16_rne(v);
@@ -651,12 +655,79 @@ __global__ __launch_bounds__(64 * W) void w4_gemv_r16_multi_kernel(const void *_
                             (unsigned)(b - S.block0[i]));
 }
 
+// LPR = 64: W rows per block of W waves.
+template <int J, int W, bool F32X>
+__global__ __launch_bounds__(64 * W) void w4_gemv_r64_kernel(
+    const void *__restrict__ x, const uint4 *__restrict__ wq, const uint16_t *__restrict__ ws,
+    void *__restrict__ y, int y_bf16, int N) {
+  gemv_r16_body<J, W, F32X, false, 64>(x, wq, ws, y, y_bf16, N, 64 * J, blockIdx.x);
+}
+
+template <int J, int W, bool F32X>
+__global__ __launch_bounds__(64 * W) void w4_gemv_r64_multi_kernel(const void *__restrict__ x,
+                                                                   Gemv1Segs S, int y_bf16) {
+  const int b = blockIdx.x;
+  const int i = S.n > 2 && b >= S.block0[2] ? 2 : S.n > 1 && b >= S.block0[1] ? 1 : 0;
+  gemv_r16_body<J, W, F32X, false, 64>(x, S.wq[i], S.ws[i], S.y[i], y_bf16, S.N[i], 64 * J,
+                                       (unsigned)(b - S.block0[i]));
+}
+
 // Waves per block of the row split: 4 (16 rows) from 4096 rows on, else 2
 // (measured at in_dim 1536, cold weights: N 6144 3.09 us with 4 waves against
 // 3.34 with 2; N 2048 2.46 us with 2 against 2.49 with 4).
 inline int r16_waves(int rows) { return rows >= 4096 ? 4 : 2; }
 
 inline bool has_r16(int G) { return G == 48 || G == 64; }
+
+// The 64-lane row split: in_dim 6144, and 12288 with BF16 x (FP32 x there
+// would hold 192 registers of x pairs per lane).  8 rows (waves) per block:
+// every block stages the whole x row (12 or 24 KB), so fewer, larger blocks
+// re-read less of it.  Measured, one row of BF16 x, N 1536, cold weights:
+// K 6144 3.40 us with 8 waves, 3.64 with 4, 3.89 with 2, 4.01 with 16 (the
+// flat split: 3.56); K 12288 4.51 us with 8 waves, 4.87 with 4 (flat: 5.47).
+inline bool has_r64(int G, bool f32x) { return G == 192 || (G == 384 && !f32x); }
+constexpr int kR64Waves = 8;
+
+template <int J, bool F32X>
+int launch_r64_i(const g4_w4 *w, const void *x, void *y, int y_bf16) {
+  constexpr int W = kR64Waves;
+  hipLaunchKernelGGL((w4_gemv_r64_kernel<J, W, F32X>), dim3((w->N + W - 1) / W), dim3(64 * W), 0,
+                     stream(), x, w->packed, w->scales, y, y_bf16, w->N);
+  G4_LAUNCH_CHECK("w4_gemv_r64_kernel");
+  return G4_OK;
+}
+
+template <bool F32X>
+int launch_r64(const g4_w4 *w, const void *x, void *y, int y_bf16) {
+  if (w->G == 192) return launch_r64_i<3, F32X>(w, x, y, y_bf16);
+  return launch_r64_i<6, false>(w, x, y, y_bf16);
+}
+
+template <int J, bool F32X>
+int launch_r64_multi_i(const g4_w4 *const *w, int n, const void *x, void *const *y, int y_bf16) {
+  constexpr int W = kR64Waves;
+  Gemv1Segs S{};
+  int blocks = 0;
+  for (int i = 0; i < n; ++i) {
+    S.wq[i] = w[i]->packed;
+    S.ws[i] = w[i]->scales;
+    S.y[i] = y[i];
+    S.N[i] = w[i]->N;
+    S.block0[i] = blocks;
+    blocks += (w[i]->N + W - 1) / W;
+  }
+  S.n = n;
+  hipLaunchKernelGGL((w4_gemv_r64_multi_kernel<J, W, F32X>), dim3(blocks), dim3(64 * W), 0,
+                     stream(), x, S, y_bf16);
+  G4_LAUNCH_CHECK("w4_gemv_r64_multi_kernel");
+  return G4_OK;
+}
+
+template <bool F32X>
+int launch_r64_multi(const g4_w4 *const *w, int n, const void *x, void *const *y, int y_bf16) {
+  if (w[0]->G == 192) return launch_r64_multi_i<3, F32X>(w, n, x, y, y_bf16);
+  return launch_r64_multi_i<6, false>(w, n, x, y, y_bf16);
+}
 
 template <int J, int W, bool F32X>
 int launch_r16_i(const g4_w4 *w, const void *x, void *y, int y_bf16) {
@@ -738,6 +809,7 @@ int gemv1_plan(const g4_w4 *w, Gemv1Plan *p) {
 template <bool F32X>
 int launch_gemv1(const g4_w4 *w, const void *x, void *y, int y_bf16) {
   if (has_r16(w->G)) return launch_r16<F32X>(w, x, y, y_bf16);
+  if (has_r64(w->G, F32X)) return launch_r64<F32X>(w, x, y, y_bf16);
   Gemv1Plan p;
   if (int rc = gemv1_plan<F32X>(w, &p)) return rc;
   // compile-time variants for the plans of the Gemma-4-E2B projections
@@ -785,6 +857,7 @@ template <bool F32X>
 int launch_gemv1_multi(const g4_w4 *const *w, int n, const void *x, void *const *y,
                        int y_bf16) {
   if (has_r16(w[0]->G)) return launch_r16_multi<F32X>(w, n, x, y, y_bf16);
+  if (has_r64(w[0]->G, F32X)) return launch_r64_multi<F32X>(w, n, x, y, y_bf16);
   Gemv1Plan p;
   if (int rc = gemv1_plan<F32X>(w[0], &p)) return rc;
   switch (p.IPL) {
