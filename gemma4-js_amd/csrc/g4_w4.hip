@@ -679,13 +679,14 @@ inline int r16_waves(int rows) { return rows >= 4096 ? 4 : 2; }
 
 inline bool has_r16(int G) { return G == 48 || G == 64; }
 
-// The 64-lane row split: in_dim 6144, and 12288 with BF16 x (FP32 x there
-// would hold 192 registers of x pairs per lane).  8 rows (waves) per block:
+// The 64-lane row split: in_dim 4096 and 6144, and 12288 with BF16 x (FP32 x
+// there would hold 192 registers of x pairs per lane).  8 rows (waves) per block:
 // every block stages the whole x row (12 or 24 KB), so fewer, larger blocks
 // re-read less of it.  Measured, one row of BF16 x, N 1536, cold weights:
 // K 6144 3.40 us with 8 waves, 3.64 with 4, 3.89 with 2, 4.01 with 16 (the
-// flat split: 3.56); K 12288 4.51 us with 8 waves, 4.87 with 4 (flat: 5.47).
-inline bool has_r64(int G, bool f32x) { return G == 192 || (G == 384 && !f32x); }
+// flat split: 3.56); K 12288 4.51 us with 8 waves, 4.87 with 4 (flat: 5.47);
+// K 4096 2.71 us (flat: 2.85), with FP32 x 2.85 us (flat: 3.28).
+inline bool has_r64(int G, bool f32x) { return G == 128 || G == 192 || (G == 384 && !f32x); }
 constexpr int kR64Waves = 8;
 
 template <int J, bool F32X>
@@ -699,6 +700,7 @@ int launch_r64_i(const g4_w4 *w, const void *x, void *y, int y_bf16) {
 
 template <bool F32X>
 int launch_r64(const g4_w4 *w, const void *x, void *y, int y_bf16) {
+  if (w->G == 128) return launch_r64_i<2, F32X>(w, x, y, y_bf16);
   if (w->G == 192) return launch_r64_i<3, F32X>(w, x, y, y_bf16);
   return launch_r64_i<6, false>(w, x, y, y_bf16);
 }
@@ -725,6 +727,7 @@ int launch_r64_multi_i(const g4_w4 *const *w, int n, const void *x, void *const 
 
 template <bool F32X>
 int launch_r64_multi(const g4_w4 *const *w, int n, const void *x, void *const *y, int y_bf16) {
+  if (w[0]->G == 128) return launch_r64_multi_i<2, F32X>(w, n, x, y, y_bf16);
   if (w[0]->G == 192) return launch_r64_multi_i<3, F32X>(w, n, x, y, y_bf16);
   return launch_r64_multi_i<6, false>(w, n, x, y, y_bf16);
 }
