@@ -493,3 +493,30 @@ def test_gemv_stamps_refuses_other_widths(g4):
         lin.stamp_waves()
     assert "row split" in str(e.value)
     lin.free()
+
+
+@pytest.mark.parametrize("k", [4096, 6144, 12288])
+@pytest.mark.parametrize("n", [1, 7, 1001])
+def test_wide_rows_ragged_out_dim(g4, oracle, n, k):
+    # the 64-lane row split (in_dim 4096, 6144, and 12288 with BF16 x) with
+    # out_dim not a multiple of its 8-row blocks: the last block's rows past
+    # out_dim re-read row out_dim - 1 and store nothing; both x dtypes, and
+    # the several-weight launch gives the single launch's bits
+    packed, scales, q = syn.w4_weights(400 + n, n, k, full_range=True)
+    p2, s2, _ = syn.w4_weights(401 + n, 9, k)
+    lin, lin2 = g4.W4Linear(packed, scales, gemm_tiles=False), g4.W4Linear(p2, s2, gemm_tiles=False)
+    x_bits, x = syn.activations(402, 1, k)
+    ref = np.asarray(oracle.w4_linear(x, packed, scales), np.float64).reshape(1, n)
+    for dt in (g4.BF16, g4.F32):
+        xb = g4.Buffer.from_array(x_bits if dt == g4.BF16 else x.astype(np.float32))
+        guard = g4.Buffer((n + 64) * 4)
+        guard.upload(np.full(n + 64, 7.0, np.float32))
+        lin.linear(xb.ptr, dt, 1, guard.ptr, g4.F32)
+        out = guard.download(np.float32)
+        assert (out[n:] == 7.0).all()  # nothing written past out_dim
+        assert rel_l2_rows(out[:n].reshape(1, n), ref) <= TOL
+        ya, yb = g4.Buffer(n * 4), g4.Buffer(9 * 4)
+        g4.W4Linear.linear_multi([lin, lin2], xb.ptr, dt, 1, [ya.ptr, yb.ptr], g4.F32)
+        assert np.array_equal(ya.download(np.uint32), out[:n].view(np.uint32))
+    lin.free()
+    lin2.free()
