@@ -1201,16 +1201,31 @@ __global__ __launch_bounds__(256) void norm_chain_xprep_kernel(
     load8(w1, ch, w1v[u]);
     if (w2) load8(w2, ch, w2v[u]);
   }
-  for (int sp = 1; sp < a_parts; ++sp)  // the other partial planes, added in order
+  // the other partial planes, added in order, two at a time: both planes'
+  // loads go out together (past a_parts plane sp0 is re-read), so a pair
+  // costs one memory round trip instead of two.  (E2B prefill of 512
+  // tokens: 9.80 -> 9.60 ms; four at a time, 256 registers and one wave per
+  // SIMD, 9.64 ms.)
+  for (int sp0 = 1; sp0 < a_parts; sp0 += 2) {
+    float t[2][kChainCpl][8];
 #pragma unroll
-    for (int u = 0; u < kChainCpl; ++u) {
-      int ch = lane + 64 * u;
-      ch = ch < nch ? ch : 0;
-      float t[8];
-      load8(a + sp * a_stride + off, ch, t);
+    for (int b = 0; b < 2; ++b) {
+      const int sp = sp0 + b < a_parts ? sp0 + b : sp0;
 #pragma unroll
-      for (int q = 0; q < 8; ++q) av[u][q] += t[q];
+      for (int u = 0; u < kChainCpl; ++u) {
+        int ch = lane + 64 * u;
+        ch = ch < nch ? ch : 0;
+        load8(a + sp * a_stride + off, ch, t[b][u]);
+      }
     }
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+      if (sp0 + b < a_parts)
+#pragma unroll
+        for (int u = 0; u < kChainCpl; ++u)
+#pragma unroll
+          for (int q = 0; q < 8; ++q) av[u][q] += t[b][u][q];
+  }
   float ss = 0.f;
 #pragma unroll
   for (int u = 0; u < kChainCpl; ++u)
