@@ -105,7 +105,12 @@ def test_norm_rope(g4, rows, heads, hd, pos0, prop, base):
     # a prompt: 512 rows over 512 keys (the matrix-core kernel, 256 row tiles)
     (512, 8, 256, 512, True, 512), (96, 8, 512, 300, False, 512), (40, 3, 64, 57, True, 11),
     # a few rows over a long cache: the key-split kernel
-    (2, 8, 256, 700, True, 512), (3, 8, 512, 900, False, 512)])
+    (2, 8, 256, 700, True, 512), (3, 8, 512, 900, False, 512),
+    # longer caches under the matrix-core kernel: windows that start past key
+    # 0, three heads (row tiles across positions), one head over a short
+    # window, one key past a multiple of 128
+    (200, 8, 512, 1000, True, 512), (129, 3, 128, 385, False, 512),
+    (257, 1, 64, 257, True, 100), (64, 8, 256, 129, False, 512)])
 def test_attention(g4, qrows, heads, hd, keylen, sliding, window):
     rng = np.random.default_rng([qrows, heads, hd, keylen, window])
     q = rng.standard_normal((qrows, heads * hd)).astype(np.float32) * 0.2
