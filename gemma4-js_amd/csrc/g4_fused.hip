@@ -1164,22 +1164,23 @@ __device__ __forceinline__ uint32_t half2_bits(_Float16 a, _Float16 b) {
 // xt[c * Mp + row] and xt[(width / 8 + c) * Mp + row].  r_out and x_out (FP32)
 // are optional.
 //
-// One wave per row, 4 rows per block: lane l holds whole chunks l, l + 64,
+// One wave per row, one row per block: lane l holds whole chunks l, l + 64,
 // ... (up to 4), so the norms and the maximum are wave reductions (no
 // barrier) and each chunk is converted where it was loaded.  Blocks are
 // dealt to the 8 XCDs round-robin; rows go to them in runs of Mp / 8, so the
 // 8 rows that share each 128-byte line of xt[c][m] are written through one
-// XCD's L2.  Grid: Mp / 4 blocks (Mp a multiple of 32); rows past `rows`
-// write zero chunks.
+// XCD's L2.  Grid: Mp blocks of 64 threads (Mp a multiple of 32); rows past
+// `rows` write zero chunks.
 constexpr int kChainCpl = 4;  // chunks per lane: width <= 64 * 4 * 8 = 2048
-__global__ __launch_bounds__(256) void norm_chain_xprep_kernel(
+__global__ __launch_bounds__(64) void norm_chain_xprep_kernel(
     const float *__restrict__ a, int a_parts, size_t a_stride, const float *__restrict__ h,
     const float *__restrict__ w1, const float *__restrict__ w2, float c, float eps, int width,
     int rows, float *__restrict__ r_out, float *__restrict__ x_out, uint4 *__restrict__ xt,
     int *__restrict__ xe, int Mp) {
   const int lane = threadIdx.x & 63;
-  const int grp = (blockIdx.x & 7) * (Mp >> 5) + (blockIdx.x >> 3);  // 4-row group
-  const int row = 4 * grp + (threadIdx.x >> 6);
+  // (4-row blocks left half of the CUs idle at 512 rows and gave each busy
+  // CU four rows of loads: E2B prefill of 512 tokens 9.69-9.72 -> 9.63-9.66 ms)
+  const int row = (blockIdx.x & 7) * (Mp >> 3) + (blockIdx.x >> 3);
   const int nch = width >> 3;
   const size_t lo_plane = (size_t)nch * Mp;
   if (row >= rows) {
@@ -1470,7 +1471,7 @@ int launch_norm_chain_xprep(const float *a, int a_parts, size_t a_stride, const 
   if (width > 64 * kChainCpl * 8 || width % 8 || rows > Mp || Mp % 32)
     return fail(G4_E_ARG, "norm chain with x pre-pass: width %d (<= 2048, multiple of 8), "
                 "rows %d <= %d (a multiple of 32)", width, rows, Mp);
-  hipLaunchKernelGGL(norm_chain_xprep_kernel, dim3(Mp / 4), dim3(256), 0, stream(), a, a_parts,
+  hipLaunchKernelGGL(norm_chain_xprep_kernel, dim3(Mp), dim3(64), 0, stream(), a, a_parts,
                      a_stride, h, w1, w2, c, eps, width, rows, r_out, x_out,
                      static_cast<uint4 *>(xt), xe, Mp);
   G4_LAUNCH_CHECK("norm_chain_xprep_kernel");
