@@ -436,7 +436,8 @@ int run_layers(g4_gemma *m, int rows, bool graph, const Diag *dg = nullptr) {
           (rc = launch_rms(m->down, rows, H, l.norm[G4_NORM_POST_FFW], eps, pfn, nullptr)))
         return rc;
     }
-    const g4_w4 *pgw = l.w[G4_PROJ_PLE_GATE];
+    const g4_w4 *pgw = l.w[G4_PROJ_PLE_GATE], *ppw = l.w[G4_PROJ_PLE_PROJ];
+    bool ple_done = false;
     if (gemm) {  // the residual itself is the PLE gate's input
       GemmXPrep xp;
       if ((rc = w4_gemm_prepare(&pgw, 1, rows, &xp))) return rc;
@@ -444,16 +445,32 @@ int run_layers(g4_gemma *m, int rows, bool graph, const Diag *dg = nullptr) {
                                         l.norm[G4_NORM_POST_FFW], nullptr, 1.f, eps, rows, H,
                                         m->fres, nullptr, xp.xt, xp.xe, xp.Mp)))
         return rc;
-      if ((rc = w4_gemm(pgw, nullptr, true, rows, m->pg, false))) return rc;
+      if (sb || !gelu_ple_xprep_fits(P, 1)) {  // the stages read the summed gate
+        if ((rc = w4_gemm(pgw, nullptr, true, rows, m->pg, false))) return rc;
+      } else {
+        // the gate's K slices (at most 8) go unsummed to gelu·ple, which writes
+        // the PLE projection's x': the slice sum and the projection's pre-pass
+        // are skipped
+        GemmParts gp;
+        GemmXPrep pxp;
+        if ((rc = w4_gemm_parts(pgw, nullptr, rows, m->pg, &gp)) ||
+            (rc = w4_gemm_prepare(&ppw, 1, rows, &pxp)) ||
+            (rc = launch_gelu_ple_xprep(gp.parts, gp.n, gp.stride, m->perlayer, i, NL, P, rows,
+                                        m->pm, pxp.xt, pxp.xe, pxp.Mp)) ||
+            (rc = w4_gemm(ppw, nullptr, true, rows, m->pp, false)))
+          return rc;
+        ple_done = true;
+      }
     } else {
       if ((rc = launch_norm_chain(dp.parts, m->ares, l.norm[G4_NORM_POST_FFW], nullptr, 1.f, eps,
                                   rows, H, m->fres, nullptr, dp.n, dp.stride)))
         return rc;
       if ((rc = g4_w4_linear(pgw, m->fres, G4_F32, rows, m->pg, G4_F32))) return rc;
     }
-    if ((rc = launch_gelu_ple(m->pg, m->perlayer, rows, i, P, NL, m->pm))) return rc;
-    if ((rc = g4_w4_linear(l.w[G4_PROJ_PLE_PROJ], m->pm, G4_F32, rows, m->pp, G4_F32)))
-      return rc;
+    if (!ple_done) {
+      if ((rc = launch_gelu_ple(m->pg, m->perlayer, rows, i, P, NL, m->pm))) return rc;
+      if ((rc = g4_w4_linear(ppw, m->pm, G4_F32, rows, m->pp, G4_F32))) return rc;
+    }
     if (sb) {
       float *pln = sb + dg->off[G4_STAGE_PLE_NORMALIZED];
       if ((rc = stage(G4_STAGE_FFW_RESIDUAL, m->fres)) || (rc = stage(G4_STAGE_PLE_GATE, m->pg)) ||

@@ -1296,6 +1296,75 @@ __global__ __launch_bounds__(64) void norm_chain_xprep_kernel(
   }
 }
 
+// The PLE gate's product gelu(gate) * ple (gelu_ple_kernel) with the PLE
+// projection GEMM's x pre-pass fused in, written as in norm_chain_xprep_kernel
+// (exponent per row, FP16 hi/lo chunks at xt[c * Mp + row] and
+// xt[(width / 8 + c) * Mp + row]); y (FP32) is optional.  The gate arrives
+// as the gate GEMM's K slices, `parts` planes pstride floats apart, added in
+// slice order as gemm_splitk_sum_kernel adds them, so y and x' equal those
+// of the three kernels this replaces.  One wave per row and one row per
+// block (rows to the XCDs in runs of Mp / 8); lane l owns chunk l, so width
+// is at most 512.  Rows past `rows` write zero chunks.
+constexpr int kPleMaxParts = 8;
+__global__ __launch_bounds__(64) void gelu_ple_xprep_kernel(
+    const float *__restrict__ gate, int parts, size_t pstride, const float *__restrict__ ple,
+    int layer, int layers, int width, int rows, float *__restrict__ y, uint4 *__restrict__ xt,
+    int *__restrict__ xe, int Mp) {
+  const int lane = threadIdx.x;
+  const int row = (blockIdx.x & 7) * (Mp >> 3) + (blockIdx.x >> 3);
+  const int nch = width >> 3;
+  const size_t lo_plane = (size_t)nch * Mp;
+  if (row >= rows) {
+    if (lane < nch) {
+      xt[(size_t)lane * Mp + row] = make_uint4(0u, 0u, 0u, 0u);
+      xt[lo_plane + (size_t)lane * Mp + row] = make_uint4(0u, 0u, 0u, 0u);
+    }
+    return;
+  }
+  const bool live = lane < nch;
+  const int ch = live ? lane : 0;  // idle lanes re-read chunk 0 and are left out
+  const size_t off = (size_t)row * width;
+  // every load first: the slices (past `parts`, slice 0 again) and the ple row
+  float g[kPleMaxParts][8], pv[8];
+#pragma unroll
+  for (int sp = 0; sp < kPleMaxParts; ++sp)
+    load8(gate + (size_t)(sp < parts ? sp : 0) * pstride + off, ch, g[sp]);
+  load8(ple + ((size_t)row * layers + layer) * width, ch, pv);
+#pragma unroll
+  for (int sp = 1; sp < kPleMaxParts; ++sp)
+    if (sp < parts)
+#pragma unroll
+      for (int q = 0; q < 8; ++q) g[0][q] += g[sp][q];
+  float v[8], mx = 0.f;
+#pragma unroll
+  for (int q = 0; q < 8; ++q) {
+    v[q] = gelu_tanh(g[0][q]) * pv[q];
+    mx = fmaxf(mx, live ? fabsf(v[q]) : 0.f);
+  }
+  if (y && live) {
+    float4 *yo = reinterpret_cast<float4 *>(y + off) + 2 * ch;
+    yo[0] = make_float4(v[0], v[1], v[2], v[3]);
+    yo[1] = make_float4(v[4], v[5], v[6], v[7]);
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+  const int e = mx > 0.f && mx <= 3.4e38f ? ilogbf(mx) - 13 : 0;
+  if (lane == 0) xe[row] = e;
+  if (!live) return;
+  _Float16 hh[8], ll[8];
+#pragma unroll
+  for (int q = 0; q < 8; ++q) {
+    const float sv = ldexpf(v[q], -e);
+    hh[q] = (_Float16)sv;
+    ll[q] = (_Float16)(sv - (float)hh[q]);
+  }
+  xt[(size_t)ch * Mp + row] = make_uint4(half2_bits(hh[0], hh[4]), half2_bits(hh[1], hh[5]),
+                                         half2_bits(hh[2], hh[6]), half2_bits(hh[3], hh[7]));
+  xt[lo_plane + (size_t)ch * Mp + row] =
+      make_uint4(half2_bits(ll[0], ll[4]), half2_bits(ll[1], ll[5]), half2_bits(ll[2], ll[6]),
+                 half2_bits(ll[3], ll[7]));
+}
+
 }  // namespace
 
 // ---- launchers used by the engine --------------------------------------------
@@ -1475,6 +1544,24 @@ int launch_norm_chain_xprep(const float *a, int a_parts, size_t a_stride, const 
                      a_stride, h, w1, w2, c, eps, width, rows, r_out, x_out,
                      static_cast<uint4 *>(xt), xe, Mp);
   G4_LAUNCH_CHECK("norm_chain_xprep_kernel");
+  return G4_OK;
+}
+
+bool gelu_ple_xprep_fits(int width, int parts) {
+  return width % 8 == 0 && width > 0 && width <= 512 && parts >= 1 && parts <= kPleMaxParts;
+}
+
+int launch_gelu_ple_xprep(const float *gate, int parts, size_t pstride, const float *ple,
+                          int layer, int layers, int width, int rows, float *y, void *xt,
+                          int *xe, int Mp) {
+  if (!gelu_ple_xprep_fits(width, parts) || rows > Mp || Mp % 32)
+    return fail(G4_E_ARG, "gelu·ple with x pre-pass: width %d (<= 512, multiple of 8), %d "
+                "gate slices (<= %d), rows %d <= %d (a multiple of 32)", width, parts,
+                kPleMaxParts, rows, Mp);
+  hipLaunchKernelGGL(gelu_ple_xprep_kernel, dim3(Mp), dim3(64), 0, stream(), gate, parts,
+                     pstride, ple, layer, layers, width, rows, y, static_cast<uint4 *>(xt), xe,
+                     Mp);
+  G4_LAUNCH_CHECK("gelu_ple_xprep_kernel");
   return G4_OK;
 }
 

@@ -56,6 +56,14 @@ int launch_norm_chain(const float *a, const float *h, const float *w1, const flo
 int launch_norm_chain_xprep(const float *a, int a_parts, size_t a_stride, const float *h,
                             const float *w1, const float *w2, float c, float eps, int rows,
                             int width, float *r_out, float *x_out, void *xt, int *xe, int Mp);
+// y = gelu(gate) * ple[:, layer] (launch_gelu_ple) written as the next prefill
+// GEMM's x' (xt, xe, Mp from w4_gemm_prepare), the gate the sum of `parts`
+// K-slice planes pstride floats apart; y optional.  Fits: width <= 512, a
+// multiple of 8, at most 8 planes.
+bool gelu_ple_xprep_fits(int width, int parts);
+int launch_gelu_ple_xprep(const float *gate, int parts, size_t pstride, const float *ple,
+                          int layer, int layers, int width, int rows, float *y, void *xt,
+                          int *xe, int Mp);
 
 // RoPE (cos, sin) tables of the current position for up to kRopeSlots
 // (base, head_dim, angles) variants, kRopeTable entries each.
