@@ -359,15 +359,18 @@ int run_layers(g4_gemma *m, int rows, bool graph, const Diag *dg = nullptr) {
     const g4_w4 *qkv[3] = {l.w[G4_PROJ_Q], l.w[G4_PROJ_K], l.w[G4_PROJ_V]};
     void *qkv_out[3] = {m->qraw, m->kraw, m->vraw};
     const int nqkv = l.kv_src < 0 ? 3 : 1;
-    if (pre_prepped)
+    GemmParts qp = {m->qraw, 1, 0};
+    if (pre_prepped && nqkv == 1)  // q alone: its K slices go to the q norm unsummed
+      rc = w4_gemm_parts(qkv[0], nullptr, rows, m->qraw, &qp);
+    else if (pre_prepped)
       rc = w4_gemm_multi(qkv, nqkv, nullptr, true, rows, qkv_out, false);
     else
       rc = g4_w4_linear_multi(qkv, nqkv, m->pre, G4_F32, rows, qkv_out, G4_F32);
     if (rc) return rc;
     if (sb && ((rc = stage(G4_STAGE_PRE_ATTENTION, m->pre)) || (rc = stage(G4_STAGE_Q_RAW, m->qraw))))
       return rc;
-    if ((rc = launch_norm_rope(m->qraw, rows, c.heads, l.hd, 0, m->pos, l.norm[G4_NORM_Q],
-                               l.rope_angles, l.rope_base, eps, m->q, false)))
+    if ((rc = launch_norm_rope(qp.parts, rows, c.heads, l.hd, 0, m->pos, l.norm[G4_NORM_Q],
+                               l.rope_angles, l.rope_base, eps, m->q, false, qp.n, qp.stride)))
       return rc;
     if (sb && (rc = stage(G4_STAGE_Q_NORM_ROPE, m->q))) return rc;
     const Layer &src = l.kv_src >= 0 ? m->L[l.kv_src] : l;

@@ -17,9 +17,11 @@ int launch_scale(const float *a, size_t n, float s, float *y);
 int launch_gelu_mul(const float *gate, const float *up, size_t n, float *y);
 int launch_gelu_ple(const float *gate, const float *ple, int rows, int layer, int width,
                     int layers, float *y);
+// x may be the sum of `parts` (<= 8) planes pstride floats apart (a GEMM's K
+// slices), added in plane order.
 int launch_norm_rope(const float *x, int rows, int heads, int hd, int pos0, const int *pos_dev,
                      const float *scale, int rope_angles, float base, float eps, float *y,
-                     bool at_pos);
+                     bool at_pos, int parts = 1, size_t pstride = 0);
 // Floats of split scratch that launch_attention needs for up to max_keylen keys.
 size_t attention_part_floats(int qrows, int heads, int hd, int max_keylen, int kpw);
 int launch_attention(const float *q, const float *k, const float *v, int qrows, int heads,

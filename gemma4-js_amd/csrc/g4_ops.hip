@@ -105,22 +105,44 @@ __global__ __launch_bounds__(kBlock) void gelu_ple_kernel(const float *__restric
 // ---- NORM_ROPE_SHADER (gpu-runtime.js:1175-1202) ----------------------------
 // One block per (row, head); thread t < hd/2 owns the rotate-half pair
 // (t, t + hd/2).  Output row index is row, or *pos_dev + row when pos_dev is
-// given and `at_pos` is set (appending k straight into a cache).
+// given and `at_pos` is set (appending k straight into a cache).  x may be
+// the sum of `parts` planes pstride floats apart (a GEMM's K slices), added
+// in plane order.
+constexpr int kNormRopeMaxParts = 8;
 __global__ __launch_bounds__(kBlock) void norm_rope_kernel(
-    const float *__restrict__ x, int heads, int hd, int pos0, const int *__restrict__ pos_dev,
-    const float *__restrict__ scale, int rope_angles, float base, float eps,
-    float *__restrict__ y, int at_pos) {
+    const float *__restrict__ x, int parts, size_t pstride, int heads, int hd, int pos0,
+    const int *__restrict__ pos_dev, const float *__restrict__ scale, int rope_angles,
+    float base, float eps, float *__restrict__ y, int at_pos) {
   __shared__ float red[4];
   const int rh = blockIdx.x;
   const int row = rh / heads, h = rh - row * heads;
   const float *xv = x + (size_t)rh * hd;
   const int half = hd >> 1, t = threadIdx.x;
   float a = 0.f, b = 0.f;
-  if (t < half) {
+  if (t < half && parts == 1) {
     a = xv[t];
     b = xv[t + half];
+  } else if (t < half) {
+    // every plane's load first (past `parts`, plane 0 again), then the adds
+    float pa[kNormRopeMaxParts], pb[kNormRopeMaxParts];
+#pragma unroll
+    for (int sp = 0; sp < kNormRopeMaxParts; ++sp) {
+      const size_t o = (size_t)(sp < parts ? sp : 0) * pstride;
+      pa[sp] = xv[o + t];
+      pb[sp] = xv[o + t + half];
+    }
+    a = pa[0];
+    b = pb[0];
+#pragma unroll
+    for (int sp = 1; sp < kNormRopeMaxParts; ++sp)
+      if (sp < parts) {
+        a += pa[sp];
+        b += pb[sp];
+      }
   }
-  const float inv = inv_rms(block_sum(a * a + b * b, red), hd, eps);
+  // the products that are fused are spelled out, so the rounding does not
+  // depend on which one the compiler would contract
+  const float inv = inv_rms(block_sum(fmaf(b, b, a * a), red), hd, eps);
   const int pos = (pos_dev ? *pos_dev : pos0) + row;
   if (t < half) {
     const float an = a * inv * scale[t], bn = b * inv * scale[t + half];
@@ -133,8 +155,8 @@ __global__ __launch_bounds__(kBlock) void norm_rope_kernel(
     }
     const size_t orow = at_pos ? (size_t)pos : (size_t)row;
     float *yv = y + (orow * heads + h) * hd;
-    yv[t] = an * cs - bn * sn;
-    yv[t + half] = bn * cs + an * sn;
+    yv[t] = fmaf(an, cs, -(bn * sn));
+    yv[t + half] = fmaf(bn, cs, an * sn);
   }
 }
 
@@ -795,10 +817,13 @@ int launch_gelu_ple(const float *gate, const float *ple, int rows, int layer, in
 
 int launch_norm_rope(const float *x, int rows, int heads, int hd, int pos0, const int *pos_dev,
                      const float *scale, int rope_angles, float base, float eps, float *y,
-                     bool at_pos) {
+                     bool at_pos, int parts, size_t pstride) {
   if (rows == 0) return G4_OK;
-  hipLaunchKernelGGL(norm_rope_kernel, dim3(rows * heads), dim3(kBlock), 0, stream(), x, heads,
-                     hd, pos0, pos_dev, scale, rope_angles, base, eps, y, (int)at_pos);
+  if (parts < 1 || parts > kNormRopeMaxParts)
+    return fail(G4_E_ARG, "norm_rope: %d planes (1..%d)", parts, kNormRopeMaxParts);
+  hipLaunchKernelGGL(norm_rope_kernel, dim3(rows * heads), dim3(kBlock), 0, stream(), x, parts,
+                     pstride, heads, hd, pos0, pos_dev, scale, rope_angles, base, eps, y,
+                     (int)at_pos);
   G4_LAUNCH_CHECK("norm_rope_kernel");
   return G4_OK;
 }
