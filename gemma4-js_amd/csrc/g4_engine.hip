@@ -387,15 +387,23 @@ int run_layers(g4_gemma *m, int rows, bool graph, const Diag *dg = nullptr) {
           return rc;
       }
     }
+    // with the GEMM path, attention may write the o projection's x' itself
+    const g4_w4 *ow = l.w[G4_PROJ_O];
+    GemmXPrep oxp = {nullptr, nullptr, 0};
+    bool o_prepped = false;
+    if (gemm && (rc = w4_gemm_prepare(&ow, 1, rows, &oxp))) return rc;
     if ((rc = launch_attention(m->q, src.kc, src.vc, rows, c.heads, l.hd, keylen_host, 0, m->pos,
-                               max_keylen, !l.full, c.window, kpw, m->part, m->ctx)))
+                               max_keylen, !l.full, c.window, kpw, m->part, m->ctx, oxp.xt,
+                               oxp.xe, oxp.Mp, gemm ? &o_prepped : nullptr)))
       return rc;
     if (sb && (rc = stage(G4_STAGE_ATTENTION_CONTEXT, m->ctx))) return rc;
     GemmParts op;
     if (dg) {  // the projection whole (no K slices left for the chain to add)
-      if ((rc = g4_w4_linear(l.w[G4_PROJ_O], m->ctx, G4_F32, rows, m->attn, G4_F32))) return rc;
+      if ((rc = g4_w4_linear(ow, m->ctx, G4_F32, rows, m->attn, G4_F32))) return rc;
       op = {m->attn, 1, 0};
-    } else if ((rc = linear_parts(l.w[G4_PROJ_O], m->ctx, rows, m->attn, &op))) {
+    } else if (o_prepped) {
+      if ((rc = w4_gemm_parts(ow, nullptr, rows, m->attn, &op))) return rc;
+    } else if ((rc = linear_parts(ow, m->ctx, rows, m->attn, &op))) {
       return rc;
     }
     if (sb) {

@@ -1150,10 +1150,6 @@ __device__ __forceinline__ float fblock_max(float v, float *red) {
   return fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
 }
 
-__device__ __forceinline__ uint32_t half2_bits(_Float16 a, _Float16 b) {
-  return (uint32_t)__builtin_bit_cast(uint16_t, a) |
-         ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
-}
 
 // norm_chain_kernel's chain for a row of up to 2048 values (a multiple of 8)
 // with the prefill GEMM's x pre-pass of its output fused in: the GEMM input

@@ -76,6 +76,13 @@ __device__ __forceinline__ uint32_t bf16_pair(uint32_t lo16, uint32_t hi16) {
   return (lo16 & 0xffffu) | (hi16 << 16);
 }
 
+// Two FP16 values as one 32-bit word, a in the low half (the pairs of the
+// prefill GEMM's x' chunks).
+__device__ __forceinline__ uint32_t half2_bits(_Float16 a, _Float16 b) {
+  return (uint32_t)__builtin_bit_cast(uint16_t, a) |
+         ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
+}
+
 // GELU, tanh form with the clamp of GELU_MUL_SHADER (gpu-runtime.js:1148-1155).
 __device__ __forceinline__ float gelu_tanh(float x) {
   const float c = 0.7978845608028654f;

@@ -24,9 +24,14 @@ int launch_norm_rope(const float *x, int rows, int heads, int hd, int pos0, cons
                      bool at_pos, int parts = 1, size_t pstride = 0);
 // Floats of split scratch that launch_attention needs for up to max_keylen keys.
 size_t attention_part_floats(int qrows, int heads, int hd, int max_keylen, int kpw);
+// With xt, xe, Mp (w4_gemm_prepare of the GEMM that takes the [qrows, heads
+// * hd] output) and x_done: where the matrix-core kernel runs and its 16-row
+// blocks hold whole query rows (heads divides 16), the output leaves as that
+// GEMM's x' instead of through `out`, and *x_done is set.
 int launch_attention(const float *q, const float *k, const float *v, int qrows, int heads,
                      int hd, int keylen, int qpos0, const int *pos_dev, int max_keylen,
-                     bool sliding, int window, int kpw, float *part, float *out);
+                     bool sliding, int window, int kpw, float *part, float *out,
+                     void *xt = nullptr, int *xe = nullptr, int Mp = 0, bool *x_done = nullptr);
 int launch_ple_mix(const float *proj, float pre_scale, const float *norm_scale,
                    const float *token_ple, int rows, int width, int layers, float eps,
                    float ple_scale, float out_scale, float *y);

@@ -181,6 +181,12 @@ struct AttnArgs {
   const int *pos_dev;   // if set: qpos0 = *pos_dev and keylen = *pos_dev + qrows
   int qrows;
   float *out;           // [qrows, H, hd] (attn_rows_mfma_kernel)
+  // attn_rows_mfma_kernel, when xt is set: the output leaves as the prefill
+  // GEMM's x' of [qrows, H * hd] rows (xt, xe, Mp of w4_gemm_prepare)
+  // instead of through `out`
+  uint4 *xt;
+  int *xe;
+  int Mp;
 };
 
 template <int DPL>
@@ -292,6 +298,18 @@ __global__ __launch_bounds__(256) void attn_rows_mfma_kernel(AttnArgs a) {
   const int keylen = a.pos_dev ? *a.pos_dev + a.qrows : a.keylen;
   const int nrows = a.qrows * H;
   const int R0 = blockIdx.x * kFaRows;
+  if (R0 >= nrows) {  // x' only: the GEMM's padding rows qrows .. Mp - 1 as zero chunks
+    if (!a.xt) return;
+    const int nch = H * (HD / 8), nq = kFaRows / H;
+    const size_t lo_plane = (size_t)nch * a.Mp;
+    for (int i = t; i < nq * nch; i += 256) {
+      const int qr = R0 / H + i / nch, ch = i % nch;
+      if (qr >= a.Mp) continue;
+      a.xt[(size_t)ch * a.Mp + qr] = make_uint4(0u, 0u, 0u, 0u);
+      a.xt[lo_plane + (size_t)ch * a.Mp + qr] = make_uint4(0u, 0u, 0u, 0u);
+    }
+    return;
+  }
   const int Rl = (R0 + kFaRows < nrows ? R0 + kFaRows : nrows) - 1;  // last live row
 
   for (int i = t; i < kFaRows * HD / 4; i += 256) {
@@ -491,15 +509,79 @@ __global__ __launch_bounds__(256) void attn_rows_mfma_kernel(AttnArgs a) {
     }
     __syncthreads();
   }
-  for (int i = t; i < kFaRows * HD / 4; i += 256) {
-    const int r = i / (HD / 4), d4 = i - r * (HD / 4);
+  if (!a.xt) {
+    for (int i = t; i < kFaRows * HD / 4; i += 256) {
+      const int r = i / (HD / 4), d4 = i - r * (HD / 4);
+      if (R0 + r >= nrows) continue;
+      const float M = fmaxf(fmaxf(wm[0][r], wm[1][r]), fmaxf(wm[2][r], wm[3][r]));
+      const float L = wl[0][r] * expf(wm[0][r] - M) + wl[1][r] * expf(wm[1][r] - M) +
+                      wl[2][r] * expf(wm[2][r] - M) + wl[3][r] * expf(wm[3][r] - M);
+      const float4 x = *reinterpret_cast<const float4 *>(&qs[r * QS + 4 * d4]);
+      reinterpret_cast<float4 *>(a.out + (size_t)(R0 + r) * HD)[d4] =
+          make_float4(x.x / L, x.y / L, x.z / L, x.w / L);
+    }
+    return;
+  }
+  // x' of the GEMM that takes these rows ([qrows, H * HD]; H divides 16, so
+  // the block holds whole query rows): the exponent of each query row from
+  // the maximum over its H heads, then the chunks of 8 values as FP16 hi/lo
+  // pairs (0,4) (1,5) (2,6) (3,7) of x * 2^-e, as gemm_xprep_fused_kernel
+  // writes them.  The values are the ones the rows above would hold.
+  __shared__ float rl[kFaRows];
+  __shared__ int qmax[kFaRows];
+  if (t < kFaRows) {
+    const float M = fmaxf(fmaxf(wm[0][t], wm[1][t]), fmaxf(wm[2][t], wm[3][t]));
+    rl[t] = wl[0][t] * expf(wm[0][t] - M) + wl[1][t] * expf(wm[1][t] - M) +
+            wl[2][t] * expf(wm[2][t] - M) + wl[3][t] * expf(wm[3][t] - M);
+    qmax[t] = 0;
+  }
+  __syncthreads();
+  constexpr int C8 = HD / 8;  // chunks per head
+  auto row_values = [&](int r, int c8, float (&v)[8]) {
+    const float L = rl[r];
+    const float4 x0 = *reinterpret_cast<const float4 *>(&qs[r * QS + 8 * c8]);
+    const float4 x1 = *reinterpret_cast<const float4 *>(&qs[r * QS + 8 * c8 + 4]);
+    v[0] = x0.x / L, v[1] = x0.y / L, v[2] = x0.z / L, v[3] = x0.w / L;
+    v[4] = x1.x / L, v[5] = x1.y / L, v[6] = x1.z / L, v[7] = x1.w / L;
+  };
+  for (int i = t; i < kFaRows * C8; i += 256) {
+    const int r = i / C8, c8 = i - r * C8;
     if (R0 + r >= nrows) continue;
-    const float M = fmaxf(fmaxf(wm[0][r], wm[1][r]), fmaxf(wm[2][r], wm[3][r]));
-    const float L = wl[0][r] * expf(wm[0][r] - M) + wl[1][r] * expf(wm[1][r] - M) +
-                    wl[2][r] * expf(wm[2][r] - M) + wl[3][r] * expf(wm[3][r] - M);
-    const float4 x = *reinterpret_cast<const float4 *>(&qs[r * QS + 4 * d4]);
-    reinterpret_cast<float4 *>(a.out + (size_t)(R0 + r) * HD)[d4] =
-        make_float4(x.x / L, x.y / L, x.z / L, x.w / L);
+    float v[8], mx = 0.f;
+    row_values(r, c8, v);
+#pragma unroll
+    for (int q = 0; q < 8; ++q) mx = fmaxf(mx, fabsf(v[q]));
+    atomicMax(&qmax[r / H], __float_as_int(mx));  // non-negative: ordered as ints
+  }
+  __syncthreads();
+  const int nch = H * C8;
+  const size_t lo_plane = (size_t)nch * a.Mp;
+  for (int i = t; i < kFaRows * C8; i += 256) {
+    const int r = i / C8, c8 = i - r * C8;
+    const int qr = (R0 + r) / H, ch = (r % H) * C8 + c8;  // R0 is a multiple of H
+    uint4 hi = make_uint4(0u, 0u, 0u, 0u), lo = hi;
+    if (R0 + r < nrows) {
+      const float mx = __int_as_float(qmax[r / H]);
+      const int e = mx > 0.f && mx <= 3.4e38f ? ilogbf(mx) - 13 : 0;
+      if (ch == 0) a.xe[qr] = e;
+      float v[8];
+      row_values(r, c8, v);
+      _Float16 hh[8], ll[8];
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        const float sv = ldexpf(v[q], -e);
+        hh[q] = (_Float16)sv;
+        ll[q] = (_Float16)(sv - (float)hh[q]);
+      }
+      hi = make_uint4(half2_bits(hh[0], hh[4]), half2_bits(hh[1], hh[5]), half2_bits(hh[2], hh[6]),
+                      half2_bits(hh[3], hh[7]));
+      lo = make_uint4(half2_bits(ll[0], ll[4]), half2_bits(ll[1], ll[5]), half2_bits(ll[2], ll[6]),
+                      half2_bits(ll[3], ll[7]));
+    }
+    if (qr < a.Mp) {
+      a.xt[(size_t)ch * a.Mp + qr] = hi;
+      a.xt[lo_plane + (size_t)ch * a.Mp + qr] = lo;
+    }
   }
 }
 
@@ -850,7 +932,9 @@ size_t attention_part_floats(int qrows, int heads, int hd, int max_keylen, int k
 
 int launch_attention(const float *q, const float *k, const float *v, int qrows, int heads,
                      int hd, int keylen, int qpos0, const int *pos_dev, int max_keylen,
-                     bool sliding, int window, int kpw, float *part, float *out) {
+                     bool sliding, int window, int kpw, float *part, float *out, void *xt,
+                     int *xe, int Mp, bool *x_done) {
+  if (x_done) *x_done = false;
   if (qrows == 0) return G4_OK;
   if (max_keylen > kDecMaxKeys * kMaxSplits)
     return fail(G4_E_ARG, "attention: %d keys exceed the supported %d", max_keylen,
@@ -890,10 +974,21 @@ int launch_attention(const float *q, const float *k, const float *v, int qrows, 
   a.nsplit = (max_keylen + kpw - 1) / kpw;
   a.pos_dev = pos_dev;
   a.qrows = qrows;
+  a.xt = nullptr;
+  a.xe = nullptr;
+  a.Mp = 0;
   // Many rows, or few keys: the matrix-core kernel (16 rows per block, no
   // merge pass).  A handful of rows over a long cache keeps the key split.
   if ((size_t)qrows * heads >= 64 || max_keylen <= 512) {
-    const dim3 fgrid((qrows * heads + kFaRows - 1) / kFaRows);
+    // x' for the next GEMM when asked for and the block's 16 rows hold whole
+    // query rows; the grid then also covers the GEMM's padding rows
+    const bool xprep = xt && x_done && kFaRows % heads == 0 && Mp >= qrows && Mp % 16 == 0;
+    if (xprep) {
+      a.xt = static_cast<uint4 *>(xt);
+      a.xe = xe;
+      a.Mp = Mp;
+    }
+    const dim3 fgrid(((xprep ? Mp : qrows) * heads + kFaRows - 1) / kFaRows);
     switch (hd) {
       case 64: hipLaunchKernelGGL(attn_rows_mfma_kernel<64>, fgrid, dim3(256), 0, stream(), a); break;
       case 128: hipLaunchKernelGGL(attn_rows_mfma_kernel<128>, fgrid, dim3(256), 0, stream(), a); break;
@@ -902,6 +997,7 @@ int launch_attention(const float *q, const float *k, const float *v, int qrows, 
       default: return fail(G4_E_ARG, "attention: head_dim %d must be 64, 128, 256 or 512", hd);
     }
     G4_LAUNCH_CHECK("attn_rows_mfma_kernel");
+    if (xprep) *x_done = true;
     return G4_OK;
   }
   const dim3 grid(a.nsplit, qrows);
