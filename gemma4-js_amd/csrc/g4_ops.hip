@@ -272,7 +272,8 @@ __global__ __launch_bounds__(64) void attn_split_kernel(AttnArgs a) {
 // are clamped into the visible range, so rows past keylen are never read.
 // The 4 waves' (max, sum, O) merge in LDS in wave order; the block writes the
 // normalised rows.  The arithmetic is the reference's softmax(q.k) . v; only
-// the summation order differs (MFMA dot chunks, online rescaling).
+// the summation order differs (MFMA dot chunks, online rescaling).  Head dims
+// up to 256; head dim 512 runs attn_rows_dsplit_kernel.
 template <typename F>
 __device__ __forceinline__ float row16_reduce(float v, F op) {
   v = op(v, dpp_f32<0xB1>(v));   // quad_perm [1,0,3,2]
@@ -284,231 +285,17 @@ __device__ __forceinline__ float row16_reduce(float v, F op) {
 
 constexpr int kFaRows = 16, kFaWaves = 4, kFaPStride = 20;
 
+// The rows of a 16-row attention block: qs holds each row's unnormalised O
+// (padded stride HD + 4) and wm / wl the per-wave (max, sum) to merge with
+// weights e^(m_w - M).  Writes the normalised rows to a.out, or with a.xt set
+// the x' of the GEMM that takes them.
 template <int HD>
-__global__ __launch_bounds__(256) void attn_rows_mfma_kernel(AttnArgs a) {
-  constexpr int QS = HD + 4;  // padded LDS row (floats): conflict-free 16-byte reads
-  constexpr int NT = HD / 16;
-  __shared__ float qs[kFaRows * QS];                 // the Q tile, later the merged O
-  __shared__ float ps[kFaWaves][kFaRows * kFaPStride];  // per wave: P[row][g * 4 + s]
-  __shared__ float wm[kFaWaves][kFaRows], wl[kFaWaves][kFaRows];
-  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
-  const int c = lane & 15, g = lane >> 4;
+__device__ __forceinline__ void attn_rows_store(const AttnArgs &a, const float *qs,
+                                                const float (*wm)[kFaRows],
+                                                const float (*wl)[kFaRows], int R0, int nrows,
+                                                int t) {
+  constexpr int QS = HD + 4;
   const int H = a.H;
-  const int qpos0 = a.pos_dev ? *a.pos_dev : a.qpos0;
-  const int keylen = a.pos_dev ? *a.pos_dev + a.qrows : a.keylen;
-  const int nrows = a.qrows * H;
-  const int R0 = blockIdx.x * kFaRows;
-  if (R0 >= nrows) {  // x' only: the GEMM's padding rows qrows .. Mp - 1 as zero chunks
-    if (!a.xt) return;
-    const int nch = H * (HD / 8), nq = kFaRows / H;
-    const size_t lo_plane = (size_t)nch * a.Mp;
-    for (int i = t; i < nq * nch; i += 256) {
-      const int qr = R0 / H + i / nch, ch = i % nch;
-      if (qr >= a.Mp) continue;
-      a.xt[(size_t)ch * a.Mp + qr] = make_uint4(0u, 0u, 0u, 0u);
-      a.xt[lo_plane + (size_t)ch * a.Mp + qr] = make_uint4(0u, 0u, 0u, 0u);
-    }
-    return;
-  }
-  const int Rl = (R0 + kFaRows < nrows ? R0 + kFaRows : nrows) - 1;  // last live row
-
-  for (int i = t; i < kFaRows * HD / 4; i += 256) {
-    const int r = i / (HD / 4), d4 = i - r * (HD / 4);
-    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (R0 + r < nrows) v = reinterpret_cast<const float4 *>(a.q + (size_t)(R0 + r) * HD)[d4];
-    *reinterpret_cast<float4 *>(&qs[r * QS + 4 * d4]) = v;
-  }
-  // keys of the block's rows: [kmin, kmax]
-  const int pos_first = qpos0 + R0 / H, pos_last = qpos0 + Rl / H;
-  int kmin = a.sliding ? pos_first - a.window + 1 : 0;
-  kmin = kmin > 0 ? kmin : 0;
-  const int kmax = pos_last < keylen - 1 ? pos_last : keylen - 1;
-  int rpos[4];
-  bool rlive[4];
-#pragma unroll
-  for (int v = 0; v < 4; ++v) {
-    const int R = R0 + 4 * g + v;
-    rlive[v] = R < nrows;
-    rpos[v] = qpos0 + (rlive[v] ? R : Rl) / H;
-  }
-  float m[4] = {-1e30f, -1e30f, -1e30f, -1e30f}, l[4] = {0.f, 0.f, 0.f, 0.f};
-  f32x4 o[NT];
-#pragma unroll
-  for (int n = 0; n < NT; ++n) o[n] = (f32x4){0.f, 0.f, 0.f, 0.f};
-  __syncthreads();
-
-  float *pw = ps[w];
-  if constexpr (HD <= 256) {
-    // The next key tile's K is loaded once this tile's scores are formed, its V
-    // once this tile's P.V is done: each load has a phase of work to land in
-    // (tile indices past the last re-read the last tile).
-    constexpr int NV = HD / 64;
-    const int kt_last = kmax / 16;
-    float4 kr[NT], vr[4][NV];
-    auto load_k = [&](int kt) {
-      kt = kt < kt_last ? kt : kt_last;
-      const int kc = kt * 16 + c < kmax ? kt * 16 + c : kmax;
-      const float *kp = a.k + (size_t)kc * HD + 4 * g;
-#pragma unroll
-      for (int j = 0; j < NT; ++j) kr[j] = *reinterpret_cast<const float4 *>(kp + 16 * j);
-    };
-    auto load_v = [&](int kt) {
-      kt = kt < kt_last ? kt : kt_last;
-#pragma unroll
-      for (int sp = 0; sp < 4; ++sp) {
-        const int kr2 = kt * 16 + 4 * sp + g < kmax ? kt * 16 + 4 * sp + g : kmax;
-        const float *vp = a.v + (size_t)kr2 * HD + 4 * c;
-#pragma unroll
-        for (int q = 0; q < NV; ++q) vr[sp][q] = *reinterpret_cast<const float4 *>(vp + 64 * q);
-      }
-    };
-    int kt = kmin / 16 + w;
-    load_k(kt);
-    load_v(kt);
-    for (; kt <= kt_last; kt += kFaWaves) {
-      const int key0 = kt * 16;
-      const float *qp = &qs[c * QS + 4 * g];
-      f32x4 sa[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) sa[i] = (f32x4){0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int j = 0; j < NT; ++j) {
-        const float4 kv = kr[j];
-        const float4 qv = *reinterpret_cast<const float4 *>(qp + 16 * j);
-        sa[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(qv.x, kv.x, sa[0], 0, 0, 0);
-        sa[1] = __builtin_amdgcn_mfma_f32_16x16x4f32(qv.y, kv.y, sa[1], 0, 0, 0);
-        sa[2] = __builtin_amdgcn_mfma_f32_16x16x4f32(qv.z, kv.z, sa[2], 0, 0, 0);
-        sa[3] = __builtin_amdgcn_mfma_f32_16x16x4f32(qv.w, kv.w, sa[3], 0, 0, 0);
-      }
-      load_k(kt + kFaWaves);
-      const f32x4 s = (sa[0] + sa[1]) + (sa[2] + sa[3]);
-      const int key = key0 + c;
-      float corr[4];
-#pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const bool ok = rlive[v] && key <= rpos[v] && key < keylen &&
-                        (!a.sliding || key > rpos[v] - a.window);
-        const float tm = row16_reduce(ok ? s[v] : -1e30f, [](float x, float y) { return fmaxf(x, y); });
-        const float mn = fmaxf(m[v], tm);
-        corr[v] = expf(m[v] - mn);
-        const float p = ok ? expf(s[v] - mn) : 0.f;
-        l[v] = l[v] * corr[v] + row16_reduce(p, [](float x, float y) { return x + y; });
-        m[v] = mn;
-        pw[(4 * g + v) * kFaPStride + (c & 3) * 4 + (c >> 2)] = p;
-      }
-#pragma unroll
-      for (int n = 0; n < NT; ++n)
-#pragma unroll
-        for (int v = 0; v < 4; ++v) o[n][v] *= corr[v];
-      const float4 pa = *reinterpret_cast<const float4 *>(&pw[c * kFaPStride + 4 * g]);
-      const float pv[4] = {pa.x, pa.y, pa.z, pa.w};
-#pragma unroll
-      for (int sp = 0; sp < 4; ++sp)
-#pragma unroll
-        for (int q = 0; q < NV; ++q) {
-          const float4 vv = vr[sp][q];
-          o[4 * q + 0] = __builtin_amdgcn_mfma_f32_16x16x4f32(pv[sp], vv.x, o[4 * q + 0], 0, 0, 0);
-          o[4 * q + 1] = __builtin_amdgcn_mfma_f32_16x16x4f32(pv[sp], vv.y, o[4 * q + 1], 0, 0, 0);
-          o[4 * q + 2] = __builtin_amdgcn_mfma_f32_16x16x4f32(pv[sp], vv.z, o[4 * q + 2], 0, 0, 0);
-          o[4 * q + 3] = __builtin_amdgcn_mfma_f32_16x16x4f32(pv[sp], vv.w, o[4 * q + 3], 0, 0, 0);
-        }
-      load_v(kt + kFaWaves);
-    }
-  } else {  // head dim 512: the prefetch registers would spill
-    for (int kt = kmin / 16 + w; kt <= kmax / 16; kt += kFaWaves) {
-      const int key0 = kt * 16;
-      // S = Q . K^T
-      const int kc = key0 + c < kmax ? key0 + c : kmax;
-      const float *kp = a.k + (size_t)kc * HD + 4 * g;
-      const float *qp = &qs[c * QS + 4 * g];
-      // four independent accumulators (dims 16j + 4g + i, i = 0..3), added
-      // pairwise: shorter rounding chains, and the MFMAs do not wait on each other
-      f32x4 sa[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) sa[i] = (f32x4){0.f, 0.f, 0.f, 0.f};
-#pragma unroll 8
-      for (int j = 0; j < NT; ++j) {
-        const float4 kv = *reinterpret_cast<const float4 *>(kp + 16 * j);
-        const float4 qv = *reinterpret_cast<const float4 *>(qp + 16 * j);
-        sa[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(qv.x, kv.x, sa[0], 0, 0, 0);
-        sa[1] = __builtin_amdgcn_mfma_f32_16x16x4f32(qv.y, kv.y, sa[1], 0, 0, 0);
-        sa[2] = __builtin_amdgcn_mfma_f32_16x16x4f32(qv.z, kv.z, sa[2], 0, 0, 0);
-        sa[3] = __builtin_amdgcn_mfma_f32_16x16x4f32(qv.w, kv.w, sa[3], 0, 0, 0);
-      }
-      const f32x4 s = (sa[0] + sa[1]) + (sa[2] + sa[3]);
-      // online softmax: lane (c, g) holds S[row 4g + v][key key0 + c]
-      const int key = key0 + c;
-      float corr[4];
-#pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const bool ok = rlive[v] && key <= rpos[v] && key < keylen &&
-                        (!a.sliding || key > rpos[v] - a.window);
-        const float tm = row16_reduce(ok ? s[v] : -1e30f, [](float x, float y) { return fmaxf(x, y); });
-        const float mn = fmaxf(m[v], tm);
-        corr[v] = expf(m[v] - mn);
-        const float p = ok ? expf(s[v] - mn) : 0.f;
-        l[v] = l[v] * corr[v] + row16_reduce(p, [](float x, float y) { return x + y; });
-        m[v] = mn;
-        pw[(4 * g + v) * kFaPStride + (c & 3) * 4 + (c >> 2)] = p;
-      }
-#pragma unroll
-      for (int n = 0; n < NT; ++n)
-#pragma unroll
-        for (int v = 0; v < 4; ++v) o[n][v] *= corr[v];
-      // P in the A layout: lane (c, g) holds P[row c][key 4 s + g], s = 0..3
-      const float4 pa = *reinterpret_cast<const float4 *>(&pw[c * kFaPStride + 4 * g]);
-      const float pv[4] = {pa.x, pa.y, pa.z, pa.w};
-      // O += P . V
-#pragma unroll
-      for (int sp = 0; sp < 4; ++sp) {
-        const int kr = key0 + 4 * sp + g < kmax ? key0 + 4 * sp + g : kmax;
-        const float *vp = a.v + (size_t)kr * HD + 4 * c;
-#pragma unroll
-        for (int q = 0; q < HD / 64; ++q) {
-          const float4 vv = *reinterpret_cast<const float4 *>(vp + 64 * q);
-          o[4 * q + 0] = __builtin_amdgcn_mfma_f32_16x16x4f32(pv[sp], vv.x, o[4 * q + 0], 0, 0, 0);
-          o[4 * q + 1] = __builtin_amdgcn_mfma_f32_16x16x4f32(pv[sp], vv.y, o[4 * q + 1], 0, 0, 0);
-          o[4 * q + 2] = __builtin_amdgcn_mfma_f32_16x16x4f32(pv[sp], vv.z, o[4 * q + 2], 0, 0, 0);
-          o[4 * q + 3] = __builtin_amdgcn_mfma_f32_16x16x4f32(pv[sp], vv.w, o[4 * q + 3], 0, 0, 0);
-        }
-      }
-    }
-  }
-
-  // merge the waves: weights e^(m_w - M), O summed into qs in wave order
-  if (c == 0)
-#pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      wm[w][4 * g + v] = m[v];
-      wl[w][4 * g + v] = l[v];
-    }
-  __syncthreads();
-  float f[4];
-#pragma unroll
-  for (int v = 0; v < 4; ++v) {
-    const int r = 4 * g + v;
-    const float M = fmaxf(fmaxf(wm[0][r], wm[1][r]), fmaxf(wm[2][r], wm[3][r]));
-    f[v] = expf(m[v] - M);
-  }
-  for (int ww = 0; ww < kFaWaves; ++ww) {
-    if (w == ww) {
-#pragma unroll
-      for (int q = 0; q < HD / 64; ++q)
-#pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          float4 *dst = reinterpret_cast<float4 *>(&qs[(4 * g + v) * QS + 64 * q + 4 * c]);
-          const float4 add = make_float4(o[4 * q][v] * f[v], o[4 * q + 1][v] * f[v],
-                                         o[4 * q + 2][v] * f[v], o[4 * q + 3][v] * f[v]);
-          if (ww == 0) {
-            *dst = add;
-          } else {
-            const float4 cur = *dst;
-            *dst = make_float4(cur.x + add.x, cur.y + add.y, cur.z + add.z, cur.w + add.w);
-          }
-        }
-    }
-    __syncthreads();
-  }
   if (!a.xt) {
     for (int i = t; i < kFaRows * HD / 4; i += 256) {
       const int r = i / (HD / 4), d4 = i - r * (HD / 4);
@@ -585,6 +372,176 @@ __global__ __launch_bounds__(256) void attn_rows_mfma_kernel(AttnArgs a) {
   }
 }
 
+template <int HD>
+__global__ __launch_bounds__(256) void attn_rows_mfma_kernel(AttnArgs a) {
+  constexpr int QS = HD + 4;  // padded LDS row (floats): conflict-free 16-byte reads
+  constexpr int NT = HD / 16;
+  __shared__ float qs[kFaRows * QS];                 // the Q tile, later the merged O
+  __shared__ float ps[kFaWaves][kFaRows * kFaPStride];  // per wave: P[row][g * 4 + s]
+  __shared__ float wm[kFaWaves][kFaRows], wl[kFaWaves][kFaRows];
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+  const int c = lane & 15, g = lane >> 4;
+  const int H = a.H;
+  const int qpos0 = a.pos_dev ? *a.pos_dev : a.qpos0;
+  const int keylen = a.pos_dev ? *a.pos_dev + a.qrows : a.keylen;
+  const int nrows = a.qrows * H;
+  const int R0 = blockIdx.x * kFaRows;
+  if (R0 >= nrows) {  // x' only: the GEMM's padding rows qrows .. Mp - 1 as zero chunks
+    if (!a.xt) return;
+    const int nch = H * (HD / 8), nq = kFaRows / H;
+    const size_t lo_plane = (size_t)nch * a.Mp;
+    for (int i = t; i < nq * nch; i += 256) {
+      const int qr = R0 / H + i / nch, ch = i % nch;
+      if (qr >= a.Mp) continue;
+      a.xt[(size_t)ch * a.Mp + qr] = make_uint4(0u, 0u, 0u, 0u);
+      a.xt[lo_plane + (size_t)ch * a.Mp + qr] = make_uint4(0u, 0u, 0u, 0u);
+    }
+    return;
+  }
+  const int Rl = (R0 + kFaRows < nrows ? R0 + kFaRows : nrows) - 1;  // last live row
+
+  for (int i = t; i < kFaRows * HD / 4; i += 256) {
+    const int r = i / (HD / 4), d4 = i - r * (HD / 4);
+    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (R0 + r < nrows) v = reinterpret_cast<const float4 *>(a.q + (size_t)(R0 + r) * HD)[d4];
+    *reinterpret_cast<float4 *>(&qs[r * QS + 4 * d4]) = v;
+  }
+  // keys of the block's rows: [kmin, kmax]
+  const int pos_first = qpos0 + R0 / H, pos_last = qpos0 + Rl / H;
+  int kmin = a.sliding ? pos_first - a.window + 1 : 0;
+  kmin = kmin > 0 ? kmin : 0;
+  const int kmax = pos_last < keylen - 1 ? pos_last : keylen - 1;
+  int rpos[4];
+  bool rlive[4];
+#pragma unroll
+  for (int v = 0; v < 4; ++v) {
+    const int R = R0 + 4 * g + v;
+    rlive[v] = R < nrows;
+    rpos[v] = qpos0 + (rlive[v] ? R : Rl) / H;
+  }
+  float m[4] = {-1e30f, -1e30f, -1e30f, -1e30f}, l[4] = {0.f, 0.f, 0.f, 0.f};
+  f32x4 o[NT];
+#pragma unroll
+  for (int n = 0; n < NT; ++n) o[n] = (f32x4){0.f, 0.f, 0.f, 0.f};
+  __syncthreads();
+
+  float *pw = ps[w];
+  static_assert(HD <= 256, "head dim 512 runs attn_rows_dsplit_kernel");
+  {
+    // The next key tile's K is loaded once this tile's scores are formed, its V
+    // once this tile's P.V is done: each load has a phase of work to land in
+    // (tile indices past the last re-read the last tile).
+    constexpr int NV = HD / 64;
+    const int kt_last = kmax / 16;
+    float4 kr[NT], vr[4][NV];
+    auto load_k = [&](int kt) {
+      kt = kt < kt_last ? kt : kt_last;
+      const int kc = kt * 16 + c < kmax ? kt * 16 + c : kmax;
+      const float *kp = a.k + (size_t)kc * HD + 4 * g;
+#pragma unroll
+      for (int j = 0; j < NT; ++j) kr[j] = *reinterpret_cast<const float4 *>(kp + 16 * j);
+    };
+    auto load_v = [&](int kt) {
+      kt = kt < kt_last ? kt : kt_last;
+#pragma unroll
+      for (int sp = 0; sp < 4; ++sp) {
+        const int kr2 = kt * 16 + 4 * sp + g < kmax ? kt * 16 + 4 * sp + g : kmax;
+        const float *vp = a.v + (size_t)kr2 * HD + 4 * c;
+#pragma unroll
+        for (int q = 0; q < NV; ++q) vr[sp][q] = *reinterpret_cast<const float4 *>(vp + 64 * q);
+      }
+    };
+    int kt = kmin / 16 + w;
+    load_k(kt);
+    load_v(kt);
+    for (; kt <= kt_last; kt += kFaWaves) {
+      const int key0 = kt * 16;
+      const float *qp = &qs[c * QS + 4 * g];
+      f32x4 sa[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) sa[i] = (f32x4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int j = 0; j < NT; ++j) {
+        const float4 kv = kr[j];
+        const float4 qv = *reinterpret_cast<const float4 *>(qp + 16 * j);
+        sa[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(qv.x, kv.x, sa[0], 0, 0, 0);
+        sa[1] = __builtin_amdgcn_mfma_f32_16x16x4f32(qv.y, kv.y, sa[1], 0, 0, 0);
+        sa[2] = __builtin_amdgcn_mfma_f32_16x16x4f32(qv.z, kv.z, sa[2], 0, 0, 0);
+        sa[3] = __builtin_amdgcn_mfma_f32_16x16x4f32(qv.w, kv.w, sa[3], 0, 0, 0);
+      }
+      load_k(kt + kFaWaves);
+      const f32x4 s = (sa[0] + sa[1]) + (sa[2] + sa[3]);
+      const int key = key0 + c;
+      float corr[4];
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const bool ok = rlive[v] && key <= rpos[v] && key < keylen &&
+                        (!a.sliding || key > rpos[v] - a.window);
+        const float tm = row16_reduce(ok ? s[v] : -1e30f, [](float x, float y) { return fmaxf(x, y); });
+        const float mn = fmaxf(m[v], tm);
+        corr[v] = expf(m[v] - mn);
+        const float p = ok ? expf(s[v] - mn) : 0.f;
+        l[v] = l[v] * corr[v] + row16_reduce(p, [](float x, float y) { return x + y; });
+        m[v] = mn;
+        pw[(4 * g + v) * kFaPStride + (c & 3) * 4 + (c >> 2)] = p;
+      }
+#pragma unroll
+      for (int n = 0; n < NT; ++n)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) o[n][v] *= corr[v];
+      const float4 pa = *reinterpret_cast<const float4 *>(&pw[c * kFaPStride + 4 * g]);
+      const float pv[4] = {pa.x, pa.y, pa.z, pa.w};
+#pragma unroll
+      for (int sp = 0; sp < 4; ++sp)
+#pragma unroll
+        for (int q = 0; q < NV; ++q) {
+          const float4 vv = vr[sp][q];
+          o[4 * q + 0] = __builtin_amdgcn_mfma_f32_16x16x4f32(pv[sp], vv.x, o[4 * q + 0], 0, 0, 0);
+          o[4 * q + 1] = __builtin_amdgcn_mfma_f32_16x16x4f32(pv[sp], vv.y, o[4 * q + 1], 0, 0, 0);
+          o[4 * q + 2] = __builtin_amdgcn_mfma_f32_16x16x4f32(pv[sp], vv.z, o[4 * q + 2], 0, 0, 0);
+          o[4 * q + 3] = __builtin_amdgcn_mfma_f32_16x16x4f32(pv[sp], vv.w, o[4 * q + 3], 0, 0, 0);
+        }
+      load_v(kt + kFaWaves);
+    }
+  }
+
+  // merge the waves: weights e^(m_w - M), O summed into qs in wave order
+  if (c == 0)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      wm[w][4 * g + v] = m[v];
+      wl[w][4 * g + v] = l[v];
+    }
+  __syncthreads();
+  float f[4];
+#pragma unroll
+  for (int v = 0; v < 4; ++v) {
+    const int r = 4 * g + v;
+    const float M = fmaxf(fmaxf(wm[0][r], wm[1][r]), fmaxf(wm[2][r], wm[3][r]));
+    f[v] = expf(m[v] - M);
+  }
+  for (int ww = 0; ww < kFaWaves; ++ww) {
+    if (w == ww) {
+#pragma unroll
+      for (int q = 0; q < HD / 64; ++q)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          float4 *dst = reinterpret_cast<float4 *>(&qs[(4 * g + v) * QS + 64 * q + 4 * c]);
+          const float4 add = make_float4(o[4 * q][v] * f[v], o[4 * q + 1][v] * f[v],
+                                         o[4 * q + 2][v] * f[v], o[4 * q + 3][v] * f[v]);
+          if (ww == 0) {
+            *dst = add;
+          } else {
+            const float4 cur = *dst;
+            *dst = make_float4(cur.x + add.x, cur.y + add.y, cur.z + add.z, cur.w + add.w);
+          }
+        }
+    }
+    __syncthreads();
+  }
+  attn_rows_store<HD>(a, qs, wm, wl, R0, nrows, t);
+}
+
 // Single-query attention (a decode step): the visible keys [lo, keylen) are
 // split evenly over the grid (at most kDecMaxKeys per block).  Block = 4
 // waves.  Phase 1: each wave takes every 4th key of the block; lane l holds
@@ -595,6 +552,165 @@ __global__ __launch_bounds__(256) void attn_rows_mfma_kernel(AttnArgs a) {
 // Phase 3: per head, 32 threads each accumulate hd/32 output dims over the
 // block's keys.  Every block writes (max, sum, output) per head, an empty
 // block (max -1e30, sum 0): attn_combine_kernel merges them.
+// The same rows with the head dimension split over the block's waves, for
+// large head dims: every wave walks every key tile of the block's rows and
+// owns dims [w DW, (w + 1) DW) of q, k, v and O (DW = HD / 4):
+//   S_w = Q[:, dims_w] . K[:, dims_w]^T   DW/4 MFMAs; the four partial S
+//        meet in LDS and every wave adds them in wave order, so all hold
+//        the same S and the same softmax (max, sum, P)
+//   O[:, dims_w] += P . V[:, dims_w]      DW/4 MFMAs
+// A wave's registers hold a quarter of the row's O and its k/v slices, so
+// the next tile's K and V are loaded during the current one.  No merge of
+// the waves is needed: O goes to LDS by dims and leaves through
+// attn_rows_store.
+template <int HD>
+__global__ __launch_bounds__(256) void attn_rows_dsplit_kernel(AttnArgs a) {
+  constexpr int QS = HD + 4;
+  constexpr int DW = HD / kFaWaves;  // dims per wave
+  constexpr int NJ = DW / 16;        // S steps of 16 dims (4 MFMAs each)
+  constexpr int NQ = DW / 64;        // 64-dim column groups of O per wave
+  __shared__ float qs[kFaRows * QS];  // the Q tile, later O
+  __shared__ f32x4 sx[2][kFaWaves][64];  // partial S per wave (two buffers)
+  __shared__ float ps[kFaWaves][kFaRows * kFaPStride];
+  __shared__ float wm[kFaWaves][kFaRows], wl[kFaWaves][kFaRows];
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+  const int c = lane & 15, g = lane >> 4;
+  const int H = a.H;
+  const int qpos0 = a.pos_dev ? *a.pos_dev : a.qpos0;
+  const int keylen = a.pos_dev ? *a.pos_dev + a.qrows : a.keylen;
+  const int nrows = a.qrows * H;
+  const int R0 = blockIdx.x * kFaRows;
+  if (R0 >= nrows) {  // x' only: the GEMM's padding rows qrows .. Mp - 1 as zero chunks
+    if (!a.xt) return;
+    const int nch = H * (HD / 8), nq = kFaRows / H;
+    const size_t lo_plane = (size_t)nch * a.Mp;
+    for (int i = t; i < nq * nch; i += 256) {
+      const int qr = R0 / H + i / nch, ch = i % nch;
+      if (qr >= a.Mp) continue;
+      a.xt[(size_t)ch * a.Mp + qr] = make_uint4(0u, 0u, 0u, 0u);
+      a.xt[lo_plane + (size_t)ch * a.Mp + qr] = make_uint4(0u, 0u, 0u, 0u);
+    }
+    return;
+  }
+  const int Rl = (R0 + kFaRows < nrows ? R0 + kFaRows : nrows) - 1;  // last live row
+  for (int i = t; i < kFaRows * HD / 4; i += 256) {
+    const int r = i / (HD / 4), d4 = i - r * (HD / 4);
+    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (R0 + r < nrows) v = reinterpret_cast<const float4 *>(a.q + (size_t)(R0 + r) * HD)[d4];
+    *reinterpret_cast<float4 *>(&qs[r * QS + 4 * d4]) = v;
+  }
+  const int pos_first = qpos0 + R0 / H, pos_last = qpos0 + Rl / H;
+  int kmin = a.sliding ? pos_first - a.window + 1 : 0;
+  kmin = kmin > 0 ? kmin : 0;
+  const int kmax = pos_last < keylen - 1 ? pos_last : keylen - 1;
+  int rpos[4];
+  bool rlive[4];
+#pragma unroll
+  for (int v = 0; v < 4; ++v) {
+    const int R = R0 + 4 * g + v;
+    rlive[v] = R < nrows;
+    rpos[v] = qpos0 + (rlive[v] ? R : Rl) / H;
+  }
+  __syncthreads();
+  const int d0 = w * DW;
+  float4 qr[NJ];  // lane (c, g): Q row c, dims d0 + 16 j + 4 g .. + 3
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) qr[j] = *reinterpret_cast<const float4 *>(&qs[c * QS + d0 + 16 * j + 4 * g]);
+  float m[4] = {-1e30f, -1e30f, -1e30f, -1e30f}, l[4] = {0.f, 0.f, 0.f, 0.f};
+  f32x4 o[4 * NQ];  // output tile 4q + e, column c: dim d0 + 64 q + 4 c + e
+#pragma unroll
+  for (int n = 0; n < 4 * NQ; ++n) o[n] = (f32x4){0.f, 0.f, 0.f, 0.f};
+  const int kt0 = kmin / 16, kt1 = kmax / 16;
+  float4 kr[NJ], vr[4][NQ];
+  // the next tile's K once this tile's partial S is formed, its V once this
+  // tile's P.V is done (past the last tile, the last one again)
+  auto load_k = [&](int kt) {
+    kt = kt < kt1 ? kt : kt1;
+    const int kc = kt * 16 + c < kmax ? kt * 16 + c : kmax;
+    const float *kp = a.k + (size_t)kc * HD + d0 + 4 * g;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) kr[j] = *reinterpret_cast<const float4 *>(kp + 16 * j);
+  };
+  auto load_v = [&](int kt) {
+    kt = kt < kt1 ? kt : kt1;
+#pragma unroll
+    for (int sp = 0; sp < 4; ++sp) {
+      const int kv = kt * 16 + 4 * sp + g < kmax ? kt * 16 + 4 * sp + g : kmax;
+      const float *vp = a.v + (size_t)kv * HD + d0 + 4 * c;
+#pragma unroll
+      for (int q = 0; q < NQ; ++q) vr[sp][q] = *reinterpret_cast<const float4 *>(vp + 64 * q);
+    }
+  };
+  load_k(kt0);
+  load_v(kt0);
+  float *pw = ps[w];
+  for (int kt = kt0; kt <= kt1; ++kt) {
+    const int b = (kt - kt0) & 1;
+    f32x4 sa[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) sa[i] = (f32x4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      const float4 kv = kr[j], qv = qr[j];
+      sa[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(qv.x, kv.x, sa[0], 0, 0, 0);
+      sa[1] = __builtin_amdgcn_mfma_f32_16x16x4f32(qv.y, kv.y, sa[1], 0, 0, 0);
+      sa[2] = __builtin_amdgcn_mfma_f32_16x16x4f32(qv.z, kv.z, sa[2], 0, 0, 0);
+      sa[3] = __builtin_amdgcn_mfma_f32_16x16x4f32(qv.w, kv.w, sa[3], 0, 0, 0);
+    }
+    load_k(kt + 1);
+    sx[b][w][lane] = (sa[0] + sa[1]) + (sa[2] + sa[3]);
+    __syncthreads();
+    const f32x4 s = ((sx[b][0][lane] + sx[b][1][lane]) + sx[b][2][lane]) + sx[b][3][lane];
+    const int key = kt * 16 + c;
+    float corr[4];
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const bool ok = rlive[v] && key <= rpos[v] && key < keylen &&
+                      (!a.sliding || key > rpos[v] - a.window);
+      const float tm = row16_reduce(ok ? s[v] : -1e30f, [](float x, float y) { return fmaxf(x, y); });
+      const float mn = fmaxf(m[v], tm);
+      corr[v] = expf(m[v] - mn);
+      const float p = ok ? expf(s[v] - mn) : 0.f;
+      l[v] = l[v] * corr[v] + row16_reduce(p, [](float x, float y) { return x + y; });
+      m[v] = mn;
+      pw[(4 * g + v) * kFaPStride + (c & 3) * 4 + (c >> 2)] = p;
+    }
+#pragma unroll
+    for (int n = 0; n < 4 * NQ; ++n)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) o[n][v] *= corr[v];
+    const float4 pa = *reinterpret_cast<const float4 *>(&pw[c * kFaPStride + 4 * g]);
+    const float pv[4] = {pa.x, pa.y, pa.z, pa.w};
+#pragma unroll
+    for (int sp = 0; sp < 4; ++sp)
+#pragma unroll
+      for (int q = 0; q < NQ; ++q) {
+        const float4 vv = vr[sp][q];
+        o[4 * q + 0] = __builtin_amdgcn_mfma_f32_16x16x4f32(pv[sp], vv.x, o[4 * q + 0], 0, 0, 0);
+        o[4 * q + 1] = __builtin_amdgcn_mfma_f32_16x16x4f32(pv[sp], vv.y, o[4 * q + 1], 0, 0, 0);
+        o[4 * q + 2] = __builtin_amdgcn_mfma_f32_16x16x4f32(pv[sp], vv.z, o[4 * q + 2], 0, 0, 0);
+        o[4 * q + 3] = __builtin_amdgcn_mfma_f32_16x16x4f32(pv[sp], vv.w, o[4 * q + 3], 0, 0, 0);
+      }
+    load_v(kt + 1);
+  }
+  // O by dims into qs, (max, sum) as wave 0's with the other waves' weights 0
+  __syncthreads();
+#pragma unroll
+  for (int v = 0; v < 4; ++v)
+#pragma unroll
+    for (int q = 0; q < NQ; ++q)
+      *reinterpret_cast<float4 *>(&qs[(4 * g + v) * QS + d0 + 64 * q + 4 * c]) =
+          make_float4(o[4 * q][v], o[4 * q + 1][v], o[4 * q + 2][v], o[4 * q + 3][v]);
+  if (c == 0)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      wm[w][4 * g + v] = w == 0 ? m[v] : -1e30f;
+      wl[w][4 * g + v] = w == 0 ? l[v] : 0.f;
+    }
+  __syncthreads();
+  attn_rows_store<HD>(a, qs, wm, wl, R0, nrows, t);
+}
+
 constexpr int kDecMaxKeys = 16;
 constexpr int kMaxSplits = 1024;
 
@@ -993,7 +1109,7 @@ int launch_attention(const float *q, const float *k, const float *v, int qrows, 
       case 64: hipLaunchKernelGGL(attn_rows_mfma_kernel<64>, fgrid, dim3(256), 0, stream(), a); break;
       case 128: hipLaunchKernelGGL(attn_rows_mfma_kernel<128>, fgrid, dim3(256), 0, stream(), a); break;
       case 256: hipLaunchKernelGGL(attn_rows_mfma_kernel<256>, fgrid, dim3(256), 0, stream(), a); break;
-      case 512: hipLaunchKernelGGL(attn_rows_mfma_kernel<512>, fgrid, dim3(256), 0, stream(), a); break;
+      case 512: hipLaunchKernelGGL(attn_rows_dsplit_kernel<512>, fgrid, dim3(256), 0, stream(), a); break;
       default: return fail(G4_E_ARG, "attention: head_dim %d must be 64, 128, 256 or 512", hd);
     }
     G4_LAUNCH_CHECK("attn_rows_mfma_kernel");
