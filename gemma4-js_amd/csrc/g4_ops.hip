@@ -289,7 +289,7 @@ constexpr int kFaRows = 16, kFaWaves = 4, kFaPStride = 20;
 // (padded stride HD + 4) and wm / wl the per-wave (max, sum) to merge with
 // weights e^(m_w - M).  Writes the normalised rows to a.out, or with a.xt set
 // the x' of the GEMM that takes them.
-template <int HD>
+template <int HD, int NTH = 256>
 __device__ __forceinline__ void attn_rows_store(const AttnArgs &a, const float *qs,
                                                 const float (*wm)[kFaRows],
                                                 const float (*wl)[kFaRows], int R0, int nrows,
@@ -297,7 +297,7 @@ __device__ __forceinline__ void attn_rows_store(const AttnArgs &a, const float *
   constexpr int QS = HD + 4;
   const int H = a.H;
   if (!a.xt) {
-    for (int i = t; i < kFaRows * HD / 4; i += 256) {
+    for (int i = t; i < kFaRows * HD / 4; i += NTH) {
       const int r = i / (HD / 4), d4 = i - r * (HD / 4);
       if (R0 + r >= nrows) continue;
       const float M = fmaxf(fmaxf(wm[0][r], wm[1][r]), fmaxf(wm[2][r], wm[3][r]));
@@ -331,7 +331,7 @@ __device__ __forceinline__ void attn_rows_store(const AttnArgs &a, const float *
     v[0] = x0.x / L, v[1] = x0.y / L, v[2] = x0.z / L, v[3] = x0.w / L;
     v[4] = x1.x / L, v[5] = x1.y / L, v[6] = x1.z / L, v[7] = x1.w / L;
   };
-  for (int i = t; i < kFaRows * C8; i += 256) {
+  for (int i = t; i < kFaRows * C8; i += NTH) {
     const int r = i / C8, c8 = i - r * C8;
     if (R0 + r >= nrows) continue;
     float v[8], mx = 0.f;
@@ -343,7 +343,7 @@ __device__ __forceinline__ void attn_rows_store(const AttnArgs &a, const float *
   __syncthreads();
   const int nch = H * C8;
   const size_t lo_plane = (size_t)nch * a.Mp;
-  for (int i = t; i < kFaRows * C8; i += 256) {
+  for (int i = t; i < kFaRows * C8; i += NTH) {
     const int r = i / C8, c8 = i - r * C8;
     const int qr = (R0 + r) / H, ch = (r % H) * C8 + c8;  // R0 is a multiple of H
     uint4 hi = make_uint4(0u, 0u, 0u, 0u), lo = hi;
@@ -563,17 +563,19 @@ __global__ __launch_bounds__(256) void attn_rows_mfma_kernel(AttnArgs a) {
 // the next tile's K and V are loaded during the current one.  No merge of
 // the waves is needed: O goes to LDS by dims and leaves through
 // attn_rows_store.
-template <int HD>
-__global__ __launch_bounds__(256) void attn_rows_dsplit_kernel(AttnArgs a) {
+template <int HD, int KG>
+__global__ __launch_bounds__(256 * KG) void attn_rows_dsplit_kernel(AttnArgs a) {
+  static_assert(KG == 1 || KG == 2, "one or two key groups");
+  constexpr int NTH = 256 * KG;
   constexpr int QS = HD + 4;
   constexpr int DW = HD / kFaWaves;  // dims per wave
   constexpr int NJ = DW / 16;        // S steps of 16 dims (4 MFMAs each)
   constexpr int NQ = DW / 64;        // 64-dim column groups of O per wave
   __shared__ float qs[kFaRows * QS];  // the Q tile, later O
-  __shared__ f32x4 sx[2][kFaWaves][64];  // partial S per wave (two buffers)
-  __shared__ float ps[kFaWaves][kFaRows * kFaPStride];
+  __shared__ f32x4 sx[2][KG][kFaWaves][64];  // partial S per wave (two buffers)
+  __shared__ float ps[KG * kFaWaves][kFaRows * kFaPStride];
   __shared__ float wm[kFaWaves][kFaRows], wl[kFaWaves][kFaRows];
-  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+  const int t = threadIdx.x, lane = t & 63, w = (t >> 6) & 3, kg = t >> 8;
   const int c = lane & 15, g = lane >> 4;
   const int H = a.H;
   const int qpos0 = a.pos_dev ? *a.pos_dev : a.qpos0;
@@ -584,7 +586,7 @@ __global__ __launch_bounds__(256) void attn_rows_dsplit_kernel(AttnArgs a) {
     if (!a.xt) return;
     const int nch = H * (HD / 8), nq = kFaRows / H;
     const size_t lo_plane = (size_t)nch * a.Mp;
-    for (int i = t; i < nq * nch; i += 256) {
+    for (int i = t; i < nq * nch; i += NTH) {
       const int qr = R0 / H + i / nch, ch = i % nch;
       if (qr >= a.Mp) continue;
       a.xt[(size_t)ch * a.Mp + qr] = make_uint4(0u, 0u, 0u, 0u);
@@ -593,7 +595,7 @@ __global__ __launch_bounds__(256) void attn_rows_dsplit_kernel(AttnArgs a) {
     return;
   }
   const int Rl = (R0 + kFaRows < nrows ? R0 + kFaRows : nrows) - 1;  // last live row
-  for (int i = t; i < kFaRows * HD / 4; i += 256) {
+  for (int i = t; i < kFaRows * HD / 4; i += NTH) {
     const int r = i / (HD / 4), d4 = i - r * (HD / 4);
     float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
     if (R0 + r < nrows) v = reinterpret_cast<const float4 *>(a.q + (size_t)(R0 + r) * HD)[d4];
@@ -641,11 +643,16 @@ __global__ __launch_bounds__(256) void attn_rows_dsplit_kernel(AttnArgs a) {
       for (int q = 0; q < NQ; ++q) vr[sp][q] = *reinterpret_cast<const float4 *>(vp + 64 * q);
     }
   };
-  load_k(kt0);
-  load_v(kt0);
-  float *pw = ps[w];
-  for (int kt = kt0; kt <= kt1; ++kt) {
-    const int b = (kt - kt0) & 1;
+  // key group kg takes tiles kt0 + kg, kt0 + kg + KG, ...; every wave runs
+  // the same number of steps (a step past kt1 re-reads tile kt1 with all of
+  // its keys masked), so the barriers match
+  const int steps = (kt1 - kt0) / KG + 1;
+  load_k(kt0 + kg);
+  load_v(kt0 + kg);
+  float *pw = ps[kg * kFaWaves + w];
+  for (int it = 0; it < steps; ++it) {
+    const int kt = kt0 + kg + it * KG;
+    const int b = it & 1;
     f32x4 sa[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) sa[i] = (f32x4){0.f, 0.f, 0.f, 0.f};
@@ -657,10 +664,11 @@ __global__ __launch_bounds__(256) void attn_rows_dsplit_kernel(AttnArgs a) {
       sa[2] = __builtin_amdgcn_mfma_f32_16x16x4f32(qv.z, kv.z, sa[2], 0, 0, 0);
       sa[3] = __builtin_amdgcn_mfma_f32_16x16x4f32(qv.w, kv.w, sa[3], 0, 0, 0);
     }
-    load_k(kt + 1);
-    sx[b][w][lane] = (sa[0] + sa[1]) + (sa[2] + sa[3]);
+    load_k(kt + KG);
+    sx[b][kg][w][lane] = (sa[0] + sa[1]) + (sa[2] + sa[3]);
     __syncthreads();
-    const f32x4 s = ((sx[b][0][lane] + sx[b][1][lane]) + sx[b][2][lane]) + sx[b][3][lane];
+    const f32x4 s =
+        ((sx[b][kg][0][lane] + sx[b][kg][1][lane]) + sx[b][kg][2][lane]) + sx[b][kg][3][lane];
     const int key = kt * 16 + c;
     float corr[4];
 #pragma unroll
@@ -691,26 +699,51 @@ __global__ __launch_bounds__(256) void attn_rows_dsplit_kernel(AttnArgs a) {
         o[4 * q + 2] = __builtin_amdgcn_mfma_f32_16x16x4f32(pv[sp], vv.z, o[4 * q + 2], 0, 0, 0);
         o[4 * q + 3] = __builtin_amdgcn_mfma_f32_16x16x4f32(pv[sp], vv.w, o[4 * q + 3], 0, 0, 0);
       }
-    load_v(kt + 1);
+    load_v(kt + KG);
   }
-  // O by dims into qs, (max, sum) as wave 0's with the other waves' weights 0
+  // O by dims into qs: each key group's (max, sum) in slot kg (the other
+  // slots weight 0), its O weighted by e^(m_kg - M) and added in key-group
+  // order, as attn_rows_store merges them
   __syncthreads();
-#pragma unroll
-  for (int v = 0; v < 4; ++v)
-#pragma unroll
-    for (int q = 0; q < NQ; ++q)
-      *reinterpret_cast<float4 *>(&qs[(4 * g + v) * QS + d0 + 64 * q + 4 * c]) =
-          make_float4(o[4 * q][v], o[4 * q + 1][v], o[4 * q + 2][v], o[4 * q + 3][v]);
-  if (c == 0)
+  if (w == 0 && c == 0)
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
-      wm[w][4 * g + v] = w == 0 ? m[v] : -1e30f;
-      wl[w][4 * g + v] = w == 0 ? l[v] : 0.f;
+      wm[kg][4 * g + v] = m[v];
+      wl[kg][4 * g + v] = l[v];
     }
+  if (t < kFaRows * (kFaWaves - KG)) {
+    wm[KG + t / kFaRows][t % kFaRows] = -1e30f;
+    wl[KG + t / kFaRows][t % kFaRows] = 0.f;
+  }
   __syncthreads();
-  attn_rows_store<HD>(a, qs, wm, wl, R0, nrows, t);
+  float f[4];
+#pragma unroll
+  for (int v = 0; v < 4; ++v) {
+    const int r = 4 * g + v;
+    f[v] = KG > 1 ? expf(m[v] - fmaxf(wm[0][r], wm[KG - 1][r])) : 1.f;
+  }
+  for (int k = 0; k < KG; ++k) {
+    if (kg == k)
+#pragma unroll
+      for (int v = 0; v < 4; ++v)
+#pragma unroll
+        for (int q = 0; q < NQ; ++q) {
+          float4 *dst = reinterpret_cast<float4 *>(&qs[(4 * g + v) * QS + d0 + 64 * q + 4 * c]);
+          const float4 add = make_float4(o[4 * q][v] * f[v], o[4 * q + 1][v] * f[v],
+                                         o[4 * q + 2][v] * f[v], o[4 * q + 3][v] * f[v]);
+          if (k == 0) {
+            *dst = add;
+          } else {
+            const float4 cur = *dst;
+            *dst = make_float4(cur.x + add.x, cur.y + add.y, cur.z + add.z, cur.w + add.w);
+          }
+        }
+    __syncthreads();
+  }
+  attn_rows_store<HD, NTH>(a, qs, wm, wl, R0, nrows, t);
 }
 
+constexpr int kDsplitKeyGroups = 2;  // key groups of attn_rows_dsplit_kernel
 constexpr int kDecMaxKeys = 16;
 constexpr int kMaxSplits = 1024;
 
@@ -1109,7 +1142,7 @@ int launch_attention(const float *q, const float *k, const float *v, int qrows, 
       case 64: hipLaunchKernelGGL(attn_rows_mfma_kernel<64>, fgrid, dim3(256), 0, stream(), a); break;
       case 128: hipLaunchKernelGGL(attn_rows_mfma_kernel<128>, fgrid, dim3(256), 0, stream(), a); break;
       case 256: hipLaunchKernelGGL(attn_rows_mfma_kernel<256>, fgrid, dim3(256), 0, stream(), a); break;
-      case 512: hipLaunchKernelGGL(attn_rows_dsplit_kernel<512>, fgrid, dim3(256), 0, stream(), a); break;
+      case 512: hipLaunchKernelGGL((attn_rows_dsplit_kernel<512, kDsplitKeyGroups>), fgrid, dim3(256 * kDsplitKeyGroups), 0, stream(), a); break;
       default: return fail(G4_E_ARG, "attention: head_dim %d must be 64, 128, 256 or 512", hd);
     }
     G4_LAUNCH_CHECK("attn_rows_mfma_kernel");
