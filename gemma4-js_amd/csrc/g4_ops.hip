@@ -563,19 +563,20 @@ __global__ __launch_bounds__(256) void attn_rows_mfma_kernel(AttnArgs a) {
 // the next tile's K and V are loaded during the current one.  No merge of
 // the waves is needed: O goes to LDS by dims and leaves through
 // attn_rows_store.
-template <int HD, int KG>
-__global__ __launch_bounds__(256 * KG) void attn_rows_dsplit_kernel(AttnArgs a) {
-  static_assert(KG == 1 || KG == 2, "one or two key groups");
-  constexpr int NTH = 256 * KG;
+template <int HD, int DQ, int KG>
+__global__ __launch_bounds__(64 * DQ * KG) void attn_rows_dsplit_kernel(AttnArgs a) {
+  static_assert(KG >= 1 && KG <= kFaWaves && DQ >= 1 && HD % (64 * DQ) == 0,
+                "up to 4 key groups of DQ waves with whole 64-dim column groups");
+  constexpr int NTH = 64 * DQ * KG;
   constexpr int QS = HD + 4;
-  constexpr int DW = HD / kFaWaves;  // dims per wave
-  constexpr int NJ = DW / 16;        // S steps of 16 dims (4 MFMAs each)
-  constexpr int NQ = DW / 64;        // 64-dim column groups of O per wave
+  constexpr int DW = HD / DQ;  // dims per wave
+  constexpr int NJ = DW / 16;  // S steps of 16 dims (4 MFMAs each)
+  constexpr int NQ = DW / 64;  // 64-dim column groups of O per wave
   __shared__ float qs[kFaRows * QS];  // the Q tile, later O
-  __shared__ f32x4 sx[2][KG][kFaWaves][64];  // partial S per wave (two buffers)
-  __shared__ float ps[KG * kFaWaves][kFaRows * kFaPStride];
+  __shared__ f32x4 sx[2][KG][DQ][64];  // partial S per wave (two buffers)
+  __shared__ float ps[KG * DQ][kFaRows * kFaPStride];
   __shared__ float wm[kFaWaves][kFaRows], wl[kFaWaves][kFaRows];
-  const int t = threadIdx.x, lane = t & 63, w = (t >> 6) & 3, kg = t >> 8;
+  const int t = threadIdx.x, lane = t & 63, w = (t >> 6) % DQ, kg = (t >> 6) / DQ;
   const int c = lane & 15, g = lane >> 4;
   const int H = a.H;
   const int qpos0 = a.pos_dev ? *a.pos_dev : a.qpos0;
@@ -649,7 +650,7 @@ __global__ __launch_bounds__(256 * KG) void attn_rows_dsplit_kernel(AttnArgs a) 
   const int steps = (kt1 - kt0) / KG + 1;
   load_k(kt0 + kg);
   load_v(kt0 + kg);
-  float *pw = ps[kg * kFaWaves + w];
+  float *pw = ps[kg * DQ + w];
   for (int it = 0; it < steps; ++it) {
     const int kt = kt0 + kg + it * KG;
     const int b = it & 1;
@@ -667,8 +668,9 @@ __global__ __launch_bounds__(256 * KG) void attn_rows_dsplit_kernel(AttnArgs a) 
     load_k(kt + KG);
     sx[b][kg][w][lane] = (sa[0] + sa[1]) + (sa[2] + sa[3]);
     __syncthreads();
-    const f32x4 s =
-        ((sx[b][kg][0][lane] + sx[b][kg][1][lane]) + sx[b][kg][2][lane]) + sx[b][kg][3][lane];
+    f32x4 s = sx[b][kg][0][lane];
+#pragma unroll
+    for (int d = 1; d < DQ; ++d) s += sx[b][kg][d][lane];
     const int key = kt * 16 + c;
     float corr[4];
 #pragma unroll
@@ -711,7 +713,7 @@ __global__ __launch_bounds__(256 * KG) void attn_rows_dsplit_kernel(AttnArgs a) 
       wm[kg][4 * g + v] = m[v];
       wl[kg][4 * g + v] = l[v];
     }
-  if (t < kFaRows * (kFaWaves - KG)) {
+  if (KG < kFaWaves && t < kFaRows * (kFaWaves - KG)) {
     wm[KG + t / kFaRows][t % kFaRows] = -1e30f;
     wl[KG + t / kFaRows][t % kFaRows] = 0.f;
   }
@@ -720,7 +722,10 @@ __global__ __launch_bounds__(256 * KG) void attn_rows_dsplit_kernel(AttnArgs a) 
 #pragma unroll
   for (int v = 0; v < 4; ++v) {
     const int r = 4 * g + v;
-    f[v] = KG > 1 ? expf(m[v] - fmaxf(wm[0][r], wm[KG - 1][r])) : 1.f;
+    float M = wm[0][r];
+#pragma unroll
+    for (int k = 1; k < KG; ++k) M = fmaxf(M, wm[k][r]);
+    f[v] = KG > 1 ? expf(m[v] - M) : 1.f;
   }
   for (int k = 0; k < KG; ++k) {
     if (kg == k)
@@ -743,7 +748,6 @@ __global__ __launch_bounds__(256 * KG) void attn_rows_dsplit_kernel(AttnArgs a) 
   attn_rows_store<HD, NTH>(a, qs, wm, wl, R0, nrows, t);
 }
 
-constexpr int kDsplitKeyGroups = 2;  // key groups of attn_rows_dsplit_kernel
 constexpr int kDecMaxKeys = 16;
 constexpr int kMaxSplits = 1024;
 
@@ -1142,7 +1146,7 @@ int launch_attention(const float *q, const float *k, const float *v, int qrows, 
       case 64: hipLaunchKernelGGL(attn_rows_mfma_kernel<64>, fgrid, dim3(256), 0, stream(), a); break;
       case 128: hipLaunchKernelGGL(attn_rows_mfma_kernel<128>, fgrid, dim3(256), 0, stream(), a); break;
       case 256: hipLaunchKernelGGL(attn_rows_mfma_kernel<256>, fgrid, dim3(256), 0, stream(), a); break;
-      case 512: hipLaunchKernelGGL((attn_rows_dsplit_kernel<512, kDsplitKeyGroups>), fgrid, dim3(256 * kDsplitKeyGroups), 0, stream(), a); break;
+      case 512: hipLaunchKernelGGL((attn_rows_dsplit_kernel<512, 4, 2>), fgrid, dim3(512), 0, stream(), a); break;
       default: return fail(G4_E_ARG, "attention: head_dim %d must be 64, 128, 256 or 512", hd);
     }
     G4_LAUNCH_CHECK("attn_rows_mfma_kernel");
