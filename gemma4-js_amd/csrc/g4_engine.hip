@@ -369,17 +369,20 @@ int run_layers(g4_gemma *m, int rows, bool graph, const Diag *dg = nullptr) {
     if (rc) return rc;
     if (sb && ((rc = stage(G4_STAGE_PRE_ATTENTION, m->pre)) || (rc = stage(G4_STAGE_Q_RAW, m->qraw))))
       return rc;
-    if ((rc = launch_norm_rope(qp.parts, rows, c.heads, l.hd, 0, m->pos, l.norm[G4_NORM_Q],
-                               l.rope_angles, l.rope_base, eps, m->q, false, qp.n, qp.stride)))
+    if (l.kv_src < 0) {
+      // q, and KVCache.append: k/v rows go straight to positions pos .. pos + rows - 1
+      if ((rc = launch_norm_rope_qkv(qp.parts, qp.n, qp.stride, m->kraw, m->vraw, rows, c.heads,
+                                     l.hd, m->pos, l.norm[G4_NORM_Q], l.norm[G4_NORM_K],
+                                     l.rope_angles, l.rope_base, eps, m->q, l.kc, l.vc)))
+        return rc;
+    } else if ((rc = launch_norm_rope(qp.parts, rows, c.heads, l.hd, 0, m->pos,
+                                      l.norm[G4_NORM_Q], l.rope_angles, l.rope_base, eps, m->q,
+                                      false, qp.n, qp.stride))) {
       return rc;
+    }
     if (sb && (rc = stage(G4_STAGE_Q_NORM_ROPE, m->q))) return rc;
     const Layer &src = l.kv_src >= 0 ? m->L[l.kv_src] : l;
     if (l.kv_src < 0) {
-      // KVCache.append: rows go straight to positions pos .. pos + rows - 1
-      if ((rc = launch_norm_rope(m->kraw, rows, 1, l.hd, 0, m->pos, l.norm[G4_NORM_K],
-                                 l.rope_angles, l.rope_base, eps, l.kc, true)))
-        return rc;
-      if ((rc = launch_rms(m->vraw, rows, l.hd, nullptr, eps, l.vc, m->pos))) return rc;
       if (sb) {
         const size_t at = (size_t)m->cache_len * l.hd;  // the appended rows
         if ((rc = stage(G4_STAGE_K_RAW, m->kraw)) || (rc = stage(G4_STAGE_V_RAW, m->vraw)) ||

@@ -52,12 +52,10 @@ __device__ __forceinline__ float inv_rms(float ss, int width, float eps) {
 // ---- RMS_SHADER (gpu-runtime.js:1104-1118) ----------------------------------
 // One block per row.  y row index = row (+ *pos_dev when given: the row goes
 // to that position of a cache).
-__global__ __launch_bounds__(kBlock) void rms_kernel(const float *__restrict__ x, int width,
-                                                     const float *__restrict__ scale, float eps,
-                                                     float *__restrict__ y,
-                                                     const int *__restrict__ pos_dev) {
-  __shared__ float red[4];
-  const int row = blockIdx.x;
+__device__ __forceinline__ void rms_row(const float *__restrict__ x, int width,
+                                        const float *__restrict__ scale, float eps,
+                                        float *__restrict__ y, const int *__restrict__ pos_dev,
+                                        int row, float *red) {
   const float *xr = x + (size_t)row * width;
   float ss = 0.f;
   for (int i = threadIdx.x; i < width; i += kBlock) ss += xr[i] * xr[i];
@@ -66,6 +64,14 @@ __global__ __launch_bounds__(kBlock) void rms_kernel(const float *__restrict__ x
   float *yr = y + (size_t)orow * width;
   for (int i = threadIdx.x; i < width; i += kBlock)
     yr[i] = xr[i] * inv * (scale ? scale[i] : 1.f);
+}
+
+__global__ __launch_bounds__(kBlock) void rms_kernel(const float *__restrict__ x, int width,
+                                                     const float *__restrict__ scale, float eps,
+                                                     float *__restrict__ y,
+                                                     const int *__restrict__ pos_dev) {
+  __shared__ float red[4];
+  rms_row(x, width, scale, eps, y, pos_dev, blockIdx.x, red);
 }
 
 // ---- ADD_SCALE_SHADER / SCALE_SHADER / GELU_MUL_SHADER ----------------------
@@ -109,12 +115,10 @@ __global__ __launch_bounds__(kBlock) void gelu_ple_kernel(const float *__restric
 // the sum of `parts` planes pstride floats apart (a GEMM's K slices), added
 // in plane order.
 constexpr int kNormRopeMaxParts = 8;
-__global__ __launch_bounds__(kBlock) void norm_rope_kernel(
+__device__ __forceinline__ void norm_rope_row(
     const float *__restrict__ x, int parts, size_t pstride, int heads, int hd, int pos0,
     const int *__restrict__ pos_dev, const float *__restrict__ scale, int rope_angles,
-    float base, float eps, float *__restrict__ y, int at_pos) {
-  __shared__ float red[4];
-  const int rh = blockIdx.x;
+    float base, float eps, float *__restrict__ y, int at_pos, int rh, float *red) {
   const int row = rh / heads, h = rh - row * heads;
   const float *xv = x + (size_t)rh * hd;
   const int half = hd >> 1, t = threadIdx.x;
@@ -158,6 +162,37 @@ __global__ __launch_bounds__(kBlock) void norm_rope_kernel(
     yv[t] = fmaf(an, cs, -(bn * sn));
     yv[t + half] = fmaf(bn, cs, an * sn);
   }
+}
+
+__global__ __launch_bounds__(kBlock) void norm_rope_kernel(
+    const float *__restrict__ x, int parts, size_t pstride, int heads, int hd, int pos0,
+    const int *__restrict__ pos_dev, const float *__restrict__ scale, int rope_angles,
+    float base, float eps, float *__restrict__ y, int at_pos) {
+  __shared__ float red[4];
+  norm_rope_row(x, parts, pstride, heads, hd, pos0, pos_dev, scale, rope_angles, base, eps, y,
+                at_pos, blockIdx.x, red);
+}
+
+// The q, k and v steps of a prefill layer that owns its KV cache, in one
+// launch: blocks [0, rows * heads) the q norm + RoPE (norm_rope_row), the next
+// rows blocks the k norm + RoPE into the cache at *pos_dev + row, the last
+// rows blocks v's RMS norm without weights into the cache (rms_row).
+__global__ __launch_bounds__(kBlock) void norm_rope_qkv_kernel(
+    const float *__restrict__ q, int qparts, size_t qpstride, const float *__restrict__ k,
+    const float *__restrict__ v, int rows, int heads, int hd, const int *__restrict__ pos_dev,
+    const float *__restrict__ qscale, const float *__restrict__ kscale, int rope_angles,
+    float base, float eps, float *__restrict__ qy, float *__restrict__ kc,
+    float *__restrict__ vc) {
+  __shared__ float red[4];
+  const int nq = rows * heads, b = blockIdx.x;
+  if (b < nq)
+    norm_rope_row(q, qparts, qpstride, heads, hd, 0, pos_dev, qscale, rope_angles, base, eps,
+                  qy, 0, b, red);
+  else if (b < nq + rows)
+    norm_rope_row(k, 1, 0, 1, hd, 0, pos_dev, kscale, rope_angles, base, eps, kc, 1, b - nq,
+                  red);
+  else
+    rms_row(v, hd, nullptr, eps, vc, pos_dev, b - nq - rows, red);
 }
 
 // ---- attention: QK_SHADER + SOFTMAX_SHADER + ATTN_OUT_SHADER ----------------
@@ -1002,6 +1037,21 @@ int grid1(size_t n, dim3 *g) {
 }  // namespace
 
 // ---- launchers shared with the engine ---------------------------------------
+
+int launch_norm_rope_qkv(const float *q, int qparts, size_t qpstride, const float *k,
+                         const float *v, int rows, int heads, int hd, const int *pos_dev,
+                         const float *qscale, const float *kscale, int rope_angles, float base,
+                         float eps, float *qy, float *kc, float *vc) {
+  if (rows == 0) return G4_OK;
+  if (qparts < 1 || qparts > kNormRopeMaxParts || hd > 2 * kBlock)
+    return fail(G4_E_ARG, "norm_rope q/k/v: %d planes (1..%d), head_dim %d", qparts,
+                kNormRopeMaxParts, hd);
+  hipLaunchKernelGGL(norm_rope_qkv_kernel, dim3(rows * (heads + 2)), dim3(kBlock), 0, stream(),
+                     q, qparts, qpstride, k, v, rows, heads, hd, pos_dev, qscale, kscale,
+                     rope_angles, base, eps, qy, kc, vc);
+  G4_LAUNCH_CHECK("norm_rope_qkv_kernel");
+  return G4_OK;
+}
 
 int launch_rms(const float *x, int rows, int width, const float *scale, float eps, float *y,
                const int *pos_dev) {
