@@ -40,9 +40,9 @@ def rel(a, b):
     return np.linalg.norm(a - b) / np.linalg.norm(b)
 
 
-def tiny_config(g4, max_seq=40):
+def tiny_config(g4, max_seq=40, heads=TINY["heads"]):
     c = g4.GemmaConfig()
-    c.hidden, c.heads, c.ple_dim, c.vocab = TINY["hidden"], TINY["heads"], TINY["ple_dim"], TINY["vocab"]
+    c.hidden, c.heads, c.ple_dim, c.vocab = TINY["hidden"], heads, TINY["ple_dim"], TINY["vocab"]
     c.layers, c.max_seq, c.window, c.eps, c.softcap = len(TINY["layers"]), max_seq, TINY["window"], 1e-6, 30.0
     for i, L in enumerate(TINY["layers"]):
         c.head_dim[i], c.intermediate[i], c.full[i] = L["head_dim"], L["intermediate"], L["full"]
@@ -52,7 +52,11 @@ def tiny_config(g4, max_seq=40):
 
 @pytest.fixture(scope="module")
 def tiny(g4):
-    H, heads, P, V = TINY["hidden"], TINY["heads"], TINY["ple_dim"], TINY["vocab"]
+    return build_tiny(g4, TINY["heads"])
+
+
+def build_tiny(g4, heads):
+    H, P, V = TINY["hidden"], TINY["ple_dim"], TINY["vocab"]
     NL = len(TINY["layers"])
     rng = np.random.default_rng(2024)
     E = syn.bf16_rne(rng.standard_normal((V, H), dtype=np.float32) * np.float32(0.05))
@@ -99,7 +103,7 @@ def tiny(g4):
                          ple_norm, final_norm, window=TINY["window"])
 
     def make_engine(max_seq=40, dense=False, table=None):
-        m = g4.Gemma(tiny_config(g4, max_seq))
+        m = g4.Gemma(tiny_config(g4, max_seq, heads))
         Eb = g4.Buffer.from_array(E)
         m.set_embedding(Eb)
         if table is not None:
@@ -142,6 +146,22 @@ def test_tiny_prefill_greedy_matches_oracle(g4, tiny):
     assert rel(got_lg, want_lg) < 1e-3
     assert tok == want_tok or near_tie(want_lg, tok)
     assert m.cache_length() == 12
+
+
+@pytest.mark.parametrize("heads,n", [(3, 9), (3, 40), (8, 9), (8, 33)])
+def test_tiny_prefill_head_counts_match_oracle(g4, heads, n):
+    # Attention hands the o projection its x' when a 16-row block holds whole
+    # query rows (heads dividing 16: 2 and 8); 3 heads take the pre-pass
+    # instead.  Prompts past the 4-row GEMV limit, with padded row blocks.
+    ref, make = build_tiny(g4, heads)
+    m = make(max_seq=64)
+    ids = syn.token_ids(90 + heads + n, n, TINY["vocab"])
+    lg = g4.Buffer(TINY["vocab"] * 4)
+    tok = m.greedy(ids, 0, lg)
+    ref.reset()
+    want_tok, want_lg = ref.greedy(ids, 0)
+    assert rel(lg.download(np.float32), want_lg) < 1e-3
+    assert tok == want_tok or near_tie(want_lg, tok)
 
 
 @pytest.mark.parametrize("n", [2, 4, 5, 9, 31, 40, 64])
