@@ -1158,7 +1158,7 @@ int launch_planned(const GemmPlan &pl, const g4_w4 *const *w, int nw, const uint
   const int sl = pl.slices;
   if (pl.rb) {
     // two blocks per CU, 3 stages; 128 x 192 tiles (64 x 192 with FP32 x,
-    // whose two x' planes double the LDS per row), gate/up 64 x (96 + 96)
+    // whose two x' planes double the LDS per row), gate/up 64 x (128 + 128)
     if (glu)
       return launch_gemm_rb<4, 4, NX, 3, 2>(w, nw, xt, xe, rows, Mp, y, y_bf16, part, sl, sum,
                                             glu);
