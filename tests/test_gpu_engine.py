@@ -164,6 +164,24 @@ def test_tiny_prefill_head_counts_match_oracle(g4, heads, n):
     assert tok == want_tok or near_tie(want_lg, tok)
 
 
+@pytest.mark.parametrize("heads", [2, 3])
+def test_tiny_prefill_in_two_chunks_matches_oracle(g4, heads):
+    # A second prompt chunk of GEMM size at position 17: attention over the
+    # cached keys plus its own (query rows from qpos0 > 0), past the 8-key
+    # window, with attention's x' hand-over (2 heads) and without (3).
+    ref, make = build_tiny(g4, heads)
+    m = make(max_seq=64)
+    ids = syn.token_ids(70 + heads, 40, TINY["vocab"])
+    m.forward(ids[:17], 0)
+    lg = g4.Buffer(TINY["vocab"] * 4)
+    tok = m.greedy(ids[17:], 17, lg)
+    ref.reset()
+    want_tok, want_lg = ref.greedy(ids, 0)
+    assert rel(lg.download(np.float32), want_lg) < 1e-3
+    assert tok == want_tok or near_tie(want_lg, tok)
+    assert m.cache_length() == 40
+
+
 @pytest.mark.parametrize("n", [2, 4, 5, 9, 31, 40, 64])
 def test_tiny_prefill_lengths_match_oracle(g4, tiny, n):
     # Prompt lengths on both sides of the GEMV/GEMM switch (4 rows) and past
