@@ -459,7 +459,7 @@ int run_layers(g4_gemma *m, int rows, bool graph, const Diag *dg = nullptr) {
                                         l.norm[G4_NORM_POST_FFW], nullptr, 1.f, eps, rows, H,
                                         m->fres, nullptr, xp.xt, xp.xe, xp.Mp)))
         return rc;
-      if (sb || !gelu_ple_xprep_fits(P, 1)) {  // the stages read the summed gate
+      if (!gelu_ple_xprep_fits(P, 1)) {
         if ((rc = w4_gemm(pgw, nullptr, true, rows, m->pg, false))) return rc;
       } else {
         // the gate's K slices (at most 8) go unsummed to gelu·ple, which writes
