@@ -110,7 +110,11 @@ def test_norm_rope(g4, rows, heads, hd, pos0, prop, base):
     # 0, three heads (row tiles across positions), one head over a short
     # window, one key past a multiple of 128
     (200, 8, 512, 1000, True, 512), (129, 3, 128, 385, False, 512),
-    (257, 1, 64, 257, True, 100), (64, 8, 256, 129, False, 512)])
+    (257, 1, 64, 257, True, 100), (64, 8, 256, 129, False, 512),
+    # head dim 512 (dim-split kernel, two key groups): one key tile (the
+    # second group's only step fully masked), three heads under a 7-key
+    # window cutting through tiles, one head over an odd tile count
+    (5, 8, 512, 9, False, 512), (17, 3, 512, 33, True, 7), (31, 1, 512, 47, False, 512)])
 def test_attention(g4, qrows, heads, hd, keylen, sliding, window):
     rng = np.random.default_rng([qrows, heads, hd, keylen, window])
     q = rng.standard_normal((qrows, heads * hd)).astype(np.float32) * 0.2
