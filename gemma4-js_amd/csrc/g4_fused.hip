@@ -1167,7 +1167,10 @@ __device__ __forceinline__ float fblock_max(float v, float *red) {
 // 8 rows that share each 128-byte line of xt[c][m] are written through one
 // XCD's L2.  Grid: Mp blocks of 64 threads (Mp a multiple of 32); rows past
 // `rows` write zero chunks.
-constexpr int kChainCpl = 4;  // chunks per lane: width <= 64 * 4 * 8 = 2048
+// CPL: chunks per lane, ceil(width / 512) (up to kChainCpl: width <= 2048), so
+// no lane loads a chunk past the row.
+constexpr int kChainCpl = 4;
+template <int CPL>
 __global__ __launch_bounds__(64) void norm_chain_xprep_kernel(
     const float *__restrict__ a, int a_parts, size_t a_stride, const float *__restrict__ h,
     const float *__restrict__ w1, const float *__restrict__ w2, float c, float eps, int width,
@@ -1188,9 +1191,9 @@ __global__ __launch_bounds__(64) void norm_chain_xprep_kernel(
   }
   const size_t off = (size_t)row * width;
   // every load first (chunks past the row re-read chunk 0 and are left out)
-  float av[kChainCpl][8], hv[kChainCpl][8], w1v[kChainCpl][8], w2v[kChainCpl][8];
+  float av[CPL][8], hv[CPL][8], w1v[CPL][8], w2v[CPL][8];
 #pragma unroll
-  for (int u = 0; u < kChainCpl; ++u) {
+  for (int u = 0; u < CPL; ++u) {
     int ch = lane + 64 * u;
     ch = ch < nch ? ch : 0;
     load8(a + off, ch, av[u]);
@@ -1204,12 +1207,12 @@ __global__ __launch_bounds__(64) void norm_chain_xprep_kernel(
   // tokens: 9.80 -> 9.60 ms; four at a time, 256 registers and one wave per
   // SIMD, 9.64 ms.)
   for (int sp0 = 1; sp0 < a_parts; sp0 += 2) {
-    float t[2][kChainCpl][8];
+    float t[2][CPL][8];
 #pragma unroll
     for (int b = 0; b < 2; ++b) {
       const int sp = sp0 + b < a_parts ? sp0 + b : sp0;
 #pragma unroll
-      for (int u = 0; u < kChainCpl; ++u) {
+      for (int u = 0; u < CPL; ++u) {
         int ch = lane + 64 * u;
         ch = ch < nch ? ch : 0;
         load8(a + sp * a_stride + off, ch, t[b][u]);
@@ -1219,41 +1222,41 @@ __global__ __launch_bounds__(64) void norm_chain_xprep_kernel(
     for (int b = 0; b < 2; ++b)
       if (sp0 + b < a_parts)
 #pragma unroll
-        for (int u = 0; u < kChainCpl; ++u)
+        for (int u = 0; u < CPL; ++u)
 #pragma unroll
           for (int q = 0; q < 8; ++q) av[u][q] += t[b][u][q];
   }
   float ss = 0.f;
 #pragma unroll
-  for (int u = 0; u < kChainCpl; ++u)
+  for (int u = 0; u < CPL; ++u)
     if (lane + 64 * u < nch)
 #pragma unroll
       for (int q = 0; q < 8; ++q) ss += av[u][q] * av[u][q];
   const float inv1 = 1.f / sqrtf(wave_sum(ss) / (float)width + eps);
-  float r[kChainCpl][8], ss2 = 0.f;
+  float r[CPL][8], ss2 = 0.f;
 #pragma unroll
-  for (int u = 0; u < kChainCpl; ++u)
+  for (int u = 0; u < CPL; ++u)
 #pragma unroll
     for (int q = 0; q < 8; ++q) {
       r[u][q] = (hv[u][q] + av[u][q] * inv1 * w1v[u][q]) * c;
       if (lane + 64 * u < nch) ss2 += r[u][q] * r[u][q];
     }
-  float xv[kChainCpl][8];
+  float xv[CPL][8];
   if (w2) {
     const float inv2 = 1.f / sqrtf(wave_sum(ss2) / (float)width + eps);
 #pragma unroll
-    for (int u = 0; u < kChainCpl; ++u)
+    for (int u = 0; u < CPL; ++u)
 #pragma unroll
       for (int q = 0; q < 8; ++q) xv[u][q] = r[u][q] * inv2 * w2v[u][q];
   } else {
 #pragma unroll
-    for (int u = 0; u < kChainCpl; ++u)
+    for (int u = 0; u < CPL; ++u)
 #pragma unroll
       for (int q = 0; q < 8; ++q) xv[u][q] = r[u][q];
   }
   float mx = 0.f;
 #pragma unroll
-  for (int u = 0; u < kChainCpl; ++u) {
+  for (int u = 0; u < CPL; ++u) {
     const int ch = lane + 64 * u;
     if (ch >= nch) continue;
     float4 *ro = r_out ? reinterpret_cast<float4 *>(r_out + off) + 2 * ch : nullptr;
@@ -1274,7 +1277,7 @@ __global__ __launch_bounds__(64) void norm_chain_xprep_kernel(
   const int e = mx > 0.f && mx <= 3.4e38f ? ilogbf(mx) - 13 : 0;
   if (lane == 0) xe[row] = e;
 #pragma unroll
-  for (int u = 0; u < kChainCpl; ++u) {
+  for (int u = 0; u < CPL; ++u) {
     const int ch = lane + 64 * u;
     if (ch >= nch) continue;
     _Float16 hh[8], ll[8];
@@ -1536,9 +1539,13 @@ int launch_norm_chain_xprep(const float *a, int a_parts, size_t a_stride, const 
   if (width > 64 * kChainCpl * 8 || width % 8 || rows > Mp || Mp % 32)
     return fail(G4_E_ARG, "norm chain with x pre-pass: width %d (<= 2048, multiple of 8), "
                 "rows %d <= %d (a multiple of 32)", width, rows, Mp);
-  hipLaunchKernelGGL(norm_chain_xprep_kernel, dim3(Mp), dim3(64), 0, stream(), a, a_parts,
-                     a_stride, h, w1, w2, c, eps, width, rows, r_out, x_out,
-                     static_cast<uint4 *>(xt), xe, Mp);
+  const int cpl = (width / 8 + 63) / 64;
+  auto kernel = cpl == 1   ? norm_chain_xprep_kernel<1>
+                : cpl == 2 ? norm_chain_xprep_kernel<2>
+                : cpl == 3 ? norm_chain_xprep_kernel<3>
+                           : norm_chain_xprep_kernel<4>;
+  hipLaunchKernelGGL(kernel, dim3(Mp), dim3(64), 0, stream(), a, a_parts, a_stride, h, w1, w2, c,
+                     eps, width, rows, r_out, x_out, static_cast<uint4 *>(xt), xe, Mp);
   G4_LAUNCH_CHECK("norm_chain_xprep_kernel");
   return G4_OK;
 }
