@@ -28,13 +28,19 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
-// Sum over a 256-thread block; every thread gets the total.
+// Sum over a block of NW waves (256 threads by default); every thread gets the
+// total.  The wave sums are added in wave order, so a block of fewer waves
+// gives the bits of a 256-thread block whose other waves hold zeros.
+template <int NW = 4>
 __device__ __forceinline__ float block_sum(float v, float *red) {
   v = wave_sum(v);
   __syncthreads();  // red may still be read by a previous call
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
   __syncthreads();
-  return red[0] + red[1] + red[2] + red[3];
+  float s = red[0];
+#pragma unroll
+  for (int w = 1; w < NW; ++w) s += red[w];
+  return s;
 }
 
 // GELU, tanh form with the shader's clamp (gpu-runtime.js:1148-1155).
@@ -113,8 +119,11 @@ __global__ __launch_bounds__(kBlock) void gelu_ple_kernel(const float *__restric
 // (t, t + hd/2).  Output row index is row, or *pos_dev + row when pos_dev is
 // given and `at_pos` is set (appending k straight into a cache).  x may be
 // the sum of `parts` planes pstride floats apart (a GEMM's K slices), added
-// in plane order.
+// in plane order.  NP: the planes loaded, parts itself up to 4, else 8 (the
+// planes past `parts` re-read plane 0 and are left out).
 constexpr int kNormRopeMaxParts = 8;
+constexpr int norm_rope_np(int parts) { return parts <= 4 ? parts : kNormRopeMaxParts; }
+template <int NP, int NW = 4>
 __device__ __forceinline__ void norm_rope_row(
     const float *__restrict__ x, int parts, size_t pstride, int heads, int hd, int pos0,
     const int *__restrict__ pos_dev, const float *__restrict__ scale, int rope_angles,
@@ -123,14 +132,11 @@ __device__ __forceinline__ void norm_rope_row(
   const float *xv = x + (size_t)rh * hd;
   const int half = hd >> 1, t = threadIdx.x;
   float a = 0.f, b = 0.f;
-  if (t < half && parts == 1) {
-    a = xv[t];
-    b = xv[t + half];
-  } else if (t < half) {
-    // every plane's load first (past `parts`, plane 0 again), then the adds
-    float pa[kNormRopeMaxParts], pb[kNormRopeMaxParts];
+  if (t < half) {
+    // every plane's load first, then the adds
+    float pa[NP], pb[NP];
 #pragma unroll
-    for (int sp = 0; sp < kNormRopeMaxParts; ++sp) {
+    for (int sp = 0; sp < NP; ++sp) {
       const size_t o = (size_t)(sp < parts ? sp : 0) * pstride;
       pa[sp] = xv[o + t];
       pb[sp] = xv[o + t + half];
@@ -138,7 +144,7 @@ __device__ __forceinline__ void norm_rope_row(
     a = pa[0];
     b = pb[0];
 #pragma unroll
-    for (int sp = 1; sp < kNormRopeMaxParts; ++sp)
+    for (int sp = 1; sp < NP; ++sp)
       if (sp < parts) {
         a += pa[sp];
         b += pb[sp];
@@ -146,7 +152,7 @@ __device__ __forceinline__ void norm_rope_row(
   }
   // the products that are fused are spelled out, so the rounding does not
   // depend on which one the compiler would contract
-  const float inv = inv_rms(block_sum(fmaf(b, b, a * a), red), hd, eps);
+  const float inv = inv_rms(block_sum<NW>(fmaf(b, b, a * a), red), hd, eps);
   const int pos = (pos_dev ? *pos_dev : pos0) + row;
   if (t < half) {
     const float an = a * inv * scale[t], bn = b * inv * scale[t + half];
@@ -164,19 +170,22 @@ __device__ __forceinline__ void norm_rope_row(
   }
 }
 
-__global__ __launch_bounds__(kBlock) void norm_rope_kernel(
+// NW waves: at least hd / 2 threads.
+template <int NP, int NW>
+__global__ __launch_bounds__(64 * NW) void norm_rope_kernel(
     const float *__restrict__ x, int parts, size_t pstride, int heads, int hd, int pos0,
     const int *__restrict__ pos_dev, const float *__restrict__ scale, int rope_angles,
     float base, float eps, float *__restrict__ y, int at_pos) {
   __shared__ float red[4];
-  norm_rope_row(x, parts, pstride, heads, hd, pos0, pos_dev, scale, rope_angles, base, eps, y,
-                at_pos, blockIdx.x, red);
+  norm_rope_row<NP, NW>(x, parts, pstride, heads, hd, pos0, pos_dev, scale, rope_angles, base,
+                        eps, y, at_pos, blockIdx.x, red);
 }
 
 // The q, k and v steps of a prefill layer that owns its KV cache, in one
 // launch: blocks [0, rows * heads) the q norm + RoPE (norm_rope_row), the next
 // rows blocks the k norm + RoPE into the cache at *pos_dev + row, the last
 // rows blocks v's RMS norm without weights into the cache (rms_row).
+template <int NP>
 __global__ __launch_bounds__(kBlock) void norm_rope_qkv_kernel(
     const float *__restrict__ q, int qparts, size_t qpstride, const float *__restrict__ k,
     const float *__restrict__ v, int rows, int heads, int hd, const int *__restrict__ pos_dev,
@@ -186,11 +195,11 @@ __global__ __launch_bounds__(kBlock) void norm_rope_qkv_kernel(
   __shared__ float red[4];
   const int nq = rows * heads, b = blockIdx.x;
   if (b < nq)
-    norm_rope_row(q, qparts, qpstride, heads, hd, 0, pos_dev, qscale, rope_angles, base, eps,
-                  qy, 0, b, red);
+    norm_rope_row<NP>(q, qparts, qpstride, heads, hd, 0, pos_dev, qscale, rope_angles, base,
+                      eps, qy, 0, b, red);
   else if (b < nq + rows)
-    norm_rope_row(k, 1, 0, 1, hd, 0, pos_dev, kscale, rope_angles, base, eps, kc, 1, b - nq,
-                  red);
+    norm_rope_row<1>(k, 1, 0, 1, hd, 0, pos_dev, kscale, rope_angles, base, eps, kc, 1, b - nq,
+                     red);
   else
     rms_row(v, hd, nullptr, eps, vc, pos_dev, b - nq - rows, red);
 }
@@ -1046,9 +1055,15 @@ int launch_norm_rope_qkv(const float *q, int qparts, size_t qpstride, const floa
   if (qparts < 1 || qparts > kNormRopeMaxParts || hd > 2 * kBlock)
     return fail(G4_E_ARG, "norm_rope q/k/v: %d planes (1..%d), head_dim %d", qparts,
                 kNormRopeMaxParts, hd);
-  hipLaunchKernelGGL(norm_rope_qkv_kernel, dim3(rows * (heads + 2)), dim3(kBlock), 0, stream(),
-                     q, qparts, qpstride, k, v, rows, heads, hd, pos_dev, qscale, kscale,
-                     rope_angles, base, eps, qy, kc, vc);
+  const int np = norm_rope_np(qparts);
+  auto kernel = np == 1   ? norm_rope_qkv_kernel<1>
+                : np == 2 ? norm_rope_qkv_kernel<2>
+                : np == 3 ? norm_rope_qkv_kernel<3>
+                : np == 4 ? norm_rope_qkv_kernel<4>
+                          : norm_rope_qkv_kernel<kNormRopeMaxParts>;
+  hipLaunchKernelGGL(kernel, dim3(rows * (heads + 2)), dim3(kBlock), 0, stream(), q, qparts,
+                     qpstride, k, v, rows, heads, hd, pos_dev, qscale, kscale, rope_angles, base,
+                     eps, qy, kc, vc);
   G4_LAUNCH_CHECK("norm_rope_qkv_kernel");
   return G4_OK;
 }
@@ -1106,9 +1121,26 @@ int launch_norm_rope(const float *x, int rows, int heads, int hd, int pos0, cons
   if (rows == 0) return G4_OK;
   if (parts < 1 || parts > kNormRopeMaxParts)
     return fail(G4_E_ARG, "norm_rope: %d planes (1..%d)", parts, kNormRopeMaxParts);
-  hipLaunchKernelGGL(norm_rope_kernel, dim3(rows * heads), dim3(kBlock), 0, stream(), x, parts,
-                     pstride, heads, hd, pos0, pos_dev, scale, rope_angles, base, eps, y,
-                     (int)at_pos);
+  if (hd > 2 * kBlock)
+    return fail(G4_E_ARG, "norm_rope: head_dim %d (at most %d)", hd, 2 * kBlock);
+  // waves for the hd / 2 pairs: 1, 2 or 4
+  const int nw = hd <= 128 ? 1 : hd <= 256 ? 2 : 4;
+  const int np = norm_rope_np(parts);
+  void (*kernel)(const float *, int, size_t, int, int, int, const int *, const float *, int,
+                 float, float, float *, int) = nullptr;
+#define G4_NR(NP)                                                                 \
+  kernel = nw == 1 ? norm_rope_kernel<NP, 1> : nw == 2 ? norm_rope_kernel<NP, 2> \
+                                             : norm_rope_kernel<NP, 4>
+  switch (np) {
+    case 1: G4_NR(1); break;
+    case 2: G4_NR(2); break;
+    case 3: G4_NR(3); break;
+    case 4: G4_NR(4); break;
+    default: G4_NR(kNormRopeMaxParts); break;
+  }
+#undef G4_NR
+  hipLaunchKernelGGL(kernel, dim3(rows * heads), dim3(64 * nw), 0, stream(), x, parts, pstride,
+                     heads, hd, pos0, pos_dev, scale, rope_angles, base, eps, y, (int)at_pos);
   G4_LAUNCH_CHECK("norm_rope_kernel");
   return G4_OK;
 }
