@@ -997,28 +997,42 @@ __global__ __launch_bounds__(kBlock) void attn_combine_kernel(const float *__res
 }
 
 // ---- PLE_MIX_SHADER (gpu-runtime.js:1250-1263) ------------------------------
-// One block per (row, layer) chunk of `width` values.  p = proj * pre_scale
-// is the input of the norm: the model's ops.scale of the projection
-// (gemma4-webgpu.js, 1/sqrt(hidden)) travels here as the same FP32 product,
-// and GPUOps.pleMix passes 1.
+// One wave per (row, layer) chunk of `width` values, four chunks per block.
+// p = proj * pre_scale is the input of the norm: the model's ops.scale of the
+// projection (gemma4-webgpu.js, 1/sqrt(hidden)) travels here as the same
+// FP32 product, and GPUOps.pleMix passes 1.
+// The sum of squares is that of a 256-thread block over the chunk (the
+// rms_kernel order): lane l plays threads l, 64 + l, 128 + l and 192 + l,
+// each adding its values d = thread (mod 256) in d order, then each set of
+// 64 threads is summed as one wave and the four sums are added in order.
+// (One 256-thread block per chunk took 21 us for the 512-token prefill's
+// 17920 chunks of 256.)
 __global__ __launch_bounds__(kBlock) void ple_mix_kernel(const float *__restrict__ proj,
                                                          float pre_scale,
                                                          const float *__restrict__ norm_scale,
                                                          const float *__restrict__ token_ple,
-                                                         int width, float eps, float ple_scale,
-                                                         float out_scale,
+                                                         int width, int chunks, float eps,
+                                                         float ple_scale, float out_scale,
                                                          float *__restrict__ y) {
-  __shared__ float red[4];
-  const size_t base = (size_t)blockIdx.x * width;
-  float ss = 0.f;
-  for (int d = threadIdx.x; d < width; d += kBlock) {
-    const float p = proj[base + d] * pre_scale;
-    ss += p * p;
-  }
-  const float inv = inv_rms(block_sum(ss, red), width, eps);
-  for (int d = threadIdx.x; d < width; d += kBlock) {
-    const float n = proj[base + d] * pre_scale * inv * norm_scale[d];
-    y[base + d] = (n + token_ple[base + d] * ple_scale) * out_scale;
+  const int lane = threadIdx.x & 63;
+  const int ck = blockIdx.x * (kBlock / 64) + (threadIdx.x >> 6);
+  if (ck >= chunks) return;  // whole waves
+  const size_t base = (size_t)ck * width;
+  float ss[4] = {0.f, 0.f, 0.f, 0.f};
+  for (int d0 = 0; d0 < width; d0 += kBlock)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int d = d0 + 64 * j + lane;
+      if (d < width) {
+        const float p = proj[base + d] * pre_scale;
+        ss[j] = fmaf(p, p, ss[j]);
+      }
+    }
+  const float tot = ((wave_sum(ss[0]) + wave_sum(ss[1])) + wave_sum(ss[2])) + wave_sum(ss[3]);
+  const float inv = inv_rms(tot, width, eps);
+  for (int d = lane; d < width; d += 64) {
+    const float pn = proj[base + d] * pre_scale * inv;
+    y[base + d] = fmaf(pn, norm_scale[d], token_ple[base + d] * ple_scale) * out_scale;
   }
 }
 
@@ -1254,8 +1268,10 @@ int launch_ple_mix(const float *proj, float pre_scale, const float *norm_scale,
                    const float *token_ple, int rows, int width, int layers, float eps,
                    float ple_scale, float out_scale, float *y) {
   if (rows == 0) return G4_OK;
-  hipLaunchKernelGGL(ple_mix_kernel, dim3(rows * layers), dim3(kBlock), 0, stream(), proj,
-                     pre_scale, norm_scale, token_ple, width, eps, ple_scale, out_scale, y);
+  const int chunks = rows * layers;
+  hipLaunchKernelGGL(ple_mix_kernel, dim3((chunks + kBlock / 64 - 1) / (kBlock / 64)),
+                     dim3(kBlock), 0, stream(), proj, pre_scale, norm_scale, token_ple, width,
+                     chunks, eps, ple_scale, out_scale, y);
   G4_LAUNCH_CHECK("ple_mix_kernel");
   return G4_OK;
 }
