@@ -997,17 +997,40 @@ __global__ __launch_bounds__(kBlock) void attn_combine_kernel(const float *__res
 }
 
 // ---- PLE_MIX_SHADER (gpu-runtime.js:1250-1263) ------------------------------
-// One wave per (row, layer) chunk of `width` values, four chunks per block.
-// p = proj * pre_scale is the input of the norm: the model's ops.scale of the
-// projection (gemma4-webgpu.js, 1/sqrt(hidden)) travels here as the same
-// FP32 product, and GPUOps.pleMix passes 1.
-// The sum of squares is that of a 256-thread block over the chunk (the
-// rms_kernel order): lane l plays threads l, 64 + l, 128 + l and 192 + l,
-// each adding its values d = thread (mod 256) in d order, then each set of
-// 64 threads is summed as one wave and the four sums are added in order.
-// (One 256-thread block per chunk took 21 us for the 512-token prefill's
-// 17920 chunks of 256.)
+// One block per (row, layer) chunk of `width` values.  p = proj * pre_scale
+// is the input of the norm: the model's ops.scale of the projection
+// (gemma4-webgpu.js, 1/sqrt(hidden)) travels here as the same FP32 product,
+// and GPUOps.pleMix passes 1.  The products that are fused are spelled out,
+// so both forms below round alike.
 __global__ __launch_bounds__(kBlock) void ple_mix_kernel(const float *__restrict__ proj,
+                                                         float pre_scale,
+                                                         const float *__restrict__ norm_scale,
+                                                         const float *__restrict__ token_ple,
+                                                         int width, float eps, float ple_scale,
+                                                         float out_scale,
+                                                         float *__restrict__ y) {
+  __shared__ float red[4];
+  const size_t base = (size_t)blockIdx.x * width;
+  float ss = 0.f;
+  for (int d = threadIdx.x; d < width; d += kBlock) {
+    const float p = proj[base + d] * pre_scale;
+    ss = fmaf(p, p, ss);
+  }
+  const float inv = inv_rms(block_sum(ss, red), width, eps);
+  for (int d = threadIdx.x; d < width; d += kBlock) {
+    const float pn = proj[base + d] * pre_scale * inv;
+    y[base + d] = fmaf(pn, norm_scale[d], token_ple[base + d] * ple_scale) * out_scale;
+  }
+}
+
+// The same with one wave per chunk, four chunks per block, for many chunks
+// (the prefill's rows x layers).  The sum of squares is the block's: lane l
+// plays threads l, 64 + l, 128 + l and 192 + l, each adding its values
+// d = thread (mod 256) in d order, then each set of 64 threads is summed as
+// one wave and the four sums are added in order.  (512-token prefill, 17920
+// chunks of 256: 18.6 against 21.1 us; one-token decode, 35 chunks: the
+// block form, 3.5 against 5.7 us.)
+__global__ __launch_bounds__(kBlock) void ple_mix_rows_kernel(const float *__restrict__ proj,
                                                          float pre_scale,
                                                          const float *__restrict__ norm_scale,
                                                          const float *__restrict__ token_ple,
@@ -1269,10 +1292,16 @@ int launch_ple_mix(const float *proj, float pre_scale, const float *norm_scale,
                    float ple_scale, float out_scale, float *y) {
   if (rows == 0) return G4_OK;
   const int chunks = rows * layers;
-  hipLaunchKernelGGL(ple_mix_kernel, dim3((chunks + kBlock / 64 - 1) / (kBlock / 64)),
+  if (chunks < 1024) {
+    hipLaunchKernelGGL(ple_mix_kernel, dim3(chunks), dim3(kBlock), 0, stream(), proj, pre_scale,
+                       norm_scale, token_ple, width, eps, ple_scale, out_scale, y);
+    G4_LAUNCH_CHECK("ple_mix_kernel");
+    return G4_OK;
+  }
+  hipLaunchKernelGGL(ple_mix_rows_kernel, dim3((chunks + kBlock / 64 - 1) / (kBlock / 64)),
                      dim3(kBlock), 0, stream(), proj, pre_scale, norm_scale, token_ple, width,
                      chunks, eps, ple_scale, out_scale, y);
-  G4_LAUNCH_CHECK("ple_mix_kernel");
+  G4_LAUNCH_CHECK("ple_mix_rows_kernel");
   return G4_OK;
 }
 
