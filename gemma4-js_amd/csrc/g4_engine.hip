@@ -360,18 +360,25 @@ int run_layers(g4_gemma *m, int rows, bool graph, const Diag *dg = nullptr) {
     void *qkv_out[3] = {m->qraw, m->kraw, m->vraw};
     const int nqkv = l.kv_src < 0 ? 3 : 1;
     GemmParts qp = {m->qraw, 1, 0};
-    if (pre_prepped && nqkv == 1)  // q alone: its K slices go to the q norm unsummed
+    const float *kin = m->kraw, *vin = m->vraw;
+    if (pre_prepped && nqkv == 1) {  // q alone: its K slices go to the q norm unsummed
       rc = w4_gemm_parts(qkv[0], nullptr, rows, m->qraw, &qp);
-    else if (pre_prepped)
-      rc = w4_gemm_multi(qkv, nqkv, nullptr, true, rows, qkv_out, false);
-    else
+    } else if (pre_prepped) {
+      // q, k and v in one launch that may split K: the q/k/v norms add the slices
+      float *outs[3] = {m->qraw, m->kraw, m->vraw};
+      GemmParts p3[3];
+      rc = w4_gemm_multi_parts(qkv, 3, nullptr, rows, outs, p3);
+      qp = p3[0];
+      kin = p3[1].parts;
+      vin = p3[2].parts;
+    } else
       rc = g4_w4_linear_multi(qkv, nqkv, m->pre, G4_F32, rows, qkv_out, G4_F32);
     if (rc) return rc;
     if (sb && ((rc = stage(G4_STAGE_PRE_ATTENTION, m->pre)) || (rc = stage(G4_STAGE_Q_RAW, m->qraw))))
       return rc;
     if (l.kv_src < 0) {
       // q, and KVCache.append: k/v rows go straight to positions pos .. pos + rows - 1
-      if ((rc = launch_norm_rope_qkv(qp.parts, qp.n, qp.stride, m->kraw, m->vraw, rows, c.heads,
+      if ((rc = launch_norm_rope_qkv(qp.parts, qp.n, qp.stride, kin, vin, rows, c.heads,
                                      l.hd, m->pos, l.norm[G4_NORM_Q], l.norm[G4_NORM_K],
                                      l.rope_angles, l.rope_base, eps, m->q, l.kc, l.vc)))
         return rc;

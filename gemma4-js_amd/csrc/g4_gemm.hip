@@ -308,6 +308,9 @@ struct GemmSegs {
   int N[kMaxGemmSegs], shift[kMaxGemmSegs];
   int t0[kMaxGemmSegs + 1];
   int n, glu;
+  // K split: weight i's planes start at part + poff[i] (rows x N[i] floats in
+  // each plane of pstride floats)
+  size_t poff[kMaxGemmSegs];
 };
 
 template <int TM, int TN, int NX, int KS, int P, bool FLAT>
@@ -591,7 +594,7 @@ __global__ __launch_bounds__(kThreads, 2) void w4_gemm_kernel(
       }
     }
   } else if (gridDim.y > 1)
-    epilogue(part + blockIdx.y * pstride);
+    epilogue(part + blockIdx.y * pstride + SG.poff[si]);
   else if (y_bf16)
     epilogue(static_cast<uint16_t *>(y));
   else
@@ -945,7 +948,7 @@ __global__ __launch_bounds__(kThreads, MINB) void w4_gemm_rb_kernel(
     }
   };
   if (gridDim.y > 1)
-    epilogue(part + blockIdx.y * pstride);
+    epilogue(part + blockIdx.y * pstride + SG.poff[si]);
   else if (y_bf16)
     epilogue(static_cast<uint16_t *>(SG.y[si]));
   else
@@ -983,6 +986,12 @@ __global__ __launch_bounds__(kThreads) void gemm_splitk_sum_kernel(const float *
 
 // Floats between consecutive split-K partial planes of rows x N outputs.
 size_t splitk_pstride(int rows, int N) { return ((size_t)rows * N + 63) & ~size_t(63); }
+// The same for the weights of one launch, side by side in each plane.
+size_t splitk_pstride(const g4_w4 *const *w, int nw, int rows) {
+  size_t n = 0;
+  for (int i = 0; i < nw; ++i) n += (size_t)rows * w[i]->N;
+  return (n + 63) & ~size_t(63);
+}
 
 // n weights (1..kMaxGemmSegs) of one input dimension, y[i] receiving weight
 // i's output; a K split (slices > 1) takes one weight.
@@ -990,7 +999,7 @@ template <int TM, int TN, int NX, int KS, int P>
 int launch_gemm(const g4_w4 *const *w, int nw, const uint4 *xt, const int *xe, int rows, int Mp,
                 void *const *ys, bool y_bf16, float *part, int slices, bool sum, bool glu) {
   constexpr int BM = 32 * TM, BN = 32 * TN;
-  if (Mp % BM != 0 || w[0]->G % (KS * slices) != 0 || (slices > 1 && nw != 1))
+  if (Mp % BM != 0 || w[0]->G % (KS * slices) != 0 || (slices > 1 && nw != 1 && sum))
     return fail(G4_E_ARG, "w4_gemm: tile %dx%d (KS %d, %d slices) does not fit rows %d, K %d",
                 BM, BN, KS, slices, rows, w[0]->K);
   GemmSegs sg{};
@@ -1009,7 +1018,12 @@ int launch_gemm(const g4_w4 *const *w, int nw, const uint4 *xt, const int *xe, i
   const int nn = glu ? (w[0]->N + BN / 2 - 1) / (BN / 2) : sg.t0[nw];
   const int xcd_map = nm % 8 == 0;
   const bool flat = P % 2 == 0 && (w[0]->G / KS / slices) % P == 0;
-  const size_t pstride = splitk_pstride(rows, w[0]->N);
+  size_t pstride = 0;
+  for (int i = 0; i < nw; ++i) {
+    sg.poff[i] = pstride;
+    pstride += (size_t)rows * w[i]->N;
+  }
+  pstride = (pstride + 63) & ~size_t(63);
   auto kernel = flat ? w4_gemm_kernel<TM, TN, NX, KS, P, true> : w4_gemm_kernel<TM, TN, NX, KS, P, false>;
   hipLaunchKernelGGL(kernel, dim3(nm * nn, slices), dim3(kThreads), 0, stream(),
                      reinterpret_cast<const u32x4 *>(xt), xe, sg, (int)y_bf16, rows, Mp,
@@ -1040,7 +1054,7 @@ int launch_gemm_rb(const g4_w4 *const *w, int nw, const uint4 *xt, const int *xe
                    bool glu) {
   constexpr int BM = 16 * TMW;
   const int BN = glu ? 32 * TNW : 64 * TNW;  // output columns per block
-  if (Mp % BM != 0 || w[0]->G % (2 * slices) != 0 || (slices > 1 && nw != 1) ||
+  if (Mp % BM != 0 || w[0]->G % (2 * slices) != 0 || (slices > 1 && nw != 1 && sum) ||
       (glu && TNW % 2 != 0))
     return fail(G4_E_ARG, "w4_gemm: tile %dx%d (%d slices) does not fit rows %d, K %d", BM, BN,
                 slices, rows, w[0]->K);
@@ -1063,7 +1077,12 @@ int launch_gemm_rb(const g4_w4 *const *w, int nw, const uint4 *xt, const int *xe
   const int nm = (rows + BM - 1) / BM;
   const int nn = glu ? (w[0]->N + BN - 1) / BN : sg.t0[nw];
   const int xcd_map = nm % 8 == 0;
-  const size_t pstride = splitk_pstride(rows, w[0]->N);
+  size_t pstride = 0;
+  for (int i = 0; i < nw; ++i) {
+    sg.poff[i] = pstride;
+    pstride += (size_t)rows * w[i]->N;
+  }
+  pstride = (pstride + 63) & ~size_t(63);
   hipLaunchKernelGGL((w4_gemm_rb_kernel<TMW, TNW, NX, P, MINB>), dim3(nm * nn, slices), dim3(kThreads),
                      0, stream(), reinterpret_cast<const u32x4 *>(xt), xe, sg, (int)y_bf16, rows,
                      Mp, w[0]->K, xcd_map, part, pstride);
@@ -1105,7 +1124,9 @@ struct GemmPlan {
 };
 constexpr int kMaxSplitK = 8;
 
-GemmPlan plan_gemm(const g4_w4 *const *w, int nw, int rows, bool f32x) {
+// multi_split: a K split may take several weights (their planes are left to
+// the caller, not summed).
+GemmPlan plan_gemm(const g4_w4 *const *w, int nw, int rows, bool f32x, bool multi_split = false) {
   const int cus = cu_count() > 0 ? cu_count() : 256;
   if (w[0]->G % 2 != 0) return {2, 2, 1, 1};
   bool tiled = true;  // the packed-weight kernel reads every weight's tile copy
@@ -1118,7 +1139,7 @@ GemmPlan plan_gemm(const g4_w4 *const *w, int nw, int rows, bool f32x) {
   };
   bool n96 = true;
   for (int i = 0; i < nw; ++i) n96 = n96 && w[i]->N % 96 == 0;
-  const int split_ok = nw == 1;  // a K split takes one weight
+  const int split_ok = nw == 1 || multi_split;  // summed K splits take one weight
   {
     // registers-B tiles: 128 x 192 (BF16 x) or 64 x 192 (FP32 x), split K
     // into slices of at least 8 stages while that keeps the grid within two
@@ -1210,14 +1231,14 @@ void xprep_layout(int K, int rows, bool f32x, int *Mp, size_t *eoff, size_t *xen
 }
 
 int gemm_scratch(const g4_w4 *const *w, int nw, bool f32x, int rows, bool prepped,
-                 GemmScratch *sc, const ExtScratch *ext) {
+                 GemmScratch *sc, const ExtScratch *ext, bool multi_split = false) {
   const g4_w4 *w0 = w[0];
   size_t eoff, xend;
   xprep_layout(w0->K, rows, f32x, &sc->Mp, &eoff, &xend);
   const size_t poff = prepped ? 0 : (xend + 255) & ~size_t(255);
-  sc->plan = plan_gemm(w, nw, rows, f32x);
+  sc->plan = plan_gemm(w, nw, rows, f32x, multi_split);
   const size_t part_bytes =
-      sc->plan.slices > 1 ? sc->plan.slices * splitk_pstride(rows, w0->N) * 4 : 0;
+      sc->plan.slices > 1 ? sc->plan.slices * splitk_pstride(w, nw, rows) * 4 : 0;
   void *ws = nullptr, *wx = nullptr;
   if (ext) {
     // one region: x', exponents, then the K-slice planes (x is never prepared here)
@@ -1256,24 +1277,28 @@ static int gemm_run(const g4_w4 *const *w, int nw, const void *x, bool f32x, int
   const int cus = cu_count() > 0 ? cu_count() : 256;
   long tiles64 = 0;
   for (int i = 0; i < nw; ++i) tiles64 += (long)((rows + 63) / 64) * ((w[i]->N + 63) / 64);
-  if (nw > 1 && tiles64 < cus && !glu && x) {
+  if (nw > 1 && tiles64 < cus && !glu && x && !keep) {
     for (int i = 0; i < nw; ++i)
       if (int rc = gemm_run(w + i, 1, x, f32x, rows, y + i, y_bf16, nullptr)) return rc;
     return G4_OK;
   }
   const g4_w4 *w0 = w[0];
   GemmScratch sc;
-  if (int rc = gemm_scratch(w, nw, f32x, rows, !x, &sc, ext)) return rc;
+  if (int rc = gemm_scratch(w, nw, f32x, rows, !x, &sc, ext, keep && nw > 1)) return rc;
   const GemmPlan plan = sc.plan;
   const int Mp = sc.Mp;
   uint4 *xt = sc.xt;
   int *xe = sc.xe;
   float *part = sc.part;
   const bool sum = !keep || plan.slices == 1;
-  if (keep) {
-    keep->parts = sum ? static_cast<const float *>(y[0]) : part;
-    keep->n = sum ? 1 : plan.slices;
-    keep->stride = splitk_pstride(rows, w0->N);
+  if (keep) {  // one entry per weight, planes side by side
+    size_t off = 0;
+    for (int i = 0; i < nw; ++i) {
+      keep[i].parts = sum ? static_cast<const float *>(y[i]) : part + off;
+      keep[i].n = sum ? 1 : plan.slices;
+      keep[i].stride = splitk_pstride(w, nw, rows);
+      off += (size_t)rows * w[i]->N;
+    }
   }
   if (!x)
     return f32x ? launch_planned<2>(plan, w, nw, xt, xe, rows, Mp, y, y_bf16, part, sum, glu)
@@ -1360,6 +1385,18 @@ int w4_gemm_prepare(const g4_w4 *const *w, int nw, int rows, GemmXPrep *out) {
   out->xt = static_cast<uint4 *>(wx);
   out->xe = reinterpret_cast<int *>(static_cast<char *>(wx) + eoff);
   return G4_OK;
+}
+
+int w4_gemm_multi_parts(const g4_w4 *const *w, int nw, const float *x, int rows,
+                        float *const *y, GemmParts *out) {
+  if (nw < 1 || nw > kMaxGemmSegs) return fail(G4_E_ARG, "w4_gemm_multi_parts: %d weights", nw);
+  void *ys[kMaxGemmSegs];
+  for (int i = 0; i < nw; ++i) {
+    if (w[i]->K != w[0]->K)
+      return fail(G4_E_ARG, "w4_gemm_multi_parts: in_dim %d and %d differ", w[0]->K, w[i]->K);
+    ys[i] = y[i];
+  }
+  return gemm_run(w, nw, x, true, rows, ys, false, out);
 }
 
 int w4_gemm_parts(const g4_w4 *w, const float *x, int rows, float *y, GemmParts *out) {

@@ -183,6 +183,11 @@ struct GemmParts {
   size_t stride;
 };
 int w4_gemm_parts(const g4_w4 *w, const float *x, int rows, float *y, GemmParts *out);
+// The same for up to 3 weights of one in_dim in one launch, out[i] for
+// weight i: its planes sit side by side with the others' in each slice plane
+// (the same n and stride for all), or y[i] itself when K is not split.
+int w4_gemm_multi_parts(const g4_w4 *const *w, int nw, const float *x, int rows,
+                        float *const *y, GemmParts *out);
 // FP32 rows (more than kMaxGemvRows): act = gelu(x . Wg^T) * (x . Wu^T) in one
 // launch, each tile holding the same columns of gate and up (the GEMM outputs
 // and the product as GELU_MUL computes them).

@@ -181,10 +181,46 @@ __global__ __launch_bounds__(64 * NW) void norm_rope_kernel(
                         eps, y, at_pos, blockIdx.x, red);
 }
 
+// v's RMS norm without weights (rms_row) when v is the sum of `parts` planes
+// pstride floats apart, added in plane order: thread t holds values t and
+// t + 256 (width <= 512).
+template <int NP>
+__device__ __forceinline__ void rms_parts_row(const float *__restrict__ x, int parts,
+                                              size_t pstride, int width, float eps,
+                                              float *__restrict__ y,
+                                              const int *__restrict__ pos_dev, int row,
+                                              float *red) {
+  const float *xr = x + (size_t)row * width;
+  float v[2] = {0.f, 0.f}, ss = 0.f;
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    const int i = threadIdx.x + u * kBlock;
+    if (i < width) {
+      float pa[NP];
+#pragma unroll
+      for (int sp = 0; sp < NP; ++sp) pa[sp] = xr[(size_t)(sp < parts ? sp : 0) * pstride + i];
+      v[u] = pa[0];
+#pragma unroll
+      for (int sp = 1; sp < NP; ++sp)
+        if (sp < parts) v[u] += pa[sp];
+      ss = fmaf(v[u], v[u], ss);
+    }
+  }
+  const float inv = inv_rms(block_sum(ss, red), width, eps);
+  float *yr = y + (size_t)(row + (pos_dev ? *pos_dev : 0)) * width;
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    const int i = threadIdx.x + u * kBlock;
+    if (i < width) yr[i] = v[u] * inv;
+  }
+}
+
 // The q, k and v steps of a prefill layer that owns its KV cache, in one
 // launch: blocks [0, rows * heads) the q norm + RoPE (norm_rope_row), the next
 // rows blocks the k norm + RoPE into the cache at *pos_dev + row, the last
-// rows blocks v's RMS norm without weights into the cache (rms_row).
+// rows blocks v's RMS norm without weights into the cache (rms_row).  q, k
+// and v are each the sum of `qparts` planes qpstride floats apart (the K
+// slices of their one GEMM launch).
 template <int NP>
 __global__ __launch_bounds__(kBlock) void norm_rope_qkv_kernel(
     const float *__restrict__ q, int qparts, size_t qpstride, const float *__restrict__ k,
@@ -198,8 +234,10 @@ __global__ __launch_bounds__(kBlock) void norm_rope_qkv_kernel(
     norm_rope_row<NP>(q, qparts, qpstride, heads, hd, 0, pos_dev, qscale, rope_angles, base,
                       eps, qy, 0, b, red);
   else if (b < nq + rows)
-    norm_rope_row<1>(k, 1, 0, 1, hd, 0, pos_dev, kscale, rope_angles, base, eps, kc, 1, b - nq,
-                     red);
+    norm_rope_row<NP>(k, qparts, qpstride, 1, hd, 0, pos_dev, kscale, rope_angles, base, eps, kc,
+                      1, b - nq, red);
+  else if (NP > 1)
+    rms_parts_row<NP>(v, qparts, qpstride, hd, eps, vc, pos_dev, b - nq - rows, red);
   else
     rms_row(v, hd, nullptr, eps, vc, pos_dev, b - nq - rows, red);
 }

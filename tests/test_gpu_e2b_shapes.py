@@ -35,6 +35,13 @@ LAYERS = [
     dict(head_dim=256, full=0, kv_source=0, intermediate=12288, rope_base=1e4, rope_prop=1.0),
     dict(head_dim=512, full=1, kv_source=1, intermediate=12288, rope_base=1e6, rope_prop=0.25),
 ]
+# A second sliding layer with its own cache after the global one: in the
+# prefill it takes its q/k/v input as the previous layer's prepared x', so q,
+# k and v run as one GEMM launch split over K (3 slices at head dim 256; the
+# global layer above splits in 2), whose slices the q/k/v norms add.
+LAYERS_OWN3 = LAYERS[:2] + [
+    dict(head_dim=256, full=0, kv_source=-1, intermediate=6144, rope_base=1e4, rope_prop=1.0)
+] + LAYERS[2:]
 STEPS, RPS = 24, 4096
 CASES = [(520, 576), (1000, 1024)]  # (prompt, max_seq)
 
@@ -49,11 +56,11 @@ def near_tie(logits, tok, tol=1e-3):
     return float(np.max(logits) - logits[tok]) <= tol
 
 
-def config(g4, max_seq):
+def config(g4, max_seq, specs=LAYERS):
     c = g4.GemmaConfig()
     c.hidden, c.heads, c.ple_dim, c.vocab = H, HEADS, P, V
-    c.layers, c.max_seq, c.window, c.eps, c.softcap = len(LAYERS), max_seq, WINDOW, 1e-6, 30.0
-    for i, L in enumerate(LAYERS):
+    c.layers, c.max_seq, c.window, c.eps, c.softcap = len(specs), max_seq, WINDOW, 1e-6, 30.0
+    for i, L in enumerate(specs):
         c.head_dim[i], c.intermediate[i], c.full[i] = L["head_dim"], L["intermediate"], L["full"]
         c.kv_source[i], c.rope_base[i], c.rope_prop[i] = L["kv_source"], L["rope_base"], L["rope_prop"]
     return c
@@ -68,13 +75,13 @@ def spread_gate(packed, scales, q):
     return packed, syn.bf16_rne(syn.bf16_to_f32(scales).reshape(scales.shape) * f)
 
 
-def build_model(g4, full_range=False):
-    """A 4-layer model at the E2B widths and its float64 oracle.  With
+def build_model(g4, full_range=False, specs=LAYERS):
+    """A model of the layers `specs` at the E2B widths and its float64 oracle.  With
     full_range every W4 weight and the PLE table draw q over all of [-8, 7]
     (W4 nibble 0 and PLE nibble 8 in every group), and each gate weight has
     row-spread scales (spread_gate), so the prefill's gate/up GEMM (one
     launch, gelu(gate) * up in its epilogue) runs with per-row shifts."""
-    NL = len(LAYERS)
+    NL = len(specs)
     rng = np.random.default_rng(1536)
     E = syn.bf16_rne(rng.standard_normal((V, H), dtype=np.float32) * np.float32(0.03))
     shards = [syn.ple_shard(17, s, RPS, NL * P, full_range=full_range) for s in range(V // RPS)]
@@ -88,7 +95,7 @@ def build_model(g4, full_range=False):
 
     top = w(NL * P, H)
     layers = []
-    for L in LAYERS:
+    for L in specs:
         hd, inter, shared = L["head_dim"], L["intermediate"], L["kv_source"] >= 0
         shapes = dict(q=(HEADS * hd, H), o=(H, HEADS * hd), gate=(inter, H), up=(inter, H),
                       down=(H, inter), ple_gate=(P, H), ple_proj=(H, P))
@@ -136,7 +143,7 @@ def build_model(g4, full_range=False):
     w_layers = [{name: g4.W4Linear(*pw) for name, pw in L["linear"].items()} for L in layers]
 
     def make_engine(max_seq):
-        m = g4.Gemma(config(g4, max_seq))
+        m = g4.Gemma(config(g4, max_seq, specs))
         m.set_embedding(E_dev)
         m.set_ple(t)
         m.set_linear(-1, "top", w_top)
@@ -163,10 +170,21 @@ def mid_full(g4):
     return build_model(g4, full_range=True)
 
 
+@pytest.fixture(scope="module")
+def mid_own3(g4):
+    return build_model(g4, specs=LAYERS_OWN3)
+
+
 @pytest.mark.parametrize("mode", ["graph", "eager"])
 @pytest.mark.parametrize("prompt,max_seq", CASES)
 def test_e2b_widths_prefill_past_window_then_decode_match_oracle(g4, mid, prompt, max_seq, mode):
     run_against_oracle(g4, mid, prompt, max_seq, mode)
+
+
+def test_e2b_widths_split_qkv_prefill_then_decode_match_oracle(g4, mid_own3):
+    # two layers with their own cache after the first: the prefill's one
+    # K-split q/k/v launch per layer (2 and 3 slices), then recorded steps
+    run_against_oracle(g4, mid_own3, 520, 576, "graph")
 
 
 def test_e2b_widths_full_nibble_range_match_oracle(g4, mid_full):
