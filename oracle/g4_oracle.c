@@ -2,7 +2,7 @@
  * g4_oracle.c - CPU restatement of the gemma4-js W4A16 / PLE hot path.
  *
  * TEST INFRASTRUCTURE, NOT PRODUCT CODE: loaded only by the tests, the smoke
- * check and the benchmark's CPU-baseline leg, as the checker.
+ * check and the benchmark's CPU-baseline leg, to check results against.
  *
  * Third-party algorithm restated here: the FP32 matMul of TF.js
  * (@tensorflow/tfjs-backend-cpu 4.22.0, pinned by package-lock.json:36 of the

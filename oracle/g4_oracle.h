@@ -2,9 +2,9 @@
  * g4_oracle.h - CPU restatement of the gemma4-js W4A16 / PLE hot path.
  *
  * TEST INFRASTRUCTURE, NOT PRODUCT CODE.  Only the tests, the smoke check
- * and the benchmark's CPU-baseline leg load this library, and only as the
- * checker: the product path (libg4hip) never calls it and never falls back
- * to it.
+ * and the benchmark's CPU-baseline leg load this library, and only to check
+ * results against: the product path (libg4hip) never calls it and never
+ * falls back to it.
  *
  * Every function restates one piece of the reference, cited by file:line
  * (paths relative to the gemma4-js repository root).  Plain C99, scalar,

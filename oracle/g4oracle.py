@@ -1,8 +1,8 @@
 """ctypes front end of the C oracle (g4_oracle.c).
 
 TEST INFRASTRUCTURE, NOT PRODUCT CODE: imported only by tests/, by
-__graft_entry__.smoke() and by bench.py's CPU-baseline leg, always as the
-checker; nothing in the product path calls it.
+__graft_entry__.smoke() and by bench.py's CPU-baseline leg, always to check
+results against; nothing in the product path calls it.
 
 Build recipe (also run by __graft_entry__.build()):
     gcc -O2 -std=c99 -fPIC -shared -fopenmp -ffp-contract=off oracle/g4_oracle.c -lm \

@@ -2,8 +2,8 @@
 custom-webgpu (gpu-runtime.js shaders, gemma4-webgpu.js Gemma4WebGPU).
 
 TEST INFRASTRUCTURE, NOT PRODUCT CODE: imported only by tests/ (and by
-__graft_entry__.smoke() / bench.py's CPU leg as the checker); nothing in the
-product path calls it.
+__graft_entry__.smoke() / bench.py's CPU leg, to check results against);
+nothing in the product path calls it.
 
 Arithmetic is float64 on float32 inputs: a higher-precision version of the
 FP32 shaders, used with a stated tolerance.  The exceptions follow the

@@ -1,6 +1,6 @@
 """Pins the decoder-layer oracle (oracle/layer_oracle.py) with closed forms,
 invariants and brute force, so a dropped term, a wrong sign or a swapped
-index in the restatement fails here before it is used as the checker."""
+index in the restatement fails here before results are checked against it."""
 import math
 
 import numpy as np
