@@ -288,8 +288,9 @@ __device__ __forceinline__ uint32_t deq_pair(uint32_t w, int t, f16x2 s2) {
 //
 // Split K: with gridDim.y > 1, block row blockIdx.y covers stages
 // [y * S, y * S + S) of the input dimension and writes its FP32 partial
-// products (already rescaled) to part + y * pstride, rows < M only; the
-// slices are then added in order by gemm_splitk_sum_kernel.
+// products (already rescaled) to part + y * pstride + poff[weight], rows < M
+// only; the slices are then added in order by gemm_splitk_sum_kernel (one
+// weight), or by the caller (several weights side by side in each plane).
 // Weights of one input dimension over the same x' in one launch: the n tiles
 // of weight i are t0[i] .. t0[i + 1] - 1 of the grid's tile axis.
 //
@@ -994,7 +995,8 @@ size_t splitk_pstride(const g4_w4 *const *w, int nw, int rows) {
 }
 
 // n weights (1..kMaxGemmSegs) of one input dimension, y[i] receiving weight
-// i's output; a K split (slices > 1) takes one weight.
+// i's output; a K split (slices > 1) that is summed here takes one weight,
+// one left to the caller (sum false) any number.
 template <int TM, int TN, int NX, int KS, int P>
 int launch_gemm(const g4_w4 *const *w, int nw, const uint4 *xt, const int *xe, int rows, int Mp,
                 void *const *ys, bool y_bf16, float *part, int slices, bool sum, bool glu) {

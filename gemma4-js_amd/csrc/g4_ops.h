@@ -22,9 +22,10 @@ int launch_gelu_ple(const float *gate, const float *ple, int rows, int layer, in
 int launch_norm_rope(const float *x, int rows, int heads, int hd, int pos0, const int *pos_dev,
                      const float *scale, int rope_angles, float base, float eps, float *y,
                      bool at_pos, int parts = 1, size_t pstride = 0);
-// A prefill layer's q norm + RoPE (q the sum of qparts planes), k norm + RoPE
-// into the cache at *pos_dev + row, and v's RMS norm (no weights) into the
-// cache, in one launch.
+// A prefill layer's q norm + RoPE, k norm + RoPE into the cache at
+// *pos_dev + row, and v's RMS norm (no weights) into the cache, in one
+// launch.  q, k and v are each the sum of qparts planes qpstride floats apart
+// (the K slices of one GEMM launch; head dim at most 512).
 int launch_norm_rope_qkv(const float *q, int qparts, size_t qpstride, const float *k,
                          const float *v, int rows, int heads, int hd, const int *pos_dev,
                          const float *qscale, const float *kscale, int rope_angles, float base,
