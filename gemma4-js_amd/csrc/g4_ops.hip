@@ -1068,13 +1068,10 @@ __global__ __launch_bounds__(kBlock) void ple_mix_kernel(const float *__restrict
 // one wave and the four sums are added in order.  (512-token prefill, 17920
 // chunks of 256: 18.6 against 21.1 us; one-token decode, 35 chunks: the
 // block form, 3.5 against 5.7 us.)
-__global__ __launch_bounds__(kBlock) void ple_mix_rows_kernel(const float *__restrict__ proj,
-                                                         float pre_scale,
-                                                         const float *__restrict__ norm_scale,
-                                                         const float *__restrict__ token_ple,
-                                                         int width, int chunks, float eps,
-                                                         float ple_scale, float out_scale,
-                                                         float *__restrict__ y) {
+__global__ __launch_bounds__(kBlock) void ple_mix_rows_kernel(
+    const float *__restrict__ proj, float pre_scale, const float *__restrict__ norm_scale,
+    const float *__restrict__ token_ple, int width, int chunks, float eps, float ple_scale,
+    float out_scale, float *__restrict__ y) {
   const int lane = threadIdx.x & 63;
   const int ck = blockIdx.x * (kBlock / 64) + (threadIdx.x >> 6);
   if (ck >= chunks) return;  // whole waves
