@@ -235,6 +235,28 @@ def test_ple_mix(g4):
                                lo.ple_mix(proj, s, tok, rows, width, layers), rtol=1e-5, atol=1e-6)
 
 
+@pytest.mark.parametrize("rows,width", [(40, 256), (33, 300)])
+def test_ple_mix_many_chunks_match_oracle_and_one_row_calls(g4, rows, width):
+    # rows x 35 layers >= 1024 chunks take one wave per chunk; each one-row
+    # call (35 chunks) takes one block per chunk.  Both add the squares in
+    # the same order, so the rows must agree bit for bit.
+    layers = 35
+    rng = np.random.default_rng(14)
+    proj = rng.standard_normal((rows, layers * width)).astype(np.float32) * 0.3
+    tok = rng.standard_normal((rows, layers * width)).astype(np.float32) * 0.05
+    s = rng.uniform(0.5, 1.5, width).astype(np.float32)
+    sd = dev(g4, s)
+    y = out(g4, rows * layers * width)
+    g4.ple_mix(dev(g4, proj), sd, dev(g4, tok), rows, width, layers, y)
+    got = y.download(np.float32).reshape(rows, -1)
+    np.testing.assert_allclose(got, lo.ple_mix(proj, s, tok, rows, width, layers),
+                               rtol=1e-5, atol=1e-6)
+    for r in (0, rows // 2, rows - 1):
+        y1 = out(g4, layers * width)
+        g4.ple_mix(dev(g4, proj[r:r + 1]), sd, dev(g4, tok[r:r + 1]), 1, width, layers, y1)
+        np.testing.assert_array_equal(y1.download(np.float32), got[r])
+
+
 def test_embed_bit_exact_and_bad_id(g4):
     vocab, width = 5000, 1536
     rng = np.random.default_rng(13)
