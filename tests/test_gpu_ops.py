@@ -82,7 +82,8 @@ def test_gelu_ple(g4):
 
 @pytest.mark.parametrize("rows,heads,hd,pos0,prop,base", [
     (1, 8, 256, 0, 1.0, 1e4), (1, 8, 256, 37, 1.0, 1e4), (3, 8, 512, 5, 0.25, 1e6),
-    (2, 1, 256, 700, 1.0, 1e4), (1, 1, 512, 767, 0.25, 1e6), (4, 2, 64, 3, 0.5, 100.0)])
+    (2, 1, 256, 700, 1.0, 1e4), (1, 1, 512, 767, 0.25, 1e6), (4, 2, 64, 3, 0.5, 100.0),
+    (2, 3, 130, 9, 1.0, 1e4), (1, 2, 384, 11, 0.5, 1e6)])  # 65 / 192 pairs: 2 / 4 waves
 def test_norm_rope(g4, rows, heads, hd, pos0, prop, base):
     rng = np.random.default_rng([rows, heads, hd, pos0])
     x = rng.standard_normal((rows, heads * hd)).astype(np.float32) * 2
